@@ -1,0 +1,262 @@
+"""Batch-1 Qwen3-4B-shape decode on one MI355X: tokens/s, ms/token and the
+fraction of the HBM roofline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload: a random-init bf16 model of the Qwen3-4B
+architecture (36 layers, hidden 2560, intermediate 9728, 32/8 heads, head
+dim 128, vocab 151936, tied embeddings, QK-norm, RoPE theta 5e6, weights
+~N(0, 0.02), seed 0), batch 1, a prompt of 128 random ids (seed 1),
+greedy decode where every token is one replay of the captured HIP graph.
+A step is one replay: the whole model streams once (8,044,544,000 weight
+bytes). W untimed replays, then exactly K timed replays bracketed by
+synchronisation; ms_per_step = time / K.
+
+Also reported, on the same JSON line:
+  roofline      the dominant kernel (fused add + RMSNorm + gate_up + SwiGLU),
+                launched over all 36 layers' weights (3.6 GB, beyond the
+                256 MB Infinity Cache) and timed with HIP events on its stream;
+                achieved = algorithmic bytes per launch / average launch time.
+  cpu_baseline  the CPU oracle (the reference's torch fallback restated) decoding
+                a bounded sample of the same workload on this host's cores,
+                from the GPU's prefill KV cache and the same weights.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gate_up_bytes(b: int, h: int, inter: int, sk: int) -> int:
+    """Algorithmic bytes of one fused gate_up launch: the [2I, H] weight, the
+    prologue's fp32 partials + bf16 residual + gain, the bf16 residual it
+    writes, and the [B, I] bf16 activation out."""
+    return 2 * (2 * inter) * h + b * h * (4 * sk + 2 + 2) + 2 * h + 2 * b * inter
+
+
+def time_dominant_kernel(model, b: int, reps: int = 3):
+    """Average duration of the fused gate_up launch, measured with HIP
+    events on the launching stream, over every layer's weights."""
+    import torch
+    from enginekernel_amd import ek_kernels as K
+
+    bufs = model.buffers(b)
+    c = model.cfg
+    res_a, res_b = bufs.res
+    bufs.o_parts.normal_(0, 0.05)
+    res_b.normal_(0, 0.5)
+    stream = torch.cuda.current_stream()
+
+    def one_pass():
+        for lay in model.layers:
+            K.parts_norm_gemv(bufs.o_parts, res_b, res_a, lay["ln2"], lay["gu"], c.rms_eps, silu=True,
+                              out=bufs.act)
+
+    one_pass()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        one_pass()
+    end.record(stream)
+    end.synchronize()
+    n = reps * len(model.layers)
+    avg_s = start.elapsed_time(end) / 1e3 / n
+    nbytes = gate_up_bytes(b, c.hidden_size, c.intermediate_size, bufs.sk_o)
+    return avg_s, nbytes, n
+
+
+def cpu_baseline(tensors, cfg, kv, first_tok, positions, s, gpu_tokens, budget_s=15.0):
+    """The oracle's decode loop (engine.py:721-743 restated) on this host's
+    cores, from the GPU prefill's KV cache, teacher-forced with the GPU's
+    tokens. Times whole decode steps (argmax included), prefill excluded."""
+    import torch
+    from oracle import ek_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
+    k_cpu, v_cpu = kv
+    b = 1
+    st = O.EagerState.__new__(O.EagerState)
+    st.k, st.v = k_cpu, v_cpu
+    st.positions = positions.clone()
+    st.slot_t = torch.zeros(b, dtype=torch.int64)
+    st.len_t = torch.full((1,), s, dtype=torch.int64)
+    st.start_t = torch.zeros(b, dtype=torch.int32)
+    tok = first_tok.clone()
+    times, agree = [], 0
+    t_start = time.perf_counter()
+    with torch.inference_mode():
+        for i in range(len(gpu_tokens)):
+            t0 = time.perf_counter()
+            hidden = om.decode(tok, st.positions, st.k, st.v, st.slot_t, st.len_t, st.start_t)
+            nxt = O.argmax_token(hidden, om.lm_head)
+            times.append(time.perf_counter() - t0)
+            agree += int(nxt.item() == gpu_tokens[i])
+            tok = torch.tensor([gpu_tokens[i]], dtype=torch.int64)
+            st.positions = st.positions + 1
+            if time.perf_counter() - t_start > budget_s and i >= 3:
+                break
+    timed = times[1:] if len(times) > 2 else times      # the first step warms caches
+    per = sum(timed) / len(timed)
+    cpu_model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(b / per, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+        "ms_per_token": round(per * 1e3, 2),
+        "sample": (f"{len(timed)} timed decode steps (of {len(times)} run) of config 4 at context "
+                   f"{s + 1}..{s + len(times)}, batch 1, torch CPU oracle, {cpu_model}"),
+        "agree_with_gpu": f"{agree}/{len(times)}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=511)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--layers", type=int, default=0, help="override the layer count (diagnostics only)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from enginekernel_amd import checkpoint as C
+    from enginekernel_amd.ek_model import Qwen3
+    from enginekernel_amd.engine import MAX_STEPS, _FastEngine
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    cfg = dict(C.QWEN3_4B)
+    if args.layers:
+        cfg["num_hidden_layers"] = args.layers
+    w_bytes = C.weight_bytes_per_token(cfg)
+    K_steps, W = args.steps, args.warmup
+    if W + K_steps + 1 > MAX_STEPS:
+        sys.exit(f"warmup + steps must stay below {MAX_STEPS}")
+
+    t0 = time.perf_counter()
+    tensors = C.random_weights(cfg, seed=0)
+    log(f"random weights generated in {time.perf_counter() - t0:.1f}s")
+    t0 = time.perf_counter()
+    model = Qwen3(None, dev, tensors=tensors, config=cfg)
+    torch.cuda.synchronize()
+    log(f"weights uploaded in {time.perf_counter() - t0:.1f}s")
+    eng = _FastEngine(model=model)
+
+    b, s = 1, args.prompt
+    g = torch.Generator().manual_seed(1)
+    prompt = [torch.randint(0, cfg["vocab_size"], (s,), generator=g).tolist()]
+    total = s + W + K_steps + 1
+    with torch.inference_mode():
+        ids, pos, pad, s, bias = eng._pack(prompt)
+        eng._ensure_cache(b, total)
+        t0 = time.perf_counter()
+        graph = eng._get_graph(b, total)
+        log(f"graph captured in {time.perf_counter() - t0:.1f}s (bucket {graph.bucket})")
+        first = eng._first_token(ids, pos, b, s, bias)
+        graph.tokens.copy_(first)
+        graph.positions.fill_(s)
+        graph.start_t.zero_()
+        graph.len_t.fill_(s)
+        graph.step_idx.zero_()
+        for _ in range(W):
+            graph.graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_wall = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(K_steps):
+            graph.graph.replay()
+        ev1.record(stream)
+        ev1.synchronize()
+        wall = time.perf_counter() - t_wall
+        step_s = ev0.elapsed_time(ev1) / 1e3 / K_steps
+        log(f"{K_steps} replays: {step_s * 1e3:.4f} ms/step (wall {wall / K_steps * 1e3:.4f})")
+        tokens = graph.out_buf[: W + K_steps, 0].cpu().tolist()
+        if graph.step_idx.item() != W + K_steps:
+            raise RuntimeError("graph step counter out of step with the replays")
+
+        dom_s, dom_bytes, dom_n = time_dominant_kernel(model, b)
+        log(f"gate_up kernel: {dom_s * 1e6:.2f} us over {dom_n} launches")
+
+        cpu = None
+        if not args.no_cpu:
+            n_kv = s + 1
+            kv = ([t[0:1, :, :n_kv].cpu().clone() for t in eng.k_cache],
+                  [t[0:1, :, :n_kv].cpu().clone() for t in eng.v_cache])
+            # the caches the oracle extends need room for the sampled steps
+            room = 64
+            kv = ([torch.cat([t, torch.zeros(1, t.shape[1], room, t.shape[3], dtype=t.dtype)], 2) for t in kv[0]],
+                  [torch.cat([t, torch.zeros(1, t.shape[1], room, t.shape[3], dtype=t.dtype)], 2) for t in kv[1]])
+            log("timing the CPU oracle baseline")
+            # GPU step 1 decoded token `first` at context s+1 and emitted tokens[0]
+            cpu = cpu_baseline(tensors, cfg, kv, first.cpu(), torch.tensor([s], dtype=torch.int64), s,
+                               tokens[:room], budget_s=args.cpu_budget)
+
+    achieved = dom_bytes / dom_s
+    line = {
+        "metric": "batch-1 decode tokens/sec + ms/token and % of HBM roofline, Qwen3-4B shape",
+        "value": round(b / step_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K_steps,
+        "warmup": W,
+        "ms_per_step": round(step_s * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights ~N(0,0.02) seed 0, random prompt ids seed 1)",
+        "config": {
+            "workload": "config 4: Qwen3-4B-architecture bf16 greedy decode, one hipGraph replay per token",
+            "batch": b, "prompt_len": s, "context_at_timed_steps": [s + W + 1, s + W + K_steps],
+            "layers": cfg["num_hidden_layers"], "hidden": cfg["hidden_size"],
+            "intermediate": cfg["intermediate_size"], "heads": [cfg["num_attention_heads"], cfg["num_key_value_heads"]],
+            "vocab": cfg["vocab_size"],
+        },
+        "ms_per_token": round(step_s * 1e3, 4),
+        "weight_bytes_per_token": w_bytes,
+        "hbm_roofline_frac": round(w_bytes / step_s / PEAK_HBM, 4),
+        "roofline": {
+            "bound": "hbm", "kernel": "gemv_kernel<PRO_PARTS,EPI_SWIGLU> (add+RMSNorm+gate_up+SwiGLU)",
+            "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+            "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_s * 1e6, 3), "launches": dom_n,
+        },
+        "cpu_baseline": cpu,
+        "first_tokens": tokens[:8],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

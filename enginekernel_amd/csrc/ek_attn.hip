@@ -1,0 +1,388 @@
+// Split-K decode attention over the static KV cache, for gfx950.
+//
+// The reference's fallback (engine/ek_model.py:475-488) rounds the softmax
+// probabilities to bf16 before the PV product: p = bf16(exp(s - M) / L) with
+// M, L the max and sum over ALL keys of the row. A one-pass flash-decode
+// cannot round there (it only knows M and L at the end), so the build splits
+// the work into two launches over the same (split, kv-head, batch) grid:
+//
+//   phase 1  [rope_attn_decode's prologue] QK-norm + RoPE of the G query
+//            heads of this kv head (and, in the split owning the new slot,
+//            of the new key, which is written to the cache with the raw
+//            value), then fp32 scores s_n = (q . k_n) * scale for the
+//            split's keys -> a score scratch row, plus the split's running
+//            max m and sum l = sum exp(s - m).
+//   phase 2  M = max_s m_s, L = sum_s l_s exp(m_s - M) from all splits;
+//            p_n = bf16(exp(s_n - M) / L); acc = sum p_n v_n (fp32) for the
+//            split's keys; the last workgroup to arrive for a (batch, kv
+//            head) adds the split partials in split order and rounds to bf16.
+//
+// Bytes: K is read once (phase 1), V once (phase 2); the score scratch adds
+// 4 bytes per key per query head (16 B per key at G = 4, against 4*D = 512 B
+// of K+V). Lane layout: D/8 lanes hold one key row (16 B each), so a wave
+// reads 64/(D/8) keys per load instruction (4 keys, 1 KiB, at D = 128); the
+// dot products are folded over those D/8 lanes with a butterfly.
+//
+// Keys below start[b] (left padding) are never read. The owner split uses
+// the new key from LDS rather than re-reading the slot it just wrote.
+
+#include "ek_common.h"
+#include "ek_abi_internal.h"
+#include "ek_hip.h"
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int NW = NT / EK_WAVE;
+constexpr int UNR = 4;   // key steps in flight per lane
+
+struct AttnParams {
+  const bf16_t* q; int64_t ldq_b; int64_t ldq_h;
+  int rope;
+  const bf16_t* qn; const bf16_t* kn;
+  const bf16_t* cos; const bf16_t* sin; int64_t ld_cs; const int64_t* positions; int64_t rope_len;
+  bf16_t* kc; bf16_t* vc; int64_t csb, csh, css, s_cap;
+  const int64_t* seq_len; const int32_t* start;
+  float* scores; int64_t score_ss;
+  float* acc; float* lsum; float* mmax; int32_t* counters; int64_t sp, gp;
+  bf16_t* out; int64_t ldo_b, ldo_h;
+  int nq, nkv, splits; int64_t chunk;
+  float sm_scale, eps;
+};
+
+struct Range { int64_t lo, hi, len; };
+
+__device__ __forceinline__ Range key_range(const AttnParams& p, int s, int b) {
+  int64_t len = *p.seq_len;
+  len = len < 0 ? 0 : (len > p.s_cap ? p.s_cap : len);
+  int64_t st = p.start[b];
+  st = st < 0 ? 0 : st;
+  int64_t lo = (int64_t)s * p.chunk;
+  int64_t hi = (s == p.splits - 1) ? len : (lo + p.chunk < len ? lo + p.chunk : len);
+  Range r;
+  r.len = len;
+  r.lo = lo;
+  r.hi = hi;
+  return r;
+}
+
+// QK-norm + rotate-half RoPE of one head (one wave); writes the bf16-valued
+// result as fp32 to `dst` (LDS) and, if `gdst`, as bf16 to global memory.
+template <int D>
+__device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w, const bf16_t* cr,
+                                               const bf16_t* sr, float eps, float* dst, bf16_t* gdst) {
+  constexpr int PER = D > 64 ? D / 64 : 1;
+  constexpr int HALF = D / 2;
+  const int lane = threadIdx.x & 63;
+  float xv[PER], xp[PER];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = lane + 64 * i;
+    const bool ok = d < D;
+    const int pd = d < HALF ? d + HALF : d - HALF;
+    xv[i] = ok ? bf2f(x[d]) : 0.f;
+    xp[i] = ok ? bf2f(x[pd]) : 0.f;
+    ss = fmaf(xv[i], xv[i], ss);
+  }
+  ss = wave_sum(ss);
+  const float rstd = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int d = lane + 64 * i;
+    if (d >= D) continue;
+    const int pd = d < HALF ? d + HALF : d - HALF;
+    const float tn = rbf(bf2f(w[d]) * rbf(xv[i] * rstd));
+    const float tp = rbf(bf2f(w[pd]) * rbf(xp[i] * rstd));
+    const float rot = d < HALF ? -tp : tp;
+    const float o = rbf(rbf(tn * bf2f(cr[d])) + rbf(rot * bf2f(sr[d])));
+    dst[d] = o;
+    if (gdst) gdst[d] = (bf16_t)f2bf(o);
+  }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
+  constexpr int LPK = D / 8;         // lanes per key row
+  constexpr int KPW = EK_WAVE / LPK; // keys per wave per load
+  constexpr int KPB = NW * KPW;      // keys per workgroup per load
+  __shared__ float qs[G][D];
+  __shared__ float knew[D];
+  __shared__ float stm[NW * KPW][G];
+  __shared__ float stl[NW * KPW][G];
+
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const Range rg = key_range(p, s, b);
+  const int64_t slot = rg.len - 1;
+  const bool owns = p.rope && slot >= rg.lo && slot < rg.hi;
+  int64_t st = p.start[b];
+  st = st < 0 ? 0 : st;
+  const int64_t lo = rg.lo > st ? rg.lo : st;
+  const int64_t hi = rg.hi;
+
+  if (p.rope) {
+    const bf16_t* row = p.q + b * p.ldq_b;
+    int64_t crow = p.positions ? p.positions[b] : b;
+    crow = crow < 0 ? 0 : (crow >= p.rope_len ? p.rope_len - 1 : crow);
+    const bf16_t* cr = p.cos + crow * p.ld_cs;
+    const bf16_t* sr = p.sin + crow * p.ld_cs;
+    const int units = G + (owns ? 2 : 0);
+    for (int u = wave; u < units; u += NW) {
+      if (u < G) {
+        head_norm_rope<D>(row + (int64_t)(h * G + u) * D, p.qn, cr, sr, p.eps, qs[u], nullptr);
+      } else if (u == G) {
+        bf16_t* kdst = p.kc + b * p.csb + h * p.csh + slot * p.css;
+        head_norm_rope<D>(row + (int64_t)(p.nq + h) * D, p.kn, cr, sr, p.eps, knew, kdst);
+      } else {
+        const bf16_t* vsrc = row + (int64_t)(p.nq + p.nkv + h) * D;
+        bf16_t* vdst = p.vc + b * p.csb + h * p.csh + slot * p.css;
+        for (int d = lane; d < D; d += EK_WAVE) vdst[d] = vsrc[d];
+      }
+    }
+  } else {
+    for (int i = tid; i < G * D; i += NT)
+      qs[i / D][i % D] = bf2f(p.q[b * p.ldq_b + (int64_t)(h * G + i / D) * p.ldq_h + i % D]);
+  }
+  __syncthreads();
+
+  const int sub = lane % LPK, grp = lane / LPK;
+  float qr[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qr[g][j] = qs[g][sub * 8 + j];
+  float kn8[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kn8[j] = owns ? knew[sub * 8 + j] : 0.f;
+
+  float mr[G], lr[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) { mr[g] = -1e30f; lr[g] = 0.f; }
+
+  const bf16_t* kb = p.kc + b * p.csb + h * p.csh + sub * 8;
+  float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
+  for (int64_t n0 = lo + wave * KPW + grp; n0 < hi; n0 += (int64_t)KPB * UNR) {
+    uint4 kv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t n = n0 + (int64_t)u * KPB;
+      kv[u] = (n < hi) ? ld16(kb + n * p.css) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t n = n0 + (int64_t)u * KPB;
+      const bool valid = n < hi;
+      float kf[8];
+      unpack8(kv[u], kf);
+      if (owns && n == slot) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) kf[j] = kn8[j];
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) d = fmaf(qr[g][j], kf[j], d);
+        d = group_sum<LPK>(d);
+        const float sc = d * p.sm_scale;
+        if (valid) {
+          if (sub == (g % LPK)) scb[(int64_t)g * p.score_ss + n] = sc;
+          const float mn = fmaxf(mr[g], sc);
+          lr[g] = lr[g] * expf(mr[g] - mn) + expf(sc - mn);
+          mr[g] = mn;
+        }
+      }
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      stm[wave * KPW + grp][g] = mr[g];
+      stl[wave * KPW + grp][g] = lr[g];
+    }
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -1e30f;
+    for (int i = 0; i < NW * KPW; ++i) M = fmaxf(M, stm[i][tid]);
+    float L = 0.f;
+    for (int i = 0; i < NW * KPW; ++i) L += stl[i][tid] * expf(stm[i][tid] - M);
+    const int64_t o = (((int64_t)b * p.nkv + h) * p.sp + s) * p.gp + tid;
+    p.mmax[o] = M;
+    p.lsum[o] = L;
+  }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
+  constexpr int LPK = D / 8;
+  constexpr int KPW = EK_WAVE / LPK;
+  constexpr int KPB = NW * KPW;
+  __shared__ float Ms[G], Ls[G];
+  __shared__ float red[NW][G][D];
+  __shared__ int last_flag;
+
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const Range rg = key_range(p, s, b);
+  int64_t st = p.start[b];
+  st = st < 0 ? 0 : st;
+  const int64_t lo = rg.lo > st ? rg.lo : st;
+  const int64_t hi = rg.hi;
+  const int64_t hbase = ((int64_t)b * p.nkv + h) * p.sp;
+
+  if (tid < G) {
+    float M = -1e30f;
+    for (int s2 = 0; s2 < p.splits; ++s2) M = fmaxf(M, p.mmax[(hbase + s2) * p.gp + tid]);
+    float L = 0.f;
+    for (int s2 = 0; s2 < p.splits; ++s2) {
+      const int64_t o = (hbase + s2) * p.gp + tid;
+      L += p.lsum[o] * expf(p.mmax[o] - M);
+    }
+    Ms[tid] = M;
+    Ls[tid] = L;
+  }
+  __syncthreads();
+  float Mr[G], Lr[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) { Mr[g] = Ms[g]; Lr[g] = Ls[g]; }
+
+  const int sub = lane % LPK, grp = lane / LPK;
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
+
+  const bf16_t* vb = p.vc + b * p.csb + h * p.csh + sub * 8;
+  const float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
+  for (int64_t n0 = lo + wave * KPW + grp; n0 < hi; n0 += (int64_t)KPB * UNR) {
+    uint4 vv[UNR];
+    float sv[UNR][G];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t n = n0 + (int64_t)u * KPB;
+      const bool valid = n < hi;
+      vv[u] = valid ? ld16(vb + n * p.css) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int g = 0; g < G; ++g) sv[u][g] = valid ? scb[(int64_t)g * p.score_ss + n] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t n = n0 + (int64_t)u * KPB;
+      if (n >= hi) continue;
+      float vf[8];
+      unpack8(vv[u], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = rbf(expf(sv[u][g] - Mr[g]) / Lr[g]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pr, vf[j], acc[g][j]);
+      }
+    }
+  }
+  // fold the key groups of the wave (lanes with equal `sub`)
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float v = acc[g][j];
+#pragma unroll
+      for (int o = LPK; o < EK_WAVE; o <<= 1) v += __shfl_xor(v, o, EK_WAVE);
+      acc[g][j] = v;
+    }
+  if (grp == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) red[wave][g][sub * 8 + j] = acc[g][j];
+  }
+  __syncthreads();
+  const bool single = p.splits == 1;
+  for (int i = tid; i < G * D; i += NT) {
+    const int g = i / D, d = i % D;
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += red[w][g][d];
+    if (single) p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d] = (bf16_t)f2bf(t);
+    else p.acc[((hbase + s) * p.gp + g) * D + d] = t;
+  }
+  if (single) return;
+  if (!last_to_arrive(p.counters + (int64_t)b * p.nkv + h, p.splits, &last_flag)) return;
+  for (int i = tid; i < G * D; i += NT) {
+    const int g = i / D, d = i % D;
+    float t = 0.f;
+    for (int s2 = 0; s2 < p.splits; ++s2)
+      t += __hip_atomic_load(p.acc + ((hbase + s2) * p.gp + g) * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d] = (bf16_t)f2bf(t);
+  }
+}
+
+template <int D, int G>
+hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
+  dim3 grid((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);
+  hipLaunchKernelGGL((attn_scores_kernel<D, G>), grid, dim3(NT), 0, st, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((attn_pv_kernel<D, G>), grid, dim3(NT), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_attn_g(const AttnParams& p, int g, int b, hipStream_t st) {
+  switch (g) {
+    case 1: return launch_attn<D, 1>(p, b, st);
+    case 2: return launch_attn<D, 2>(p, b, st);
+    case 4: return launch_attn<D, 4>(p, b, st);
+    case 8: return launch_attn<D, 8>(p, b, st);
+    default: return ek_fail(hipErrorInvalidValue, "attn: query heads per kv head must be 1, 2, 4 or 8");
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
+                   const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
+                   void* k_cache, void* v_cache, int64_t csb, int64_t csh, int64_t css, int64_t s_cap,
+                   const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* acc,
+                   float* lsum, float* mmax, int32_t* counters, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
+                   int64_t ldo_h, int64_t b, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits,
+                   int64_t chunk, float sm_scale, float eps, void* stream) {
+  EK_GUARD();
+  if (b < 1 || b > 65535 || n_kv < 1 || n_q < n_kv || n_q % n_kv)
+    return ek_fail(hipErrorInvalidValue, "attn: bad batch or head counts");
+  const int64_t g = n_q / n_kv;
+  if (splits < 1 || splits > sp || chunk < 1 || g > gp)
+    return ek_fail(hipErrorInvalidValue, "attn: splits/chunk exceed the workspace");
+  if (score_ss < s_cap) return ek_fail(hipErrorInvalidValue, "attn: score scratch shorter than the cache");
+  if (rope && (!qn || !kn || !cos || !sin || rope_len < 1))
+    return ek_fail(hipErrorInvalidValue, "attn: rope mode needs qn, kn, cos, sin");
+  if (css % 8 || csh % 8 || csb % 8 || (reinterpret_cast<uintptr_t>(k_cache) & 15) ||
+      (reinterpret_cast<uintptr_t>(v_cache) & 15))
+    return ek_fail(hipErrorInvalidValue, "attn: cache rows must be 16-byte aligned");
+  AttnParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = (const bf16_t*)q; p.ldq_b = ldq_b; p.ldq_h = ldq_h; p.rope = rope;
+  p.qn = (const bf16_t*)qn; p.kn = (const bf16_t*)kn;
+  p.cos = (const bf16_t*)cos; p.sin = (const bf16_t*)sin; p.ld_cs = ld_cs; p.positions = positions;
+  p.rope_len = rope_len;
+  p.kc = (bf16_t*)k_cache; p.vc = (bf16_t*)v_cache; p.csb = csb; p.csh = csh; p.css = css; p.s_cap = s_cap;
+  p.seq_len = seq_len; p.start = start;
+  p.scores = scores; p.score_ss = score_ss;
+  p.acc = acc; p.lsum = lsum; p.mmax = mmax; p.counters = counters; p.sp = sp; p.gp = gp;
+  p.out = (bf16_t*)out; p.ldo_b = ldo_b; p.ldo_h = ldo_h;
+  p.nq = (int)n_q; p.nkv = (int)n_kv; p.splits = (int)splits; p.chunk = chunk;
+  p.sm_scale = sm_scale; p.eps = eps;
+  hipStream_t st = (hipStream_t)stream;
+  switch (head_dim) {
+    case 32: return launch_attn_g<32>(p, (int)g, (int)b, st);
+    case 64: return launch_attn_g<64>(p, (int)g, (int)b, st);
+    case 128: return launch_attn_g<128>(p, (int)g, (int)b, st);
+    default: return ek_fail(hipErrorInvalidValue, "attn: head_dim must be 32, 64 or 128");
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,96 @@
+// Shared device helpers for the gfx950 decode kernels.
+//
+// bf16 values travel as raw 16-bit patterns (uint16_t) so that every
+// rounding point is explicit: bf2f widens exactly, f2bf rounds to nearest
+// even once. bf16 x bf16 products are exact in fp32 (8+8 significant bits),
+// so an fp32 FMA chain over bf16 operands rounds only the running sum.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define EK_WAVE 64
+
+typedef uint16_t bf16_t;
+
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// round an fp32 value to the nearest bf16 and widen it back
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// the low / high bf16 of a packed 32-bit word, widened
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  f[0] = lo_bf(v.x); f[1] = hi_bf(v.x);
+  f[2] = lo_bf(v.y); f[3] = hi_bf(v.y);
+  f[4] = lo_bf(v.z); f[5] = hi_bf(v.z);
+  f[6] = lo_bf(v.w); f[7] = hi_bf(v.w);
+}
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+
+// sum of 8 products of two packed-bf16 chunks, added to acc in order
+__device__ __forceinline__ float dot8_acc(const uint4& w, const uint4& x, float acc) {
+  acc = fmaf(lo_bf(w.x), lo_bf(x.x), acc);
+  acc = fmaf(hi_bf(w.x), hi_bf(x.x), acc);
+  acc = fmaf(lo_bf(w.y), lo_bf(x.y), acc);
+  acc = fmaf(hi_bf(w.y), hi_bf(x.y), acc);
+  acc = fmaf(lo_bf(w.z), lo_bf(x.z), acc);
+  acc = fmaf(hi_bf(w.z), hi_bf(x.z), acc);
+  acc = fmaf(lo_bf(w.w), lo_bf(x.w), acc);
+  acc = fmaf(hi_bf(w.w), hi_bf(x.w), acc);
+  return acc;
+}
+
+// butterfly sum over all 64 lanes of a wave (every lane gets the total)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, EK_WAVE);
+  return v;
+}
+
+// butterfly sum over aligned groups of `width` lanes (width a power of two)
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, EK_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, EK_WAVE));
+  return v;
+}
+
+// 16-byte global load of 8 bf16
+__device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+// Release this workgroup's global writes and count it in; returns true in
+// the last workgroup to arrive (which then observes every other
+// workgroup's writes). The counter is reset by that last workgroup, so it
+// is zero again when the next launch that uses it starts. Every thread of
+// the workgroup must call this.
+__device__ __forceinline__ bool last_to_arrive(int* counter, int total, int* lds_flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    int last = (prev == total - 1);
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = last;
+  }
+  __syncthreads();
+  bool last = *lds_flag != 0;
+  if (last) __threadfence();
+  return last;
+}

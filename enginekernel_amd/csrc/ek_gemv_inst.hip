@@ -1,0 +1,57 @@
+// One (prologue, epilogue) pair of the GEMV family, instantiated over batch
+// tiles, chunks per lane and rows per wave. The build compiles this file
+// once per pair with -DEK_PRO=<prologue> -DEK_EPI=<epilogue> so that the
+// instantiations compile in parallel.
+
+#include "ek_gemv_impl.h"
+
+#ifndef EK_PRO
+#error "compile with -DEK_PRO=<prologue> -DEK_EPI=<epilogue>"
+#endif
+
+namespace ekg {
+namespace {
+
+template <int PRO, int EPI, int BM, int KPL, int RPW>
+hipError_t launch_t(const GemvParams& p, dim3 grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_kernel<PRO, EPI, BM, KPL, RPW>), grid, dim3(NTHR), lds, st, p);
+  return hipGetLastError();
+}
+
+template <int PRO, int EPI, int BM, int RPW>
+hipError_t launch_k(const GemvParams& p, int kpl, dim3 grid, size_t lds, hipStream_t st) {
+  switch (kpl) {
+    case 1: return launch_t<PRO, EPI, BM, 1, RPW>(p, grid, lds, st);
+    case 5: return launch_t<PRO, EPI, BM, 5, RPW>(p, grid, lds, st);
+    case 8: return launch_t<PRO, EPI, BM, 8, RPW>(p, grid, lds, st);
+    case 19: return launch_t<PRO, EPI, BM, 19, RPW>(p, grid, lds, st);
+    default: return launch_t<PRO, EPI, BM, 4, RPW>(p, grid, lds, st);
+  }
+}
+
+template <int PRO, int EPI, int BM>
+hipError_t launch_r(const GemvParams& p, int kpl, int rpw, dim3 grid, size_t lds, hipStream_t st) {
+  if (rpw == 1) return launch_k<PRO, EPI, BM, 1>(p, kpl, grid, lds, st);
+  if (rpw == 2) return launch_k<PRO, EPI, BM, 2>(p, kpl, grid, lds, st);
+  return launch_k<PRO, EPI, BM, 4>(p, kpl, grid, lds, st);
+}
+
+template <int PRO, int EPI>
+hipError_t launch_b(const GemvParams& p, int bm, int kpl, int rpw, dim3 grid, size_t lds, hipStream_t st) {
+  switch (bm) {
+    case 1: return launch_r<PRO, EPI, 1>(p, kpl, rpw, grid, lds, st);
+    case 2: return launch_r<PRO, EPI, 2>(p, kpl, rpw, grid, lds, st);
+    case 4: return launch_r<PRO, EPI, 4>(p, kpl, rpw, grid, lds, st);
+    default: return launch_r<PRO, EPI, 8>(p, kpl, rpw, grid, lds, st);
+  }
+}
+
+}  // namespace
+
+template <>
+hipError_t launch_pair<EK_PRO, EK_EPI>(const GemvParams& p, int bm, int kpl, int rpw, dim3 grid, size_t lds,
+                                       hipStream_t st) {
+  return launch_b<EK_PRO, EK_EPI>(p, bm, kpl, rpw, grid, lds, st);
+}
+
+}  // namespace ekg

@@ -1,0 +1,491 @@
+"""The reference's ek_kernels call surface, on hand-written gfx950 HIP kernels.
+
+Same function names, argument order and return conventions as
+jeojdi1/EngineKernel `engine/ek_kernels.py` (cited per function), so a caller
+of that module can import this one instead. Every function launches through
+the C ABI of libek_hip.so (include/ek_hip.h) on torch's current stream; none
+has a CPU fallback: on CPU tensors or without the library they raise.
+
+Shapes are checked on the host before any launch, so a wrong shape is a
+Python exception rather than a kernel reading out of bounds.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import _hip
+from ._hip import HipKernelError, HipUnavailable, call, ptr, stream
+
+__all__ = [
+    "has_hip", "probe_hip", "disable_hip", "has_triton", "probe_triton", "disable_triton",
+    "rms_norm", "add_rms_norm", "silu_mul", "qk_norm_rope_kv", "gemv", "gemv_parts",
+    "add_rms_norm_parts", "gemv_swiglu", "norm_gemv", "flash_decode", "rope_attn_decode",
+    "plan_splits", "group_pad", "attn_warps", "make_workspace", "parts_norm_gemv",
+    "embed_norm_gemv", "lm_head_argmax", "_next_pow2", "_cdiv", "_torch_rms_norm",
+    "HipUnavailable", "HipKernelError",
+]
+
+_DISABLED = False
+_BF16 = torch.bfloat16
+
+
+# ----------------------------------------------------------------------------
+# availability (ek_kernels.py:44-70: has_triton / disable_triton / probe_triton)
+# ----------------------------------------------------------------------------
+def has_hip() -> bool:
+    return not _DISABLED and _hip.available()
+
+
+def disable_hip() -> None:
+    global _DISABLED
+    _DISABLED = True
+
+
+def probe_hip() -> bool:
+    """Load the library and run one kernel on the GPU (ek_kernels.py:53-70)."""
+    global _DISABLED
+    if _DISABLED or not torch.cuda.is_available():
+        return False
+    try:
+        x = torch.ones(2, 64, device="cuda", dtype=_BF16)
+        w = torch.ones(64, device="cuda", dtype=_BF16)
+        y = rms_norm(x, w, 1e-6)
+        torch.cuda.synchronize()
+        if not torch.isfinite(y.float()).all():
+            raise RuntimeError("bad output")
+    except Exception:
+        _DISABLED = True
+    return not _DISABLED
+
+
+# the reference's names for the same three functions
+has_triton = has_hip
+disable_triton = disable_hip
+probe_triton = probe_hip
+
+
+def _next_pow2(n: int) -> int:
+    """ek_kernels.py:73-77."""
+    p = 1
+    while p < n:
+        p <<= 1
+    return p
+
+
+def _cdiv(a: int, b: int) -> int:
+    """ek_kernels.py:80-81."""
+    return -(-a // b)
+
+
+def _torch_rms_norm(x, w, eps):
+    """The RMSNorm formula of ek_kernels.py:1025-1028, exported (as the
+    reference exports it) for callers' own comparisons. No kernel path here
+    calls it."""
+    xf = x.float()
+    xn = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xn.to(x.dtype)
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _gpu(*ts) -> None:
+    if _DISABLED:
+        raise HipUnavailable("HIP kernels were disabled (disable_hip())")
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise HipUnavailable("enginekernel_amd kernels run on the GPU only; got a CPU tensor")
+
+
+def _rows(t, name: str, dtype=_BF16):
+    _need(t.dtype == dtype, f"{name}: expected {dtype}, got {t.dtype}")
+    _need(t.dim() >= 1 and t.stride(-1) == 1, f"{name}: last dimension must be contiguous")
+    return t
+
+
+# ----------------------------------------------------------------------------
+# norms and activations
+# ----------------------------------------------------------------------------
+def rms_norm(x, w, eps):
+    """ek_kernels.py:1031-1042 -> y = w (x) bf16(x * rsqrt(mean(x^2) + eps))."""
+    _gpu(x, w)
+    shape = x.shape
+    x2 = _rows(x.reshape(-1, shape[-1]), "rms_norm x")
+    y = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    call("ek_rms_norm", ptr(x2), ptr(w.contiguous()), ptr(y), x2.shape[0], shape[-1], x2.stride(0),
+         y.stride(0), float(eps), stream())
+    return y.view(shape)
+
+
+def add_rms_norm(x, residual, w, eps):
+    """ek_kernels.py:1045-1059: residual += x (bf16, in place); returns
+    (rmsnorm(residual) * w, residual)."""
+    _gpu(x, residual, w)
+    shape = x.shape
+    x2 = _rows(x.reshape(-1, shape[-1]), "add_rms_norm x")
+    r2 = _rows(residual.view(-1, shape[-1]), "add_rms_norm residual")
+    y = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    call("ek_add_rms_norm", ptr(x2), ptr(r2), ptr(w.contiguous()), ptr(y), x2.shape[0], shape[-1],
+         x2.stride(0), r2.stride(0), y.stride(0), float(eps), stream())
+    return y.view(shape), residual
+
+
+def silu_mul(gu):
+    """ek_kernels.py:1062-1076: gu [..., 2I] -> bf16(silu(gate)) (x) up, [..., I]."""
+    _gpu(gu)
+    shape = list(gu.shape)
+    n = shape[-1] // 2
+    x2 = _rows(gu.reshape(-1, shape[-1]), "silu_mul")
+    y = torch.empty(x2.shape[0], n, dtype=gu.dtype, device=gu.device)
+    call("ek_silu_mul", ptr(x2), ptr(y), x2.shape[0], n, x2.stride(0), y.stride(0), stream())
+    shape[-1] = n
+    return y.view(shape)
+
+
+def qk_norm_rope_kv(qkv, qn, kn, cos, sin, k_cache, v_cache, slot_base, n_q, n_kv, eps, m_per_batch):
+    """ek_kernels.py:1110-1146: QK-norm + rotary on the fused QKV rows, q in
+    place, rotated k and raw v written to the caches at slot_base[b] + row.
+    Slots outside the cache are skipped."""
+    _gpu(qkv, k_cache, v_cache, slot_base)
+    d = qn.shape[0]
+    m = qkv.shape[0]
+    _rows(qkv, "qkv")
+    _need(qkv.shape[1] >= (n_q + 2 * n_kv) * d, "qkv: too narrow for the head counts")
+    _need(cos.shape[0] >= m and sin.shape[0] >= m and cos.stride(0) == sin.stride(0), "cos/sin rows")
+    _need(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(), "k/v cache layouts differ")
+    _need(k_cache.stride(-1) == 1 and k_cache.shape[1] == n_kv and k_cache.shape[3] == d, "cache shape")
+    _need(m % m_per_batch == 0 and slot_base.dtype == torch.int64 and
+          slot_base.numel() >= m // m_per_batch, "slot_base")
+    _need(k_cache.shape[0] >= m // m_per_batch, "cache batch")
+    call("ek_qk_norm_rope_kv", ptr(qkv), ptr(qn), ptr(kn), ptr(cos), ptr(sin), ptr(k_cache), ptr(v_cache),
+         ptr(slot_base), m, qkv.stride(0), cos.stride(0), n_q, n_kv, d, k_cache.stride(0),
+         k_cache.stride(1), k_cache.stride(2), k_cache.shape[2], m_per_batch, float(eps), stream())
+    return qkv
+
+
+# ----------------------------------------------------------------------------
+# projections
+# ----------------------------------------------------------------------------
+def _check_proj(x, w, name):
+    _gpu(x, w)
+    _rows(x, name + " x")
+    _rows(w, name + " w")
+    _need(x.dim() == 2 and w.dim() == 2 and x.shape[1] == w.shape[1], f"{name}: x [M,K] and w [N,K] disagree")
+    _need(x.shape[1] % 8 == 0, f"{name}: K must be a multiple of 8")
+
+
+def gemv(x, w, out=None, cfg=None):
+    """ek_kernels.py:1322-1347: x [M, K], w [N, K] -> bf16 [M, N] (fp32 accumulate).
+    `cfg` (the reference's Triton block sizes) is accepted and ignored."""
+    _check_proj(x, w, "gemv")
+    m, k = x.shape
+    n = w.shape[0]
+    y = torch.empty(m, n, device=x.device, dtype=x.dtype) if out is None else out
+    _need(y.shape == (m, n) and y.stride(-1) == 1, "gemv: out shape")
+    call("ek_gemv", ptr(x), ptr(w), ptr(y), m, n, k, x.stride(0), w.stride(0), y.stride(0), stream())
+    return y
+
+
+def gemv_parts(x, w, sk=None, out=None):
+    """ek_kernels.py:1277-1293: fp32 split-K partials [sk, M, N] (M <= 8).
+    sk defaults to the fewest splits whose activation rows fit the LDS
+    stage (1 at batch 1: on gfx950 one wave streams a whole row of K). `out`
+    (optional, contiguous fp32 [sk, M, N]) receives the partials."""
+    _check_proj(x, w, "gemv_parts")
+    m, k = x.shape
+    n = w.shape[0]
+    sk = int(sk or os.environ.get("ENGINE_SPLIT_K", "0") or parts_splits(m, k))
+    _need(1 <= m <= 8, "gemv_parts: M must be 1..8")
+    _need(k % (8 * sk) == 0, "gemv_parts: K must split into multiples of 8")
+    parts = torch.empty(sk, m, n, device=x.device, dtype=torch.float32) if out is None else out
+    _need(parts.shape == (sk, m, n) and parts.is_contiguous() and parts.dtype == torch.float32, "parts out")
+    call("ek_gemv_parts", ptr(x), ptr(w), ptr(parts), m, n, k, x.stride(0), w.stride(0), sk, stream())
+    return parts
+
+
+ACT_STAGE_BYTES = 48 * 1024   # the kernels' per-workgroup activation stage
+
+
+def parts_splits(m: int, k: int) -> int:
+    """Smallest split-K count whose per-split activation rows (m padded to
+    1/2/4/8, times K / sk bf16) fit the kernels' LDS activation stage."""
+    bm = 1 if m <= 1 else 2 if m <= 2 else 4 if m <= 4 else 8
+    sk = 1
+    while bm * (k // sk) * 2 > ACT_STAGE_BYTES or (k % (8 * sk)):
+        sk += 1
+        if sk > k // 8:
+            raise ValueError(f"no split of K={k} fits {m} rows")
+    return sk
+
+
+def add_rms_norm_parts(parts, residual, w, eps):
+    """ek_kernels.py:1296-1304: residual += bf16(sum(parts)) in place;
+    returns (norm * w, residual)."""
+    _gpu(parts, residual, w)
+    sk, m, n = parts.shape
+    _need(parts.dtype == torch.float32 and parts.is_contiguous(), "parts: contiguous fp32 [sk, M, N]")
+    _rows(residual, "residual")
+    _need(residual.shape == (m, n), "residual shape")
+    y = torch.empty(m, n, device=parts.device, dtype=residual.dtype)
+    call("ek_add_rms_norm_parts", ptr(parts), ptr(residual), ptr(w), ptr(y), sk, m, n, residual.stride(0),
+         y.stride(0), float(eps), stream())
+    return y, residual
+
+
+def gemv_swiglu(x, w):
+    """ek_kernels.py:1247-1261: w is the fused [2I, K] gate/up matrix ->
+    bf16(silu(bf16 gate)) (x) bf16(up), [M, I] (M <= 8)."""
+    _check_proj(x, w, "gemv_swiglu")
+    m, k = x.shape
+    i = w.shape[0] // 2
+    _need(1 <= m <= 8, "gemv_swiglu: M must be 1..8")
+    y = torch.empty(m, i, device=x.device, dtype=x.dtype)
+    call("ek_gemv_swiglu", ptr(x), ptr(w), ptr(y), m, i, k, x.stride(0), w.stride(0), y.stride(0), stream())
+    return y
+
+
+def norm_gemv(x, residual, norm_w, w, eps, silu=False):
+    """ek_kernels.py:1220-1244: y = proj(rmsnorm(x + residual)); returns
+    (y, x + residual). residual=None: no add (the returned residual is x).
+    silu=True: w is the fused [2I, K] gate/up matrix and y = silu(gate)*up."""
+    _check_proj(x, w, "norm_gemv")
+    m, k = x.shape
+    _need(1 <= m <= 8, "norm_gemv: M must be 1..8")
+    n = w.shape[0] // 2 if silu else w.shape[0]
+    y = torch.empty(m, n, device=x.device, dtype=x.dtype)
+    has_add = residual is not None
+    r_out = torch.empty_like(x) if has_add else x
+    if has_add:
+        _rows(residual, "residual")
+    call("ek_norm_gemv", ptr(x), ptr(residual) if has_add else None, ptr(r_out) if has_add else None,
+         ptr(norm_w), ptr(w), ptr(y), m, n, k, x.stride(0), residual.stride(0) if has_add else 0,
+         r_out.stride(0), w.stride(0), y.stride(0), float(eps), 1 if silu else 0, stream())
+    return y, r_out
+
+
+def parts_norm_gemv(parts, residual, residual_out, norm_w, w, eps, silu=False, out=None, rpw=0):
+    """The decode layer's fused consumer: r = bf16(residual + bf16(sum parts))
+    -> residual_out; y = proj(rmsnorm(r) * norm_w) [+ SwiGLU]. The
+    composition of add_rms_norm_parts (ek_kernels.py:1296) with gemv (:1322)
+    or gemv_swiglu (:1247) in one launch. residual_out must not alias
+    residual (other workgroups still read it)."""
+    _gpu(parts, residual, residual_out, w)
+    sk, m, k = parts.shape
+    _need(parts.dtype == torch.float32 and parts.is_contiguous(), "parts: contiguous fp32")
+    _need(residual.shape == (m, k) and residual_out.shape == (m, k), "residual shapes")
+    _need(residual.data_ptr() != residual_out.data_ptr(), "residual_out must not alias residual")
+    _need(w.shape[1] == k and w.stride(-1) == 1, "w shape")
+    n = w.shape[0] // 2 if silu else w.shape[0]
+    y = torch.empty(m, n, device=parts.device, dtype=_BF16) if out is None else out
+    call("ek_parts_norm_gemv", ptr(parts), sk, ptr(residual), ptr(residual_out), ptr(norm_w), ptr(w), ptr(y),
+         m, n, k, residual.stride(0), residual_out.stride(0), w.stride(0), y.stride(0), float(eps),
+         1 if silu else 0, rpw, stream())
+    return y
+
+
+def embed_norm_gemv(tokens, embed, residual_out, norm_w, w, eps, slot_t=None, len_t=None, out=None, rpw=0):
+    """The decode step's first projection: residual_out = embed[tokens];
+    y = proj(rmsnorm(residual_out) * norm_w). With slot_t/len_t it also
+    performs the step's `slot_t <- len_t; len_t += 1` (ek_model.py:375-376)."""
+    _gpu(tokens, embed, residual_out, w)
+    m = tokens.shape[0]
+    k = embed.shape[1]
+    _need(tokens.dtype == torch.int64 and tokens.is_contiguous(), "tokens: int64")
+    _need(w.shape[1] == k and residual_out.shape == (m, k), "shapes")
+    if len_t is not None:
+        _need(slot_t is not None and slot_t.dtype == torch.int64 and len_t.dtype == torch.int64
+              and slot_t.numel() >= m, "slot_t/len_t")
+    n = w.shape[0]
+    y = torch.empty(m, n, device=tokens.device, dtype=_BF16) if out is None else out
+    call("ek_embed_norm_gemv", ptr(tokens), ptr(embed), embed.stride(0), embed.shape[0], ptr(residual_out),
+         ptr(norm_w), ptr(w), ptr(y), m, n, k, residual_out.stride(0), w.stride(0), y.stride(0), float(eps),
+         ptr(slot_t) if len_t is not None else None, ptr(len_t), rpw, stream())
+    return y
+
+
+class ArgmaxScratch:
+    """Per-workgroup partials and the arrival counter of lm_head_argmax."""
+
+    def __init__(self, m: int, vocab: int, device, rpw: int = 4):
+        self.rpw = rpw
+        blocks = _cdiv(vocab, 4 * rpw)
+        self.cap = blocks * m
+        self.val = torch.empty(self.cap, dtype=torch.float32, device=device)
+        self.idx = torch.empty(self.cap, dtype=torch.int32, device=device)
+        self.counter = torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def lm_head_argmax(hidden, lm_head, scratch: ArgmaxScratch, out_tok=None, logits=None,
+                   parts=None, residual=None, norm_w=None, eps=1e-6, state=None, max_steps=0):
+    """ek_model.py:490-493 argmax_token as one kernel: bf16 logits and the
+    first-index argmax. With parts/residual/norm_w the final add + RMSNorm
+    (ek_model.py:413-416) runs in its prologue instead of taking `hidden`.
+    state = (tokens, positions, out_buf, step_idx) also performs the graph
+    step's bookkeeping (engine.py:289-292)."""
+    fused = parts is not None
+    src = residual if fused else hidden
+    _gpu(src, lm_head)
+    m, k = src.shape
+    vocab = lm_head.shape[0]
+    _need(lm_head.shape[1] == k and lm_head.stride(-1) == 1, "lm_head shape")
+    _need(1 <= m <= 8, "lm_head_argmax: M must be 1..8")
+    _need(scratch.cap >= _cdiv(vocab, 4 * scratch.rpw) * m, "argmax scratch too small")
+    if out_tok is None:
+        out_tok = torch.empty(m, dtype=torch.int64, device=src.device)
+    if logits is not None:
+        _need(logits.shape == (m, vocab) and logits.stride(-1) == 1 and logits.dtype == _BF16, "logits")
+    st = (None,) * 4
+    if state is not None:
+        tokens, positions, out_buf, step_idx = state
+        _need(out_buf.dtype == torch.int32 and out_buf.shape[1] == m and out_buf.is_contiguous(), "out_buf")
+        st = (tokens, positions, out_buf, step_idx)
+        max_steps = out_buf.shape[0]
+    if fused:
+        _need(parts.dtype == torch.float32 and parts.is_contiguous() and parts.shape[1:] == (m, k), "parts")
+    call("ek_lm_head_argmax", ptr(hidden) if not fused else None, ptr(parts) if fused else None,
+         parts.shape[0] if fused else 0, ptr(residual) if fused else None, ptr(norm_w) if fused else None,
+         float(eps), ptr(lm_head), m, vocab, k, 0 if fused else hidden.stride(0),
+         residual.stride(0) if fused else 0, lm_head.stride(0), ptr(logits),
+         logits.stride(0) if logits is not None else 0, ptr(scratch.val), ptr(scratch.idx), scratch.cap,
+         ptr(scratch.counter), ptr(out_tok), ptr(st[0]), ptr(st[1]), ptr(st[2]), ptr(st[3]), max_steps,
+         scratch.rpw, stream())
+    return out_tok
+
+
+# ----------------------------------------------------------------------------
+# attention
+# ----------------------------------------------------------------------------
+_SMS = None
+
+
+def _sm_count() -> int:
+    """Compute units of device 0 (ek_kernels.py:1158-1163); 256 on MI355X."""
+    global _SMS
+    if _SMS is None:
+        _SMS = (torch.cuda.get_device_properties(0).multi_processor_count
+                if torch.cuda.is_available() else 256)
+    return _SMS
+
+
+def group_pad(n_heads: int, n_kv: int) -> int:
+    """ek_kernels.py:1350-1352 (the padded query-group size of the workspace)."""
+    return max(16, _next_pow2(n_heads // n_kv))
+
+
+def attn_warps() -> int:
+    """ek_kernels.py:1384-1386. The HIP kernels always run 4 waves of 64."""
+    return int(os.environ.get("ENGINE_ATTN_WARPS", "0")) or 4
+
+
+def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta: int = 0):
+    """ek_kernels.py:1355-1381: (splits, chunk, block_n). Aims for two
+    workgroups per compute unit across (batch x kv heads x splits); one
+    split when batch x kv heads already covers 0.8 of the CUs; chunk is a
+    multiple of block_n with splits * chunk >= bucket."""
+    sms = _sm_count()
+    target_cta = target_cta or int(os.environ.get("ENGINE_ATTN_CTA", "0")) or 2 * sms
+    base = batch * n_kv
+    if base >= sms * float(os.environ.get("ENGINE_ATTN_FILL", "0.8")):
+        splits = 1
+    else:
+        splits = max(1, min(32, _cdiv(target_cta, base)))
+    if not block_n:
+        block_n = int(os.environ.get("ENGINE_ATTN_BLOCK", "0"))
+    if not block_n:
+        block_n = 128 if (splits == 1 and base <= sms) else 64
+    splits = max(1, min(splits, _cdiv(bucket, block_n)))
+    chunk = _cdiv(_cdiv(bucket, splits), block_n) * block_n
+    return splits, chunk, block_n
+
+
+def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, device, splits=None, chunk=None):
+    """The attention workspace: the reference's 7-tuple (acc, lsum, mmax, out,
+    splits, chunk, block_n) of engine.py:273-282, extended with the score
+    scratch [B, n_q, bucket] fp32 and the per-(b, kv head) arrival counters."""
+    s, c, bn = plan_splits(b, n_kv, bucket)
+    if splits is not None:
+        s = splits
+        c = chunk if chunk is not None else _cdiv(bucket, s)
+    sp = _next_pow2(s)
+    gp = group_pad(n_q, n_kv)
+    acc = torch.zeros((b, n_kv, sp, gp, head_dim), dtype=torch.float32, device=device)
+    lsum = torch.zeros((b, n_kv, sp, gp), dtype=torch.float32, device=device)
+    mmax = torch.full((b, n_kv, sp, gp), -1e30, dtype=torch.float32, device=device)
+    out = torch.empty((b, n_q, head_dim), dtype=_BF16, device=device)
+    scores = torch.empty((b, n_q, bucket), dtype=torch.float32, device=device)
+    counters = torch.zeros(b * n_kv, dtype=torch.int32, device=device)
+    return (acc, lsum, mmax, out, s, c, bn, scores, counters)
+
+
+_SCRATCH: dict = {}
+
+
+def _attn_scratch(ws, b, n_q, n_kv, s_cap, device):
+    """Score scratch and counters for a reference-style 7-tuple workspace
+    (allocated once per shape; eager callers only)."""
+    if len(ws) >= 9:
+        return ws[7], ws[8]
+    key = (device, b, n_q, n_kv, s_cap)
+    if key not in _SCRATCH:
+        _SCRATCH[key] = (torch.empty((b, n_q, s_cap), dtype=torch.float32, device=device),
+                         torch.zeros(b * n_kv, dtype=torch.int32, device=device))
+    return _SCRATCH[key]
+
+
+def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, seq_len_t, start_t,
+          workspace, sm_scale, n_q, eps):
+    acc, lsum, mmax, out, splits, chunk, _block_n = workspace[:7]
+    b = out.shape[0]
+    n_kv, s_cap, d = k_cache.shape[1], k_cache.shape[2], k_cache.shape[3]
+    _need(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(), "k/v cache layouts differ")
+    _need(k_cache.dtype == _BF16 and k_cache.stride(-1) == 1 and k_cache.shape[0] >= b, "cache")
+    _need(n_q % n_kv == 0 and out.shape[1] == n_q and out.shape[2] == d, "head counts / workspace")
+    _need(acc.shape[:2] == (b, n_kv) and acc.shape[2] >= splits and acc.is_contiguous(), "acc workspace")
+    _need(lsum.shape == acc.shape[:4] and mmax.shape == acc.shape[:4], "lsum/mmax workspace")
+    _need(splits * chunk >= 1, "splits/chunk")
+    _need(seq_len_t.dtype == torch.int64 and start_t.dtype == torch.int32 and start_t.numel() >= b, "len/start")
+    scores, counters = _attn_scratch(workspace, b, n_q, n_kv, s_cap, out.device)
+    _need(scores.shape[0] >= b and scores.shape[1] == n_q and scores.is_contiguous(), "score scratch")
+    # the workspace bounds the attended length, as the reference's chunk plan does
+    s_cap = min(s_cap, scores.shape[2])
+    _need(counters.numel() >= b * n_kv, "counters")
+    ld_cs = cos.stride(0) if cos is not None else 0
+    rope_len = cos.shape[0] if cos is not None else 0
+    call("ek_attn_decode", ptr(q), ldq_b, ldq_h, rope, ptr(qn), ptr(kn), ptr(cos), ptr(sin), ld_cs,
+         ptr(positions), rope_len, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+         k_cache.stride(2), s_cap, ptr(seq_len_t), ptr(start_t), ptr(scores), scores.stride(1), ptr(acc),
+         ptr(lsum), ptr(mmax), ptr(counters), acc.shape[2], acc.shape[3], ptr(out), out.stride(0),
+         out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), stream())
+    return out
+
+
+def flash_decode(q, k_cache, v_cache, seq_len_t, start_t, workspace, sm_scale):
+    """ek_kernels.py:1389-1416: q [B, HQ, D] (already rotated); caches
+    [B, HKV, S, D]; seq_len_t (int64 [1]) / start_t (int32 [B]) on device.
+    Keys [start_b, seq_len) are attended. Returns workspace's out [B, HQ, D]."""
+    _gpu(q, k_cache, v_cache)
+    _rows(q, "q")
+    return _attn(q, q.stride(0), q.stride(1), 0, None, None, None, None, None, k_cache, v_cache,
+                 seq_len_t, start_t, workspace, sm_scale, q.shape[1], 0.0)
+
+
+def rope_attn_decode(qkv, qn, kn, cos, sin, k_cache, v_cache, seq_len_t, start_t, workspace,
+                     sm_scale, n_q, eps, positions=None):
+    """ek_kernels.py:1476-1507: QK-norm + rotary + cache write + decode
+    attention from the raw fused QKV rows [B, (n_q + 2*n_kv)*D]; seq_len_t
+    already counts the new token. cos/sin are per-row [B, D] tables, or the
+    full tables when `positions` (int64 [B]) selects the rows."""
+    _gpu(qkv, k_cache, v_cache)
+    _rows(qkv, "qkv")
+    n_kv, d = k_cache.shape[1], k_cache.shape[3]
+    _need(qkv.shape[1] >= (n_q + 2 * n_kv) * d, "qkv too narrow")
+    _need(cos.stride(0) == sin.stride(0) and cos.shape == sin.shape and cos.shape[1] >= d, "cos/sin")
+    if positions is None:
+        _need(cos.shape[0] >= qkv.shape[0], "cos/sin need a row per batch row")
+    return _attn(qkv, qkv.stride(0), d, 1, qn, kn, cos, sin, positions, k_cache, v_cache, seq_len_t,
+                 start_t, workspace, sm_scale, n_q, eps)

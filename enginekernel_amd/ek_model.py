@@ -1,0 +1,318 @@
+"""Qwen3 on the gfx950 decode kernels: the reference's ek_model API.
+
+Same class names, constructor and methods as jeojdi1/EngineKernel
+`engine/ek_model.py` (cited per method): Qwen3Config(path), Qwen3(path,
+device, dtype) with .prefill, .decode, .argmax_token, .ensure_rope,
+.use_gemv_for and the fused-weight layer dicts (qkv/o/gu/down and their
+transposed views, ln1/ln2/qn/kn). Additions: Qwen3.from_random (seeded
+random-init weights), Qwen3.step (the whole graph step, argmax and
+bookkeeping included).
+
+The decode step is six launches per layer, every one a hand-written HIP
+kernel (ek_kernels):
+    embed|parts+add+norm+qkv  ->  attention phase 1 (QK-norm, RoPE, KV write,
+    scores)  ->  attention phase 2 (softmax, PV, split combine)  ->  o_proj
+    ->  parts+add+norm+gate_up+SwiGLU  ->  down_proj
+then one lm_head + final norm + argmax + step-advance launch. The residual
+stream ping-pongs between two buffers so that the one workgroup writing the
+new residual never races the workgroups still reading the old one.
+
+The prefill (out of this build's hot-path scope) runs the same norms and
+RoPE/KV-write kernels with torch (hipBLASLt) projections and an fp32 attention.
+"""
+
+from __future__ import annotations
+
+import glob
+import json
+import os
+
+import torch
+import torch.nn.functional as F
+
+from . import ek_kernels as K
+from .checkpoint import random_weights
+
+
+class Qwen3Config:
+    """ek_model.py:26-42, plus transformers-5's `rope_parameters.rope_theta`
+    (a config.json written by transformers 5 has no top-level rope_theta)."""
+
+    def __init__(self, path: str | None = None, cfg: dict | None = None):
+        if cfg is None:
+            with open(os.path.join(path, "config.json")) as f:
+                cfg = json.load(f)
+        self.raw = dict(cfg)
+        self.hidden_size = cfg["hidden_size"]
+        self.num_layers = cfg["num_hidden_layers"]
+        self.num_heads = cfg["num_attention_heads"]
+        self.num_kv_heads = cfg["num_key_value_heads"]
+        self.head_dim = cfg.get("head_dim", self.hidden_size // self.num_heads)
+        self.intermediate_size = cfg["intermediate_size"]
+        self.vocab_size = cfg["vocab_size"]
+        self.rms_eps = cfg.get("rms_norm_eps", 1e-6)
+        theta = cfg.get("rope_theta")
+        if theta is None:
+            theta = (cfg.get("rope_parameters") or {}).get("rope_theta", 10000.0)
+        self.rope_theta = float(theta)
+        self.tie_embeddings = cfg.get("tie_word_embeddings", False)
+        self.max_position = cfg.get("max_position_embeddings", 32768)
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+
+
+def shard_map(path: str) -> dict:
+    """ek_model.py:45-60: tensor name -> safetensors file."""
+    index = os.path.join(path, "model.safetensors.index.json")
+    if os.path.exists(index):
+        with open(index) as f:
+            return json.load(f)["weight_map"]
+    files = sorted(glob.glob(os.path.join(path, "*.safetensors")))
+    if not files:
+        raise FileNotFoundError(f"no safetensors under {path}")
+    from safetensors import safe_open
+
+    out = {}
+    for fn in files:
+        with safe_open(fn, framework="pt", device="cpu") as f:
+            for k in f.keys():
+                out[k] = os.path.basename(fn)
+    return out
+
+
+def load_tensors(path: str, dtype=torch.bfloat16) -> dict:
+    """Every tensor of a local HF checkpoint, on the CPU, as `dtype`."""
+    from safetensors import safe_open
+
+    wmap = shard_map(path)
+    out = {}
+    for fn in sorted(set(wmap.values())):
+        with safe_open(os.path.join(path, fn), framework="pt", device="cpu") as f:
+            for k in f.keys():
+                out[k] = f.get_tensor(k).to(dtype)
+    return out
+
+
+def fuse_layer(tensors: dict, i: int) -> dict:
+    """ek_model.py:139-160: q/k/v and gate/up concatenated along the output
+    dimension ([out, in] row-major, a contiguous K per output row)."""
+    p = f"model.layers.{i}."
+    qkv = torch.cat([tensors[p + "self_attn.q_proj.weight"], tensors[p + "self_attn.k_proj.weight"],
+                     tensors[p + "self_attn.v_proj.weight"]], dim=0).contiguous()
+    gu = torch.cat([tensors[p + "mlp.gate_proj.weight"], tensors[p + "mlp.up_proj.weight"]], dim=0).contiguous()
+    return {
+        "qkv": qkv, "gu": gu,
+        "o": tensors[p + "self_attn.o_proj.weight"].contiguous(),
+        "down": tensors[p + "mlp.down_proj.weight"].contiguous(),
+        "ln1": tensors[p + "input_layernorm.weight"].contiguous(),
+        "ln2": tensors[p + "post_attention_layernorm.weight"].contiguous(),
+        "qn": tensors[p + "self_attn.q_norm.weight"].contiguous(),
+        "kn": tensors[p + "self_attn.k_norm.weight"].contiguous(),
+    }
+
+
+def rope_tables(head_dim: int, theta: float, max_len: int, dtype=torch.bfloat16):
+    """ek_model.py:164-174, computed on the CPU (fp32, then rounded to bf16)
+    so that every device sees the same bytes."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    t = torch.arange(max_len, dtype=torch.float32)
+    freqs = torch.outer(t, inv)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype).contiguous(), emb.sin().to(dtype).contiguous()
+
+
+class _StepBuffers:
+    """Activations of one decode step at batch b (allocated once, reused by
+    every step and by graph captures)."""
+
+    def __init__(self, cfg: Qwen3Config, b: int, device):
+        h = cfg.hidden_size
+        bf = torch.bfloat16
+        self.res = (torch.empty(b, h, dtype=bf, device=device), torch.empty(b, h, dtype=bf, device=device))
+        self.qkv = torch.empty(b, cfg.q_size + 2 * cfg.kv_size, dtype=bf, device=device)
+        self.sk_o = K.parts_splits(b, cfg.q_size)
+        self.sk_down = K.parts_splits(b, cfg.intermediate_size)
+        self.o_parts = torch.empty(self.sk_o, b, h, dtype=torch.float32, device=device)
+        self.act = torch.empty(b, cfg.intermediate_size, dtype=bf, device=device)
+        self.down_parts = torch.empty(self.sk_down, b, h, dtype=torch.float32, device=device)
+        self.hidden = torch.empty(b, h, dtype=bf, device=device)
+        self.argmax = K.ArgmaxScratch(b, cfg.vocab_size, device)
+        self.next_tok = torch.empty(b, dtype=torch.int64, device=device)
+
+
+class Qwen3(torch.nn.Module):
+    """ek_model.py:63-115 (constructor), on the HIP kernels only."""
+
+    MAX_ROWS = 8   # rows per decode launch (the kernels' batch tile)
+
+    def __init__(self, model_path: str | None, device: torch.device, dtype=torch.bfloat16, *,
+                 tensors: dict | None = None, config: dict | None = None):
+        super().__init__()
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise K.HipUnavailable("Qwen3 runs on the HIP kernels and needs a GPU device")
+        if not K.has_hip():
+            raise K.HipUnavailable("libek_hip.so is not loadable or no GPU is visible")
+        self.cfg = Qwen3Config(model_path, config)
+        self.device = device
+        self.dtype = dtype
+        if tensors is None:
+            tensors = load_tensors(model_path, dtype)
+        self._load(tensors)
+        self._build_rope(self.cfg.max_position if self.cfg.max_position <= 16384 else 16384)
+        self.sm_scale = self.cfg.head_dim ** -0.5
+        self.zero_slot = torch.zeros(1024, dtype=torch.int64, device=device)
+        self._bufs: dict = {}
+        # the prefill's hipBLASLt projections: no reduced-precision bf16 reductions
+        torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
+
+    @classmethod
+    def from_random(cls, config: dict, device, seed: int = 0, dtype=torch.bfloat16):
+        """A seeded random-init model (weights ~N(0, 0.02), norm gains 1)."""
+        return cls(None, device, dtype, tensors=random_weights(config, seed), config=config)
+
+    # ------------------------------------------------------------------
+    def _load(self, tensors: dict):
+        """ek_model.py:117-162, from CPU tensors: fuse per layer, then upload."""
+        c, dev = self.cfg, self.device
+        self.embed = tensors["model.embed_tokens.weight"].to(dev, self.dtype).contiguous()
+        self.final_norm = tensors["model.norm.weight"].to(dev, self.dtype).contiguous()
+        self.lm_head = (self.embed if c.tie_embeddings
+                        else tensors["lm_head.weight"].to(dev, self.dtype).contiguous())
+        self.lm_head_t = self.lm_head.t()
+        self.layers = []
+        for i in range(c.num_layers):
+            lay = {k: v.to(dev, self.dtype) for k, v in fuse_layer(tensors, i).items()}
+            for key in ("qkv", "o", "gu", "down"):
+                lay[key + "_t"] = lay[key].t()
+            self.layers.append(lay)
+
+    def _build_rope(self, max_len: int):
+        cos, sin = rope_tables(self.cfg.head_dim, self.cfg.rope_theta, max_len, self.dtype)
+        self.cos = cos.to(self.device)
+        self.sin = sin.to(self.device)
+        self.rope_len = max_len
+
+    def ensure_rope(self, max_len: int):
+        """ek_model.py:176-178."""
+        if max_len > self.rope_len:
+            self._build_rope(max(max_len, self.rope_len * 2))
+
+    def use_gemv_for(self, rows: int) -> bool:
+        """ek_model.py:214-266 chose Triton or cuBLAS by timing. Here the
+        decode projections are always the HIP kernels, for 1..MAX_ROWS rows."""
+        return 1 <= rows <= self.MAX_ROWS
+
+    def buffers(self, b: int) -> _StepBuffers:
+        if b not in self._bufs:
+            self._bufs[b] = _StepBuffers(self.cfg, b, self.device)
+        return self._bufs[b]
+
+    # ------------------------------------------------------------------
+    def _prefill_attn(self, q, k, v, attn_bias):
+        """Causal GQA attention of the prompt in fp32 (q [B, HQ, S, D] bf16,
+        k/v [B, HKV, S, D]); the stand-in for the reference's SDPA call
+        (ek_model.py:315-323). Query rows with no visible key (left padding)
+        attend to themselves so that their K/V stay finite."""
+        b, hq, s, d = q.shape
+        rep = hq // k.shape[1]
+        qf = q.float().contiguous()
+        kf = k.float().repeat_interleave(rep, 1).transpose(-1, -2).contiguous()
+        vf = v.float().repeat_interleave(rep, 1).contiguous()
+        scores = torch.matmul(qf, kf) * self.sm_scale
+        if attn_bias is None:
+            allow = torch.ones((s, s), dtype=torch.bool, device=q.device).tril()[None, None]
+        else:
+            allow = attn_bias == 0
+        allow = allow | (~allow.any(-1, keepdim=True)
+                         & torch.eye(s, dtype=torch.bool, device=q.device)[None, None])
+        scores = scores.masked_fill(~allow, float("-inf"))
+        p = torch.softmax(scores, dim=-1)
+        return torch.matmul(p, vf).to(q.dtype)
+
+    def prefill(self, input_ids, positions, k_cache, v_cache, attn_bias=None):
+        """ek_model.py:280-334: input_ids/positions [B, S]; writes cache slots
+        [0, S); returns the final-normed hidden of each row's last position."""
+        c = self.cfg
+        b, s = input_ids.shape
+        cos = self.cos.index_select(0, positions.reshape(-1))
+        sin = self.sin.index_select(0, positions.reshape(-1))
+        zero_slot = self.zero_slot[:b] if b <= self.zero_slot.numel() else torch.zeros(
+            b, dtype=torch.int64, device=self.device)
+        residual = F.embedding(input_ids, self.embed).reshape(b * s, c.hidden_size)
+        x = None
+        for i, layer in enumerate(self.layers):
+            if i == 0:
+                x = K.rms_norm(residual, layer["ln1"], c.rms_eps)
+            else:
+                x, residual = K.add_rms_norm(x, residual, layer["ln1"], c.rms_eps)
+            qkv = torch.matmul(x, layer["qkv_t"])
+            K.qk_norm_rope_kv(qkv, layer["qn"], layer["kn"], cos, sin, k_cache[i], v_cache[i], zero_slot,
+                              c.num_heads, c.num_kv_heads, c.rms_eps, s)
+            q = qkv[:, : c.q_size].view(b, s, c.num_heads, c.head_dim).transpose(1, 2)
+            o = self._prefill_attn(q, k_cache[i][:, :, :s], v_cache[i][:, :, :s], attn_bias)
+            o = o.transpose(1, 2).reshape(b * s, c.q_size)
+            x = torch.matmul(o, layer["o_t"])
+            x, residual = K.add_rms_norm(x, residual, layer["ln2"], c.rms_eps)
+            x = torch.matmul(K.silu_mul(torch.matmul(x, layer["gu_t"])), layer["down_t"])
+        residual = residual + x
+        last = residual.view(b, s, c.hidden_size)[:, -1, :].contiguous()
+        return K.rms_norm(last, self.final_norm, c.rms_eps)
+
+    # ------------------------------------------------------------------
+    def _layers(self, tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws) -> _StepBuffers:
+        """All layers of one decode step; leaves the last down_proj partials
+        and the residual in the step buffers (final norm not applied)."""
+        c = self.cfg
+        b = tokens.shape[0]
+        if not self.use_gemv_for(b):
+            raise ValueError(f"decode batch {b} exceeds {self.MAX_ROWS} rows per launch")
+        bufs = self.buffers(b)
+        res_a, res_b = bufs.res
+        for i, layer in enumerate(self.layers):
+            if i == 0:
+                K.embed_norm_gemv(tokens, self.embed, res_b, layer["ln1"], layer["qkv"], c.rms_eps,
+                                  slot_t=slot_t, len_t=len_t, out=bufs.qkv)
+            else:
+                K.parts_norm_gemv(bufs.down_parts, res_a, res_b, layer["ln1"], layer["qkv"], c.rms_eps,
+                                  out=bufs.qkv)
+            o = K.rope_attn_decode(bufs.qkv, layer["qn"], layer["kn"], self.cos, self.sin, k_cache[i],
+                                   v_cache[i], len_t, start_t, ws, self.sm_scale, c.num_heads, c.rms_eps,
+                                   positions=positions)
+            K.gemv_parts(o.view(b, c.q_size), layer["o"], sk=bufs.sk_o, out=bufs.o_parts)
+            K.parts_norm_gemv(bufs.o_parts, res_b, res_a, layer["ln2"], layer["gu"], c.rms_eps, silu=True,
+                              out=bufs.act)
+            K.gemv_parts(bufs.act, layer["down"], sk=bufs.sk_down, out=bufs.down_parts)
+        return bufs
+
+    def decode(self, tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws=None):
+        """ek_model.py:360-416: one decode step for tokens/positions [B];
+        slot_t <- len_t; len_t += 1; returns the final-normed hidden [B, H].
+        ws: the attention workspace (engine._make_ws); built on the fly if None."""
+        if ws is None:
+            ws = K.make_workspace(tokens.shape[0], self.cfg.num_heads, self.cfg.num_kv_heads,
+                                  self.cfg.head_dim, k_cache[0].shape[2], self.device)
+        bufs = self._layers(tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws)
+        res_a = bufs.res[0]
+        hidden, _ = K.add_rms_norm_parts(bufs.down_parts, res_a, self.final_norm, self.cfg.rms_eps)
+        return hidden
+
+    def argmax_token(self, hidden, logits=None):
+        """ek_model.py:490-493: first index of the max bf16 logit, [B] int64."""
+        b = hidden.shape[0]
+        if not self.use_gemv_for(b):
+            return torch.cat([self.argmax_token(hidden[i:i + self.MAX_ROWS].contiguous())
+                              for i in range(0, b, self.MAX_ROWS)])
+        bufs = self.buffers(b)
+        out = torch.empty(b, dtype=torch.int64, device=hidden.device)
+        return K.lm_head_argmax(hidden.contiguous(), self.lm_head, bufs.argmax, out_tok=out, logits=logits)
+
+    def step(self, tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws, out_buf, step_idx,
+             logits=None):
+        """The whole graph step of engine.py:284-292 in HIP launches: decode,
+        final add + norm + lm_head + argmax (one kernel), then tokens <- next,
+        positions += 1, out_buf[step_idx] <- next, step_idx += 1."""
+        bufs = self._layers(tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws)
+        return K.lm_head_argmax(None, self.lm_head, bufs.argmax, out_tok=bufs.next_tok, logits=logits,
+                                parts=bufs.down_parts, residual=bufs.res[0], norm_w=self.final_norm,
+                                eps=self.cfg.rms_eps, state=(tokens, positions, out_buf, step_idx))

@@ -1,0 +1,363 @@
+"""Greedy-decode engine over the gfx950 kernels: the reference's Engine API.
+
+Mirrors jeojdi1/EngineKernel `engine/engine.py` (non-speculative path):
+`Engine(model_path).generate(input_ids, max_new_tokens)` yields one list of B
+token ids per step. The decode step is captured once per (batch, bucket) as a
+HIP graph (torch.cuda.graph over the C-ABI launches) that advances the
+device-resident token, position, length and output index itself, so N tokens
+are N graph replays with no host round trip; the host keeps LOOKAHEAD
+replays queued and reads tokens back through pinned memory and events.
+
+Failure handling: the fast tier never degrades silently. If the HIP library
+or GPU is missing, construction raises. A caller may pass `fallback`, a
+factory of another engine (for example a CPU reference); then a failure at
+load or mid-stream switches to it, and the deterministic greedy sequence is
+replayed with the already-yielded steps skipped (engine.py:770-824).
+"""
+
+from __future__ import annotations
+
+import gc
+import os
+
+import torch
+
+from . import ek_kernels as K
+from .ek_kernels import _next_pow2, group_pad, plan_splits  # noqa: F401  (reference re-exports)
+from .ek_model import Qwen3
+
+MAX_STEPS = 4096
+LOOKAHEAD = int(os.environ.get("ENGINE_LOOKAHEAD", "2"))
+
+
+def _pinned(shape, dtype):
+    """Pinned staging if page-locking is allowed, pageable otherwise (engine.py:105-110)."""
+    try:
+        return torch.empty(shape, dtype=dtype, pin_memory=True)
+    except Exception:
+        return torch.empty(shape, dtype=dtype)
+
+
+def _rows(input_ids):
+    """Lists, tuples, numpy arrays or tensors -> list[list[int]] (engine.py:113-117)."""
+    if hasattr(input_ids, "tolist"):
+        input_ids = input_ids.tolist()
+    return [r.tolist() if hasattr(r, "tolist") else [int(t) for t in r] for r in input_ids]
+
+
+class _Graph:
+    """engine.py:172-174: one captured decode step and its device state."""
+    __slots__ = ("graph", "tokens", "positions", "slot_t", "len_t", "start_t",
+                 "out_buf", "step_idx", "ws", "batch", "bucket")
+
+
+class _FastEngine:
+    @torch.inference_mode()
+    def __init__(self, model_path: str | None = None, model: Qwen3 | None = None) -> None:
+        """engine.py:184-223."""
+        if not torch.cuda.is_available():
+            raise K.HipUnavailable("no GPU visible: the HIP engine cannot run")
+        self.device = torch.device(f"cuda:{torch.cuda.current_device()}")
+        if not K.probe_hip():
+            raise K.HipUnavailable("libek_hip.so failed its load-and-run probe")
+        self.hip = True
+        self.model = model if model is not None else Qwen3(model_path, self.device)
+        cfg = self.model.cfg
+        self.n_kv = cfg.num_kv_heads
+        self.head_dim = cfg.head_dim
+        self.n_layers = cfg.num_layers
+        self.graphs: dict = {}
+        self.pool = torch.cuda.graph_pool_handle()
+        self.k_cache: list = []
+        self.v_cache: list = []
+        self.cache_b = 0
+        self.cache_s = 0
+        self.host_buf = None
+        self.host_b = 0
+        self.last_stats = (0, 0)
+        self.events = [torch.cuda.Event() for _ in range(LOOKAHEAD + 2)]
+        # graphs bake in the cos/sin pointers, so size the table once, here
+        self.model.ensure_rope(16384 + MAX_STEPS)
+
+    # -- memory ---------------------------------------------------------
+    def _release(self):
+        """engine.py:229-237."""
+        self.graphs.clear()
+        self.k_cache, self.v_cache = [], []
+        self.cache_b = self.cache_s = 0
+        self.pool = None
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        self.pool = torch.cuda.graph_pool_handle()
+
+    def _alloc_cache(self, b: int, s: int):
+        """engine.py:239-251: one [B, n_kv, S, D] bf16 tensor per layer for K and V."""
+        shape = (b, self.n_kv, s, self.head_dim)
+        self.k_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+                        for _ in range(self.n_layers)]
+        self.v_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+                        for _ in range(self.n_layers)]
+        self.cache_b, self.cache_s = b, s
+
+    def _ensure_cache(self, b: int, s: int):
+        """engine.py:253-263: S rounded up to 256; grown to the union of requests."""
+        s = -(-s // 256) * 256
+        if b <= self.cache_b and s <= self.cache_s:
+            return
+        nb, ns = max(b, self.cache_b), max(s, self.cache_s)
+        self._release()
+        try:
+            self._alloc_cache(nb, ns)
+        except Exception:
+            self.k_cache = self.v_cache = []
+            torch.cuda.empty_cache()
+            self._alloc_cache(b, s)
+
+    def _ensure_host(self, b: int):
+        if self.host_buf is None or self.host_b < b:
+            self.host_buf = _pinned((MAX_STEPS, b), torch.int32)
+            self.host_b = b
+
+    # -- graph capture --------------------------------------------------
+    def _make_ws(self, b: int, bucket: int):
+        """engine.py:273-282 (plus the score scratch and arrival counters)."""
+        cfg = self.model.cfg
+        return K.make_workspace(b, cfg.num_heads, self.n_kv, self.head_dim, bucket, self.device)
+
+    def _step_body(self, g: _Graph, kv):
+        """engine.py:284-292, as HIP launches only (argmax and bookkeeping fused)."""
+        k, v = kv
+        self.model.step(g.tokens, g.positions, k, v, g.slot_t, g.len_t, g.start_t, g.ws, g.out_buf, g.step_idx)
+
+    def _capture(self, b: int, bucket: int) -> _Graph:
+        """engine.py:294-330: warm up on a side stream, then capture one step."""
+        dev = self.device
+        g = _Graph()
+        g.batch, g.bucket = b, bucket
+        g.tokens = torch.zeros(b, dtype=torch.int64, device=dev)
+        g.positions = torch.zeros(b, dtype=torch.int64, device=dev)
+        g.slot_t = torch.zeros(b, dtype=torch.int64, device=dev)
+        g.len_t = torch.zeros(1, dtype=torch.int64, device=dev)
+        g.start_t = torch.zeros(b, dtype=torch.int32, device=dev)
+        g.out_buf = torch.zeros((MAX_STEPS, b), dtype=torch.int32, device=dev)
+        g.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        g.ws = self._make_ws(b, bucket)
+        kv = ([t[:b] for t in self.k_cache], [t[:b] for t in self.v_cache])
+        self.model.buffers(b)
+        warm = max(1, bucket // 2)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                g.len_t.fill_(warm)
+                g.positions.fill_(warm)
+                g.step_idx.zero_()
+                self._step_body(g, kv)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g.len_t.fill_(warm)
+        g.positions.fill_(warm)
+        g.step_idx.zero_()
+        g.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g.graph, pool=self.pool):
+            self._step_body(g, kv)
+        torch.cuda.synchronize()
+        return g
+
+    def _bucket(self, need: int) -> int:
+        return -(-need // 256) * 256
+
+    def _get_graph(self, b: int, total: int) -> _Graph:
+        """engine.py:456-470."""
+        bucket = self._bucket(total)
+        key = (b, bucket)
+        if key not in self.graphs:
+            self.graphs[key] = self._capture(b, bucket)
+        return self.graphs[key]
+
+    def _first_token(self, ids, pos, b, s, bias):
+        kv_k = [t[:b] for t in self.k_cache]
+        kv_v = [t[:b] for t in self.v_cache]
+        return self.model.argmax_token(self.model.prefill(ids, pos, kv_k, kv_v, bias))
+
+    # -- inputs ---------------------------------------------------------
+    def _pack(self, input_ids):
+        """engine.py:541-570: left-pad to a rectangle, one H2D copy each for
+        ids and positions (pads at position 0), and an additive bf16 -inf
+        mask (causal and key >= pad) for ragged batches."""
+        b = len(input_ids)
+        lens = [len(x) for x in input_ids]
+        s = max(lens)
+        pad = [s - n for n in lens]
+        dev = self.device
+        if min(lens) == s:
+            ids_c = torch.as_tensor(input_ids, dtype=torch.int64)
+            pos_c = torch.arange(s, dtype=torch.int64).expand(b, s)
+        else:
+            ids_c = torch.zeros((b, s), dtype=torch.int64)
+            pos_c = torch.zeros((b, s), dtype=torch.int64)
+            for i, seq in enumerate(input_ids):
+                ids_c[i, pad[i]:] = torch.as_tensor(seq, dtype=torch.int64)
+                pos_c[i, pad[i]:] = torch.arange(lens[i], dtype=torch.int64)
+        ids = ids_c.to(dev, non_blocking=True)
+        pos = pos_c.to(dev, non_blocking=True)
+        bias = None
+        if max(pad) > 0:
+            key_ok = torch.zeros((b, s), dtype=torch.bool)
+            for i, p in enumerate(pad):
+                key_ok[i, p:] = True
+            allow = torch.ones((s, s), dtype=torch.bool).tril()[None] & key_ok[:, None, :]
+            bias = torch.zeros((b, 1, s, s), dtype=torch.bfloat16)
+            bias.masked_fill_(~allow.unsqueeze(1), float("-inf"))
+            bias = bias.to(dev, non_blocking=True)
+        return ids, pos, pad, s, bias
+
+    # -- public API -----------------------------------------------------
+    @torch.inference_mode()
+    def generate(self, input_ids, max_new_tokens: int):
+        """engine.py:573-634 (the non-speculative graph path)."""
+        input_ids = _rows(input_ids)
+        max_new_tokens = int(max_new_tokens)
+        b = len(input_ids)
+        ids, pos, pad, s, bias = self._pack(input_ids)
+        total = s + max_new_tokens
+        if total + 1 > self.model.rope_len:
+            self.model.ensure_rope(total + 1)
+            self.graphs.clear()
+            self.pool = torch.cuda.graph_pool_handle()
+        if max_new_tokens > MAX_STEPS or b > self.model.MAX_ROWS:
+            yield from self._generate_eager(ids, pos, pad, s, bias, max_new_tokens)
+            return
+
+        self._ensure_cache(b, total)
+        self._ensure_host(b)
+        g = self._get_graph(b, total)
+        first = self._first_token(ids, pos, b, s, bias)
+
+        pad_t = torch.as_tensor(pad, dtype=torch.int32)
+        g.tokens.copy_(first)
+        g.positions.copy_((s - pad_t).to(torch.int64), non_blocking=True)
+        g.start_t.copy_(pad_t, non_blocking=True)
+        g.len_t.fill_(s)
+        g.step_idx.zero_()
+
+        host = self.host_buf
+        events = self.events
+        stream = torch.cuda.current_stream()
+        launched = 0
+
+        def launch():
+            nonlocal launched
+            step = launched + 1
+            g.graph.replay()
+            host[step, :b].copy_(g.out_buf[launched], non_blocking=True)
+            events[step % len(events)].record(stream)
+            launched += 1
+
+        yield first.to(torch.int32).cpu().tolist()
+        for _ in range(min(LOOKAHEAD, max_new_tokens - 1)):
+            launch()
+        for j in range(1, max_new_tokens):
+            if launched < max_new_tokens - 1:
+                launch()
+            events[j % len(events)].synchronize()
+            yield host[j, :b].tolist()
+        self.last_stats = (launched, max_new_tokens - 1)
+
+    def _generate_eager(self, ids, pos, pad, s, bias, max_new_tokens):
+        """engine.py:721-743 on the HIP kernels without graphs: zero caches,
+        prefill, then (n-1) x decode + argmax, in row groups of MAX_ROWS."""
+        cfg = self.model.cfg
+        b = ids.shape[0]
+        total = s + max_new_tokens
+        shape = (b, cfg.num_kv_heads, total, cfg.head_dim)
+        k = [torch.zeros(shape, dtype=self.model.dtype, device=self.device) for _ in range(cfg.num_layers)]
+        v = [torch.zeros(shape, dtype=self.model.dtype, device=self.device) for _ in range(cfg.num_layers)]
+        hidden = self.model.prefill(ids, pos, k, v, bias)
+        tok = self.model.argmax_token(hidden)
+        yield tok.tolist()
+        positions = torch.as_tensor([s - p for p in pad], dtype=torch.int64, device=self.device)
+        start_t = torch.as_tensor(pad, dtype=torch.int32, device=self.device)
+        groups = [(r0, min(b, r0 + self.model.MAX_ROWS)) for r0 in range(0, b, self.model.MAX_ROWS)]
+        state = []
+        for r0, r1 in groups:
+            state.append((torch.zeros(r1 - r0, dtype=torch.int64, device=self.device),
+                          torch.full((1,), s, dtype=torch.int64, device=self.device),
+                          K.make_workspace(r1 - r0, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, total,
+                                           self.device)))
+        for _ in range(max_new_tokens - 1):
+            outs = []
+            for (r0, r1), (slot_t, len_t, ws) in zip(groups, state):
+                hidden = self.model.decode(tok[r0:r1].contiguous(), positions[r0:r1].contiguous(),
+                                           [t[r0:r1] for t in k], [t[r0:r1] for t in v], slot_t, len_t,
+                                           start_t[r0:r1].contiguous(), ws)
+                outs.append(self.model.argmax_token(hidden))
+            tok = torch.cat(outs)
+            positions = positions + 1
+            yield tok.tolist()
+
+
+class Engine:
+    """engine.py:770-830: the entry point. `fallback`, if given, is a
+    zero-argument factory of another engine used when the HIP tier fails."""
+
+    def __init__(self, model_path: str | None = None, *, model: Qwen3 | None = None, fallback=None) -> None:
+        self.model_path = model_path
+        self.tier = "hip"
+        self._frozen = False
+        self._fallback = fallback
+        try:
+            self._impl = _FastEngine(model_path, model=model)
+        except Exception:
+            if fallback is None:
+                raise
+            self._impl = None
+            self._use_fallback()
+
+    def _use_fallback(self):
+        self._impl = None
+        gc.collect()
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+        self._impl = self._fallback()
+        self.tier = "fallback"
+
+    def generate(self, input_ids, max_new_tokens: int):
+        """engine.py:793-808: the cyclic GC is off for the duration of a
+        request, and the long-lived heap is frozen after the first."""
+        was_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            yield from self._generate(input_ids, max_new_tokens)
+        finally:
+            if not self._frozen:
+                self._frozen = True
+                gc.collect()
+                gc.freeze()
+            if was_enabled:
+                gc.enable()
+
+    def _generate(self, input_ids, max_new_tokens: int):
+        """engine.py:810-824: greedy decoding is deterministic, so after a
+        switch the fallback replays the request and skips what was yielded."""
+        done = 0
+        if self.tier == "hip":
+            try:
+                for step in self._impl.generate(input_ids, max_new_tokens):
+                    done += 1
+                    yield step
+                return
+            except Exception:
+                if self._fallback is None:
+                    raise
+                self._use_fallback()
+        for i, step in enumerate(self._impl.generate(input_ids, max_new_tokens)):
+            if i >= done:
+                yield step
+
+    def __getattr__(self, name):
+        impl = self.__dict__.get("_impl")
+        if impl is None:
+            raise AttributeError(name)
+        return getattr(impl, name)

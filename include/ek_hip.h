@@ -1,0 +1,150 @@
+/* C ABI of libek_hip.so: the gfx950 kernels of the Qwen3 decode hot path.
+ *
+ * Every entry point takes raw device pointers, element counts and strides
+ * (in elements), scalars by value, and the hipStream_t to launch on (as a
+ * void*). It launches asynchronously and returns a hipError_t as int: 0 on
+ * success; on a rejected argument, hipErrorInvalidValue (1) and a message
+ * readable through ek_last_error(). No entry point allocates, synchronizes
+ * or clears the HIP error state, so every one of them may be recorded into
+ * a HIP graph. Device scalars that a graph replay must re-read (sequence
+ * length, start offsets, tokens, positions, step index) are passed as
+ * pointers. bf16 tensors are raw 16-bit patterns; rows handed to 16-byte
+ * loads must be 16-byte aligned with lengths that are multiples of 8.
+ *
+ * Citations name the reference interface each entry point replaces
+ * (jeojdi1/EngineKernel, paths relative to its root).
+ */
+#ifndef EK_HIP_H
+#define EK_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library identification and the last argument-check message of this thread. */
+const char* ek_version(void);
+const char* ek_last_error(void);
+/* Compute units and gfx architecture name of the current device. */
+int ek_device_info(int* n_cu, char* arch, int arch_len);
+
+/* rms_norm: y[m,:] = w (x) bf16(x * rsqrt(mean(x^2) + eps)).
+ * Replaces engine/ek_kernels.py:1031-1042 (rms_norm, kernel :89-103). */
+int ek_rms_norm(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t ldx, int64_t ldy,
+                float eps, void* stream);
+
+/* add_rms_norm: residual = bf16(residual + x) in place; y = rms_norm(residual).
+ * Replaces engine/ek_kernels.py:1045-1059 (kernel :105-123). */
+int ek_add_rms_norm(const void* x, void* residual, const void* w, void* y, int64_t m, int64_t n, int64_t ldx,
+                    int64_t ldr, int64_t ldy, float eps, void* stream);
+
+/* add_rms_norm_parts: x = bf16(sum_s parts[s]) over fp32 partials [sk, m, n];
+ * residual = bf16(residual + x) in place; y = rms_norm(residual).
+ * Replaces engine/ek_kernels.py:1296-1304 (kernel :447-470). */
+int ek_add_rms_norm_parts(const float* parts, void* residual, const void* w, void* y, int64_t sk, int64_t m,
+                          int64_t n, int64_t ldr, int64_t ldy, float eps, void* stream);
+
+/* silu_mul: y[m, :n] = bf16(silu_fp32(gu[m, :n])) (x) gu[m, n:2n].
+ * Replaces engine/ek_kernels.py:1062-1076 (kernel :125-143). */
+int ek_silu_mul(const void* gu, void* y, int64_t m, int64_t n, int64_t ldgu, int64_t ldy, void* stream);
+
+/* qk_norm_rope_kv: per-head RMSNorm + rotate-half RoPE on fused qkv rows
+ * [m, (n_q + 2 n_kv) * head_dim]; q rotated in place; rotated k and raw v
+ * written to caches [B, n_kv, S, D] at slot_base[row / m_per_batch] + row %
+ * m_per_batch (slots outside [0, s_cap) are skipped). cos/sin rows are
+ * indexed by qkv row with stride ld_cs.
+ * Replaces engine/ek_kernels.py:1110-1146 (kernel :223-279). */
+int ek_qk_norm_rope_kv(void* qkv, const void* qn, const void* kn, const void* cos, const void* sin,
+                       void* k_cache, void* v_cache, const int64_t* slot_base, int64_t m, int64_t ld_qkv,
+                       int64_t ld_cs, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t csb, int64_t csh,
+                       int64_t css, int64_t s_cap, int64_t m_per_batch, float eps, void* stream);
+
+/* gemv: y[m, n] = bf16(sum_k x[m, k] * w[n, k]) with fp32 accumulation.
+ * Replaces engine/ek_kernels.py:1322-1347 (gemv, kernel :281-308). */
+int ek_gemv(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldw,
+            int64_t ldy, void* stream);
+
+/* gemv_parts: fp32 split-K partials parts[s, m, n] over sk equal K slices (m <= 8).
+ * Replaces engine/ek_kernels.py:1277-1293 (kernel :413-445). */
+int ek_gemv_parts(const void* x, const void* w, float* parts, int64_t m, int64_t n, int64_t k, int64_t ldx,
+                  int64_t ldw, int64_t sk, void* stream);
+
+/* gemv_swiglu: w is the fused [2*inter, k] gate-over-up matrix;
+ * y[m, i] = bf16(silu(bf16 gate_i)) (x) bf16(up_i) (m <= 8).
+ * Replaces engine/ek_kernels.py:1247-1261 (kernel :375-411). */
+int ek_gemv_swiglu(const void* x, const void* w, void* y, int64_t m, int64_t inter, int64_t k, int64_t ldx,
+                   int64_t ldw, int64_t ldy, void* stream);
+
+/* norm_gemv: [residual add] + RMSNorm prologue + projection [+ SwiGLU epilogue].
+ * residual == NULL: no add (the normalised input is x itself). Otherwise
+ * r = bf16(x + residual) is written to residual_out (which must not alias x
+ * or residual) and normalised. silu != 0: w is [2n, k] gate-over-up (m <= 8).
+ * Replaces engine/ek_kernels.py:1220-1244 (kernel :310-373). */
+int ek_norm_gemv(const void* x, const void* residual, void* residual_out, const void* norm_w, const void* w,
+                 void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldr, int64_t ldro, int64_t ldw,
+                 int64_t ldy, float eps, int silu, void* stream);
+
+/* parts_norm_gemv: the decode layer's consumer projection. r = bf16(residual +
+ * bf16(sum_s parts[s])) over fp32 partials [sk_in, m, k]; r -> residual_out;
+ * y = projection of rms_norm(r) [+ SwiGLU]. The composition
+ * add_rms_norm_parts (engine/ek_kernels.py:1296) -> gemv (:1322) /
+ * gemv_swiglu (:1247), as one launch. rpw: output rows per wave (0: default). */
+int ek_parts_norm_gemv(const float* parts, int64_t sk_in, const void* residual, void* residual_out,
+                       const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldr,
+                       int64_t ldro, int64_t ldw, int64_t ldy, float eps, int silu, int64_t rpw, void* stream);
+
+/* embed_norm_gemv: the decode step's first layer. r = embed[tokens[b]] ->
+ * residual_out; y = projection of rms_norm(r). When len_t != NULL it also
+ * performs the step's slot/length advance (slot_t[b] = *len_t; *len_t += 1).
+ * The composition F.embedding -> rms_norm -> qkv projection and the
+ * slot_t/len_t update of engine/ek_model.py:375-388, as one launch. */
+int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, int64_t vocab, void* residual_out,
+                       const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldro,
+                       int64_t ldw, int64_t ldy, float eps, int64_t* slot_t, int64_t* len_t, int64_t rpw,
+                       void* stream);
+
+/* attn_decode: split-K decode attention over caches [B, n_kv, S, D] (D in
+ * {32, 64, 128}, n_q / n_kv in {1, 2, 4, 8}) for keys [start[b], *seq_len).
+ * rope != 0: q is the raw fused qkv row (stride ldq_b); the query heads are
+ * QK-normed and rotated, and the new key (rotated) and value (raw) are
+ * written at slot *seq_len - 1 -- rope_attn_decode, engine/ek_kernels.py:
+ * 1476-1507 (kernel :678-780). rope == 0: q [B, n_q, D] is already rotated
+ * -- flash_decode, engine/ek_kernels.py:1389-1416 (kernel :534-615). The
+ * split combine (kernel :988-1019) is fused: partials acc [B, n_kv, sp, gp,
+ * D], lsum/mmax [B, n_kv, sp, gp], score scratch [B, n_q, score_ss]; the
+ * last workgroup per (b, kv head) combines, using counters [B * n_kv]
+ * (zero before the first call; left zero by every call). Probabilities are
+ * rounded to bf16 before the PV product, as in engine/ek_model.py:475-488.
+ * cos/sin rows: positions[b] when positions != NULL, else row b. */
+int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
+                   const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
+                   void* k_cache, void* v_cache, int64_t csb, int64_t csh, int64_t css, int64_t s_cap,
+                   const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* acc,
+                   float* lsum, float* mmax, int32_t* counters, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
+                   int64_t ldo_h, int64_t b, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits,
+                   int64_t chunk, float sm_scale, float eps, void* stream);
+
+/* lm_head_argmax: logits = bf16(h . w^T) over the vocabulary and the
+ * first-index argmax per row -> out_tok[b] (int64). The hidden row h is x
+ * (parts == NULL) or, fused, rms_norm(bf16(residual + bf16(sum_s parts[s])))
+ * with gain norm_w (the decode's final add + norm, engine/ek_model.py:413-416).
+ * logits (nullable) receives the bf16 logits. am_val/am_idx (>= am_cap
+ * entries, >= blocks * m) hold per-workgroup partials; counter (one int32,
+ * zero before the first call) is left zero. When st_tokens != NULL the last
+ * workgroup also advances the decode state: st_tokens[b] = token,
+ * st_positions[b] += 1, st_out[*st_step * m + b] = token (if *st_step <
+ * max_steps), *st_step += 1.
+ * Replaces engine/ek_model.py:490-493 (argmax_token) and the step bookkeeping
+ * of engine/engine.py:289-292. */
+int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const void* residual, const void* norm_w,
+                      float eps, const void* w, int64_t m, int64_t vocab, int64_t k, int64_t ldx, int64_t ldr,
+                      int64_t ldw, void* logits, int64_t ld_logits, float* am_val, int32_t* am_idx, int64_t am_cap,
+                      int32_t* counter, int64_t* out_tok, int64_t* st_tokens, int64_t* st_positions,
+                      int32_t* st_out, int64_t* st_step, int64_t max_steps, int64_t rpw, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EK_HIP_H */

@@ -1,0 +1,84 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol
+include/ek_hip.h declares, reports argument errors without touching a GPU,
+and the product path refuses CPU tensors (there is no CPU fallback)."""
+
+import ctypes
+import os
+
+import pytest
+import torch
+
+from enginekernel_amd import _hip
+from enginekernel_amd import ek_kernels as K
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _hip.load()
+    declared = _hip.declared_symbols()
+    assert len(declared) == 16
+    for name in declared:
+        assert hasattr(lib, name), name
+    # the ctypes signature table covers every kernel entry point
+    assert set(_hip.SIGNATURES) == set(declared) - {"ek_version", "ek_last_error", "ek_device_info"}
+    assert lib.ek_version().startswith(b"enginekernel_amd")
+
+
+def test_signature_arity_matches_header():
+    """Argument counts in the ctypes table equal the header prototypes."""
+    import re
+    text = open(_hip.HEADER).read()
+    for name, argtypes in _hip.SIGNATURES.items():
+        proto = re.search(name + r"\s*\(([^)]*)\)", text, flags=re.S).group(1)
+        assert len([a for a in proto.split(",") if a.strip()]) == len(argtypes), name
+
+
+def test_argument_errors_return_invalid_value_without_a_gpu():
+    lib = _hip.load()
+    # m = 0 is rejected by the host-side check before any HIP call
+    rc = lib.ek_gemv(None, None, None, 0, 16, 64, 64, 64, 16, None)
+    assert rc == 1
+    assert b"empty" in lib.ek_last_error()
+    rc = lib.ek_attn_decode(*([None, 0, 0, 0] + [None] * 4 + [0, None, 0] + [None] * 2 + [0] * 4 +
+                              [None] * 3 + [0] + [None] * 4 + [0, 0, None, 0, 0] + [0, 32, 8, 128, 1, 64] +
+                              [0.1, 1e-6, None]))
+    assert rc == 1 and b"head counts" in lib.ek_last_error()
+    with pytest.raises(_hip.HipKernelError) as e:
+        _hip.call("ek_silu_mul", None, None, 1, 7, 8, 8, None)      # n not a multiple of 8
+    assert e.value.code == 1
+
+
+def test_kernels_refuse_cpu_tensors():
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    with pytest.raises(K.HipUnavailable):
+        K.rms_norm(x, w, 1e-6)
+    with pytest.raises(K.HipUnavailable):
+        K.gemv(x, torch.zeros(8, 64, dtype=torch.bfloat16))
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_hip.HipUnavailable):
+        _hip.load(str(tmp_path / "nope.so"))
+
+
+def test_model_refuses_cpu_device():
+    from enginekernel_amd.checkpoint import QWEN3_TINY
+    from enginekernel_amd.ek_model import Qwen3
+    with pytest.raises(K.HipUnavailable):
+        Qwen3(None, torch.device("cpu"), tensors={}, config=dict(QWEN3_TINY))
+
+
+@pytest.mark.parametrize("b,bucket", [(1, 768), (1, 32768), (4, 2048), (8, 8192), (16, 1024), (3, 256)])
+def test_plan_splits_invariants(b, bucket):
+    splits, chunk, block_n = K.plan_splits(b, 8, bucket)
+    assert 1 <= splits <= 32 and chunk % block_n == 0
+    assert splits * chunk >= bucket                      # every key of the bucket is covered
+    assert (splits - 1) * chunk < bucket                 # no split starts past the bucket
+    ws = K.make_workspace(b, 32, 8, 128, bucket, "cpu")
+    assert ws[0].shape == (b, 8, K._next_pow2(splits), K.group_pad(32, 8), 128)
+    assert ws[7].shape == (b, 32, bucket) and ws[8].shape == (b * 8,) and not ws[8].any()
+
+
+def test_group_pad_and_helpers():
+    assert K.group_pad(32, 8) == 16 and K.group_pad(64, 2) == 32
+    assert K._next_pow2(1) == 1 and K._next_pow2(17) == 32 and K._cdiv(7, 2) == 4

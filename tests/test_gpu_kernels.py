@@ -1,0 +1,370 @@
+"""Per-kernel parity of the HIP path against the CPU oracle and float64
+references (mirrors the reference's bench/test_kernels.py, plus the
+BASELINE GEMV and attention configurations).
+
+Tolerances are stated per test. The kernels follow the oracle's rounding
+points, so most outputs are bitwise equal; the remaining differences come
+from fp32 summation order (GPU tree vs CPU vector order) or a 1-ulp
+difference of exp/rsqrt, each of which can move a bf16 rounding by one ulp.
+"""
+
+import pytest
+import torch
+
+from enginekernel_amd import ek_kernels as K
+from oracle import ek_oracle as O
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _ulp(x):
+    a = x.abs().double().clamp_min(2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+def assert_close_ulps(got, want, ulps=1, min_equal=0.999, name=""):
+    """Every element within `ulps` bf16 ulps of the reference and at least
+    `min_equal` of them bitwise equal."""
+    got, want = got.detach().cpu(), want.detach().cpu()
+    assert got.shape == want.shape, (name, got.shape, want.shape)
+    diff = (got.double() - want.double()).abs()
+    bound = ulps * _ulp(want) + 1e-30
+    bad = diff > bound
+    assert not bad.any(), f"{name}: {int(bad.sum())} elements beyond {ulps} ulp, max diff {diff.max().item():.3g}"
+    eq = (got == want).float().mean().item()
+    assert eq >= min_equal, f"{name}: only {eq:.5f} bitwise equal"
+
+
+def check_scale(got, want, tol, name=""):
+    """bench/test_kernels.py:18-33: max |err| / max |ref| <= tol."""
+    got, want = got.detach().float().cpu(), want.detach().float().cpu()
+    err = (got - want).abs().max().item()
+    scale = max(want.abs().max().item(), 1e-6)
+    assert err / scale <= tol, f"{name}: {err / scale:.3g} > {tol}"
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ----------------------------------------------------------------------------
+# norms, SiLU, QK-norm/RoPE (bench/test_kernels.py:36-119)
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize("m", [1, 16, 8192])
+def test_rms_norm_and_add_rms_norm(dev, m):
+    g = _gen(m)
+    x = torch.randn(m, 2560, generator=g).to(BF)
+    w = torch.randn(2560, generator=g).to(BF)
+    r = torch.randn(m, 2560, generator=g).to(BF)
+    assert_close_ulps(K.rms_norm(x.to(dev), w.to(dev), 1e-6), O.rms_norm(x, w, 1e-6), name="rms_norm")
+    rd = r.to(dev)
+    y, r_out = K.add_rms_norm(x.to(dev), rd, w.to(dev), 1e-6)
+    y_ref, r_ref = O.add_rms_norm(x, r, w, 1e-6)
+    assert r_out.data_ptr() == rd.data_ptr()                      # updated in place
+    assert torch.equal(r_out.cpu(), r_ref)                        # bf16 add: exact
+    assert_close_ulps(y, y_ref, name="add_rms_norm")
+
+
+@pytest.mark.parametrize("m", [1, 16, 8192])
+def test_silu_mul(dev, m):
+    gu = (torch.randn(m, 2 * 9728, generator=_gen(m)) * 2).to(BF)
+    assert_close_ulps(K.silu_mul(gu.to(dev)), O.silu_mul(gu), name="silu_mul")
+
+
+@pytest.mark.parametrize("b,mpb,d,nq,nkv", [(1, 1, 128, 32, 8), (4, 1, 128, 32, 8), (2, 16, 128, 32, 8),
+                                             (3, 5, 32, 4, 2)])
+def test_qk_norm_rope_kv(dev, b, mpb, d, nq, nkv):
+    g = _gen(b * 100 + mpb)
+    m, smax = b * mpb, 64
+    qkv = torch.randn(m, (nq + 2 * nkv) * d, generator=g).to(BF)
+    qn = torch.randn(d, generator=g).to(BF)
+    kn = torch.randn(d, generator=g).to(BF)
+    cos = torch.randn(m, d, generator=g).to(BF)
+    sin = torch.randn(m, d, generator=g).to(BF)
+    base = 7 if mpb == 1 else 0
+    slot = torch.full((b,), base, dtype=torch.int64)
+    kc = torch.zeros(b, nkv, smax, d, dtype=BF)
+    vc = torch.zeros_like(kc)
+    want = qkv.clone()
+    O.qk_norm_rope_kv(want, qn, kn, cos, sin, kc, vc, slot, nq, nkv, 1e-6, mpb)
+    got = qkv.to(dev)
+    kcd, vcd = torch.zeros_like(kc).to(dev), torch.zeros_like(vc).to(dev)
+    K.qk_norm_rope_kv(got, qn.to(dev), kn.to(dev), cos.to(dev), sin.to(dev), kcd, vcd, slot.to(dev),
+                      nq, nkv, 1e-6, mpb)
+    assert_close_ulps(got, want, name="q in place")
+    assert_close_ulps(kcd, kc, name="k cache")                   # includes "elsewhere untouched"
+    assert torch.equal(vcd.cpu(), vc)                             # raw v: exact
+
+
+# ----------------------------------------------------------------------------
+# projections (BASELINE config 2 shapes)
+# ----------------------------------------------------------------------------
+SHAPES = [("qkv", 6144, 2560), ("gate_up", 19456, 2560), ("o", 2560, 4096), ("down", 2560, 9728),
+          ("lm_head", 151936, 2560)]
+
+
+def _proj_ref(x, w):
+    """bf16(x . w^T) from a float64 product on the CPU (the exact sum, rounded once)."""
+    return (x.double() @ w.double().t()).to(torch.float32).to(BF)
+
+
+@pytest.mark.parametrize("name,n,k", SHAPES)
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemv_shapes(dev, name, n, k, m):
+    g = _gen(n + m)
+    x = (torch.randn(m, k, generator=g) * 0.02).to(BF)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(BF)
+    got = K.gemv(x.to(dev), w.to(dev))
+    want = _proj_ref(x, w)
+    assert_close_ulps(got, want, ulps=1, min_equal=0.99, name=f"gemv {name} m={m}")
+    check_scale(got, want, 2e-2)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemv_swiglu_and_silu_epilogue(dev, m):
+    """The fused gate/up projection with its SiLU*up epilogue on the 19456
+    output (config 2) against the unfused composition."""
+    g = _gen(7 + m)
+    x = (torch.randn(m, 2560, generator=g) * 0.02).to(BF)
+    w = (torch.randn(19456, 2560, generator=g) * 0.02).to(BF)
+    want = O.silu_mul(_proj_ref(x, w))
+    got = K.gemv_swiglu(x.to(dev), w.to(dev))
+    assert_close_ulps(got, want, ulps=2, min_equal=0.99, name="gemv_swiglu")
+    got2 = K.silu_mul(K.gemv(x.to(dev), w.to(dev)))
+    assert_close_ulps(got2, want, ulps=2, min_equal=0.99, name="gemv+silu_mul")
+
+
+@pytest.mark.parametrize("m,sk", [(1, 1), (1, 2), (4, 2), (8, 4)])
+def test_gemv_parts_and_add_rms_norm_parts(dev, m, sk):
+    g = _gen(11 + m)
+    x = (torch.randn(m, 9728, generator=g) * 0.02).to(BF)
+    w = (torch.randn(2560, 9728, generator=g) * 0.02).to(BF)
+    r = (torch.randn(m, 2560, generator=g) * 0.5).to(BF)
+    nw = (1 + 0.1 * torch.randn(2560, generator=g)).to(BF)
+    parts = K.gemv_parts(x.to(dev), w.to(dev), sk=sk)
+    assert parts.shape == (sk, m, 2560)
+    exact = x.double() @ w.double().t()
+    assert (parts.sum(0).double().cpu() - exact).abs().max() <= 1e-5 * exact.abs().max() + 1e-7
+    rd = r.to(dev)
+    y, r_out = K.add_rms_norm_parts(parts, rd, nw.to(dev), 1e-6)
+    y_ref, r_ref = O.add_rms_norm(_proj_ref(x, w), r, nw, 1e-6)
+    assert_close_ulps(r_out, r_ref, ulps=1, min_equal=0.99, name="residual")
+    assert_close_ulps(y, y_ref, ulps=2, min_equal=0.99, name="norm")
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_norm_gemv_fused_prologues(dev, m):
+    """norm_gemv (no add / add), parts_norm_gemv and embed_norm_gemv against
+    the composition of the oracle's norms and an exact projection."""
+    g = _gen(13 + m)
+    H, N, I = 2560, 6144, 9728
+    x = (torch.randn(m, H, generator=g) * 0.3).to(BF)
+    r = (torch.randn(m, H, generator=g) * 0.3).to(BF)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(BF)
+    w = (torch.randn(N, H, generator=g) * 0.02).to(BF)
+    wgu = (torch.randn(2 * I, H, generator=g) * 0.02).to(BF)
+    d = lambda t: t.to(dev)
+    y, r1 = K.norm_gemv(d(x), None, d(nw), d(w), 1e-6)
+    assert_close_ulps(y, _proj_ref(O.rms_norm(x, nw, 1e-6), w), ulps=2, min_equal=0.98, name="norm_gemv")
+    y, r2 = K.norm_gemv(d(x), d(r), d(nw), d(wgu), 1e-6, silu=True)
+    xn, rr = O.add_rms_norm(x, r, nw, 1e-6)
+    assert torch.equal(r2.cpu(), rr)
+    assert_close_ulps(y, O.silu_mul(_proj_ref(xn, wgu)), ulps=2, min_equal=0.98, name="norm_gemv silu")
+    # split-K partials as the addend
+    parts = (torch.randn(2, m, H, generator=g) * 0.1)
+    r_out = torch.empty(m, H, dtype=BF, device=dev)
+    y = K.parts_norm_gemv(d(parts), d(r), r_out, d(nw), d(w), 1e-6)
+    xsum = parts.sum(0).to(BF)
+    xn, rr = O.add_rms_norm(xsum, r, nw, 1e-6)
+    assert_close_ulps(r_out, rr, ulps=1, min_equal=0.999, name="parts residual")
+    assert_close_ulps(y, _proj_ref(xn, w), ulps=2, min_equal=0.98, name="parts_norm_gemv")
+    # embedding gather + slot/length advance
+    emb = (torch.randn(1000, H, generator=g) * 0.02).to(BF)
+    tok = torch.randint(0, 1000, (m,), generator=g)
+    slot = torch.zeros(m, dtype=torch.int64, device=dev)
+    ln = torch.full((1,), 41, dtype=torch.int64, device=dev)
+    y = K.embed_norm_gemv(d(tok), d(emb), r_out, d(nw), d(w), 1e-6, slot_t=slot, len_t=ln)
+    assert torch.equal(r_out.cpu(), emb[tok])
+    assert slot.tolist() == [41] * m and ln.item() == 42
+    assert_close_ulps(y, _proj_ref(O.rms_norm(emb[tok], nw, 1e-6), w), ulps=2, min_equal=0.98, name="embed")
+
+
+# ----------------------------------------------------------------------------
+# lm_head + argmax
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize("m", [1, 4])
+def test_lm_head_argmax(dev, m):
+    g = _gen(17 + m)
+    V, H = 151936, 2560
+    h = torch.randn(m, H, generator=g).to(BF)
+    e = (torch.randn(V, H, generator=g) * 0.02).to(BF)
+    # planted exact tie: the best row duplicated at a higher index must lose
+    ref = _proj_ref(h, e)
+    best = ref.float().argmax(-1)
+    e[V - 5] = e[best[0]]
+    ref = _proj_ref(h, e)
+    scratch = K.ArgmaxScratch(m, V, dev)
+    logits = torch.empty(m, V, dtype=BF, device=dev)
+    tok = K.lm_head_argmax(h.to(dev), e.to(dev), scratch, logits=logits)
+    assert_close_ulps(logits, ref, ulps=1, min_equal=0.99, name="logits")
+    # exact on the kernel's own logits; equal to the reference unless a near-tie moved
+    assert tok.tolist() == torch.argmax(logits.cpu(), -1).tolist()
+    want = torch.argmax(ref, -1)
+    for i in range(m):
+        if tok[i].item() != want[i].item():
+            gap = ref[i, want[i]].float() - ref[i, tok[i].item()].float()
+            assert gap <= _ulp(ref[i, want[i]].double()), "argmax differs beyond a one-ulp near-tie"
+    assert tok[0].item() == best[0].item()
+    assert scratch.counter.item() == 0                           # left zero for the next call
+
+
+def test_lm_head_argmax_step_state(dev):
+    """The fused bookkeeping: tokens <- next, positions += 1,
+    out_buf[step] <- next, step += 1 (engine.py:289-292)."""
+    m, V, H = 2, 4096, 256
+    g = _gen(3)
+    h = torch.randn(m, H, generator=g).to(BF).to(dev)
+    e = (torch.randn(V, H, generator=g) * 0.02).to(BF).to(dev)
+    scratch = K.ArgmaxScratch(m, V, dev)
+    tokens = torch.zeros(m, dtype=torch.int64, device=dev)
+    pos = torch.tensor([5, 9], dtype=torch.int64, device=dev)
+    out_buf = torch.full((4, m), -1, dtype=torch.int32, device=dev)
+    step = torch.zeros(1, dtype=torch.int64, device=dev)
+    for i in range(5):                                           # the 5th exceeds out_buf: guarded
+        K.lm_head_argmax(h, e, scratch, state=(tokens, pos, out_buf, step))
+    want = torch.argmax((h.float() @ e.float().t()).to(BF).float(), -1)
+    assert tokens.tolist() == want.tolist()
+    assert pos.tolist() == [10, 14] and step.item() == 5
+    assert out_buf.tolist() == [want.tolist()] * 4
+
+
+# ----------------------------------------------------------------------------
+# attention (bench/test_kernels.py:122-155)
+# ----------------------------------------------------------------------------
+def _ref_attn64(q, kc, vc, seq_len, start):
+    """bench/test_kernels.py:122-130 in float64 (no bf16 rounding of p)."""
+    b, hq, d = q.shape
+    rep = hq // kc.shape[1]
+    k = kc[:, :, :seq_len].repeat_interleave(rep, 1).double()
+    v = vc[:, :, :seq_len].repeat_interleave(rep, 1).double()
+    s = torch.einsum("bhd,bhsd->bhs", q.double(), k) * (d ** -0.5)
+    idx = torch.arange(seq_len)
+    s = s.masked_fill(idx[None, None, :] < start[:, None, None], float("-inf"))
+    return torch.einsum("bhs,bhsd->bhd", torch.softmax(s, -1), v)
+
+
+ATTN_CASES = [(1, 1024, 600, 0), (4, 2048, 2048, 0), (16, 1024, 640, 0), (3, 1024, 97, 0), (2, 1024, 500, 37)]
+
+
+@pytest.mark.parametrize("b,smax,slen,pad", ATTN_CASES)
+def test_flash_decode_reference_cases(dev, b, smax, slen, pad):
+    hq, hkv, d = 32, 8, 128
+    g = _gen(b * 1000 + slen)
+    q = torch.randn(b, hq, d, generator=g).to(BF)
+    kc = torch.randn(b, hkv, smax, d, generator=g).to(BF)
+    vc = torch.randn(b, hkv, smax, d, generator=g).to(BF)
+    start = torch.full((b,), pad, dtype=torch.int32)
+    splits, chunk, bn = K.plan_splits(b, hkv, smax)
+    sp, gp = K._next_pow2(splits), K.group_pad(hq, hkv)
+    ws = (torch.zeros(b, hkv, sp, gp, d, dtype=torch.float32, device=dev),
+          torch.zeros(b, hkv, sp, gp, dtype=torch.float32, device=dev),
+          torch.full((b, hkv, sp, gp), -1e30, dtype=torch.float32, device=dev),
+          torch.empty(b, hq, d, dtype=BF, device=dev), splits, chunk, bn)     # the reference's 7-tuple
+    got = K.flash_decode(q.to(dev), kc.to(dev), vc.to(dev), torch.tensor([slen], device=dev),
+                         start.to(dev), ws, d ** -0.5)
+    check_scale(got, _ref_attn64(q, kc, vc, slen, start), 3e-2, "vs fp64 softmax")
+    assert_close_ulps(got, O.decode_attn(q, kc, vc, slen, start, d ** -0.5), ulps=1, min_equal=0.99,
+                      name="vs oracle (bf16 p)")
+
+
+@pytest.mark.parametrize("L", [512, 4096, 16384, 32768])
+def test_attention_config3_lengths_and_split_sweep(dev, L):
+    """32/8 heads, D=128, capacity 32768, L filled. The
+    split count changes only fp32 summation order: every split count must
+    agree with one split to within one bf16 ulp."""
+    hq, hkv, d, cap = 32, 8, 128, 32768
+    g = _gen(L)
+    q = torch.randn(1, hq, d, generator=g).to(BF).to(dev)
+    kc = torch.randn(1, hkv, cap, d, generator=g).to(BF).to(dev)
+    vc = torch.randn(1, hkv, cap, d, generator=g).to(BF).to(dev)
+    start = torch.zeros(1, dtype=torch.int32, device=dev)
+    ln = torch.tensor([L], device=dev)
+    outs = {}
+    for splits in (1, 4, 32, 64):
+        ws = K.make_workspace(1, hq, hkv, d, cap, dev, splits=splits, chunk=-(-cap // splits))
+        outs[splits] = K.flash_decode(q, kc, vc, ln, start, ws, d ** -0.5).clone()
+    for s in (4, 32, 64):
+        assert_close_ulps(outs[s], outs[1], ulps=1, min_equal=0.98, name=f"splits {s} vs 1")
+    if L <= 4096:
+        want = O.decode_attn(q.cpu(), kc.cpu()[:, :, :L], vc.cpu()[:, :, :L], L, start.cpu(), d ** -0.5)
+        assert_close_ulps(outs[32], want, ulps=1, min_equal=0.99, name="vs oracle")
+
+
+@pytest.mark.parametrize("b,d,nq,nkv,slen,pad", [(1, 128, 32, 8, 129, 0), (3, 128, 32, 8, 300, 11),
+                                                 (3, 32, 4, 2, 17, 5), (8, 128, 32, 8, 700, 0)])
+def test_rope_attn_decode(dev, b, d, nq, nkv, slen, pad):
+    """Fused QK-norm + RoPE + KV write + attention against the oracle's
+    qk_norm_rope_kv followed by its fallback attention."""
+    g = _gen(slen + b)
+    smax = 1024
+    qkv = torch.randn(b, (nq + 2 * nkv) * d, generator=g).to(BF)
+    qn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF)
+    kn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF)
+    cos_t, sin_t = O.build_rope(d, 1e6, 2048)
+    pos = torch.randint(0, 2000, (b,), generator=g)
+    kc = torch.randn(b, nkv, smax, d, generator=g).to(BF)
+    vc = torch.randn(b, nkv, smax, d, generator=g).to(BF)
+    start = torch.full((b,), pad, dtype=torch.int32)
+    # oracle: slot = slen - 1 (seq_len counts the new token)
+    q_ref, kc_ref, vc_ref = qkv.clone(), kc.clone(), vc.clone()
+    O.qk_norm_rope_kv(q_ref, qn, kn, cos_t[pos], sin_t[pos], kc_ref, vc_ref,
+                      torch.full((b,), slen - 1, dtype=torch.int64), nq, nkv, 1e-6, 1)
+    want = O.decode_attn(q_ref[:, :nq * d].view(b, nq, d), kc_ref, vc_ref, slen, start, d ** -0.5)
+    kcd, vcd = kc.to(dev), vc.to(dev)
+    ws = K.make_workspace(b, nq, nkv, d, smax, dev)
+    got = K.rope_attn_decode(qkv.to(dev), qn.to(dev), kn.to(dev), cos_t.to(dev), sin_t.to(dev), kcd, vcd,
+                             torch.tensor([slen], device=dev), start.to(dev), ws, d ** -0.5, nq, 1e-6,
+                             positions=pos.to(dev))
+    assert_close_ulps(got, want, ulps=1, min_equal=0.99, name="rope_attn_decode")
+    assert_close_ulps(kcd[:, :, slen - 1], kc_ref[:, :, slen - 1], ulps=1, name="new k")
+    assert torch.equal(vcd[:, :, slen - 1].cpu(), vc_ref[:, :, slen - 1])
+    keep = torch.ones(smax, dtype=torch.bool)
+    keep[slen - 1] = False
+    assert torch.equal(kcd[:, :, keep].cpu(), kc[:, :, keep]) and torch.equal(vcd[:, :, keep].cpu(), vc[:, :, keep])
+    assert not ws[8].any()                                       # arrival counters left at zero
+
+
+# ----------------------------------------------------------------------------
+# graph capture of C-ABI launches
+# ----------------------------------------------------------------------------
+def test_graph_replay_matches_eager(dev):
+    """A captured chain of C-ABI launches (no memset nodes) replays to the
+    eager result every time, with eager work and syncs between replays."""
+    g = _gen(5)
+    x = (torch.randn(1, 2560, generator=g) * 0.3).to(BF).to(dev)
+    w = (torch.randn(6144, 2560, generator=g) * 0.02).to(BF).to(dev)
+    nw = torch.ones(2560, dtype=BF, device=dev)
+    e = (torch.randn(4096, 6144, generator=g) * 0.02).to(BF).to(dev)
+    scratch = K.ArgmaxScratch(1, 4096, dev)
+    out = torch.empty(1, dtype=torch.int64, device=dev)
+
+    def body():
+        y, _ = K.norm_gemv(x, None, nw, w, 1e-6)
+        return K.lm_head_argmax(y, e, scratch, out_tok=out)
+
+    eager = body().clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    for i in range(4):
+        out.fill_(-1)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        _ = (x.float() * 2).sum().item()                         # eager work between replays
