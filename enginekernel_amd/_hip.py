@@ -34,19 +34,20 @@ SIGNATURES = {
     "ek_silu_mul": [_P, _P, _I64, _I64, _I64, _I64, _P],
     "ek_qk_norm_rope_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                            _I64, _I64, _I64, _I64, _I64, _F, _P],
-    "ek_gemv": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
-    "ek_gemv_parts": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
-    "ek_gemv_swiglu": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
-    "ek_norm_gemv": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I, _P],
+    "ek_gemv": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "ek_gemv_parts": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "ek_gemv_swiglu": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
+    "ek_norm_gemv": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _I,
+                     _I64, _I64, _P],
     "ek_parts_norm_gemv": [_P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F,
-                           _I, _I64, _P],
+                           _I, _I64, _I64, _P],
     "ek_embed_norm_gemv": [_P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
-                           _P, _P, _I64, _P],
+                           _P, _P, _I64, _I64, _P],
     "ek_attn_decode": [_P, _I64, _I64, _I, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64,
-                       _I64, _P, _P, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
+                       _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
                        _I64, _I64, _I64, _I64, _F, _F, _P],
     "ek_lm_head_argmax": [_P, _P, _I64, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
-                          _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64, _I64, _P],
+                          _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
 }
 
 

@@ -12,19 +12,27 @@
 //            value), then fp32 scores s_n = (q . k_n) * scale for the
 //            split's keys -> a score scratch row, plus the split's running
 //            max m and sum l = sum exp(s - m).
-//   phase 2  M = max_s m_s, L = sum_s l_s exp(m_s - M) from all splits;
-//            p_n = bf16(exp(s_n - M) / L); acc = sum p_n v_n (fp32) for the
-//            split's keys; the last workgroup to arrive for a (batch, kv
-//            head) adds the split partials in split order and rounds to bf16.
+//   phase 2  one workgroup per (batch, kv head, chunk of DC head dims) over
+//            ALL keys: M = max_s m_s, L = sum_s l_s exp(m_s - M) from the
+//            splits' statistics; p_n = bf16(exp(s_n - M) / L); out =
+//            bf16(sum_n p_n v_n[chunk]) (fp32 sum). Splitting the head
+//            dimension instead of the keys leaves nothing to combine, so no
+//            workgroup waits on another: the eight L2s of the chip are not
+//            coherent, and a cross-workgroup handoff inside a kernel would
+//            need a full L2 write-back per workgroup.
 //
 // Bytes: K is read once (phase 1), V once (phase 2); the score scratch adds
-// 4 bytes per key per query head (16 B per key at G = 4, against 4*D = 512 B
-// of K+V). Lane layout: D/8 lanes hold one key row (16 B each), so a wave
-// reads 64/(D/8) keys per load instruction (4 keys, 1 KiB, at D = 128); the
-// dot products are folded over those D/8 lanes with a butterfly.
+// 4 bytes per key per query head written, and read once per dim chunk (at
+// G = 4, D = 128, DC = 32: 16 B written + 64 B read per key, against 512 B
+// of K+V). Lane layout: a key row's chunk of 16 B per lane, so a wave reads
+// 64/(D/8) keys per load instruction in phase 1 (4 keys, 1 KiB at D = 128)
+// and 64/(DC/8) keys in phase 2 (16 keys at DC = 32); dot products are
+// folded over the lanes of a key with a butterfly.
 //
 // Keys below start[b] (left padding) are never read. The owner split uses
-// the new key from LDS rather than re-reading the slot it just wrote.
+// the new key from LDS rather than re-reading the slot it just wrote. The
+// first key loads are issued before the QK-norm/RoPE work so that their
+// latency overlaps it.
 
 #include "ek_common.h"
 #include "ek_abi_internal.h"
@@ -44,7 +52,7 @@ struct AttnParams {
   bf16_t* kc; bf16_t* vc; int64_t csb, csh, css, s_cap;
   const int64_t* seq_len; const int32_t* start;
   float* scores; int64_t score_ss;
-  float* acc; float* lsum; float* mmax; int32_t* counters; int64_t sp, gp;
+  float* lsum; float* mmax; int64_t sp, gp;
   bf16_t* out; int64_t ldo_b, ldo_h;
   int nq, nkv, splits; int64_t chunk;
   float sm_scale, eps;
@@ -121,6 +129,17 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
   const int64_t lo = rg.lo > st ? rg.lo : st;
   const int64_t hi = rg.hi;
 
+  const int sub = lane % LPK, grp = lane / LPK;
+  const bf16_t* kb = p.kc + b * p.csb + h * p.csh + sub * 8;
+  // first key tiles in flight before the QK-norm/RoPE work
+  uint4 kv[UNR];
+  const int64_t first = lo + wave * KPW + grp;
+#pragma unroll
+  for (int u = 0; u < UNR; ++u) {
+    const int64_t n = first + (int64_t)u * KPB;
+    kv[u] = (n < hi) ? ld16(kb + n * p.css) : make_uint4(0, 0, 0, 0);
+  }
+
   if (p.rope) {
     const bf16_t* row = p.q + b * p.ldq_b;
     int64_t crow = p.positions ? p.positions[b] : b;
@@ -146,7 +165,6 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
   }
   __syncthreads();
 
-  const int sub = lane % LPK, grp = lane / LPK;
   float qr[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -160,14 +178,14 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
 #pragma unroll
   for (int g = 0; g < G; ++g) { mr[g] = -1e30f; lr[g] = 0.f; }
 
-  const bf16_t* kb = p.kc + b * p.csb + h * p.csh + sub * 8;
   float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
-  for (int64_t n0 = lo + wave * KPW + grp; n0 < hi; n0 += (int64_t)KPB * UNR) {
-    uint4 kv[UNR];
+  for (int64_t n0 = first; n0 < hi; n0 += (int64_t)KPB * UNR) {
+    if (n0 != first) {
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int64_t n = n0 + (int64_t)u * KPB;
-      kv[u] = (n < hi) ? ld16(kb + n * p.css) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < UNR; ++u) {
+        const int64_t n = n0 + (int64_t)u * KPB;
+        kv[u] = (n < hi) ? ld16(kb + n * p.css) : make_uint4(0, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
@@ -214,24 +232,40 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
   }
 }
 
-template <int D, int G>
+template <int D, int G, int DC>
 __global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
-  constexpr int LPK = D / 8;
-  constexpr int KPW = EK_WAVE / LPK;
+  constexpr int LPK = DC / 8;          // lanes per key (16 B of the chunk each)
+  constexpr int KPW = EK_WAVE / LPK;   // keys per wave per load
   constexpr int KPB = NW * KPW;
   __shared__ float Ms[G], Ls[G];
-  __shared__ float red[NW][G][D];
-  __shared__ int last_flag;
+  __shared__ float red[NW][G][DC];
 
-  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int bh = blockIdx.x;
+  const int b = bh / p.nkv, h = bh % p.nkv;
+  const int d0 = blockIdx.y * DC;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const Range rg = key_range(p, s, b);
-  int64_t st = p.start[b];
-  st = st < 0 ? 0 : st;
-  const int64_t lo = rg.lo > st ? rg.lo : st;
-  const int64_t hi = rg.hi;
-  const int64_t hbase = ((int64_t)b * p.nkv + h) * p.sp;
+  int64_t len = *p.seq_len;
+  len = len < 0 ? 0 : (len > p.s_cap ? p.s_cap : len);
+  int64_t lo = p.start[b];
+  lo = lo < 0 ? 0 : lo;
+  const int64_t hi = len;
 
+  const int sub = lane % LPK, grp = lane / LPK;
+  const bf16_t* vb = p.vc + b * p.csb + h * p.csh + d0 + sub * 8;
+  const float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
+  const int64_t first = lo + wave * KPW + grp;
+  uint4 vv[UNR];
+  float sv[UNR][G];
+#pragma unroll
+  for (int u = 0; u < UNR; ++u) {
+    const int64_t n = first + (int64_t)u * KPB;
+    const bool valid = n < hi;
+    vv[u] = valid ? ld16(vb + n * p.css) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < G; ++g) sv[u][g] = valid ? scb[(int64_t)g * p.score_ss + n] : 0.f;
+  }
+
+  const int64_t hbase = ((int64_t)b * p.nkv + h) * p.sp;
   if (tid < G) {
     float M = -1e30f;
     for (int s2 = 0; s2 < p.splits; ++s2) M = fmaxf(M, p.mmax[(hbase + s2) * p.gp + tid]);
@@ -248,25 +282,22 @@ __global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
 #pragma unroll
   for (int g = 0; g < G; ++g) { Mr[g] = Ms[g]; Lr[g] = Ls[g]; }
 
-  const int sub = lane % LPK, grp = lane / LPK;
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
 
-  const bf16_t* vb = p.vc + b * p.csb + h * p.csh + sub * 8;
-  const float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
-  for (int64_t n0 = lo + wave * KPW + grp; n0 < hi; n0 += (int64_t)KPB * UNR) {
-    uint4 vv[UNR];
-    float sv[UNR][G];
+  for (int64_t n0 = first; n0 < hi; n0 += (int64_t)KPB * UNR) {
+    if (n0 != first) {
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int64_t n = n0 + (int64_t)u * KPB;
-      const bool valid = n < hi;
-      vv[u] = valid ? ld16(vb + n * p.css) : make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < UNR; ++u) {
+        const int64_t n = n0 + (int64_t)u * KPB;
+        const bool valid = n < hi;
+        vv[u] = valid ? ld16(vb + n * p.css) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-      for (int g = 0; g < G; ++g) sv[u][g] = valid ? scb[(int64_t)g * p.score_ss + n] : 0.f;
+        for (int g = 0; g < G; ++g) sv[u][g] = valid ? scb[(int64_t)g * p.score_ss + n] : 0.f;
+      }
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
@@ -282,7 +313,7 @@ __global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
       }
     }
   }
-  // fold the key groups of the wave (lanes with equal `sub`)
+  // fold the key groups of the wave (lanes with equal `sub`), then the waves
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -299,33 +330,26 @@ __global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
       for (int j = 0; j < 8; ++j) red[wave][g][sub * 8 + j] = acc[g][j];
   }
   __syncthreads();
-  const bool single = p.splits == 1;
-  for (int i = tid; i < G * D; i += NT) {
-    const int g = i / D, d = i % D;
+  for (int i = tid; i < G * DC; i += NT) {
+    const int g = i / DC, d = i % DC;
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) t += red[w][g][d];
-    if (single) p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d] = (bf16_t)f2bf(t);
-    else p.acc[((hbase + s) * p.gp + g) * D + d] = t;
-  }
-  if (single) return;
-  if (!last_to_arrive(p.counters + (int64_t)b * p.nkv + h, p.splits, &last_flag)) return;
-  for (int i = tid; i < G * D; i += NT) {
-    const int g = i / D, d = i % D;
-    float t = 0.f;
-    for (int s2 = 0; s2 < p.splits; ++s2)
-      t += __hip_atomic_load(p.acc + ((hbase + s2) * p.gp + g) * D + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d] = (bf16_t)f2bf(t);
+    p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d0 + d] = (bf16_t)f2bf(t);
   }
 }
 
 template <int D, int G>
 hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
-  dim3 grid((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);
-  hipLaunchKernelGGL((attn_scores_kernel<D, G>), grid, dim3(NT), 0, st, p);
+  dim3 grid1((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);
+  hipLaunchKernelGGL((attn_scores_kernel<D, G>), grid1, dim3(NT), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((attn_pv_kernel<D, G>), grid, dim3(NT), 0, st, p);
+  // (b, kv head) in x: the D/DC chunk workgroups of one head share an XCD
+  // (workgroups are dealt round-robin over the 8 XCDs by linear id)
+  constexpr int DC = D >= 32 ? 32 : D;
+  dim3 grid2((unsigned)(b * p.nkv), (unsigned)(D / DC));
+  hipLaunchKernelGGL((attn_pv_kernel<D, G, DC>), grid2, dim3(NT), 0, st, p);
   return hipGetLastError();
 }
 
@@ -347,12 +371,12 @@ extern "C" {
 int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
                    const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
                    void* k_cache, void* v_cache, int64_t csb, int64_t csh, int64_t css, int64_t s_cap,
-                   const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* acc,
-                   float* lsum, float* mmax, int32_t* counters, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
+                   const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* lsum,
+                   float* mmax, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
                    int64_t ldo_h, int64_t b, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits,
                    int64_t chunk, float sm_scale, float eps, void* stream) {
   EK_GUARD();
-  if (b < 1 || b > 65535 || n_kv < 1 || n_q < n_kv || n_q % n_kv)
+  if (b < 1 || b * n_kv > 0x7fffffff || n_kv < 1 || n_q < n_kv || n_q % n_kv || b > 65535)
     return ek_fail(hipErrorInvalidValue, "attn: bad batch or head counts");
   const int64_t g = n_q / n_kv;
   if (splits < 1 || splits > sp || chunk < 1 || g > gp)
@@ -372,7 +396,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
   p.kc = (bf16_t*)k_cache; p.vc = (bf16_t*)v_cache; p.csb = csb; p.csh = csh; p.css = css; p.s_cap = s_cap;
   p.seq_len = seq_len; p.start = start;
   p.scores = scores; p.score_ss = score_ss;
-  p.acc = acc; p.lsum = lsum; p.mmax = mmax; p.counters = counters; p.sp = sp; p.gp = gp;
+  p.lsum = lsum; p.mmax = mmax; p.sp = sp; p.gp = gp;
   p.out = (bf16_t*)out; p.ldo_b = ldo_b; p.ldo_h = ldo_h;
   p.nq = (int)n_q; p.nkv = (int)n_kv; p.splits = (int)splits; p.chunk = chunk;
   p.sm_scale = sm_scale; p.eps = eps;

@@ -1,5 +1,10 @@
 // C-ABI entry points of the GEMV family (kernel template: ek_gemv_impl.h;
 // instantiations: ek_gemv_inst.hip, one object per prologue/epilogue pair).
+//
+// Every entry point takes two tuning arguments: rpw (output rows per wave,
+// 1, 2 or 4; 0 = default) and blocks (the grid cap: workgroups loop over row
+// groups, so a grid of a few workgroups per CU streams any height; 0 =
+// default of 4 per CU). Neither changes results.
 
 #include <cstring>
 
@@ -10,8 +15,6 @@
 namespace ekg {
 namespace {
 
-
-// ----------------------------------------------------------------------------
 int pick_kpl(int64_t nch) {
   if (nch <= 64) return 1;
   if (nch == 320) return 5;    // K = 2560
@@ -26,14 +29,29 @@ bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 
 
 int bm_for(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8; }
 
+// compute units of the current device (cached per device index)
+int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cache[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 // Launch one GEMV-family kernel. sk > 1 splits the reduction over
-// blockIdx.y (EPI_PARTS only). rpw == 0 picks the default rows per wave.
-hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int rpw, hipStream_t st) {
+// blockIdx.y (EPI_PARTS only). The grid width used goes to *gx_out.
+hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int64_t rpw, int64_t blocks,
+                    hipStream_t st, int64_t* gx_out = nullptr) {
   if (p.m < 1 || p.m > 8) return ek_fail(hipErrorInvalidValue, "gemv: batch rows must be 1..8 per launch");
   if (k <= 0 || k % 8 || sk < 1 || k % (8 * sk))
     return ek_fail(hipErrorInvalidValue, "gemv: K must be a positive multiple of 8*splits");
   if (sk > 1 && epi != EPI_PARTS) return ek_fail(hipErrorInvalidValue, "gemv: split-K needs the partials epilogue");
   if (sk > 1 && pro != PRO_X) return ek_fail(hipErrorInvalidValue, "gemv: split-K needs a plain x prologue");
+  if (sk > 65535) return ek_fail(hipErrorInvalidValue, "gemv: too many splits");
   p.ks = k / sk;
   if (!aligned16(p.w) || p.ldw % 8 || (p.x && (!aligned16(p.x) || p.ldx % 8)) ||
       (p.res && (!aligned16(p.res) || p.ldr % 8)) || (p.res_out && (!aligned16(p.res_out) || p.ldro % 8)) ||
@@ -41,14 +59,20 @@ hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int r
     return ek_fail(hipErrorInvalidValue, "gemv: operand rows must be 16-byte aligned (strides multiples of 8)");
   const int bm = bm_for(p.m);
   const size_t lds = (size_t)bm * p.ks * sizeof(bf16_t);
-  if (lds > kMaxLds) return ek_fail(hipErrorInvalidValue, "gemv: batch rows x K exceed the 48 KiB activation stage (split K)");
+  if (lds > kMaxLds)
+    return ek_fail(hipErrorInvalidValue, "gemv: batch rows x K exceed the 48 KiB activation stage (split K)");
   if (rpw <= 0) rpw = (epi == EPI_ARGMAX) ? 4 : 1;
-  const int64_t rows_per_blk = (int64_t)NWAVE * rpw;
-  const int64_t gx = (p.n + rows_per_blk - 1) / rows_per_blk;
+  if (rpw != 1 && rpw != 2 && rpw != 4) return ek_fail(hipErrorInvalidValue, "gemv: rows per wave must be 1, 2 or 4");
+  const int64_t rows_per_grp = (int64_t)NWAVE * rpw;
+  const int64_t ngroups = (p.n + rows_per_grp - 1) / rows_per_grp;
+  if (blocks <= 0) blocks = 4 * (int64_t)cu_count();
+  const int64_t gx = ngroups < blocks ? ngroups : blocks;
   if (gx <= 0 || gx > 0x7fffffff) return ek_fail(hipErrorInvalidValue, "gemv: bad grid");
+  if (gx_out) *gx_out = gx;
   dim3 grid((unsigned)gx, (unsigned)sk);
   const int kpl = pick_kpl(p.ks / 8);
-#define EK_CASE(PR, EP) if (pro == PR && epi == EP) return launch_pair<PR, EP>(p, bm, kpl, rpw, grid, lds, st);
+#define EK_CASE(PR, EP) \
+  if (pro == PR && epi == EP) return launch_pair<PR, EP>(p, bm, kpl, (int)rpw, grid, lds, st);
   EK_CASE(PRO_X, EPI_BF16)
   EK_CASE(PRO_X, EPI_PARTS)
   EK_CASE(PRO_X, EPI_SWIGLU)
@@ -63,6 +87,54 @@ hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int r
   EK_CASE(PRO_EMBED, EPI_BF16)
 #undef EK_CASE
   return ek_fail(hipErrorInvalidValue, "gemv: unsupported prologue/epilogue pair");
+}
+
+// One workgroup: the first-index argmax over `parts` per-workgroup partials
+// of each of m rows, then the optional decode-step bookkeeping.
+__global__ __launch_bounds__(NTHR) void argmax_reduce_kernel(const float* __restrict__ am_val,
+                                                             const int32_t* __restrict__ am_idx, int64_t parts,
+                                                             int m, int64_t* out_tok, int64_t* st_tokens,
+                                                             int64_t* st_positions, int32_t* st_out,
+                                                             int64_t* st_step, int64_t max_steps) {
+  __shared__ float tbv[NTHR];
+  __shared__ int tbi[NTHR];
+  for (int b = 0; b < m; ++b) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int64_t blk = threadIdx.x; blk < parts; blk += NTHR) {
+      const float v = am_val[blk * m + b];
+      const int i = am_idx[blk * m + b];
+      if (i != 0x7fffffff && (bi == 0x7fffffff || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
+    }
+    tbv[threadIdx.x] = bv;
+    tbi[threadIdx.x] = bi;
+    __syncthreads();
+    for (int s = NTHR / 2; s > 0; s >>= 1) {
+      if (threadIdx.x < (unsigned)s) {
+        const float v = tbv[threadIdx.x + s];
+        const int i = tbi[threadIdx.x + s];
+        const float cv = tbv[threadIdx.x];
+        const int ci = tbi[threadIdx.x];
+        if (i != 0x7fffffff && (ci == 0x7fffffff || v > cv || (v == cv && i < ci))) {
+          tbv[threadIdx.x] = v;
+          tbi[threadIdx.x] = i;
+        }
+      }
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+      const int64_t tok = tbi[0] == 0x7fffffff ? 0 : tbi[0];
+      if (out_tok) out_tok[b] = tok;
+      if (st_tokens) {
+        st_tokens[b] = tok;
+        st_positions[b] += 1;
+        const int64_t step = *st_step;
+        if (step >= 0 && step < max_steps) st_out[step * m + b] = (int32_t)tok;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && st_tokens) *st_step += 1;
 }
 
 GemvParams zero_params() {
@@ -81,8 +153,8 @@ using namespace ekg;
 // ============================================================================
 extern "C" {
 
-int ek_gemv(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k,
-            int64_t ldx, int64_t ldw, int64_t ldy, void* stream) {
+int ek_gemv(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldw,
+            int64_t ldy, int64_t rpw, int64_t blocks, void* stream) {
   EK_GUARD();
   if (m < 1 || n < 1) return ek_fail(hipErrorInvalidValue, "gemv: empty shape");
   hipStream_t st = (hipStream_t)stream;
@@ -93,38 +165,38 @@ int ek_gemv(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t
     p.w = (const bf16_t*)w; p.ldw = ldw; p.n = n; p.m = (int)mt;
     p.x = (const bf16_t*)x + m0 * ldx; p.ldx = ldx;
     p.y = (bf16_t*)y + m0 * ldy; p.ldy = ldy;
-    hipError_t e = run_gemv(PRO_X, EPI_BF16, p, k, 1, 0, st);
+    hipError_t e = run_gemv(PRO_X, EPI_BF16, p, k, 1, rpw, blocks, st);
     if (e != hipSuccess) return e;
     m0 += mt;
   }
   return hipSuccess;
 }
 
-int ek_gemv_parts(const void* x, const void* w, float* parts, int64_t m, int64_t n, int64_t k,
-                  int64_t ldx, int64_t ldw, int64_t sk, void* stream) {
+int ek_gemv_parts(const void* x, const void* w, float* parts, int64_t m, int64_t n, int64_t k, int64_t ldx,
+                  int64_t ldw, int64_t sk, int64_t rpw, int64_t blocks, void* stream) {
   EK_GUARD();
   if (m < 1 || m > 8 || n < 1) return ek_fail(hipErrorInvalidValue, "gemv_parts: m must be 1..8");
   GemvParams p = zero_params();
   p.w = (const bf16_t*)w; p.ldw = ldw; p.n = n; p.m = (int)m;
   p.x = (const bf16_t*)x; p.ldx = ldx;
   p.p_out = parts;
-  return run_gemv(PRO_X, EPI_PARTS, p, k, sk, 0, (hipStream_t)stream);
+  return run_gemv(PRO_X, EPI_PARTS, p, k, sk, rpw, blocks, (hipStream_t)stream);
 }
 
-int ek_gemv_swiglu(const void* x, const void* w, void* y, int64_t m, int64_t inter, int64_t k,
-                   int64_t ldx, int64_t ldw, int64_t ldy, void* stream) {
+int ek_gemv_swiglu(const void* x, const void* w, void* y, int64_t m, int64_t inter, int64_t k, int64_t ldx,
+                   int64_t ldw, int64_t ldy, int64_t rpw, int64_t blocks, void* stream) {
   EK_GUARD();
   if (m < 1 || m > 8 || inter < 1) return ek_fail(hipErrorInvalidValue, "gemv_swiglu: m must be 1..8");
   GemvParams p = zero_params();
   p.w = (const bf16_t*)w; p.ldw = ldw; p.n = inter; p.m = (int)m; p.up_off = inter;
   p.x = (const bf16_t*)x; p.ldx = ldx;
   p.y = (bf16_t*)y; p.ldy = ldy;
-  return run_gemv(PRO_X, EPI_SWIGLU, p, k, 1, 0, (hipStream_t)stream);
+  return run_gemv(PRO_X, EPI_SWIGLU, p, k, 1, rpw, blocks, (hipStream_t)stream);
 }
 
-int ek_norm_gemv(const void* x, const void* residual, void* residual_out, const void* norm_w,
-                 const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldr,
-                 int64_t ldro, int64_t ldw, int64_t ldy, float eps, int silu, void* stream) {
+int ek_norm_gemv(const void* x, const void* residual, void* residual_out, const void* norm_w, const void* w,
+                 void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldr, int64_t ldro, int64_t ldw,
+                 int64_t ldy, float eps, int silu, int64_t rpw, int64_t blocks, void* stream) {
   EK_GUARD();
   if (m < 1 || m > 8 || n < 1) return ek_fail(hipErrorInvalidValue, "norm_gemv: m must be 1..8");
   GemvParams p = zero_params();
@@ -135,13 +207,13 @@ int ek_norm_gemv(const void* x, const void* residual, void* residual_out, const 
   p.nw = (const bf16_t*)norm_w; p.eps = eps;
   p.y = (bf16_t*)y; p.ldy = ldy;
   const int pro = residual ? PRO_ADD_NORM : PRO_NORM;
-  return run_gemv(pro, silu ? EPI_SWIGLU : EPI_BF16, p, k, 1, 0, (hipStream_t)stream);
+  return run_gemv(pro, silu ? EPI_SWIGLU : EPI_BF16, p, k, 1, rpw, blocks, (hipStream_t)stream);
 }
 
 int ek_parts_norm_gemv(const float* parts, int64_t sk_in, const void* residual, void* residual_out,
-                       const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k,
-                       int64_t ldr, int64_t ldro, int64_t ldw, int64_t ldy, float eps, int silu,
-                       int64_t rpw, void* stream) {
+                       const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldr,
+                       int64_t ldro, int64_t ldw, int64_t ldy, float eps, int silu, int64_t rpw, int64_t blocks,
+                       void* stream) {
   EK_GUARD();
   if (m < 1 || m > 8 || n < 1 || sk_in < 1) return ek_fail(hipErrorInvalidValue, "parts_norm_gemv: bad shape");
   GemvParams p = zero_params();
@@ -151,15 +223,16 @@ int ek_parts_norm_gemv(const float* parts, int64_t sk_in, const void* residual, 
   p.res_out = (bf16_t*)residual_out; p.ldro = ldro;
   p.nw = (const bf16_t*)norm_w; p.eps = eps;
   p.y = (bf16_t*)y; p.ldy = ldy;
-  return run_gemv(PRO_PARTS, silu ? EPI_SWIGLU : EPI_BF16, p, k, 1, (int)rpw, (hipStream_t)stream);
+  return run_gemv(PRO_PARTS, silu ? EPI_SWIGLU : EPI_BF16, p, k, 1, rpw, blocks, (hipStream_t)stream);
 }
 
-int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, int64_t vocab,
-                       void* residual_out, const void* norm_w, const void* w, void* y, int64_t m,
-                       int64_t n, int64_t k, int64_t ldro, int64_t ldw, int64_t ldy, float eps,
-                       int64_t* slot_t, int64_t* len_t, int64_t rpw, void* stream) {
+int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, int64_t vocab, void* residual_out,
+                       const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldro,
+                       int64_t ldw, int64_t ldy, float eps, int64_t* slot_t, int64_t* len_t, int64_t rpw,
+                       int64_t blocks, void* stream) {
   EK_GUARD();
   if (m < 1 || m > 8 || n < 1) return ek_fail(hipErrorInvalidValue, "embed_norm_gemv: m must be 1..8");
+  if (len_t && !slot_t) return ek_fail(hipErrorInvalidValue, "embed_norm_gemv: len_t needs slot_t");
   GemvParams p = zero_params();
   p.w = (const bf16_t*)w; p.ldw = ldw; p.n = n; p.m = (int)m;
   p.tokens = tokens; p.embed = (const bf16_t*)embed; p.lde = lde; p.vocab = vocab;
@@ -167,20 +240,24 @@ int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, in
   p.nw = (const bf16_t*)norm_w; p.eps = eps;
   p.slot_t = slot_t; p.len_t = len_t;
   p.y = (bf16_t*)y; p.ldy = ldy;
-  return run_gemv(PRO_EMBED, EPI_BF16, p, k, 1, (int)rpw, (hipStream_t)stream);
+  return run_gemv(PRO_EMBED, EPI_BF16, p, k, 1, rpw, blocks, (hipStream_t)stream);
 }
 
-int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const void* residual,
-                      const void* norm_w, float eps, const void* w, int64_t m, int64_t vocab, int64_t k,
-                      int64_t ldx, int64_t ldr, int64_t ldw, void* logits, int64_t ld_logits,
-                      float* am_val, int32_t* am_idx, int64_t am_cap, int32_t* counter, int64_t* out_tok,
-                      int64_t* st_tokens, int64_t* st_positions, int32_t* st_out, int64_t* st_step,
-                      int64_t max_steps, int64_t rpw, void* stream) {
+int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const void* residual, const void* norm_w,
+                      float eps, const void* w, int64_t m, int64_t vocab, int64_t k, int64_t ldx, int64_t ldr,
+                      int64_t ldw, void* logits, int64_t ld_logits, float* am_val, int32_t* am_idx, int64_t am_cap,
+                      int64_t* out_tok, int64_t* st_tokens, int64_t* st_positions, int32_t* st_out,
+                      int64_t* st_step, int64_t max_steps, int64_t rpw, int64_t blocks, void* stream) {
   EK_GUARD();
   if (m < 1 || m > 8 || vocab < 1) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: m must be 1..8");
+  if (st_tokens && (!st_positions || !st_out || !st_step))
+    return ek_fail(hipErrorInvalidValue, "lm_head_argmax: step state needs tokens, positions, out and step");
   if (rpw <= 0) rpw = 4;
-  const int64_t blocks = (vocab + NWAVE * rpw - 1) / (NWAVE * rpw);
-  if (blocks * m > am_cap) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: partial buffer too small");
+  if (rpw != 1 && rpw != 2 && rpw != 4) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: rpw must be 1, 2 or 4");
+  if (blocks <= 0) blocks = 4 * (int64_t)cu_count();
+  const int64_t groups = (vocab + NWAVE * rpw - 1) / (NWAVE * rpw);
+  const int64_t gx = groups < blocks ? groups : blocks;
+  if (gx * m > am_cap) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: partial buffer too small");
   GemvParams p = zero_params();
   p.w = (const bf16_t*)w; p.ldw = ldw; p.n = vocab; p.m = (int)m;
   p.x = (const bf16_t*)x; p.ldx = ldx;
@@ -188,11 +265,16 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
   p.res = (const bf16_t*)residual; p.ldr = ldr;
   p.nw = (const bf16_t*)norm_w; p.eps = eps;
   p.y = (bf16_t*)logits; p.ldy = ld_logits;
-  p.am_val = am_val; p.am_idx = am_idx; p.counter = counter; p.out_tok = out_tok;
-  p.st_tokens = st_tokens; p.st_positions = st_positions; p.st_out = st_out; p.st_step = st_step;
-  p.max_steps = max_steps;
+  p.am_val = am_val; p.am_idx = am_idx;
   const int pro = parts ? PRO_PARTS : PRO_X;
-  return run_gemv(pro, EPI_ARGMAX, p, k, 1, (int)rpw, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  int64_t used = 0;
+  hipError_t e = run_gemv(pro, EPI_ARGMAX, p, k, 1, rpw, blocks, st, &used);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(NTHR), 0, st, (const float*)am_val,
+                     (const int32_t*)am_idx, used, (int)m, out_tok, st_tokens, st_positions, st_out, st_step,
+                     max_steps);
+  return hipGetLastError();
 }
 
 }  // extern "C"

@@ -58,10 +58,8 @@ struct GemvParams {
   bf16_t* y; int64_t ldy;
   float* p_out;      // [gridDim.y][m][n]
   int64_t up_off;    // SWIGLU: first row of the up half
-  // argmax
-  float* am_val; int32_t* am_idx; int32_t* counter;
-  int64_t* out_tok;
-  int64_t* st_tokens; int64_t* st_positions; int32_t* st_out; int64_t* st_step; int64_t max_steps;
+  // argmax partials, one (value, index) per workgroup and batch row
+  float* am_val; int32_t* am_idx;
 };
 
 // ----------------------------------------------------------------------------
@@ -179,6 +177,14 @@ __device__ __forceinline__ void prologue(const GemvParams& p, bf16_t* xs, float 
 
 // ----------------------------------------------------------------------------
 // the kernel
+//
+// Rows are dealt out in groups of NWAVE * RPW (RPW consecutive rows per
+// wave). A workgroup handles groups blockIdx.x, blockIdx.x + gridDim.x, ...
+// so a grid of a few workgroups per CU streams the whole matrix after one
+// prologue. When a row fits one block of KPL chunks per lane (every decode
+// shape), the loads of the next group are issued chunk by chunk as the
+// current group's chunks are consumed, so the HBM stream never drains
+// between groups.
 // ----------------------------------------------------------------------------
 template <int PRO, int EPI, int BM, int KPL, int RPW>
 __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams p) {
@@ -186,165 +192,146 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams p) {
   bf16_t* xs = reinterpret_cast<bf16_t*>(smem_raw);
   __shared__ float red[NWAVE][BM];
   constexpr int R2 = (EPI == EPI_SWIGLU) ? 2 * RPW : RPW;
+  constexpr int ROWS = NWAVE * RPW;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t ks = p.ks;
   const int64_t nch = ks >> 3;
   const int64_t kbase = (int64_t)blockIdx.y * ks;
-  const int64_t row0 = ((int64_t)blockIdx.x * NWAVE + wave) * RPW;
+  const int64_t ngroups = (p.n + ROWS - 1) / ROWS;
+  const bool one_block = nch <= (int64_t)KPL * EK_WAVE;
 
-  const bf16_t* wrow[R2];
+  // row r of this wave in group g (out-of-range rows read row 0; dropped)
+  auto wrow = [&](int64_t g, int r) -> const bf16_t* {
+    const int rr = (EPI == EPI_SWIGLU && r >= RPW) ? r - RPW : r;
+    int64_t n = g * ROWS + wave * RPW + rr;
+    if (n >= p.n) n = 0;
+    if (EPI == EPI_SWIGLU && r >= RPW) n += p.up_off;
+    return p.w + n * p.ldw + kbase;
+  };
+
+  float best_v[BM];
+  int best_i[BM];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    int64_t n = row0 + r;
-    if (n >= p.n) n = 0;   // out-of-range rows read row 0; their results are dropped
-    wrow[r] = p.w + n * p.ldw + kbase;
-    if constexpr (EPI == EPI_SWIGLU) wrow[RPW + r] = p.w + (p.up_off + n) * p.ldw + kbase;
+  for (int b = 0; b < BM; ++b) { best_v[b] = -INFINITY; best_i[b] = 0x7fffffff; }
+
+  int64_t g = blockIdx.x;
+  uint4 wv[R2][KPL];
+  if (one_block && g < ngroups) {
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int64_t c = j * EK_WAVE + lane;
+#pragma unroll
+      for (int r = 0; r < R2; ++r) wv[r][j] = (c < nch) ? ld16(wrow(g, r) + c * 8) : make_uint4(0, 0, 0, 0);
+    }
   }
+  prologue<PRO, BM>(p, xs, red);
+  __syncthreads();
 
-  float acc[R2][BM];
+  for (; g < ngroups; g += gridDim.x) {
+    const int64_t gn = g + gridDim.x;
+    const bool more = gn < ngroups;
+    float acc[R2][BM];
 #pragma unroll
-  for (int r = 0; r < R2; ++r)
+    for (int r = 0; r < R2; ++r)
 #pragma unroll
-    for (int b = 0; b < BM; ++b) acc[r][b] = 0.f;
+      for (int b = 0; b < BM; ++b) acc[r][b] = 0.f;
 
-  for (int64_t cb = 0; cb < nch; cb += KPL * EK_WAVE) {
-    uint4 wv[R2][KPL];
+    if (one_block) {
 #pragma unroll
-    for (int j = 0; j < KPL; ++j) {
-      const int64_t c = cb + j * EK_WAVE + lane;
+      for (int j = 0; j < KPL; ++j) {
+        const int64_t c = j * EK_WAVE + lane;
+        uint4 cur[R2];
 #pragma unroll
-      for (int r = 0; r < R2; ++r)
-        wv[r][j] = (c < nch) ? ld16(wrow[r] + c * 8) : make_uint4(0, 0, 0, 0);
-    }
-    if (cb == 0) {
-      prologue<PRO, BM>(p, xs, red);
-      __syncthreads();
-    }
+        for (int r = 0; r < R2; ++r) cur[r] = wv[r][j];
+        if (more && c < nch) {
 #pragma unroll
-    for (int j = 0; j < KPL; ++j) {
-      const int64_t c = cb + j * EK_WAVE + lane;
-      if (c < nch) {
+          for (int r = 0; r < R2; ++r) wv[r][j] = ld16(wrow(gn, r) + c * 8);
+        }
+        if (c < nch) {
 #pragma unroll
-        for (int b = 0; b < BM; ++b) {
-          const uint4 xv = *reinterpret_cast<const uint4*>(xs + b * ks + c * 8);
+          for (int b = 0; b < BM; ++b) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(xs + b * ks + c * 8);
 #pragma unroll
-          for (int r = 0; r < R2; ++r) acc[r][b] = dot8_acc(wv[r][j], xv, acc[r][b]);
+            for (int r = 0; r < R2; ++r) acc[r][b] = dot8_acc(cur[r], xv, acc[r][b]);
+          }
+        }
+      }
+    } else {
+      for (int64_t cb = 0; cb < nch; cb += KPL * EK_WAVE) {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) {
+          const int64_t c = cb + j * EK_WAVE + lane;
+#pragma unroll
+          for (int r = 0; r < R2; ++r) wv[r][j] = (c < nch) ? ld16(wrow(g, r) + c * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) {
+          const int64_t c = cb + j * EK_WAVE + lane;
+          if (c < nch) {
+#pragma unroll
+            for (int b = 0; b < BM; ++b) {
+              const uint4 xv = *reinterpret_cast<const uint4*>(xs + b * ks + c * 8);
+#pragma unroll
+              for (int r = 0; r < R2; ++r) acc[r][b] = dot8_acc(wv[r][j], xv, acc[r][b]);
+            }
+          }
         }
       }
     }
-  }
 
 #pragma unroll
-  for (int r = 0; r < R2; ++r)
+    for (int r = 0; r < R2; ++r)
 #pragma unroll
-    for (int b = 0; b < BM; ++b) acc[r][b] = wave_sum(acc[r][b]);
+      for (int b = 0; b < BM; ++b) acc[r][b] = wave_sum(acc[r][b]);
 
-  if constexpr (EPI == EPI_BF16 || EPI == EPI_PARTS || EPI == EPI_SWIGLU) {
+    const int64_t row0 = g * ROWS + wave * RPW;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
+      const int64_t n = row0 + r;
 #pragma unroll
       for (int b = 0; b < BM; ++b) {
-        if (lane != ((r * BM + b) & 63)) continue;
-        const int64_t n = row0 + r;
-        if (n >= p.n || b >= p.m) continue;
-        if constexpr (EPI == EPI_BF16) {
-          p.y[b * p.ldy + n] = (bf16_t)f2bf(acc[r][b]);
+        if constexpr (EPI == EPI_ARGMAX) {
+          // rows reach a wave in increasing order: strict > keeps the first max
+          const float v = rbf(acc[r][b]);
+          if (n < p.n && (v > best_v[b] || best_i[b] == 0x7fffffff)) { best_v[b] = v; best_i[b] = (int)n; }
+        }
+        if (lane != ((r * BM + b) & 63) || n >= p.n || b >= p.m) continue;
+        if constexpr (EPI == EPI_BF16 || EPI == EPI_ARGMAX) {
+          if (EPI == EPI_BF16 || p.y) p.y[b * p.ldy + n] = (bf16_t)f2bf(acc[r][b]);
         } else if constexpr (EPI == EPI_PARTS) {
           p.p_out[((int64_t)blockIdx.y * p.m + b) * p.n + n] = acc[r][b];
         } else {
-          const float g = rbf(acc[r][b]);
+          const float gt = rbf(acc[r][b]);
           const float u = rbf(acc[RPW + r][b]);
-          const float s = rbf(g / (1.0f + expf(-g)));
+          const float s = rbf(gt / (1.0f + expf(-gt)));
           p.y[b * p.ldy + n] = (bf16_t)f2bf(s * u);
         }
       }
     }
-  } else {  // EPI_ARGMAX
+  }
+
+  if constexpr (EPI == EPI_ARGMAX) {
+    // per-workgroup (value, index) partials; ek_argmax_reduce finishes
     __shared__ float wbv[NWAVE][BM];
     __shared__ int wbi[NWAVE][BM];
-    __shared__ float tbv[NTHR];
-    __shared__ int tbi[NTHR];
-    __shared__ int last_flag;
     if (lane == 0) {
 #pragma unroll
-      for (int b = 0; b < BM; ++b) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const int64_t n = row0 + r;
-          const float v = rbf(acc[r][b]);
-          if (n < p.n && (v > bv || bi == 0x7fffffff)) { bv = v; bi = (int)n; }
-        }
-        wbv[wave][b] = bv;
-        wbi[wave][b] = bi;
-      }
-    }
-    // optional logits
-    if (p.y) {
-#pragma unroll
-      for (int r = 0; r < RPW; ++r)
-#pragma unroll
-        for (int b = 0; b < BM; ++b) {
-          const int64_t n = row0 + r;
-          if (lane == ((r * BM + b) & 63) && n < p.n && b < p.m)
-            p.y[b * p.ldy + n] = (bf16_t)f2bf(acc[r][b]);
-        }
+      for (int b = 0; b < BM; ++b) { wbv[wave][b] = best_v[b]; wbi[wave][b] = best_i[b]; }
     }
     __syncthreads();
     if (threadIdx.x < (unsigned)p.m) {
       const int b = threadIdx.x;
-      float bv = wbv[0][b];
-      int bi = wbi[0][b];
-      for (int w = 1; w < NWAVE; ++w) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int w = 0; w < NWAVE; ++w) {
         const float v = wbv[w][b];
         const int i = wbi[w][b];
-        if (i != 0x7fffffff && (bi == 0x7fffffff || v > bv)) { bv = v; bi = i; }
+        if (i != 0x7fffffff && (bi == 0x7fffffff || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
       }
       p.am_val[(int64_t)blockIdx.x * p.m + b] = bv;
       p.am_idx[(int64_t)blockIdx.x * p.m + b] = bi;
     }
-    if (!last_to_arrive(p.counter, gridDim.x, &last_flag)) return;
-    // the last workgroup: reduce the per-workgroup partials, lowest index wins ties
-    for (int b = 0; b < p.m; ++b) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int64_t blk = threadIdx.x; blk < gridDim.x; blk += NTHR) {
-        const float v = __hip_atomic_load(p.am_val + blk * p.m + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int i = __hip_atomic_load(p.am_idx + blk * p.m + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (i == 0x7fffffff) continue;
-        if (bi == 0x7fffffff || v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-      }
-      tbv[threadIdx.x] = bv;
-      tbi[threadIdx.x] = bi;
-      __syncthreads();
-      for (int s = NTHR / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < (unsigned)s) {
-          const float v = tbv[threadIdx.x + s];
-          const int i = tbi[threadIdx.x + s];
-          const float cv = tbv[threadIdx.x];
-          const int ci = tbi[threadIdx.x];
-          if (i != 0x7fffffff && (ci == 0x7fffffff || v > cv || (v == cv && i < ci))) {
-            tbv[threadIdx.x] = v;
-            tbi[threadIdx.x] = i;
-          }
-        }
-        __syncthreads();
-      }
-      if (threadIdx.x == 0) {
-        const int64_t tok = tbi[0] == 0x7fffffff ? 0 : tbi[0];
-        if (p.out_tok) p.out_tok[b] = tok;
-        if (p.st_tokens) {
-          p.st_tokens[b] = tok;
-          p.st_positions[b] += 1;
-          const int64_t step = *p.st_step;
-          if (step >= 0 && step < p.max_steps) p.st_out[step * p.m + b] = (int32_t)tok;
-        }
-      }
-      __syncthreads();
-    }
-    if (threadIdx.x == 0 && p.st_tokens) *p.st_step += 1;
   }
 }
 

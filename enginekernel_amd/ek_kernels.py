@@ -31,6 +31,24 @@ __all__ = [
 _DISABLED = False
 _BF16 = torch.bfloat16
 
+# GEMV-family launch shape per (kernel, N, K[, rows]): (rows per wave, grid
+# cap). (0, 0) is the library's default (1 row per wave, 4 workgroups per
+# CU; lm_head 4 rows per wave). Results never depend on these. The entries
+# below are the fastest of a rows-per-wave x grid-cap sweep on MI355X at
+# batch 1 (weights rotated past the 256 MB Infinity Cache).
+TUNE: dict = {
+    ("parts_norm", 6144, 2560): (1, 512),        # add + RMSNorm + fused qkv
+    ("parts_norm_silu", 9728, 2560): (1, 768),   # add + RMSNorm + gate_up + SwiGLU
+    ("embed_norm", 6144, 2560): (1, 512),        # embedding + RMSNorm + qkv (layer 0)
+    ("parts", 2560, 4096): (1, 1024),            # o_proj
+    ("parts", 2560, 9728): (1, 512),             # down_proj
+    ("lm_head", 151936, 2560): (1, 512),         # lm_head + argmax partials
+}
+
+
+def _tune(kind: str, n: int, k: int, m: int):
+    return TUNE.get((kind, n, k, m), TUNE.get((kind, n, k), (0, 0)))
+
 
 # ----------------------------------------------------------------------------
 # availability (ek_kernels.py:44-70: has_triton / disable_triton / probe_triton)
@@ -187,7 +205,8 @@ def gemv(x, w, out=None, cfg=None):
     n = w.shape[0]
     y = torch.empty(m, n, device=x.device, dtype=x.dtype) if out is None else out
     _need(y.shape == (m, n) and y.stride(-1) == 1, "gemv: out shape")
-    call("ek_gemv", ptr(x), ptr(w), ptr(y), m, n, k, x.stride(0), w.stride(0), y.stride(0), stream())
+    call("ek_gemv", ptr(x), ptr(w), ptr(y), m, n, k, x.stride(0), w.stride(0), y.stride(0),
+         *_tune("gemv", n, k, m), stream())
     return y
 
 
@@ -204,7 +223,8 @@ def gemv_parts(x, w, sk=None, out=None):
     _need(k % (8 * sk) == 0, "gemv_parts: K must split into multiples of 8")
     parts = torch.empty(sk, m, n, device=x.device, dtype=torch.float32) if out is None else out
     _need(parts.shape == (sk, m, n) and parts.is_contiguous() and parts.dtype == torch.float32, "parts out")
-    call("ek_gemv_parts", ptr(x), ptr(w), ptr(parts), m, n, k, x.stride(0), w.stride(0), sk, stream())
+    call("ek_gemv_parts", ptr(x), ptr(w), ptr(parts), m, n, k, x.stride(0), w.stride(0), sk,
+         *_tune("parts", n, k, m), stream())
     return parts
 
 
@@ -245,7 +265,8 @@ def gemv_swiglu(x, w):
     i = w.shape[0] // 2
     _need(1 <= m <= 8, "gemv_swiglu: M must be 1..8")
     y = torch.empty(m, i, device=x.device, dtype=x.dtype)
-    call("ek_gemv_swiglu", ptr(x), ptr(w), ptr(y), m, i, k, x.stride(0), w.stride(0), y.stride(0), stream())
+    call("ek_gemv_swiglu", ptr(x), ptr(w), ptr(y), m, i, k, x.stride(0), w.stride(0), y.stride(0),
+         *_tune("swiglu", i, k, m), stream())
     return y
 
 
@@ -264,11 +285,12 @@ def norm_gemv(x, residual, norm_w, w, eps, silu=False):
         _rows(residual, "residual")
     call("ek_norm_gemv", ptr(x), ptr(residual) if has_add else None, ptr(r_out) if has_add else None,
          ptr(norm_w), ptr(w), ptr(y), m, n, k, x.stride(0), residual.stride(0) if has_add else 0,
-         r_out.stride(0), w.stride(0), y.stride(0), float(eps), 1 if silu else 0, stream())
+         r_out.stride(0), w.stride(0), y.stride(0), float(eps), 1 if silu else 0,
+         *_tune("norm_silu" if silu else "norm", n, k, m), stream())
     return y, r_out
 
 
-def parts_norm_gemv(parts, residual, residual_out, norm_w, w, eps, silu=False, out=None, rpw=0):
+def parts_norm_gemv(parts, residual, residual_out, norm_w, w, eps, silu=False, out=None):
     """The decode layer's fused consumer: r = bf16(residual + bf16(sum parts))
     -> residual_out; y = proj(rmsnorm(r) * norm_w) [+ SwiGLU]. The
     composition of add_rms_norm_parts (ek_kernels.py:1296) with gemv (:1322)
@@ -284,11 +306,11 @@ def parts_norm_gemv(parts, residual, residual_out, norm_w, w, eps, silu=False, o
     y = torch.empty(m, n, device=parts.device, dtype=_BF16) if out is None else out
     call("ek_parts_norm_gemv", ptr(parts), sk, ptr(residual), ptr(residual_out), ptr(norm_w), ptr(w), ptr(y),
          m, n, k, residual.stride(0), residual_out.stride(0), w.stride(0), y.stride(0), float(eps),
-         1 if silu else 0, rpw, stream())
+         1 if silu else 0, *_tune("parts_norm_silu" if silu else "parts_norm", n, k, m), stream())
     return y
 
 
-def embed_norm_gemv(tokens, embed, residual_out, norm_w, w, eps, slot_t=None, len_t=None, out=None, rpw=0):
+def embed_norm_gemv(tokens, embed, residual_out, norm_w, w, eps, slot_t=None, len_t=None, out=None):
     """The decode step's first projection: residual_out = embed[tokens];
     y = proj(rmsnorm(residual_out) * norm_w). With slot_t/len_t it also
     performs the step's `slot_t <- len_t; len_t += 1` (ek_model.py:375-376)."""
@@ -304,20 +326,18 @@ def embed_norm_gemv(tokens, embed, residual_out, norm_w, w, eps, slot_t=None, le
     y = torch.empty(m, n, device=tokens.device, dtype=_BF16) if out is None else out
     call("ek_embed_norm_gemv", ptr(tokens), ptr(embed), embed.stride(0), embed.shape[0], ptr(residual_out),
          ptr(norm_w), ptr(w), ptr(y), m, n, k, residual_out.stride(0), w.stride(0), y.stride(0), float(eps),
-         ptr(slot_t) if len_t is not None else None, ptr(len_t), rpw, stream())
+         ptr(slot_t) if len_t is not None else None, ptr(len_t), *_tune("embed_norm", n, k, m), stream())
     return y
 
 
 class ArgmaxScratch:
-    """Per-workgroup partials and the arrival counter of lm_head_argmax."""
+    """Per-workgroup (value, index) partials of lm_head_argmax: room for the
+    widest grid any launch shape can use (one row per wave)."""
 
-    def __init__(self, m: int, vocab: int, device, rpw: int = 4):
-        self.rpw = rpw
-        blocks = _cdiv(vocab, 4 * rpw)
-        self.cap = blocks * m
+    def __init__(self, m: int, vocab: int, device):
+        self.cap = _cdiv(vocab, 4) * m
         self.val = torch.empty(self.cap, dtype=torch.float32, device=device)
         self.idx = torch.empty(self.cap, dtype=torch.int32, device=device)
-        self.counter = torch.zeros(1, dtype=torch.int32, device=device)
 
 
 def lm_head_argmax(hidden, lm_head, scratch: ArgmaxScratch, out_tok=None, logits=None,
@@ -334,7 +354,7 @@ def lm_head_argmax(hidden, lm_head, scratch: ArgmaxScratch, out_tok=None, logits
     vocab = lm_head.shape[0]
     _need(lm_head.shape[1] == k and lm_head.stride(-1) == 1, "lm_head shape")
     _need(1 <= m <= 8, "lm_head_argmax: M must be 1..8")
-    _need(scratch.cap >= _cdiv(vocab, 4 * scratch.rpw) * m, "argmax scratch too small")
+    _need(scratch.cap >= _cdiv(vocab, 4) * m, "argmax scratch too small")
     if out_tok is None:
         out_tok = torch.empty(m, dtype=torch.int64, device=src.device)
     if logits is not None:
@@ -352,8 +372,8 @@ def lm_head_argmax(hidden, lm_head, scratch: ArgmaxScratch, out_tok=None, logits
          float(eps), ptr(lm_head), m, vocab, k, 0 if fused else hidden.stride(0),
          residual.stride(0) if fused else 0, lm_head.stride(0), ptr(logits),
          logits.stride(0) if logits is not None else 0, ptr(scratch.val), ptr(scratch.idx), scratch.cap,
-         ptr(scratch.counter), ptr(out_tok), ptr(st[0]), ptr(st[1]), ptr(st[2]), ptr(st[3]), max_steps,
-         scratch.rpw, stream())
+         ptr(out_tok), ptr(st[0]), ptr(st[1]), ptr(st[2]), ptr(st[3]), max_steps,
+         *_tune("lm_head", vocab, k, m), stream())
     return out_tok
 
 
@@ -406,7 +426,8 @@ def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta
 def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, device, splits=None, chunk=None):
     """The attention workspace: the reference's 7-tuple (acc, lsum, mmax, out,
     splits, chunk, block_n) of engine.py:273-282, extended with the score
-    scratch [B, n_q, bucket] fp32 and the per-(b, kv head) arrival counters."""
+    scratch [B, n_q, bucket] fp32. `acc` is kept for callers that index the
+    tuple; the kernels need no per-split output partials."""
     s, c, bn = plan_splits(b, n_kv, bucket)
     if splits is not None:
         s = splits
@@ -418,22 +439,20 @@ def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, devi
     mmax = torch.full((b, n_kv, sp, gp), -1e30, dtype=torch.float32, device=device)
     out = torch.empty((b, n_q, head_dim), dtype=_BF16, device=device)
     scores = torch.empty((b, n_q, bucket), dtype=torch.float32, device=device)
-    counters = torch.zeros(b * n_kv, dtype=torch.int32, device=device)
-    return (acc, lsum, mmax, out, s, c, bn, scores, counters)
+    return (acc, lsum, mmax, out, s, c, bn, scores)
 
 
 _SCRATCH: dict = {}
 
 
-def _attn_scratch(ws, b, n_q, n_kv, s_cap, device):
-    """Score scratch and counters for a reference-style 7-tuple workspace
-    (allocated once per shape; eager callers only)."""
-    if len(ws) >= 9:
-        return ws[7], ws[8]
-    key = (device, b, n_q, n_kv, s_cap)
+def _attn_scratch(ws, b, n_q, s_cap, device):
+    """The score scratch; for a reference-style 7-tuple workspace it is
+    allocated once per shape (eager callers only)."""
+    if len(ws) >= 8:
+        return ws[7]
+    key = (device, b, n_q, s_cap)
     if key not in _SCRATCH:
-        _SCRATCH[key] = (torch.empty((b, n_q, s_cap), dtype=torch.float32, device=device),
-                         torch.zeros(b * n_kv, dtype=torch.int32, device=device))
+        _SCRATCH[key] = torch.empty((b, n_q, s_cap), dtype=torch.float32, device=device)
     return _SCRATCH[key]
 
 
@@ -445,21 +464,20 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
     _need(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(), "k/v cache layouts differ")
     _need(k_cache.dtype == _BF16 and k_cache.stride(-1) == 1 and k_cache.shape[0] >= b, "cache")
     _need(n_q % n_kv == 0 and out.shape[1] == n_q and out.shape[2] == d, "head counts / workspace")
-    _need(acc.shape[:2] == (b, n_kv) and acc.shape[2] >= splits and acc.is_contiguous(), "acc workspace")
-    _need(lsum.shape == acc.shape[:4] and mmax.shape == acc.shape[:4], "lsum/mmax workspace")
+    _need(lsum.shape[:2] == (b, n_kv) and lsum.shape[2] >= splits and lsum.shape[3] >= n_q // n_kv
+          and lsum.is_contiguous() and mmax.shape == lsum.shape and mmax.is_contiguous(), "lsum/mmax workspace")
     _need(splits * chunk >= 1, "splits/chunk")
     _need(seq_len_t.dtype == torch.int64 and start_t.dtype == torch.int32 and start_t.numel() >= b, "len/start")
-    scores, counters = _attn_scratch(workspace, b, n_q, n_kv, s_cap, out.device)
+    scores = _attn_scratch(workspace, b, n_q, s_cap, out.device)
     _need(scores.shape[0] >= b and scores.shape[1] == n_q and scores.is_contiguous(), "score scratch")
     # the workspace bounds the attended length, as the reference's chunk plan does
     s_cap = min(s_cap, scores.shape[2])
-    _need(counters.numel() >= b * n_kv, "counters")
     ld_cs = cos.stride(0) if cos is not None else 0
     rope_len = cos.shape[0] if cos is not None else 0
     call("ek_attn_decode", ptr(q), ldq_b, ldq_h, rope, ptr(qn), ptr(kn), ptr(cos), ptr(sin), ld_cs,
          ptr(positions), rope_len, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
-         k_cache.stride(2), s_cap, ptr(seq_len_t), ptr(start_t), ptr(scores), scores.stride(1), ptr(acc),
-         ptr(lsum), ptr(mmax), ptr(counters), acc.shape[2], acc.shape[3], ptr(out), out.stride(0),
+         k_cache.stride(2), s_cap, ptr(seq_len_t), ptr(start_t), ptr(scores), scores.stride(1),
+         ptr(lsum), ptr(mmax), lsum.shape[2], lsum.shape[3], ptr(out), out.stride(0),
          out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), stream())
     return out
 

@@ -120,7 +120,7 @@ class _FastEngine:
 
     # -- graph capture --------------------------------------------------
     def _make_ws(self, b: int, bucket: int):
-        """engine.py:273-282 (plus the score scratch and arrival counters)."""
+        """engine.py:273-282 (plus the attention score scratch)."""
         cfg = self.model.cfg
         return K.make_workspace(b, cfg.num_heads, self.n_kv, self.head_dim, bucket, self.device)
 

@@ -60,21 +60,25 @@ int ek_qk_norm_rope_kv(void* qkv, const void* qn, const void* kn, const void* co
                        int64_t ld_cs, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t csb, int64_t csh,
                        int64_t css, int64_t s_cap, int64_t m_per_batch, float eps, void* stream);
 
+/* GEMV-family tuning arguments (results do not depend on them): rpw =
+ * output rows per wave (1, 2 or 4; 0 = default), blocks = grid cap (0 =
+ * four workgroups per CU; workgroups loop over row groups). */
+
 /* gemv: y[m, n] = bf16(sum_k x[m, k] * w[n, k]) with fp32 accumulation.
  * Replaces engine/ek_kernels.py:1322-1347 (gemv, kernel :281-308). */
 int ek_gemv(const void* x, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldw,
-            int64_t ldy, void* stream);
+            int64_t ldy, int64_t rpw, int64_t blocks, void* stream);
 
 /* gemv_parts: fp32 split-K partials parts[s, m, n] over sk equal K slices (m <= 8).
  * Replaces engine/ek_kernels.py:1277-1293 (kernel :413-445). */
 int ek_gemv_parts(const void* x, const void* w, float* parts, int64_t m, int64_t n, int64_t k, int64_t ldx,
-                  int64_t ldw, int64_t sk, void* stream);
+                  int64_t ldw, int64_t sk, int64_t rpw, int64_t blocks, void* stream);
 
 /* gemv_swiglu: w is the fused [2*inter, k] gate-over-up matrix;
  * y[m, i] = bf16(silu(bf16 gate_i)) (x) bf16(up_i) (m <= 8).
  * Replaces engine/ek_kernels.py:1247-1261 (kernel :375-411). */
 int ek_gemv_swiglu(const void* x, const void* w, void* y, int64_t m, int64_t inter, int64_t k, int64_t ldx,
-                   int64_t ldw, int64_t ldy, void* stream);
+                   int64_t ldw, int64_t ldy, int64_t rpw, int64_t blocks, void* stream);
 
 /* norm_gemv: [residual add] + RMSNorm prologue + projection [+ SwiGLU epilogue].
  * residual == NULL: no add (the normalised input is x itself). Otherwise
@@ -83,7 +87,7 @@ int ek_gemv_swiglu(const void* x, const void* w, void* y, int64_t m, int64_t int
  * Replaces engine/ek_kernels.py:1220-1244 (kernel :310-373). */
 int ek_norm_gemv(const void* x, const void* residual, void* residual_out, const void* norm_w, const void* w,
                  void* y, int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldr, int64_t ldro, int64_t ldw,
-                 int64_t ldy, float eps, int silu, void* stream);
+                 int64_t ldy, float eps, int silu, int64_t rpw, int64_t blocks, void* stream);
 
 /* parts_norm_gemv: the decode layer's consumer projection. r = bf16(residual +
  * bf16(sum_s parts[s])) over fp32 partials [sk_in, m, k]; r -> residual_out;
@@ -92,7 +96,8 @@ int ek_norm_gemv(const void* x, const void* residual, void* residual_out, const 
  * gemv_swiglu (:1247), as one launch. rpw: output rows per wave (0: default). */
 int ek_parts_norm_gemv(const float* parts, int64_t sk_in, const void* residual, void* residual_out,
                        const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldr,
-                       int64_t ldro, int64_t ldw, int64_t ldy, float eps, int silu, int64_t rpw, void* stream);
+                       int64_t ldro, int64_t ldw, int64_t ldy, float eps, int silu, int64_t rpw, int64_t blocks,
+                       void* stream);
 
 /* embed_norm_gemv: the decode step's first layer. r = embed[tokens[b]] ->
  * residual_out; y = projection of rms_norm(r). When len_t != NULL it also
@@ -102,7 +107,7 @@ int ek_parts_norm_gemv(const float* parts, int64_t sk_in, const void* residual, 
 int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, int64_t vocab, void* residual_out,
                        const void* norm_w, const void* w, void* y, int64_t m, int64_t n, int64_t k, int64_t ldro,
                        int64_t ldw, int64_t ldy, float eps, int64_t* slot_t, int64_t* len_t, int64_t rpw,
-                       void* stream);
+                       int64_t blocks, void* stream);
 
 /* attn_decode: split-K decode attention over caches [B, n_kv, S, D] (D in
  * {32, 64, 128}, n_q / n_kv in {1, 2, 4, 8}) for keys [start[b], *seq_len).
@@ -110,29 +115,29 @@ int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, in
  * QK-normed and rotated, and the new key (rotated) and value (raw) are
  * written at slot *seq_len - 1 -- rope_attn_decode, engine/ek_kernels.py:
  * 1476-1507 (kernel :678-780). rope == 0: q [B, n_q, D] is already rotated
- * -- flash_decode, engine/ek_kernels.py:1389-1416 (kernel :534-615). The
- * split combine (kernel :988-1019) is fused: partials acc [B, n_kv, sp, gp,
- * D], lsum/mmax [B, n_kv, sp, gp], score scratch [B, n_q, score_ss]; the
- * last workgroup per (b, kv head) combines, using counters [B * n_kv]
- * (zero before the first call; left zero by every call). Probabilities are
+ * -- flash_decode, engine/ek_kernels.py:1389-1416 (kernel :534-615). Two
+ * launches: per-split scores into the scratch [B, n_q, score_ss] with the
+ * split's max/sum in mmax/lsum [B, n_kv, sp, gp]; then the softmax-weighted
+ * value sum per (b, kv head, chunk of head dims), so the reference's split
+ * combine (kernel :988-1019) has nothing left to merge. Probabilities are
  * rounded to bf16 before the PV product, as in engine/ek_model.py:475-488.
  * cos/sin rows: positions[b] when positions != NULL, else row b. */
 int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
                    const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
                    void* k_cache, void* v_cache, int64_t csb, int64_t csh, int64_t css, int64_t s_cap,
-                   const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* acc,
-                   float* lsum, float* mmax, int32_t* counters, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
-                   int64_t ldo_h, int64_t b, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits,
-                   int64_t chunk, float sm_scale, float eps, void* stream);
+                   const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* lsum,
+                   float* mmax, int64_t sp, int64_t gp, void* out, int64_t ldo_b, int64_t ldo_h, int64_t b,
+                   int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits, int64_t chunk, float sm_scale,
+                   float eps, void* stream);
 
 /* lm_head_argmax: logits = bf16(h . w^T) over the vocabulary and the
  * first-index argmax per row -> out_tok[b] (int64). The hidden row h is x
  * (parts == NULL) or, fused, rms_norm(bf16(residual + bf16(sum_s parts[s])))
  * with gain norm_w (the decode's final add + norm, engine/ek_model.py:413-416).
- * logits (nullable) receives the bf16 logits. am_val/am_idx (>= am_cap
- * entries, >= blocks * m) hold per-workgroup partials; counter (one int32,
- * zero before the first call) is left zero. When st_tokens != NULL the last
- * workgroup also advances the decode state: st_tokens[b] = token,
+ * logits (nullable) receives the bf16 logits. am_val/am_idx (am_cap entries,
+ * at least grid width * m) hold per-workgroup partials, which a second
+ * one-workgroup launch reduces. When st_tokens != NULL that launch also
+ * advances the decode state: st_tokens[b] = token,
  * st_positions[b] += 1, st_out[*st_step * m + b] = token (if *st_step <
  * max_steps), *st_step += 1.
  * Replaces engine/ek_model.py:490-493 (argmax_token) and the step bookkeeping
@@ -140,8 +145,8 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
 int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const void* residual, const void* norm_w,
                       float eps, const void* w, int64_t m, int64_t vocab, int64_t k, int64_t ldx, int64_t ldr,
                       int64_t ldw, void* logits, int64_t ld_logits, float* am_val, int32_t* am_idx, int64_t am_cap,
-                      int32_t* counter, int64_t* out_tok, int64_t* st_tokens, int64_t* st_positions,
-                      int32_t* st_out, int64_t* st_step, int64_t max_steps, int64_t rpw, void* stream);
+                      int64_t* out_tok, int64_t* st_tokens, int64_t* st_positions, int32_t* st_out,
+                      int64_t* st_step, int64_t max_steps, int64_t rpw, int64_t blocks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -95,12 +95,19 @@ def _decode_parity(cfg, tensors, prompts, steps, dev):
             st.positions = st.positions + 1
             positions = positions + 1
         assert torch.equal(len_t.cpu(), st.len_t)
-        for i in range(cfg["num_hidden_layers"]):   # the caches the decode wrote agree
-            n = int(st.len_t.item())
+        # the prefill slots are untouched; the slots the decode wrote agree
+        # with the oracle's: values are raw projections (an ulp apart at
+        # most), keys also pass QK-norm and RoPE, whose rounded products
+        # amplify a 1-ulp input difference into several rounded elements
+        n = int(st.len_t.item())
+        for i in range(cfg["num_hidden_layers"]):
             for bi in range(b):
-                a = kd[i][bi, :, pad[bi]:n].cpu()
-                r = st.k[i][bi, :, pad[bi]:n]
-                assert ((a.double() - r.double()).abs() <= 2 * _ulp(r) + 1e-30).all()
+                for got_c, ref_c, floor in ((kd[i], st.k[i], 0.5), (vd[i], st.v[i], 0.9)):
+                    assert torch.equal(got_c[bi, :, :s].cpu(), ref_c[bi, :, :s])
+                    a = got_c[bi, :, s:n].cpu().float()
+                    r = ref_c[bi, :, s:n].float()
+                    assert (a - r).abs().max().item() <= 2e-2 * r.abs().max().item()
+                    assert (a == r).float().mean().item() >= floor
     return out
 
 
@@ -140,3 +147,64 @@ def test_engine_4b_shapes_tokens(dev):
     want = list(O.generate_eager(om, prompts, 16))
     assert got[0] == want[0]              # the prefill's first token
     assert got == want
+
+
+def test_decode_parity_full_depth_against_the_noise_floor(dev):
+    """The full 36-layer Qwen3-4B shape, 12 teacher-forced steps. Through 36
+    random-init layers an fp32 summation-order change alone moves the
+    oracle's own logits by ~0.13 (0.03 at 2 layers): that drift, measured
+    here by re-running the oracle with its projections accumulated in a
+    different order (fp32 upcast matmul), is the noise floor. The HIP path
+    must stay within 1.5x that floor plus 2 bf16 ulps, and may pick a
+    different token only where the oracle's own top-2 gap is <= 2 ulps."""
+    cfg = dict(C.QWEN3_4B)
+    tensors = C.random_weights(cfg, seed=0)
+    om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
+    gm = Qwen3(None, dev, tensors=tensors, config=cfg)
+    g = torch.Generator().manual_seed(1)
+    prompts = [torch.randint(0, 151936, (128,), generator=g).tolist()]
+    ids, pos, pad, s, bias = O.pack(prompts)
+    steps = 12
+    total = s + steps + 1
+    st = O.EagerState(om, 1, s, pad, total)
+    with torch.inference_mode():
+        hidden = om.prefill(ids, pos, st.k, st.v, bias)
+        tok = O.argmax_token(hidden, om.lm_head)
+        st2 = O.EagerState(om, 1, s, pad, total)
+        st2.k = [t.clone() for t in st.k]
+        st2.v = [t.clone() for t in st.v]
+        kd = [t.to(dev) for t in st.k]
+        vd = [t.to(dev) for t in st.v]
+        positions = st.positions.to(dev)
+        slot_t = torch.zeros(1, dtype=torch.int64, device=dev)
+        len_t = torch.full((1,), s, dtype=torch.int64, device=dev)
+        start_t = torch.zeros(1, dtype=torch.int32, device=dev)
+        ws = K.make_workspace(1, 32, 8, 128, total, dev)
+        proj = om._proj
+        reordered = lambda x, layer, key: torch.matmul(x.float(), layer[key].float().t()).to(BF)
+        agree = 0
+        for _ in range(steps):
+            om._proj = proj
+            l_ref = O.lm_logits(om.decode(tok, st.positions, st.k, st.v, st.slot_t, st.len_t, st.start_t),
+                                om.lm_head).float()[0]
+            om._proj = reordered
+            l_alt = O.lm_logits(om.decode(tok, st2.positions, st2.k, st2.v, st2.slot_t, st2.len_t,
+                                          st2.start_t), om.lm_head).float()[0]
+            h = gm.decode(tok.to(dev), positions, kd, vd, slot_t, len_t, start_t, ws)
+            logits = torch.empty(1, 151936, dtype=BF, device=dev)
+            t_gpu = int(gm.argmax_token(h, logits=logits)[0])
+            floor = (l_alt - l_ref).abs().max().item()
+            err = (logits.cpu().float()[0] - l_ref).abs().max().item()
+            ulp = _ulp(l_ref.max().double()).item()
+            assert err <= 1.5 * floor + 2 * ulp, (err, floor)
+            t_ref = int(torch.argmax(l_ref))
+            if t_gpu == t_ref:
+                agree += 1
+            else:
+                assert (l_ref[t_ref] - l_ref[t_gpu]).item() <= 2 * ulp
+            tok = torch.tensor([t_ref])
+            for x in (st, st2):
+                x.positions = x.positions + 1
+            positions = positions + 1
+        om._proj = proj
+    assert agree >= steps - 2
