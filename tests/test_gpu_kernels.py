@@ -278,7 +278,10 @@ def _ref_attn64(q, kc, vc, seq_len, start):
     return torch.einsum("bhs,bhsd->bhd", torch.softmax(s, -1), v)
 
 
-ATTN_CASES = [(1, 1024, 600, 0), (4, 2048, 2048, 0), (16, 1024, 640, 0), (3, 1024, 97, 0), (2, 1024, 500, 37)]
+# Rows whose scores fit in LDS (G * s_cap * 4 bytes <= 32 KiB: s_cap <= 2048 at
+# G = 4) take the single-launch kernel; longer ones the two-phase pair.
+ATTN_CASES = [(1, 1024, 600, 0), (4, 2048, 2048, 0), (16, 1024, 640, 0), (3, 1024, 97, 0), (2, 1024, 500, 37),
+              (2, 4096, 1500, 37), (1, 4096, 4096, 0)]
 
 
 @pytest.mark.parametrize("b,smax,slen,pad", ATTN_CASES)
@@ -328,13 +331,16 @@ def test_attention_config3_lengths_and_split_sweep(dev, L):
         assert_close_ulps(outs[32], want, min_equal=0.99, name="vs oracle", abs_tol=2.0 ** -13 * vmax)
 
 
-@pytest.mark.parametrize("b,d,nq,nkv,slen,pad", [(1, 128, 32, 8, 129, 0), (3, 128, 32, 8, 300, 11),
-                                                 (3, 32, 4, 2, 17, 5), (8, 128, 32, 8, 700, 0)])
-def test_rope_attn_decode(dev, b, d, nq, nkv, slen, pad):
+@pytest.mark.parametrize("b,d,nq,nkv,slen,pad,smax", [
+    (1, 128, 32, 8, 129, 0, 1024), (3, 128, 32, 8, 300, 11, 1024), (3, 32, 4, 2, 17, 5, 1024),
+    (8, 128, 32, 8, 700, 0, 1024), (1, 64, 16, 2, 333, 3, 1024), (1, 128, 32, 8, 1, 0, 256),
+    (1, 128, 32, 8, 129, 0, 4096), (3, 128, 32, 8, 2000, 11, 4096), (2, 64, 16, 2, 333, 3, 2048)])
+def test_rope_attn_decode(dev, b, d, nq, nkv, slen, pad, smax):
     """Fused QK-norm + RoPE + KV write + attention against the oracle's
-    qk_norm_rope_kv followed by its fallback attention."""
+    qk_norm_rope_kv followed by its fallback attention, on the single-launch
+    kernel (short score rows) and on the two-phase pair (s_cap 4096 at G = 4,
+    s_cap 2048 at G = 8)."""
     g = _gen(slen + b)
-    smax = 1024
     qkv = torch.randn(b, (nq + 2 * nkv) * d, generator=g).to(BF)
     qn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF)
     kn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF)

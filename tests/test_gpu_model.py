@@ -96,18 +96,21 @@ def _decode_parity(cfg, tensors, prompts, steps, dev):
             positions = positions + 1
         assert torch.equal(len_t.cpu(), st.len_t)
         # the prefill slots are untouched; the slots the decode wrote agree
-        # with the oracle's: values are raw projections (an ulp apart at
-        # most), keys also pass QK-norm and RoPE, whose rounded products
-        # amplify a 1-ulp input difference into several rounded elements
+        # with the oracle's. Layer 0 sees identical inputs (the embedding
+        # rows), so its new values are the same rounded projections (>= 99%
+        # bitwise); deeper layers inherit ulp-level residual differences and
+        # are held to the scale bound
         n = int(st.len_t.item())
         for i in range(cfg["num_hidden_layers"]):
             for bi in range(b):
-                for got_c, ref_c, floor in ((kd[i], st.k[i], 0.5), (vd[i], st.v[i], 0.9)):
+                for got_c, ref_c in ((kd[i], st.k[i]), (vd[i], st.v[i])):
                     assert torch.equal(got_c[bi, :, :s].cpu(), ref_c[bi, :, :s])
                     a = got_c[bi, :, s:n].cpu().float()
                     r = ref_c[bi, :, s:n].float()
                     assert (a - r).abs().max().item() <= 2e-2 * r.abs().max().item()
-                    assert (a == r).float().mean().item() >= floor
+            a = vd[0][:, :, s:n].cpu()
+            if i == 0:
+                assert (a == st.v[0][:, :, s:n]).float().mean().item() >= 0.99
     return out
 
 
