@@ -2,6 +2,7 @@
 fraction of the HBM roofline.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py --probe-traffic     (the launches the PMC traffic profile counts)
 
 Workload: a random-init bf16 model of the Qwen3-4B
 architecture (36 layers, hidden 2560, intermediate 9728, 32/8 heads, head
@@ -34,6 +35,13 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
+
+# HBM bytes per fused gate_up launch at batch 1, from two rocprofv3 PMC runs of
+# `bench.py --probe-traffic` (FETCH_SIZE, then WRITE_SIZE), each scaled by what
+# the same counter reads for a 256 MiB device copy (FETCH 0.50007, WRITE 1.0):
+# 48,795.5 KiB / 0.50007 fetched + 81.2 KiB written. Measured on
+# gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1>; re-measure when that kernel changes.
+GATE_UP_TRAFFIC_B1 = 100_003_000
 
 
 def log(msg: str) -> None:
@@ -77,6 +85,40 @@ def time_dominant_kernel(model, b: int, reps: int = 3):
     avg_s = start.elapsed_time(end) / 1e3 / n
     nbytes = gate_up_bytes(b, c.hidden_size, c.intermediate_size, bufs.sk_o)
     return avg_s, nbytes, n
+
+
+def probe_traffic(b: int = 1, layers: int = 36) -> None:
+    """The launches a `rocprofv3 --pmc FETCH_SIZE` (then `WRITE_SIZE`) run
+    counts: one plain device copy of 256 MiB (the calibration: its
+    algorithmic traffic is 256 MiB read + 256 MiB written), then the fused
+    gate_up launch once over each of `layers` distinct weight copies (3.6 GB
+    at 36, beyond the 256 MB Infinity Cache), at the Qwen3-4B shape."""
+    import torch
+    from enginekernel_amd import checkpoint as C
+    from enginekernel_amd import ek_kernels as K
+
+    dev = torch.device("cuda:0")
+    h, inter = C.QWEN3_4B["hidden_size"], C.QWEN3_4B["intermediate_size"]
+    src = torch.empty(128 << 20, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    g = torch.Generator(device=dev).manual_seed(0)
+    ws = [torch.empty(2 * inter, h, dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g)
+          for _ in range(layers)]
+    sk = K.parts_splits(b, 4096)
+    parts = torch.empty(sk, b, h, dtype=torch.float32, device=dev).normal_(0, 0.05, generator=g)
+    res = torch.empty(b, h, dtype=torch.bfloat16, device=dev).normal_(0, 0.5, generator=g)
+    res_out = torch.empty_like(res)
+    nw = torch.ones(h, dtype=torch.bfloat16, device=dev)
+    act = torch.empty(b, inter, dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    for w in ws:
+        K.parts_norm_gemv(parts, res, res_out, nw, w, 1e-6, silu=True, out=act)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "traffic", "copy_bytes": 2 * src.numel(), "gate_up_launches": layers,
+                      "gate_up_bytes": gate_up_bytes(b, h, inter, sk), "sk": sk}), flush=True)
 
 
 def cpu_baseline(tensors, cfg, kv, first_tok, positions, s, gpu_tokens, budget_s=15.0):
@@ -139,11 +181,15 @@ def main():
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (diagnostics only)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--probe-traffic", action="store_true", help="run only the launches of the PMC traffic profile")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
+    if args.probe_traffic:
+        probe_traffic()
+        return
 
     import torch
     from enginekernel_amd import checkpoint as C
@@ -249,7 +295,7 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": "gemv_kernel<PRO_PARTS,EPI_SWIGLU> (add+RMSNorm+gate_up+SwiGLU)",
             "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+            "frac": round(achieved / PEAK_HBM, 4), "traffic": GATE_UP_TRAFFIC_B1 if b == 1 else None,
             "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_s * 1e6, 3), "launches": dom_n,
         },
         "cpu_baseline": cpu,

@@ -1,4 +1,6 @@
-// Split-K decode attention over the static KV cache, for gfx950.
+// Decode attention over the static KV cache, for gfx950. Rows whose scores
+// fit in LDS take a single launch (attn_fused_kernel, below); longer rows the
+// two-phase split-K pair described here.
 //
 // The reference's fallback (engine/ek_model.py:475-488) rounds the softmax
 // probabilities to bf16 before the PV product: p = bf16(exp(s - M) / L) with

@@ -115,12 +115,15 @@ int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, in
  * QK-normed and rotated, and the new key (rotated) and value (raw) are
  * written at slot *seq_len - 1 -- rope_attn_decode, engine/ek_kernels.py:
  * 1476-1507 (kernel :678-780). rope == 0: q [B, n_q, D] is already rotated
- * -- flash_decode, engine/ek_kernels.py:1389-1416 (kernel :534-615). Two
- * launches: per-split scores into the scratch [B, n_q, score_ss] with the
- * split's max/sum in mmax/lsum [B, n_kv, sp, gp]; then the softmax-weighted
- * value sum per (b, kv head, chunk of head dims), so the reference's split
- * combine (kernel :988-1019) has nothing left to merge. Probabilities are
- * rounded to bf16 before the PV product, as in engine/ek_model.py:475-488.
+ * -- flash_decode, engine/ek_kernels.py:1389-1416 (kernel :534-615).
+ * When n_q / n_kv * s_cap * 4 <= 32 KiB, one launch per (b, kv head, 32 head
+ * dims) keeps the row's scores in LDS (scores, lsum, mmax, splits and chunk
+ * are then unused). Otherwise two launches: per-split scores into the scratch
+ * [B, n_q, score_ss] with the split's max/sum in mmax/lsum [B, n_kv, sp, gp];
+ * then the softmax-weighted value sum per (b, kv head, chunk of head dims).
+ * Either way the reference's split combine (kernel :988-1019) has nothing
+ * left to merge. Probabilities are rounded to bf16 before the PV product, as
+ * in engine/ek_model.py:475-488.
  * cos/sin rows: positions[b] when positions != NULL, else row b. */
 int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
                    const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
