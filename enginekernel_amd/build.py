@@ -22,7 +22,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libek_hip.so")
-SOURCES = ["ek_abi.hip", "ek_norm.hip", "ek_gemv.hip", "ek_attn.hip"]
+SOURCES = ["ek_abi.hip", "ek_norm.hip", "ek_gemv.hip", "ek_attn.hip", "ek_step.hip"]
+# head dims of the persistent decode-step kernel; ek_step_inst.hip is compiled once per head dim
+STEP_HEAD_DIMS = [32, 64, 128]
 # (prologue, epilogue) pairs of the GEMV family; ek_gemv_inst.hip is compiled
 # once per pair (must match EK_GEMV_PAIRS in csrc/ek_gemv_impl.h)
 GEMV_PAIRS = [(0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 2), (2, 0), (2, 2),
@@ -44,6 +46,8 @@ def _units():
     for pro, epi in GEMV_PAIRS:
         out.append(("ek_gemv_inst.hip", f"ek_gemv_inst_{pro}_{epi}",
                     [f"-DEK_PRO={pro}", f"-DEK_EPI={epi}"]))
+    for d in STEP_HEAD_DIMS:
+        out.append(("ek_step_inst.hip", f"ek_step_inst_{d}", [f"-DEK_STEP_D={d}"]))
     return out
 
 

@@ -38,6 +38,7 @@
 
 #include "ek_common.h"
 #include "ek_abi_internal.h"
+#include "ek_attn_impl.h"
 #include "ek_hip.h"
 
 namespace {
@@ -74,41 +75,6 @@ __device__ __forceinline__ Range key_range(const AttnParams& p, int s, int b) {
   r.lo = lo;
   r.hi = hi;
   return r;
-}
-
-// QK-norm + rotate-half RoPE of one head (one wave); writes the bf16-valued
-// result as fp32 to `dst` (LDS) and, if `gdst`, as bf16 to global memory.
-template <int D>
-__device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w, const bf16_t* cr,
-                                               const bf16_t* sr, float eps, float* dst, bf16_t* gdst) {
-  constexpr int PER = D > 64 ? D / 64 : 1;
-  constexpr int HALF = D / 2;
-  const int lane = threadIdx.x & 63;
-  float xv[PER], xp[PER];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane + 64 * i;
-    const bool ok = d < D;
-    const int pd = d < HALF ? d + HALF : d - HALF;
-    xv[i] = ok ? bf2f(x[d]) : 0.f;
-    xp[i] = ok ? bf2f(x[pd]) : 0.f;
-    ss = fmaf(xv[i], xv[i], ss);
-  }
-  ss = wave_sum(ss);
-  const float rstd = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane + 64 * i;
-    if (d >= D) continue;
-    const int pd = d < HALF ? d + HALF : d - HALF;
-    const float tn = rbf(bf2f(w[d]) * rbf(xv[i] * rstd));
-    const float tp = rbf(bf2f(w[pd]) * rbf(xp[i] * rstd));
-    const float rot = d < HALF ? -tp : tp;
-    const float o = rbf(rbf(tn * bf2f(cr[d])) + rbf(rot * bf2f(sr[d])));
-    dst[d] = o;
-    if (gdst) gdst[d] = (bf16_t)f2bf(o);
-  }
 }
 
 template <int D, int G>
@@ -151,10 +117,10 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
     const int units = G + (owns ? 2 : 0);
     for (int u = wave; u < units; u += NW) {
       if (u < G) {
-        head_norm_rope<D>(row + (int64_t)(h * G + u) * D, p.qn, cr, sr, p.eps, qs[u], nullptr);
+        eka::head_norm_rope<D>(row + (int64_t)(h * G + u) * D, p.qn, cr, sr, p.eps, qs[u], nullptr);
       } else if (u == G) {
         bf16_t* kdst = p.kc + b * p.csb + h * p.csh + slot * p.css;
-        head_norm_rope<D>(row + (int64_t)(p.nq + h) * D, p.kn, cr, sr, p.eps, knew, kdst);
+        eka::head_norm_rope<D>(row + (int64_t)(p.nq + h) * D, p.kn, cr, sr, p.eps, knew, kdst);
       } else {
         const bf16_t* vsrc = row + (int64_t)(p.nq + p.nkv + h) * D;
         bf16_t* vdst = p.vc + b * p.csb + h * p.csh + slot * p.css;
@@ -341,304 +307,49 @@ __global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
   }
 }
 
-// ----------------------------------------------------------------------------
-// Single-launch variant for short rows (the score row of a head fits in LDS):
-// one workgroup per (batch, kv head, chunk of 32 head dims), both products on
-// the matrix cores (v_mfma_f32_16x16x32_bf16: bf16 products are exact in
-// fp32, sums are fp32).
-//
-//   scores   per tile of 16 keys, S^T[16 x 16] = K_tile[16 x D] . Q^T[D x 16]
-//            with the G query heads in the first G columns, scaled, into an
-//            LDS row per head. Each lane also keeps the running max and
-//            exp-sum of the scores it produced; the lanes and waves merge
-//            them into the row's M and L. Every chunk workgroup of a head
-//            computes all of the head's scores; when B * n_kv is a multiple of
-//            8 those workgroups sit on one XCD (workgroups are dealt
-//            round-robin over the 8 XCDs by linear id), so the repeated K
-//            reads hit its L2.
-//   softmax  p = bf16(exp(s - M) / L) in place, one exp per score, spread
-//            over all threads.
-//   PV       per tile of 32 keys, O[16 x 16] += P[16 x 32] . V[32 x 16] per
-//            16 head dims, the heads in the first G rows. V arrives as 16 B per
-//            lane and is re-laid through a per-wave LDS tile into the B
-//            operand (8 keys of one dim per lane), so the key sum happens
-//            inside the MFMA. The waves' partial outputs are added through
-//            LDS and rounded to bf16 once.
-//
-// Nothing crosses workgroups, so attention is one launch with no score
-// scratch. In rope mode every workgroup norms/rotates its query heads and the
-// new key (which stands in for the cache row at the new slot), takes the raw
-// new value from the qkv row (likewise), and the chunk-0 workgroup also
-// stores both in the cache. Rounding points are those of the two-phase
-// kernels. The first K tiles are loaded at entry, before the QK-norm/RoPE
-// work, and the first V tiles right after it, so both overlap the work
-// before their use.
-//
-// MFMA lane layout (16x16x32): lane l = r + 16 q (r < 16, q < 4) holds
-// A[row r][k = 8q .. 8q+7], B[k = 8q .. 8q+7][col r] and C[rows 4q .. 4q+3][col r].
-// ----------------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int FNT = 512;
-constexpr int FNW = FNT / EK_WAVE;
-constexpr int FTU = 4;     // 16-key score tiles in flight per wave
-constexpr int FPT = 2;     // 32-key PV tiles in flight per wave
-constexpr int FDC = 32;    // head dims per workgroup
-constexpr int VTS = FDC + 4;   // LDS row of a staged V tile (bf16; 72 B keeps reads conflict-free)
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8_t, u); }
-
-__device__ __forceinline__ f32x4_t mfma16x16x32(const uint4& a, const uint4& b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
-}
-
-// merge a (max, sum of exp(s - max)) pair into another
-__device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2) {
-  const float mn = fmaxf(m, m2);
-  l = l * expf(m - mn) + l2 * expf(m2 - mn);
-  m = mn;
-}
-
+// Single-launch variant (rows whose scores fit in LDS): one 512-thread
+// workgroup per (batch row, kv head, 32 head dims), the unit of
+// ek_attn_impl.h.
 template <int D, int G>
-__global__ __launch_bounds__(FNT) void attn_fused_kernel(AttnParams p) {
-  constexpr int KS = D / 32;   // 32-dim k-steps of a score tile
-  static_assert(G <= 8 && D % 32 == 0, "tile shape");
-  extern __shared__ float sc_lds[];   // [G][s_cap] scores by key - lo
-  __shared__ float qs[G][D];
-  __shared__ float knew[D];
-  __shared__ __align__(16) uint16_t vnew[FDC];
-  __shared__ float stm[FNW][8], stl[FNW][8];
-  __shared__ __align__(16) uint16_t vt[FNW][32][VTS];
-  __shared__ float outp[FNW][G][FDC];
-
+__global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
+  extern __shared__ __align__(16) unsigned char lds[];
   const int bh = blockIdx.x;
   const int b = bh / p.nkv, h = bh % p.nkv;
-  const int d0 = blockIdx.y * FDC;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r16 = lane & 15, q4 = lane >> 4;
-  const int64_t cap = p.s_cap;
   int64_t len = *p.seq_len;
-  len = len < 0 ? 0 : (len > cap ? cap : len);
+  len = len < 0 ? 0 : (len > p.s_cap ? p.s_cap : len);
   int64_t lo = p.start[b];
   lo = lo < 0 ? 0 : lo;
-  const int64_t hi = len;
-  const int64_t nrel = hi > lo ? hi - lo : 0;   // keys attended
-  const int64_t slot = len - 1;
-  const bool fresh = p.rope && slot >= lo;      // the new key/value come from the qkv row
-  const int64_t srel = slot - lo;
-
-  // first K tiles in flight before any other work: lane holds key row r16
-  // of the tile, dims 32 i + 8 q4 .. +7
-  const bf16_t* kb = p.kc + b * p.csb + h * p.csh + 8 * q4;
-  const int64_t ntile = (nrel + 15) >> 4;
-  uint4 kt[FTU][KS];
-#pragma unroll
-  for (int u = 0; u < FTU; ++u) {
-    const int64_t rel = ((int64_t)(wave + u * FNW) << 4) + r16;
-#pragma unroll
-    for (int i = 0; i < KS; ++i)
-      kt[u][i] = rel < nrel ? ld16(kb + (lo + rel) * p.css + 32 * i) : make_uint4(0, 0, 0, 0);
-  }
-
+  eka::AttnUnit u;
   if (p.rope) {
     const bf16_t* row = p.q + b * p.ldq_b;
+    u.qh = row + (int64_t)h * G * D;
+    u.q_stride = D;
+    u.kh = row + (int64_t)(p.nq + h) * D;
+    u.vh = row + (int64_t)(p.nq + p.nkv + h) * D;
     int64_t crow = p.positions ? p.positions[b] : b;
     crow = crow < 0 ? 0 : (crow >= p.rope_len ? p.rope_len - 1 : crow);
-    const bf16_t* cr = p.cos + crow * p.ld_cs;
-    const bf16_t* sr = p.sin + crow * p.ld_cs;
-    const bool writer = blockIdx.y == 0 && slot >= 0;
-    const int units = G + ((fresh || writer) ? 1 : 0);
-    for (int u = wave; u < units; u += FNW) {
-      if (u < G) {
-        head_norm_rope<D>(row + (int64_t)(h * G + u) * D, p.qn, cr, sr, p.eps, qs[u], nullptr);
-      } else {
-        bf16_t* kdst = writer ? p.kc + b * p.csb + h * p.csh + slot * p.css : nullptr;
-        head_norm_rope<D>(row + (int64_t)(p.nq + h) * D, p.kn, cr, sr, p.eps, knew, kdst);
-      }
-    }
-    if (writer && wave == FNW - 1) {
-      const bf16_t* vsrc = row + (int64_t)(p.nq + p.nkv + h) * D;
-      bf16_t* vdst = p.vc + b * p.csb + h * p.csh + slot * p.css;
-      for (int d = lane; d < D; d += EK_WAVE) vdst[d] = vsrc[d];
-    }
-    if (fresh && tid < FDC) vnew[tid] = row[(int64_t)(p.nq + p.nkv + h) * D + d0 + tid];
+    u.cr = p.cos + crow * p.ld_cs;
+    u.sr = p.sin + crow * p.ld_cs;
   } else {
-    for (int i = tid; i < G * D; i += FNT)
-      qs[i / D][i % D] = bf2f(p.q[b * p.ldq_b + (int64_t)(h * G + i / D) * p.ldq_h + i % D]);
+    u.qh = p.q + b * p.ldq_b + (int64_t)h * G * p.ldq_h;
+    u.q_stride = p.ldq_h;
+    u.kh = u.vh = nullptr;
+    u.cr = u.sr = nullptr;
   }
-
-  // first V tiles in flight: 16 B chunks c = lane + 64 m of the 32 x 32 tile,
-  // key c / 4, dims 8 (c % 4) .. +7
-  const int vkey = lane >> 2, vsub = lane & 3;
-  const bf16_t* vb = p.vc + b * p.csb + h * p.csh + d0 + 8 * vsub;
-  const int64_t ntile32 = (nrel + 31) >> 5;
-  uint4 vreg[FPT][2];
-#pragma unroll
-  for (int u = 0; u < FPT; ++u) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int64_t rel = ((int64_t)(wave + u * FNW) << 5) + vkey + 16 * m;
-      vreg[u][m] = (rel < nrel && !(fresh && rel == srel)) ? ld16(vb + (lo + rel) * p.css) : make_uint4(0, 0, 0, 0);
-    }
-  }
-  __syncthreads();
-
-  // ---- scores. B operand = Q^T: q[g = r16][32 i + 8 q4 .. +7], zero for g >= G
-  uint4 qb[KS];
-#pragma unroll
-  for (int i = 0; i < KS; ++i) {
-    const int g = r16 < G ? r16 : 0;
-    uint32_t w[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int dd = 32 * i + 8 * q4 + 2 * e;
-      w[e] = r16 < G ? (f2bf(qs[g][dd]) | (f2bf(qs[g][dd + 1]) << 16)) : 0u;
-    }
-    qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-  float mrun = -1e30f, lrun = 0.f;   // this lane's scores: head r16, running max / exp-sum
-  for (int64_t t0 = wave; t0 < ntile; t0 += (int64_t)FNW * FTU) {
-    if (t0 != wave) {
-#pragma unroll
-      for (int u = 0; u < FTU; ++u) {
-        const int64_t rel = ((t0 + u * FNW) << 4) + r16;
-#pragma unroll
-        for (int i = 0; i < KS; ++i)
-          kt[u][i] = rel < nrel ? ld16(kb + (lo + rel) * p.css + 32 * i) : make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < FTU; ++u) {
-      const int64_t tb = (t0 + u * FNW) << 4;
-      if (tb >= nrel) break;
-      if (fresh && tb + r16 == srel) {   // the new key, not the cache row
-#pragma unroll
-        for (int i = 0; i < KS; ++i) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int dd = 32 * i + 8 * q4 + 2 * e;
-            w[e] = f2bf(knew[dd]) | (f2bf(knew[dd + 1]) << 16);
-          }
-          kt[u][i] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < KS; ++i) c = mfma16x16x32(kt[u][i], qb[i], c);
-      if (r16 < G) {
-        float sv[4];
-        float mx = mrun;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t rel = tb + 4 * q4 + e;
-          sv[e] = c[e] * p.sm_scale;
-          if (rel < nrel) {
-            sc_lds[(int64_t)r16 * cap + rel] = sv[e];
-            mx = fmaxf(mx, sv[e]);
-          }
-        }
-        float add = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (tb + 4 * q4 + e < nrel) add += expf(sv[e] - mx);
-        lrun = lrun * expf(mrun - mx) + add;
-        mrun = mx;
-      }
-    }
-  }
-  // merge over the four lane rows of a head, then over the waves
-#pragma unroll
-  for (int o = 16; o < EK_WAVE; o <<= 1) {
-    const float m2 = __shfl_xor(mrun, o, EK_WAVE);
-    const float l2 = __shfl_xor(lrun, o, EK_WAVE);
-    merge_ml(mrun, lrun, m2, l2);
-  }
-  if (q4 == 0 && r16 < G) {
-    stm[wave][r16] = mrun;
-    stl[wave][r16] = lrun;
-  }
-  __syncthreads();
-  // p = bf16(exp(s - M) / L) in place, once per score: thread -> head tid % G
-  {
-    const int g = tid % G;
-    float M = stm[0][g], L = stl[0][g];
-#pragma unroll
-    for (int w = 1; w < FNW; ++w) merge_ml(M, L, stm[w][g], stl[w][g]);
-    float* row = sc_lds + (int64_t)g * cap;
-    for (int64_t n = tid / G; n < nrel; n += FNT / G) row[n] = rbf(expf(row[n] - M) / L);
-  }
-  __syncthreads();
-
-  // ---- PV. A operand = P: p[head r16][keys 8 q4 .. +7 of the tile], zero for
-  // r16 >= G and past the last key.
-  f32x4_t acc[2];
-  acc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  acc[1] = acc[0];
-  const float* prow = sc_lds + (int64_t)(r16 < G ? r16 : 0) * cap;
-  uint16_t (*vtw)[VTS] = vt[wave];
-  for (int64_t t0 = wave; t0 < ntile32; t0 += (int64_t)FNW * FPT) {
-    if (t0 != wave) {
-#pragma unroll
-      for (int u = 0; u < FPT; ++u) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const int64_t rel = ((t0 + u * FNW) << 5) + vkey + 16 * m;
-          vreg[u][m] = (rel < nrel && !(fresh && rel == srel)) ? ld16(vb + (lo + rel) * p.css) : make_uint4(0, 0, 0, 0);
-        }
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < FPT; ++u) {
-      const int64_t tb = (t0 + u * FNW) << 5;
-      if (tb >= nrel) break;
-      // stage the V tile: key rows of 32 dims (the new value at the new slot)
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        uint4 v = vreg[u][m];
-        if (fresh && tb + vkey + 16 * m == srel) v = *reinterpret_cast<const uint4*>(&vnew[8 * vsub]);
-        uint2* dst = reinterpret_cast<uint2*>(&vtw[vkey + 16 * m][8 * vsub]);
-        dst[0] = make_uint2(v.x, v.y);
-        dst[1] = make_uint2(v.z, v.w);
-      }
-      const int64_t rel0 = tb + 8 * q4;
-      uint32_t pw[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t ra = rel0 + 2 * e;
-        const float pa = (r16 < G && ra < nrel) ? prow[ra] : 0.f;        // exact bf16 values
-        const float pb = (r16 < G && ra + 1 < nrel) ? prow[ra + 1] : 0.f;
-        pw[e] = (__float_as_uint(pa) >> 16) | (__float_as_uint(pb) & 0xffff0000u);
-      }
-      const uint4 pa4 = make_uint4(pw[0], pw[1], pw[2], pw[3]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        uint32_t bw[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          bw[e] = (uint32_t)vtw[8 * q4 + 2 * e][16 * j + r16] | ((uint32_t)vtw[8 * q4 + 2 * e + 1][16 * j + r16] << 16);
-        acc[j] = mfma16x16x32(pa4, make_uint4(bw[0], bw[1], bw[2], bw[3]), acc[j]);
-      }
-    }
-  }
-  // C rows 4 q4 + e are heads; add the waves' partial outputs through LDS
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int g = 4 * q4 + e;
-    if (g < G) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) outp[wave][g][16 * j + r16] = acc[j][e];
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < G * FDC; i += FNT) {
-    const int g = i / FDC, d = i % FDC;
-    float t = 0.f;
-#pragma unroll
-    for (int w = 0; w < FNW; ++w) t += outp[w][g][d];
-    p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d0 + d] = (bf16_t)f2bf(t);
-  }
+  u.rope = p.rope;
+  u.qn = p.qn; u.kn = p.kn;
+  u.eps = p.eps; u.sm_scale = p.sm_scale;
+  u.kc = p.kc + b * p.csb + h * p.csh;
+  u.vc = p.vc + b * p.csb + h * p.csh;
+  u.css = p.css;
+  u.cap = p.s_cap;
+  u.lo = lo; u.hi = len;
+  u.writer = blockIdx.y == 0;
+  u.d0 = blockIdx.y * eka::FDC;
+  u.out = p.out + b * p.ldo_b + (int64_t)h * G * p.ldo_h;
+  u.out_stride = p.ldo_h;
+  u.coherent_out = false;
+  eka::attn_unit<D, G>(u, lds);
 }
 
 // Score rows up to this many bytes per workgroup take the single-launch path
@@ -649,10 +360,10 @@ template <int D, int G>
 hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
   constexpr int DC = D >= 32 ? 32 : D;
   // short rows: one fused launch (the whole score row of a head in LDS)
-  const size_t lds = (size_t)G * p.s_cap * sizeof(float);
-  if (lds <= kFusedScoreLds) {
-    dim3 grid((unsigned)(b * p.nkv), (unsigned)(D / FDC));
-    hipLaunchKernelGGL((attn_fused_kernel<D, G>), grid, dim3(FNT), lds, st, p);
+  if ((size_t)G * p.s_cap * sizeof(float) <= kFusedScoreLds) {
+    dim3 grid((unsigned)(b * p.nkv), (unsigned)(D / eka::FDC));
+    const size_t lds = eka::AttnLds<D, G>::bytes(p.s_cap);
+    hipLaunchKernelGGL((attn_fused_kernel<D, G>), grid, dim3(eka::FNT), lds, st, p);
     return hipGetLastError();
   }
   dim3 grid1((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);

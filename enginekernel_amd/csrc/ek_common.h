@@ -72,8 +72,18 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// 16-byte global load of 8 bf16
-__device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// index of this thread's wave in the workgroup, as a wave-uniform (scalar) value
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// 16-byte load of 8 bf16 from global memory. The pointer is taken as a
+// global (not flat) address, so the load is a global_load_dwordx4 even when
+// the pointer itself was read from memory; callers pass device memory only.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t global_u32x4_t;
+__device__ __forceinline__ uint4 ld16(const bf16_t* p) {
+  const u32x4_t v = *(global_u32x4_t*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // Release this workgroup's global writes and count it in; returns true in
 // the last workgroup to arrive (which then observes every other

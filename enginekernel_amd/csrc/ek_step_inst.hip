@@ -1,0 +1,43 @@
+// Instantiations of the persistent decode-step kernel for one head dim:
+// compiled once per head dim with -DEK_STEP_D=<32|64|128> so that the
+// instantiations build in parallel.
+
+#include "ek_step_impl.h"
+
+#ifndef EK_STEP_D
+#error "compile with -DEK_STEP_D=<head dim>"
+#endif
+
+namespace eks {
+
+template <int BM, int D, int G>
+static hipError_t launch_one(const StepArgs& a, int nwg, hipStream_t st) {
+  const size_t lds = step_lds_bytes<BM, D, G>(a.kpad_max, a.part_max, a.s_cap, a.o_rows, a.nq * D);
+  static bool attr_done = false;   // allow more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU)
+  if (!attr_done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<BM, D, G>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+    if (e != hipSuccess) return e;
+    attr_done = true;
+  }
+  hipLaunchKernelGGL((step_kernel<BM, D, G>), dim3(nwg), dim3(SNT), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int BM>
+static hipError_t launch_g(const StepArgs& a, int g, int nwg, hipStream_t st) {
+  switch (g) {
+    case 1: return launch_one<BM, EK_STEP_D, 1>(a, nwg, st);
+    case 2: return launch_one<BM, EK_STEP_D, 2>(a, nwg, st);
+    case 4: return launch_one<BM, EK_STEP_D, 4>(a, nwg, st);
+    case 8: return launch_one<BM, EK_STEP_D, 8>(a, nwg, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <>
+hipError_t launch_step<1, EK_STEP_D>(const StepArgs& a, int g, int nwg, hipStream_t st) {
+  return launch_g<1>(a, g, nwg, st);
+}
+
+}  // namespace eks

@@ -378,6 +378,94 @@ def lm_head_argmax(hidden, lm_head, scratch: ArgmaxScratch, out_tok=None, logits
 
 
 # ----------------------------------------------------------------------------
+# the whole decode step as one persistent launch
+# ----------------------------------------------------------------------------
+def decode_step_plan(hidden: int, inter: int, n_q: int, n_kv: int, head_dim: int, vocab: int, m: int,
+                     s_cap: int, n_layers: int):
+    """(arena bytes, argmax entries, barrier bytes, grid) when the persistent
+    decode-step kernel handles this shape, else None (see decode_step)."""
+    import ctypes
+    lib = _hip.load()
+    sizes = (ctypes.c_int64 * 4)()
+    rc = lib.ek_decode_step_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, sizes)
+    if rc != 0:
+        return None
+    return tuple(int(v) for v in sizes)
+
+
+class StepScratch:
+    """Device state of the persistent decode step: the activation arena, the
+    argmax partials, the barrier block and the error word, sized by
+    decode_step_plan. One per (model, batch); launches sharing it must not
+    overlap."""
+
+    def __init__(self, sizes, device):
+        arena_bytes, am, bar_bytes, grid = sizes
+        self.arena = torch.empty((arena_bytes + 1) // 2, dtype=_BF16, device=device)
+        self.am_val = torch.empty(am, dtype=torch.float32, device=device)
+        self.am_idx = torch.empty(am, dtype=torch.int32, device=device)
+        self.barrier = torch.zeros((bar_bytes + 3) // 4, dtype=torch.int32, device=device)
+        self.err = torch.zeros(1, dtype=torch.int32, device=device)
+        self.arena_bytes, self.am_cap, self.grid = arena_bytes, am, grid
+
+    def layer_views(self, cfg, m: int = 1):
+        """The arena's per-layer activations of the last launch, as views:
+        r_in (residual entering the layer), r_mid (after attention), qkv,
+        att (attention output), o, act (SwiGLU output), dn (down output)."""
+        h, inter = cfg.hidden_size, cfg.intermediate_size
+        qw, qkvw = cfg.num_heads * cfg.head_dim, (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
+        ls = m * (4 * h + qkvw + qw + inter)
+        out = []
+        for l in range(cfg.num_layers):
+            o = l * ls
+            d = {}
+            for name, w in (("r_in", h), ("r_mid", h), ("qkv", qkvw), ("att", qw), ("o", h), ("act", inter),
+                            ("dn", h)):
+                d[name] = self.arena[o:o + m * w].view(m, w)
+                o += m * w
+            out.append(d)
+        return out
+
+    def check(self) -> None:
+        """Raise if a launch abandoned a barrier wait (and re-arm the state)."""
+        if int(self.err.item()):
+            self.err.zero_()
+            self.barrier.zero_()
+            raise RuntimeError("decode_step: a grid barrier wait timed out; the step's outputs are invalid")
+
+
+def layer_table(layers, k_cache, v_cache, device) -> torch.Tensor:
+    """The device pointer table [n_layers, 10] of decode_step: qkv, o, gu,
+    down, ln1, ln2, qn, kn, k_cache, v_cache addresses per layer."""
+    rows = [[lay["qkv"].data_ptr(), lay["o"].data_ptr(), lay["gu"].data_ptr(), lay["down"].data_ptr(),
+             lay["ln1"].data_ptr(), lay["ln2"].data_ptr(), lay["qn"].data_ptr(), lay["kn"].data_ptr(),
+             kc.data_ptr(), vc.data_ptr()] for lay, kc, vc in zip(layers, k_cache, v_cache)]
+    return torch.tensor(rows, dtype=torch.int64).to(device)
+
+
+def decode_step(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap, tokens, positions, len_t,
+                slot_t, start_t, out_buf, step_idx, scratch: StepScratch, out_tok=None):
+    """ek_model.py:360-416 + :490-493 + engine.py:288-292 (the captured step
+    body) as ONE persistent launch: every layer, the final norm, lm_head, the
+    first-index argmax and the step bookkeeping (tokens <- next, positions +=
+    1, slot_t <- len, len += 1, out_buf[step_idx] <- next, step_idx += 1).
+    Batch 1; `table` from layer_table; k_cache0 gives the cache strides."""
+    _gpu(tokens, embed, lm_head, k_cache0)
+    m = tokens.shape[0]
+    _need(out_buf.dtype == torch.int32 and out_buf.shape[1] == m and out_buf.is_contiguous(), "out_buf")
+    _need(table.dtype == torch.int64 and table.shape == (cfg.num_layers, 10) and table.is_contiguous(), "table")
+    _need(embed.stride(-1) == 1 and lm_head.stride(-1) == 1 and cos.stride(0) == sin.stride(0), "weights")
+    call("ek_decode_step", ptr(table), cfg.num_layers, cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
+         cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, m, float(cfg.rms_eps), float(cfg.head_dim ** -0.5),
+         ptr(embed), embed.stride(0), ptr(lm_head), ptr(final_norm), ptr(cos), ptr(sin), cos.stride(0),
+         cos.shape[0], k_cache0.stride(0), k_cache0.stride(1), k_cache0.stride(2), s_cap,
+         ptr(tokens), ptr(positions), ptr(len_t), ptr(slot_t), ptr(start_t), ptr(out_buf), ptr(step_idx),
+         out_buf.shape[0], ptr(out_tok), ptr(scratch.arena), scratch.arena_bytes, ptr(scratch.am_val),
+         ptr(scratch.am_idx), scratch.am_cap, ptr(scratch.barrier), ptr(scratch.err), stream())
+    return tokens
+
+
+# ----------------------------------------------------------------------------
 # attention
 # ----------------------------------------------------------------------------
 _SMS = None

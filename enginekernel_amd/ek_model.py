@@ -138,6 +138,7 @@ class _StepBuffers:
         self.hidden = torch.empty(b, h, dtype=bf, device=device)
         self.argmax = K.ArgmaxScratch(b, cfg.vocab_size, device)
         self.next_tok = torch.empty(b, dtype=torch.int64, device=device)
+        self.step = None   # K.StepScratch of the persistent step, made on first use
 
 
 class Qwen3(torch.nn.Module):
@@ -163,6 +164,11 @@ class Qwen3(torch.nn.Module):
         self.sm_scale = self.cfg.head_dim ** -0.5
         self.zero_slot = torch.zeros(1024, dtype=torch.int64, device=device)
         self._bufs: dict = {}
+        self._plans: dict = {}
+        self._tables: dict = {}
+        # the whole step as one persistent launch where its plan allows (opt-in:
+        # ENGINE_PERSISTENT=1; the per-kernel graph step is the default)
+        self.persistent = os.environ.get("ENGINE_PERSISTENT", "0") == "1"
         # the prefill's hipBLASLt projections: no reduced-precision bf16 reductions
         torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
 
@@ -307,11 +313,52 @@ class Qwen3(torch.nn.Module):
         out = torch.empty(b, dtype=torch.int64, device=hidden.device)
         return K.lm_head_argmax(hidden.contiguous(), self.lm_head, bufs.argmax, out_tok=out, logits=logits)
 
+    def persistent_plan(self, b: int, s_cap: int):
+        """decode_step_plan for this model at batch b and score capacity s_cap
+        (None when the persistent step does not handle the shape)."""
+        key = (b, s_cap)
+        if key not in self._plans:
+            c = self.cfg
+            self._plans[key] = K.decode_step_plan(c.hidden_size, c.intermediate_size, c.num_heads,
+                                                  c.num_kv_heads, c.head_dim, c.vocab_size, b, s_cap,
+                                                  c.num_layers)
+        return self._plans[key]
+
+    def _layer_table(self, k_cache, v_cache):
+        key = tuple(t.data_ptr() for t in k_cache) + tuple(t.data_ptr() for t in v_cache)
+        tab = self._tables.get(key)
+        if tab is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("decode_step: build the layer table (run one step) before capturing")
+            tab = self._tables[key] = K.layer_table(self.layers, k_cache, v_cache, self.device)
+        return tab
+
+    def check_step_error(self) -> None:
+        """Raise if a persistent step abandoned a barrier wait."""
+        for bufs in self._bufs.values():
+            if bufs.step is not None:
+                bufs.step.check()
+
     def step(self, tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws, out_buf, step_idx,
              logits=None):
-        """The whole graph step of engine.py:284-292 in HIP launches: decode,
-        final add + norm + lm_head + argmax (one kernel), then tokens <- next,
-        positions += 1, out_buf[step_idx] <- next, step_idx += 1."""
+        """The whole graph step of engine.py:284-292: decode, final add + norm
+        + lm_head + argmax, then tokens <- next, positions += 1, out_buf[step_idx]
+        <- next, step_idx += 1. At batch 1 (and rows whose attention scores fit
+        in LDS) it is one persistent launch (K.decode_step); otherwise HIP
+        launches per layer with the last three fused into one kernel."""
+        b = tokens.shape[0]
+        s_cap = k_cache[0].shape[2]
+        if ws is not None and len(ws) >= 8:
+            s_cap = min(s_cap, ws[7].shape[2])
+        plan = self.persistent_plan(b, s_cap) if (self.persistent and logits is None) else None
+        if plan is not None:
+            bufs = self.buffers(b)
+            if bufs.step is None:
+                bufs.step = K.StepScratch(plan, self.device)
+            K.decode_step(self._layer_table(k_cache, v_cache), self.cfg, self.embed, self.lm_head, self.final_norm,
+                          self.cos, self.sin, k_cache[0], s_cap, tokens, positions, len_t, slot_t, start_t,
+                          out_buf, step_idx, bufs.step, out_tok=bufs.next_tok)
+            return bufs.next_tok
         bufs = self._layers(tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws)
         return K.lm_head_argmax(None, self.lm_head, bufs.argmax, out_tok=bufs.next_tok, logits=logits,
                                 parts=bufs.down_parts, residual=bufs.res[0], norm_w=self.final_norm,

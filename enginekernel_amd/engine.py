@@ -263,6 +263,7 @@ class _FastEngine:
             events[j % len(events)].synchronize()
             yield host[j, :b].tolist()
         self.last_stats = (launched, max_new_tokens - 1)
+        self.model.check_step_error()
 
     def _generate_eager(self, ids, pos, pad, s, bias, max_new_tokens):
         """engine.py:721-743 on the HIP kernels without graphs: zero caches,

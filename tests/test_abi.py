@@ -15,7 +15,7 @@ from enginekernel_amd import ek_kernels as K
 def test_library_exports_every_declared_symbol():
     lib = _hip.load()
     declared = _hip.declared_symbols()
-    assert len(declared) == 16
+    assert len(declared) == 18
     for name in declared:
         assert hasattr(lib, name), name
     # the ctypes signature table covers every kernel entry point
@@ -45,6 +45,23 @@ def test_argument_errors_return_invalid_value_without_a_gpu():
     with pytest.raises(_hip.HipKernelError) as e:
         _hip.call("ek_silu_mul", None, None, 1, 7, 8, 8, None)      # n not a multiple of 8
     assert e.value.code == 1
+
+
+def test_decode_step_plan_rejects_unsupported_shapes_without_a_gpu():
+    lib = _hip.load()
+    sizes = (ctypes.c_int64 * 4)()
+    # 4B shape at batch 2: the persistent step takes batch 1 only
+    rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 2, 768, 36, sizes)
+    assert rc == 1 and b"batch" in lib.ek_last_error()
+    # 32 query heads per kv head: not a supported group
+    rc = lib.ek_decode_step_plan(2560, 9728, 32, 1, 128, 151936, 1, 768, 36, sizes)
+    assert rc == 1 and b"query heads" in lib.ek_last_error()
+    # a score row of 4 x 8192 fp32 does not fit the unit's 32 KiB
+    rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 8192, 36, sizes)
+    assert rc == 1 and b"LDS" in lib.ek_last_error()
+    zeros = [None if t is ctypes.c_void_p else 0.0 if t is ctypes.c_float else 0
+             for t in _hip.SIGNATURES["ek_decode_step"]]
+    assert lib.ek_decode_step(*zeros) == 1
 
 
 def test_kernels_refuse_cpu_tensors():
