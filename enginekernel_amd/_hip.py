@@ -52,7 +52,7 @@ SIGNATURES = {
     "ek_decode_step": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _F,
                        _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                        _P, _P, _P, _P, _P, _P, _P, _I64, _P,
-                       _P, _I64, _P, _P, _I64, _P, _P, _P],
+                       _P, _I64, _P, _P, _P],
 }
 
 

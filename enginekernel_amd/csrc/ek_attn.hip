@@ -348,7 +348,11 @@ __global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
   u.d0 = blockIdx.y * eka::FDC;
   u.out = p.out + b * p.ldo_b + (int64_t)h * G * p.ldo_h;
   u.out_stride = p.ldo_h;
-  u.coherent_out = false;
+  u.ll_out = nullptr;
+  u.ll_ep = 0;
+#ifdef EK_STEP_TRACE
+  u.trace_row = nullptr;
+#endif
   eka::attn_unit<D, G>(u, lds);
 }
 

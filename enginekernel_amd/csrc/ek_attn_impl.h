@@ -23,8 +23,8 @@
 // In rope mode the unit norms/rotates its query heads and the new key (which
 // stands in for the cache row at the new slot), takes the raw new value
 // (likewise), and the writer unit also stores both in the cache. The first K
-// tiles are loaded on entry, before the QK-norm/RoPE work, and the first V
-// tiles right after it, so both overlap the work before their use.
+// and V tiles are loaded on entry, before the q/k/v heads are awaited and
+// before the QK-norm/RoPE work, so both overlap the work before their use.
 //
 // MFMA lane layout (16x16x32): lane l = r + 16 q (r < 16, q < 4) holds
 // A[row r][k = 8q .. 8q+7], B[k = 8q .. 8q+7][col r] and C[rows 4q .. 4q+3][col r].
@@ -108,8 +108,20 @@ struct AttnUnit {
   bool writer;                           // stores the new key/value at slot hi - 1
   int d0;                                // first head dim of this unit
   bf16_t* out; int64_t out_stride;       // out[g * out_stride + d0 + d]
-  bool coherent_out;                     // device-scope stores (read by other workgroups of the same launch)
+  // When set, the output goes instead to 8-byte words {bf16 pair, epoch} at
+  // ll_out[(g * out_stride + d0 + d) / 2] (device scope: read by other
+  // workgroups of the same launch, which poll for the epoch)
+  unsigned long long* ll_out; uint32_t ll_ep;
+#ifdef EK_STEP_TRACE
+  int64_t* trace_row;                    // per-stage timestamps of this unit (trace builds)
+#endif
 };
+
+#ifdef EK_STEP_TRACE
+#define EK_ATTN_MARK(ev) do { if (threadIdx.x == 0 && a.trace_row) a.trace_row[ev] = wall_clock64(); } while (0)
+#else
+#define EK_ATTN_MARK(ev) do { } while (0)
+#endif
 
 __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(size_t)15; }
 
@@ -128,8 +140,15 @@ struct AttnLds {
   }
 };
 
-template <int D, int G, int FTU = eka::FTU, int FPT = eka::FPT>
-__device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds) {
+struct NoPre {
+  __device__ bool operator()() const { return true; }
+};
+
+// `pre` runs once the first K and V tiles are in flight and before the q/k/v
+// heads are read (the persistent step waits there for them); false abandons
+// the unit.
+template <int D, int G, int FTU = eka::FTU, int FPT = eka::FPT, typename PRE = NoPre>
+__device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds, PRE pre = PRE()) {
   constexpr int KS = D / 32;   // 32-dim k-steps of a score tile
   static_assert(G <= 8 && D % 32 == 0, "tile shape");
   using L = AttnLds<D, G>;
@@ -143,7 +162,12 @@ __device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds)
   uint16_t (*vt)[32][VTS] = reinterpret_cast<uint16_t (*)[32][VTS]>(fx + L::QS + L::KNEW + L::VNEW + 2 * L::ST);
   float (*outp)[G][FDC] = reinterpret_cast<float (*)[G][FDC]>(fx + L::QS + L::KNEW + L::VNEW + 2 * L::ST + L::VT);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  // the thread index is made opaque here so that the per-lane offsets below
+  // are computed per call rather than hoisted out of a caller's loop (where
+  // they would stay live, in registers, across everything else it does)
+  int tid_o = threadIdx.x;
+  __asm__ volatile("" : "+v"(tid_o));
+  const int tid = tid_o, lane = tid & 63, wave = wave_id();
   const int r16 = lane & 15, q4 = lane >> 4;
   const int64_t cap = a.cap;
   const int64_t lo = a.lo, hi = a.hi;
@@ -166,6 +190,23 @@ __device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds)
       kt[u][i] = rel < nrel ? ld16(kb + (lo + rel) * a.css + 32 * i) : make_uint4(0, 0, 0, 0);
   }
 
+  // first V tiles in flight: 16 B chunks c = lane + 64 m of the 32 x 32 tile,
+  // key c / 4, dims 8 (c % 4) .. +7
+  const int vkey = lane >> 2, vsub = lane & 3;
+  const bf16_t* vb = a.vc + d0 + 8 * vsub;
+  const int64_t ntile32 = (nrel + 31) >> 5;
+  uint4 vreg[FPT][2];
+#pragma unroll
+  for (int u = 0; u < FPT; ++u) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const int64_t rel = ((int64_t)(wave + u * FNW) << 5) + vkey + 16 * m;
+      vreg[u][m] = (rel < nrel && !(fresh && rel == srel)) ? ld16(vb + (lo + rel) * a.css) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  if (!pre()) return false;
+  EK_ATTN_MARK(15);
+
   if (a.rope) {
     const bool writer = a.writer && slot >= 0;
     const int units = G + ((fresh || writer) ? 1 : 0);
@@ -186,21 +227,8 @@ __device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds)
     for (int i = tid; i < G * D; i += FNT) qs[i / D][i % D] = bf2f(a.qh[(i / D) * a.q_stride + i % D]);
   }
 
-  // first V tiles in flight: 16 B chunks c = lane + 64 m of the 32 x 32 tile,
-  // key c / 4, dims 8 (c % 4) .. +7
-  const int vkey = lane >> 2, vsub = lane & 3;
-  const bf16_t* vb = a.vc + d0 + 8 * vsub;
-  const int64_t ntile32 = (nrel + 31) >> 5;
-  uint4 vreg[FPT][2];
-#pragma unroll
-  for (int u = 0; u < FPT; ++u) {
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int64_t rel = ((int64_t)(wave + u * FNW) << 5) + vkey + 16 * m;
-      vreg[u][m] = (rel < nrel && !(fresh && rel == srel)) ? ld16(vb + (lo + rel) * a.css) : make_uint4(0, 0, 0, 0);
-    }
-  }
   __syncthreads();
+  EK_ATTN_MARK(16);
 
   // ---- scores. B operand = Q^T: q[g = r16][32 i + 8 q4 .. +7], zero for g >= G
   uint4 qb[KS];
@@ -278,6 +306,7 @@ __device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds)
     stl[wave][r16] = lrun;
   }
   __syncthreads();
+  EK_ATTN_MARK(17);
   // p = bf16(exp(s - M) / L) in place, once per score: thread -> head tid % G
   {
     const int g = tid % G;
@@ -288,6 +317,7 @@ __device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds)
     for (int64_t n = tid / G; n < nrel; n += FNT / G) row[n] = rbf(expf(row[n] - M) / Lsum);
   }
   __syncthreads();
+  EK_ATTN_MARK(18);
 
   // ---- PV. A operand = P: p[head r16][keys 8 q4 .. +7 of the tile], zero for
   // r16 >= G and past the last key.
@@ -350,17 +380,26 @@ __device__ __forceinline__ void attn_unit(const AttnUnit& a, unsigned char* lds)
     }
   }
   __syncthreads();
+  EK_ATTN_MARK(19);
+  if (a.ll_out) {
+    for (int i = tid; i < G * FDC / 2; i += FNT) {
+      const int g = i / (FDC / 2), d = 2 * (i % (FDC / 2));
+      float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < FNW; ++w) { t0 += outp[w][g][d]; t1 += outp[w][g][d + 1]; }
+      const unsigned long long word = ((unsigned long long)a.ll_ep << 32) | pack2(t0, t1);
+      __hip_atomic_store(a.ll_out + (g * a.out_stride + d0 + d) / 2, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return true;
+  }
   for (int i = tid; i < G * FDC; i += FNT) {
     const int g = i / FDC, d = i % FDC;
     float t = 0.f;
 #pragma unroll
     for (int w = 0; w < FNW; ++w) t += outp[w][g][d];
-    bf16_t* dst = a.out + g * a.out_stride + d0 + d;
-    if (a.coherent_out)
-      __hip_atomic_store(dst, (bf16_t)f2bf(t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-      *dst = (bf16_t)f2bf(t);
+    a.out[g * a.out_stride + d0 + d] = (bf16_t)f2bf(t);
   }
+  return true;
 }
 
 }  // namespace eka

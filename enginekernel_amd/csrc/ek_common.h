@@ -66,6 +66,25 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Sum over all 64 lanes through DPP moves (no LDS traffic): pairs and quads
+// by quad permutes, rows of 16 by row rotates, then rows 0+1 and 2+3 by
+// row broadcasts; the total is exact in lane 63 (other lanes hold partial
+// sums) and is returned wave-uniform. The summation order is fixed.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_plus(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
+  return v + __int_as_float(moved);
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_plus<0xB1>(v);        // quad_perm [1,0,3,2]
+  v = dpp_plus<0x4E>(v);        // quad_perm [2,3,0,1]
+  v = dpp_plus<0x124>(v);       // row_ror:4
+  v = dpp_plus<0x128>(v);       // row_ror:8  -> every lane holds its row's sum
+  v = dpp_plus<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v = dpp_plus<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, EK_WAVE));

@@ -6,14 +6,14 @@
 #include "ek_hip.h"
 
 namespace eks {
-template <> hipError_t launch_step<1, 32>(const StepArgs&, int, int, hipStream_t);
-template <> hipError_t launch_step<1, 64>(const StepArgs&, int, int, hipStream_t);
-template <> hipError_t launch_step<1, 128>(const StepArgs&, int, int, hipStream_t);
+template <> hipError_t launch_step<32>(const StepArgs&, int, int, hipStream_t);
+template <> hipError_t launch_step<64>(const StepArgs&, int, int, hipStream_t);
+template <> hipError_t launch_step<128>(const StepArgs&, int, int, hipStream_t);
 }  // namespace eks
 
 namespace {
 
-constexpr int64_t kSpin = int64_t(1) << 22;           // barrier polls before giving up (~0.1-0.5 s)
+constexpr int64_t kSpin = int64_t(1) << 20;           // polls of one hand-over wait before giving up (~1 s)
 constexpr size_t kLdsLimit = 160 * 1024 - 1024;       // dynamic LDS per workgroup (static arrays aside)
 constexpr int64_t kFusedScoreLds = 32 * 1024;         // score row bytes per attention unit
 
@@ -29,18 +29,16 @@ int step_grid() {
 
 struct Plan {
   int nwg, kpad_max, part_max, o_rows;
-  int64_t arena_bytes, am_entries;
+  int64_t arena_bytes;
   size_t lds;
 };
 
-size_t lds_for(int m, int d, int g, int kpad_max, int part_max, int64_t s_cap, int o_rows, int qw) {
-  const size_t gemv = eka::align16((size_t)m * kpad_max * 2) + eka::align16((size_t)part_max * eks::SNW * m * 4) +
-                      (size_t)o_rows * qw * 2;
-  size_t attn = eka::align16((size_t)(g + 2) * d * 2) + eka::align16((size_t)g * s_cap * 4);
+size_t attn_lds(int d, int g, int64_t s_cap) {
+  size_t attn = eka::align16((size_t)(g + 6) * d * 2) + eka::align16((size_t)g * s_cap * 4);
   attn += eka::align16((size_t)g * d * 4) + eka::align16((size_t)d * 4) + eka::align16((size_t)eka::FDC * 2) +
           2 * eka::align16((size_t)eka::FNW * 8 * 4) + eka::align16((size_t)eka::FNW * 32 * eka::VTS * 2) +
           eka::align16((size_t)eka::FNW * g * eka::FDC * 4);
-  return gemv > attn ? gemv : attn;
+  return attn;
 }
 
 // Returns an error (with a message) when the shape is outside what the kernel handles.
@@ -56,28 +54,30 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   if (n_layers < 1 || hidden < eks::CH || inter < eks::CH || vocab < 1 || hidden % eks::CH || inter % eks::CH ||
       (n_q * head_dim) % eks::CH)
     return ek_fail(hipErrorInvalidValue, "decode_step: hidden, intermediate and n_q * head_dim must be multiples of 512");
-  if (hidden > 2 * 8 * eks::SNT)
-    return ek_fail(hipErrorInvalidValue, "decode_step: hidden must be at most 8192");
+  if (hidden > 2 * eks::NGW * eks::SNT)
+    return ek_fail(hipErrorInvalidValue, "decode_step: hidden must be at most 4096");
   if (hidden > (1 << 20) || inter > (1 << 20) || vocab > (1 << 30) || n_q * head_dim > (1 << 20))
     return ek_fail(hipErrorInvalidValue, "decode_step: sizes too large");
   if (s_cap < 1 || g * s_cap * 4 > kFusedScoreLds)
     return ek_fail(hipErrorInvalidValue, "decode_step: the attention row does not fit in LDS (use the per-kernel step)");
   p.nwg = step_grid();
-  if (p.nwg < 1) return ek_fail(hipErrorInvalidValue, "decode_step: no device");
-  const int n_attn = (int)(m * n_kv * (head_dim / eka::FDC));
-  if (n_attn >= p.nwg) return ek_fail(hipErrorInvalidValue, "decode_step: too many attention units for the grid");
+  if (p.nwg < 1 || p.nwg > eks::MAX_WG) return ek_fail(hipErrorInvalidValue, "decode_step: unsupported device");
+  const int n_attn = (int)(n_kv * (head_dim / eka::FDC));
+  if (4 * n_attn > p.nwg) return ek_fail(hipErrorInvalidValue, "decode_step: too many attention units for the grid");
   const int qw = (int)(n_q * head_dim), qkvw = (int)((n_q + 2 * n_kv) * head_dim);
   int kmax = (int)hidden;
   kmax = kmax > qw ? kmax : qw;
   kmax = kmax > (int)inter ? kmax : (int)inter;
   p.kpad_max = eks::kpad_of(kmax);
-  p.o_rows = eks::cdiv_i((int)hidden, p.nwg - n_attn);
-  p.part_max = eks::part_rows_max((int)hidden, (int)inter, qkvw, (int)vocab, p.nwg);
-  p.part_max = p.part_max > p.o_rows ? p.part_max : p.o_rows;
-  p.lds = lds_for((int)m, (int)head_dim, (int)g, p.kpad_max, p.part_max, s_cap, p.o_rows, qw);
+  const int n_gemv = p.nwg - n_attn;   // projection workgroups
+  p.o_rows = 2 * eks::cdiv_i((int)hidden / 2, n_gemv);
+  p.part_max = eks::part_rows_max((int)hidden, (int)inter, qkvw, (int)vocab, n_gemv, p.o_rows);
+  const size_t gemv = eks::step_rr_bytes((int)hidden) + eka::align16((size_t)p.kpad_max * 2) +
+                      eka::align16((size_t)p.part_max * eks::SNW * 4) + (size_t)p.o_rows * qw * 2;
+  const size_t attn = attn_lds((int)head_dim, (int)g, s_cap);
+  p.lds = gemv > attn ? gemv : attn;
   if (p.lds > kLdsLimit) return ek_fail(hipErrorInvalidValue, "decode_step: LDS plan exceeds the workgroup limit");
-  p.arena_bytes = n_layers * eks::arena_layer_elems((int)m, (int)hidden, (int)inter, qkvw, qw) * 2;
-  p.am_entries = (int64_t)p.nwg * m;
+  p.arena_bytes = 8 * eks::arena_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg);
   return hipSuccess;
 }
 
@@ -93,7 +93,7 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
   if (e != hipSuccess) return e;
   if (sizes) {
     sizes[0] = p.arena_bytes;
-    sizes[1] = p.am_entries;
+    sizes[1] = 0;
     sizes[2] = (int64_t)sizeof(eks::Bar);
     sizes[3] = p.nwg;
   }
@@ -106,17 +106,16 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
                    const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb, int64_t csh, int64_t css,
                    int64_t s_cap, int64_t* tokens, int64_t* positions, int64_t* len_t, int64_t* slot_t,
                    const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
-                   void* arena, int64_t arena_bytes, float* am_val, int32_t* am_idx, int64_t am_cap, void* barrier,
-                   int* err, void* stream) {
+                   void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream) {
   EK_GUARD();
   Plan p;
   hipError_t e = make_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
   if (e != hipSuccess) return e;
   if (!layer_ptrs || !embed || !lm_head || !final_norm || !cos || !sin || !tokens || !positions || !len_t ||
-      !slot_t || !start_t || !out_buf || !step_idx || !arena || !am_val || !am_idx || !barrier || !err)
+      !slot_t || !start_t || !out_buf || !step_idx || !arena || !barrier || !err)
     return ek_fail(hipErrorInvalidValue, "decode_step: null pointer argument");
-  if (arena_bytes < p.arena_bytes || am_cap < p.am_entries)
-    return ek_fail(hipErrorInvalidValue, "decode_step: arena or argmax scratch smaller than the plan");
+  if (arena_bytes < p.arena_bytes)
+    return ek_fail(hipErrorInvalidValue, "decode_step: arena smaller than the plan");
   if (rope_len < 1 || ld_cs < head_dim || lde < hidden || css % 8 || csh % 8 || csb % 8 ||
       (reinterpret_cast<uintptr_t>(arena) & 15) || (reinterpret_cast<uintptr_t>(embed) & 15))
     return ek_fail(hipErrorInvalidValue, "decode_step: bad strides or alignment");
@@ -129,15 +128,15 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
   a.ld_cs = ld_cs; a.rope_len = rope_len; a.csb = csb; a.csh = csh; a.css = css; a.s_cap = s_cap;
   a.tokens = tokens; a.positions = positions; a.len_t = len_t; a.slot_t = slot_t; a.start_t = start_t;
   a.out_buf = out_buf; a.step_idx = step_idx; a.max_steps = max_steps; a.out_tok = out_tok;
-  a.arena = (bf16_t*)arena; a.am_val = am_val; a.am_idx = am_idx;
+  a.arena = (eks::llw_t*)arena;
   a.bar = (eks::Bar*)barrier; a.err = err; a.spin = kSpin;
   a.kpad_max = p.kpad_max; a.part_max = p.part_max; a.o_rows = p.o_rows;
   const int g = (int)(n_q / n_kv);
   hipStream_t st = (hipStream_t)stream;
   switch (head_dim) {
-    case 32: return eks::launch_step<1, 32>(a, g, p.nwg, st);
-    case 64: return eks::launch_step<1, 64>(a, g, p.nwg, st);
-    default: return eks::launch_step<1, 128>(a, g, p.nwg, st);
+    case 32: return eks::launch_step<32>(a, g, p.nwg, st);
+    case 64: return eks::launch_step<64>(a, g, p.nwg, st);
+    default: return eks::launch_step<128>(a, g, p.nwg, st);
   }
 }
 

@@ -1,35 +1,37 @@
-// The whole Qwen3 decode step as one persistent launch (gfx950).
+// The whole Qwen3 decode step (batch 1) as one persistent launch (gfx950).
 //
-// One 512-thread workgroup per CU runs every phase of the step in order --
-// per layer: RMSNorm + qkv projection, attention, o projection, residual add
-// + RMSNorm + gate/up projection + SwiGLU, down projection; then the final
-// add + norm, lm_head and argmax, and the step's bookkeeping -- with a grid
-// barrier between phases instead of a kernel boundary. What a kernel boundary
-// cannot do and this does: while a workgroup finishes one phase, its waves
-// already load the first weight chunks of the next phase (weights never depend
-// on activations), so the HBM stream does not stop at the ~180 phase
-// boundaries of a step.
+// One 512-thread workgroup per CU runs every phase of the step -- per layer:
+// residual add + RMSNorm + qkv projection, attention, o projection, residual
+// add + RMSNorm + gate/up projection + SwiGLU, down projection; then the
+// final add + norm, lm_head and argmax, and the step's bookkeeping.
 //
-// Projections. A phase's output units (rows; gate/up row pairs for SwiGLU)
-// are split evenly over the workgroups; a workgroup's (row, 1 KiB chunk)
-// items are split evenly over its 8 waves, so no wave idles on a short row
-// count. Each lane streams 16 B of a chunk (a wave reads 1 KiB per load
-// instruction, fully coalesced) through an 8-deep register ring that crosses
-// row and phase boundaries; fp32 FMA accumulation (bf16 products are exact),
-// a butterfly per row segment, and a fixed-order sum of the waves' segment
-// partials in LDS. Activations (at most 2 rows of <= 9728 bf16) are staged
-// once per phase in LDS.
+// No grid barriers. Every value one workgroup hands to another travels in an
+// 8-byte word {two bf16, epoch} stored with one device-scope store; the
+// consumer polls the words themselves until each carries this launch's epoch.
+// A hand-over therefore costs one store-to-load trip (about a microsecond
+// under full HBM load) instead of a store drain, a barrier round trip and a
+// separate load. Every workgroup keeps its own copy of the residual row in
+// LDS and applies the same bf16 adds to it, so the residual never travels.
+// The eight XCD L2 caches are not coherent with each other: the words are
+// stored and loaded with device scope (past the L2), and each location is
+// written once per launch (one arena region per layer), so an old epoch can
+// never be mistaken for a new one. Each workgroup advances its own epoch
+// counter at entry, so all workgroups of a launch agree on it without
+// talking. Every wait is bounded: a workgroup that polls past the limit sets
+// the error word and leaves, and every other workgroup leaves at its next
+// wait.
 //
-// Data between workgroups. The eight XCD L2 caches are not coherent with each
-// other. Every activation a phase hands to the next lives in a per-layer
-// buffer of an arena that each launch writes exactly once per element, with
-// device-scope stores (write-through past the L2), and is read with
-// device-scope loads. A workgroup's stores are complete (s_waitcnt) before it
-// arrives at the barrier; the barrier is a counter per XCD group plus a top
-// counter and a generation word (each on its own 256-byte line), reset by its
-// last arrivers, so it needs no clearing between launches. Every wait is
-// bounded: a workgroup that spins past the limit sets the error word and
-// leaves, and so does every other workgroup at its next wait.
+// Weights never depend on activations: before each wait a workgroup's waves
+// load the first weight chunks of the coming phase into a register ring, and
+// the workgroups without attention work copy their o_proj rows into LDS while
+// attention runs, so the HBM stream keeps going across the hand-overs.
+//
+// Projections: a phase's output rows (gate/up row pairs for SwiGLU) are split
+// evenly over the workgroups in pairs (so that every output word is produced
+// by one workgroup); a workgroup's (row, 1 KiB chunk) items are split evenly
+// over its 8 waves. Lanes stream 16 B of a chunk (a wave reads 1 KiB per load
+// instruction); fp32 FMA accumulation (bf16 products are exact), a butterfly
+// per row segment, and a fixed-order sum of the waves' partials in LDS.
 //
 // Rounding points are the reference fallback's (engine/ek_model.py:360-416,
 // 475-493): bf16 residual adds, fp32 norm statistics rounded to bf16 before
@@ -49,13 +51,23 @@ constexpr int SNW = SNT / EK_WAVE;     // 8 waves
 constexpr int NB = 8;                  // weight chunks in flight per wave
 constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
 constexpr int LW_FIELDS = 10;          // per-layer pointer table row
-constexpr int STU = 2;                 // attention: 16-key score tiles in flight per wave
-constexpr int SPT = 1;                 // attention: 32-key PV tiles in flight per wave
+constexpr int ATU = 6;                 // attention: 16-key score tiles per wave held in registers
+constexpr int APT = 3;                 // attention: 32-key PV tiles per wave held in registers
+constexpr int LLW = 10;                // hand-over words in flight per thread
+constexpr int NGW = 4;                 // norm gain words per thread (hidden <= 2 * NGW * SNT)
+constexpr int MAX_WG = 1024;
+
+typedef unsigned long long llw_t;
 
 // per-layer pointer table: [n_layers][LW_FIELDS] device addresses
 enum { LW_QKV = 0, LW_O, LW_GU, LW_DOWN, LW_LN1, LW_LN2, LW_QN, LW_KN, LW_KC, LW_VC };
 
-struct Bar { unsigned sub[8][64]; unsigned top[64]; unsigned gen[64]; };
+// launch state, zeroed once by the host
+struct Bar {
+  unsigned ep[MAX_WG];   // per-workgroup launch epoch
+  int64_t* trace;        // -DEK_STEP_TRACE builds: per-phase timestamps [wg][layer][24]
+  int64_t pad[7];
+};
 
 struct StepArgs {
   const int64_t* lw;
@@ -67,8 +79,7 @@ struct StepArgs {
   int64_t csb, csh, css, s_cap;
   int64_t* tokens; int64_t* positions; int64_t* len_t; int64_t* slot_t; const int32_t* start_t;
   int32_t* out_buf; int64_t* step_idx; int64_t max_steps; int64_t* out_tok;
-  bf16_t* arena;
-  float* am_val; int32_t* am_idx;
+  llw_t* arena;
   Bar* bar; int* err; int64_t spin;
   int kpad_max, part_max, o_rows;      // LDS plan (host-computed, see make_plan in ek_step.hip)
 };
@@ -76,89 +87,89 @@ struct StepArgs {
 __host__ __device__ constexpr int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int kpad_of(int k) { return cdiv_i(k, CH) * CH; }
 
-// largest unit count of one workgroup over the step's projections, times the
-// rows per unit (2 for the gate/up pairs)
-__host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int vocab, int nwg) {
-  int r = cdiv_i(qkvw, nwg);
-  r = r > cdiv_i(h, nwg) ? r : cdiv_i(h, nwg);
-  r = r > 2 * cdiv_i(inter, nwg) ? r : 2 * cdiv_i(inter, nwg);
+// words per layer of the hand-over arena: qkv, attention out, o out, act, down out
+__host__ __device__ inline int64_t arena_layer_words(int h, int inter, int qkvw, int qw) {
+  return (int64_t)(qkvw + qw + h + inter + h) / 2;
+}
+// the whole arena: every layer, then two argmax words per workgroup
+__host__ __device__ inline int64_t arena_words(int nl, int h, int inter, int qkvw, int qw, int nwg) {
+  return nl * arena_layer_words(h, inter, qkvw, qw) + 2 * (int64_t)nwg;
+}
+
+// rows of one workgroup's largest phase share (units in pairs, or single
+// rows for lm_head), times two for the gate/up phase
+__host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int vocab, int nwg, int o_rows) {
+  int r = 2 * cdiv_i(qkvw / 2, nwg);
+  r = r > 2 * cdiv_i(h / 2, nwg) ? r : 2 * cdiv_i(h / 2, nwg);
+  r = r > 4 * cdiv_i(inter / 2, nwg) ? r : 4 * cdiv_i(inter / 2, nwg);
   r = r > cdiv_i(vocab, nwg) ? r : cdiv_i(vocab, nwg);
+  r = r > o_rows ? r : o_rows;
   return r;
 }
 
-// elements per layer of the activation arena at batch bm
-__host__ __device__ inline int64_t arena_layer_elems(int bm, int h, int inter, int qkvw, int qw) {
-  return (int64_t)bm * (4 * h + qkvw + qw + inter);
-}
+#ifdef EK_STEP_TRACE
+#define EK_TS(ev) do { if (threadIdx.x == 0 && trace) trace[((int64_t)blockIdx.x * 40 + (tl)) * 24 + (ev)] = wall_clock64(); } while (0)
+#else
+#define EK_TS(ev) do { } while (0)
+#endif
 
 // ---------------------------------------------------------------------------
-// device-scope (cross-XCD) loads and stores
+// hand-over words
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint4 ld16_dev(const bf16_t* p) {
-  const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-  const uint64_t x = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint64_t y = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_uint4((uint32_t)x, (uint32_t)(x >> 32), (uint32_t)y, (uint32_t)(y >> 32));
+__device__ __forceinline__ void ll_put(llw_t* p, uint32_t data, uint32_t ep) {
+  __hip_atomic_store(p, ((llw_t)ep << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void st16_dev(bf16_t* p, uint4 v) {
-  uint64_t* q = reinterpret_cast<uint64_t*>(p);
-  __hip_atomic_store(q, (uint64_t)v.x | ((uint64_t)v.y << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(q + 1, (uint64_t)v.z | ((uint64_t)v.w << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ llw_t ll_get(const llw_t* p) {
+  return __hip_atomic_load(const_cast<llw_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void st_bf16_dev(bf16_t* p, float v) {
-  __hip_atomic_store(p, (bf16_t)f2bf(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+__device__ __forceinline__ bool ll_ok(llw_t v, uint32_t ep) { return (uint32_t)(v >> 32) == ep; }
 
-// ---------------------------------------------------------------------------
-// grid barrier (all workgroups co-resident: one per CU). Every thread calls
-// drain() first, so that its stores are performed before thread 0 arrives.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void drain() {
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);
-  __asm__ volatile("" ::: "memory");
-}
-
-__device__ __forceinline__ bool grid_sync(Bar* b, unsigned& gen, int* err, int64_t spin, bool wait, int* s_ok) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned nb = gridDim.x;
-    const unsigned grp = blockIdx.x & 7u;
-    const unsigned gsize = (nb - grp + 7u) / 8u;
-    const unsigned ngrp = nb < 8u ? nb : 8u;
-    const unsigned target = gen + 1u;
-    const unsigned a = __hip_atomic_fetch_add(&b->sub[grp][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (a == gsize - 1u) {
-      __hip_atomic_store(&b->sub[grp][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_s_waitcnt(0);
-      const unsigned t = __hip_atomic_fetch_add(&b->top[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t == ngrp - 1u) {
-        __hip_atomic_store(&b->top[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        __hip_atomic_store(&b->gen[0], target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Wait until the n words src(i), i < n, carry epoch ep and store their data
+// halves in dst[i] (LDS). Thread t handles i = t + k * SNT; up to LLW words
+// per thread are in flight at once, and only the words not yet valid are
+// loaded again. False (the error word set) when a wait runs out.
+template <int W = LLW, typename SRC>
+__device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* dst, int* err, int64_t spin) {
+  const int tid = threadIdx.x;
+  for (int base = 0; base < n; base += W * SNT) {
+    llw_t v[W];
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int i = base + tid + k * SNT;
+      v[k] = i < n ? ll_get(src(i)) : ((llw_t)ep << 32);
+    }
+    int64_t it = 0;
+    while (true) {
+      bool done = true;
+#pragma unroll
+      for (int k = 0; k < W; ++k) done = done && ll_ok(v[k], ep);
+      if (done) break;
+      if (++it > spin) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
+      if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int i = base + tid + k * SNT;
+        if (!ll_ok(v[k], ep)) v[k] = ll_get(src(i));
       }
     }
-    int ok = 1;
-    if (wait) {
-      int64_t it = 0;
-      while ((int)(__hip_atomic_load(&b->gen[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-        if ((++it & 1023) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) { ok = 0; break; }
-        if (it > spin) {
-          __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int i = base + tid + k * SNT;
+      if (i < n) dst[i] = (uint32_t)v[k];
     }
-    gen = target;
-    *s_ok = ok;
   }
-  __syncthreads();
-  return *s_ok != 0;
+  return true;
 }
+
+struct LinSrc {   // words [0, n) of one region
+  const llw_t* p;
+  __device__ const llw_t* operator()(int i) const { return p + i; }
+};
 
 // ---------------------------------------------------------------------------
 // projections
@@ -169,12 +180,13 @@ struct Gp {
   int units;         // output units
   int pair;          // 1: unit u is rows u and up_off + u (gate/up)
   int up_off;
+  int gran;          // units per workgroup share come in multiples of gran
   int wg0, nwg;      // the units are spread over workgroups [wg0, wg0 + nwg)
 };
 
-__device__ __forceinline__ Gp make_gp(const bf16_t* w, int k, int units, int pair) {
+__device__ __forceinline__ Gp make_gp(const bf16_t* w, int k, int units, int pair, int gran) {
   Gp g;
-  g.w = w; g.K = k; g.C = cdiv_i(k, CH); g.units = units; g.pair = pair; g.up_off = units;
+  g.w = w; g.K = k; g.C = cdiv_i(k, CH); g.units = units; g.pair = pair; g.up_off = units; g.gran = gran;
   g.wg0 = 0; g.nwg = gridDim.x;
   return g;
 }
@@ -183,8 +195,9 @@ __device__ __forceinline__ Gp make_gp(const bf16_t* w, int k, int units, int pai
 __device__ __forceinline__ void unit_range(const Gp& g, int& u0, int& u1) {
   const int w = (int)blockIdx.x - g.wg0;
   if (w < 0 || w >= g.nwg) { u0 = u1 = 0; return; }
-  u0 = (int)((int64_t)g.units * w / g.nwg);
-  u1 = (int)((int64_t)g.units * (w + 1) / g.nwg);
+  const int64_t n = g.units / g.gran;
+  u0 = g.gran * (int)(n * w / g.nwg);
+  u1 = g.gran * (int)(n * (w + 1) / g.nwg);
 }
 
 struct WaveItems { int i0, n; };
@@ -234,28 +247,38 @@ struct Ring {
 };
 
 // The first NB items of phase `pn` into this wave's ring, issued ahead of a
-// barrier so that they load while the workgroup waits. Wave 0 runs the
-// barrier's atomics, whose results would wait behind these loads (vector
-// memory counts drain in order), so it loads its items after the barrier.
-__device__ __forceinline__ void prefetch_phase(const Gp* pn, Ring& ring) {
-  ring.ready = false;
-  const int wave = wave_id();
-  if (!pn || wave == 0) return;
-  const Span sn = make_span(*pn, wave);
+// wait so that they load while the workgroup waits for its inputs.
+__device__ __forceinline__ void prefetch_phase(const Gp& pn, Ring& ring) {
+  const Span sn = make_span(pn, wave_id());
   const int loff = (threadIdx.x & 63) * 8;
 #pragma unroll
   for (int u = 0; u < NB; ++u) ring.r[u] = ld16(span_item(sn, sn.i0 + (u < sn.n ? u : 0)) + loff);
   ring.ready = true;
 }
 
+// Bring items [NB, NB + L2T) of this wave's share of phase `pn` into the L2
+// (one 4-byte load per 64-byte sector), so that the phase later reads them
+// from L2 instead of HBM. The loaded words are folded into `sink`, which the
+// caller consumes where it waits anyway.
+constexpr int L2T = 12;
+__device__ __forceinline__ void l2_touch(const Gp& pn, uint32_t& sink) {
+  const Span sn = make_span(pn, wave_id());
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < L2T / 4; ++j) {
+    const int i = NB + 4 * j + (lane >> 4);
+    if (i < sn.n) sink ^= *reinterpret_cast<const uint32_t*>(span_item(sn, sn.i0 + i) + (lane & 15) * 32);
+  }
+}
+
 // One projection phase: partial dot products of this wave's items into
-// part[(row_local * SNW + wave) * BM + b]. Items go in blocks of NB: the
-// loads of block i + 1 are issued (all NB at once) before block i is
-// consumed, so NB to 2 NB chunks are always in flight. The ring holds block 0
-// on entry when prefetch_phase loaded it. Loads past the end re-read item 0
-// (never consumed).
-template <int BM>
-__device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t* xs, int kpad, float* part) {
+// part[row_local * SNW + wave]. The ring is consumed in order and each slot
+// is refilled, right after its chunk is consumed, with the item NB places
+// ahead, so NB chunks stay in flight and a refill never waits for anything
+// but its own slot's previous load. The ring holds items 0 .. NB-1 on entry
+// when prefetch_phase loaded them. Loads past the end re-read item 0 (never
+// consumed).
+__device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t* xs, float* part) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const Span sp = make_span(P, wave);
   const int n = sp.n;
@@ -264,38 +287,38 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
 #pragma unroll
     for (int u = 0; u < NB; ++u) ring.r[u] = ld16(span_item(sp, sp.i0 + (u < n ? u : 0)) + loff);
   }
-  const int nblk = (n + NB - 1) / NB;
   int r = sp.i0 / P.C, ch = sp.i0 - (sp.i0 / P.C) * P.C;   // consume position (row-local, chunk)
-
-  float acc[BM];
-#pragma unroll
-  for (int b = 0; b < BM; ++b) acc[b] = 0.f;
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int nb0 = (blk + 1) * NB;   // first item of the next block
-    uint4 nx[NB];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) nx[u] = ld16(span_item(sp, sp.i0 + (nb0 + u < n ? nb0 + u : 0)) + loff);
+  float acc = 0.f;
+  int k0 = 0;
+  for (; k0 + NB <= n; k0 += NB) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-      const int k = blk * NB + u;
-      if (k < n) {
-        const uint4 wv = ring.r[u];
-#pragma unroll
-        for (int b = 0; b < BM; ++b)
-          acc[b] = dot8_acc(wv, *reinterpret_cast<const uint4*>(xs + b * kpad + ch * CH + loff), acc[b]);
-        if (ch == P.C - 1 || k == n - 1) {
-#pragma unroll
-          for (int b = 0; b < BM; ++b) {
-            const float sum = wave_sum(acc[b]);
-            if (lane == 0) part[(r * SNW + wave) * BM + b] = sum;
-            acc[b] = 0.f;
-          }
-        }
-        if (++ch == P.C) { ch = 0; ++r; }
+      acc = dot8_acc(ring.r[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+      const int kn = k0 + u + NB;
+      ring.r[u] = ld16(span_item(sp, sp.i0 + (kn < n ? kn : 0)) + loff);
+      if (ch == P.C - 1) {
+        const float sum = wave_sum_dpp(acc);
+        if (lane == 0) part[r * SNW + wave] = sum;
+        acc = 0.f;
       }
+      if (++ch == P.C) { ch = 0; ++r; }
     }
+  }
 #pragma unroll
-    for (int u = 0; u < NB; ++u) ring.r[u] = nx[u];
+  for (int u = 0; u < NB; ++u) {
+    if (k0 + u < n) {
+      acc = dot8_acc(ring.r[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+      if (ch == P.C - 1 || k0 + u == n - 1) {
+        const float sum = wave_sum_dpp(acc);
+        if (lane == 0) part[r * SNW + wave] = sum;
+        acc = 0.f;
+      }
+      if (++ch == P.C) { ch = 0; ++r; }
+    }
+  }
+  if (k0 == n && n > 0 && ch != 0) {   // the wave's items ended inside a row at a block edge
+    const float sum = wave_sum_dpp(acc);
+    if (lane == 0) part[r * SNW + wave] = sum;
   }
   ring.ready = false;
 }
@@ -323,70 +346,75 @@ __device__ __forceinline__ void stage_rows_lds(const Gp& P, bf16_t* wl) {
 }
 
 // A plain projection phase whose rows stage_rows_lds put in LDS: same item
-// split and partials as gemv_phase, weights read from LDS.
-template <int BM>
-__device__ __forceinline__ void gemv_lds_phase(const Gp& P, const bf16_t* wl, const bf16_t* xs, int kpad, float* part) {
+// split and partials as gemv_phase, weights read from LDS, LB items' reads
+// issued before any is consumed.
+constexpr int LB = 4;
+__device__ __forceinline__ void gemv_lds_phase(const Gp& P, const bf16_t* wl, const bf16_t* xs, float* part) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   int u0, u1;
   unit_range(P, u0, u1);
   const WaveItems wr = wave_items(P, u1 - u0, wave);
   const int loff = lane * 8;
   int r = wr.i0 / P.C, ch = wr.i0 - (wr.i0 / P.C) * P.C;
-  float acc[BM];
+  float acc = 0.f;
+  for (int k0 = 0; k0 < wr.n; k0 += LB) {
+    uint4 wv[LB], xv[LB];
+    int rl = r, cl = ch;
 #pragma unroll
-  for (int b = 0; b < BM; ++b) acc[b] = 0.f;
-#pragma unroll 4
-  for (int k = 0; k < wr.n; ++k) {
-    const uint4 wv = *reinterpret_cast<const uint4*>(wl + (int64_t)r * P.K + ch * CH + loff);
+    for (int u = 0; u < LB; ++u) {
+      if (k0 + u < wr.n) {
+        wv[u] = *reinterpret_cast<const uint4*>(wl + (int64_t)rl * P.K + cl * CH + loff);
+        xv[u] = *reinterpret_cast<const uint4*>(xs + cl * CH + loff);
+      }
+      if (++cl == P.C) { cl = 0; ++rl; }
+    }
 #pragma unroll
-    for (int b = 0; b < BM; ++b)
-      acc[b] = dot8_acc(wv, *reinterpret_cast<const uint4*>(xs + b * kpad + ch * CH + loff), acc[b]);
-    if (ch == P.C - 1 || k == wr.n - 1) {
-#pragma unroll
-      for (int b = 0; b < BM; ++b) {
-        const float sum = wave_sum(acc[b]);
-        if (lane == 0) part[(r * SNW + wave) * BM + b] = sum;
-        acc[b] = 0.f;
+    for (int u = 0; u < LB; ++u) {
+      const int k = k0 + u;
+      if (k < wr.n) {
+        acc = dot8_acc(wv[u], xv[u], acc);
+        if (ch == P.C - 1 || k == wr.n - 1) {
+          const float sum = wave_sum_dpp(acc);
+          if (lane == 0) part[r * SNW + wave] = sum;
+          acc = 0.f;
+        }
+        if (++ch == P.C) { ch = 0; ++r; }
       }
     }
-    if (++ch == P.C) { ch = 0; ++r; }
   }
 }
 
 // sum of the waves' partials of row_local r, fixed order
-template <int BM>
-__device__ __forceinline__ float row_sum(const float* part, int r, int b) {
+__device__ __forceinline__ float row_sum(const float* part, int r) {
   float s = 0.f;
 #pragma unroll
-  for (int w = 0; w < SNW; ++w) s += part[(r * SNW + w) * BM + b];
+  for (int w = 0; w < SNW; ++w) s += part[r * SNW + w];
   return s;
 }
 
-// y = bf16(sum) for this workgroup's units
-template <int BM>
-__device__ __forceinline__ void epilogue_bf16(const Gp& P, const float* part, bf16_t* out, int ldo) {
+// out word (u0 + 2i) / 2 = {bf16(row u0 + 2i), bf16(row u0 + 2i + 1)} for this workgroup's rows
+__device__ __forceinline__ void epilogue_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0;
-  for (int i = threadIdx.x; i < nu * BM; i += SNT) {
-    const int ul = i / BM, b = i - ul * BM;
-    st_bf16_dev(out + (int64_t)b * ldo + u0 + ul, row_sum<BM>(part, ul, b));
-  }
+  const int np = (u1 - u0) / 2;
+  for (int i = threadIdx.x; i < np; i += SNT)
+    ll_put(out + u0 / 2 + i, pack2(row_sum(part, 2 * i), row_sum(part, 2 * i + 1)), ep);
 }
 
 // act = bf16(bf16(silu(bf16 g)) * bf16 u)   (ek_kernels.py:1247-1261, :1062-1076)
-template <int BM>
-__device__ __forceinline__ void epilogue_swiglu(const Gp& P, const float* part, bf16_t* out, int ldo) {
+__device__ __forceinline__ float swiglu_one(const float* part, int nu, int ul) {
+  const float gt = rbf(row_sum(part, ul));
+  const float up = rbf(row_sum(part, nu + ul));
+  const float s = rbf(gt / (1.0f + expf(-gt)));
+  return s * up;
+}
+
+__device__ __forceinline__ void epilogue_swiglu_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0;
-  for (int i = threadIdx.x; i < nu * BM; i += SNT) {
-    const int ul = i / BM, b = i - ul * BM;
-    const float gt = rbf(row_sum<BM>(part, ul, b));
-    const float up = rbf(row_sum<BM>(part, nu + ul, b));
-    const float s = rbf(gt / (1.0f + expf(-gt)));
-    st_bf16_dev(out + (int64_t)b * ldo + u0 + ul, s * up);
-  }
+  const int nu = u1 - u0, np = nu / 2;
+  for (int i = threadIdx.x; i < np; i += SNT)
+    ll_put(out + u0 / 2 + i, pack2(swiglu_one(part, nu, 2 * i), swiglu_one(part, nu, 2 * i + 1)), ep);
 }
 
 // (a better, b) under "larger value, then lower index"; index 0x7fffffff = none
@@ -394,371 +422,431 @@ __device__ __forceinline__ bool am_better(float v, int i, float cv, int ci) {
   return i != 0x7fffffff && (ci == 0x7fffffff || v > cv || (v == cv && i < ci));
 }
 
-// this workgroup's first-index argmax of the bf16 logits -> am_val/am_idx[wg * BM + b]
-template <int BM>
-__device__ __forceinline__ void epilogue_argmax(const Gp& P, const float* part, float* sv, int* si, float* am_val, int32_t* am_idx) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+// this workgroup's first-index argmax of the bf16 logits -> two words at am
+__device__ __forceinline__ void wg_argmax(float bv, int bi, float* sv, int* si, float& ov, int& oi) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(bv, o, EK_WAVE);
+    const int i = __shfl_xor(bi, o, EK_WAVE);
+    if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+  if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+  __syncthreads();
+  ov = sv[0]; oi = si[0];
+  for (int w = 1; w < SNW; ++w)
+    if (am_better(sv[w], si[w], ov, oi)) { ov = sv[w]; oi = si[w]; }
+}
+
+__device__ __forceinline__ void epilogue_argmax_ll(const Gp& P, const float* part, float* sv, int* si, llw_t* am,
+                                                   uint32_t ep) {
   int u0, u1;
   unit_range(P, u0, u1);
   const int nu = u1 - u0;
-  float bv[BM];
-  int bi[BM];
-#pragma unroll
-  for (int b = 0; b < BM; ++b) { bv[b] = -INFINITY; bi[b] = 0x7fffffff; }
-  for (int ul = tid; ul < nu; ul += SNT) {
-#pragma unroll
-    for (int b = 0; b < BM; ++b) {
-      const float v = rbf(row_sum<BM>(part, ul, b));
-      if (am_better(v, u0 + ul, bv[b], bi[b])) { bv[b] = v; bi[b] = u0 + ul; }
-    }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int ul = threadIdx.x; ul < nu; ul += SNT) {
+    const float v = rbf(row_sum(part, ul));
+    if (am_better(v, u0 + ul, bv, bi)) { bv = v; bi = u0 + ul; }
   }
-#pragma unroll
-  for (int b = 0; b < BM; ++b) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float v = __shfl_xor(bv[b], o, EK_WAVE);
-      const int i = __shfl_xor(bi[b], o, EK_WAVE);
-      if (am_better(v, i, bv[b], bi[b])) { bv[b] = v; bi[b] = i; }
-    }
-    if (lane == 0) { sv[wave * BM + b] = bv[b]; si[wave * BM + b] = bi[b]; }
-  }
-  __syncthreads();
-  if (tid < BM) {
-    float v = sv[tid];
-    int i = si[tid];
-    for (int w = 1; w < SNW; ++w)
-      if (am_better(sv[w * BM + tid], si[w * BM + tid], v, i)) { v = sv[w * BM + tid]; i = si[w * BM + tid]; }
-    __hip_atomic_store(am_val + blockIdx.x * BM + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(am_idx + blockIdx.x * BM + tid, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  float ov;
+  int oi;
+  wg_argmax(bv, bi, sv, si, ov, oi);
+  if (threadIdx.x == 0) {
+    ll_put(am + 2 * blockIdx.x, __float_as_uint(ov), ep);
+    ll_put(am + 2 * blockIdx.x + 1, (uint32_t)oi, ep);
   }
 }
 
 // ---------------------------------------------------------------------------
-// prologues: the phase's activation rows -> xs [BM][kpad] (bf16, zero-padded)
+// prologues
 // ---------------------------------------------------------------------------
-template <int BM>
 __device__ __forceinline__ void zero_part(float* part, int n) {
   for (int i = threadIdx.x; i < n; i += SNT) part[i] = 0.f;
 }
 
-template <int BM>
 __device__ __forceinline__ void zero_pad(bf16_t* xs, int k, int kpad) {
-  for (int i = threadIdx.x; i < BM * (kpad - k); i += SNT) {
-    const int b = i / (kpad - k), e = i - b * (kpad - k);
-    xs[b * kpad + k + e] = 0;
+  for (int i = k + threadIdx.x; i < kpad; i += SNT) xs[i] = 0;
+}
+
+// the norm gain's words of this thread (i = tid + j * SNT), loaded ahead of a wait
+__device__ __forceinline__ void load_gain(const bf16_t* nw, int k, uint32_t* gw) {
+  const uint32_t* g32 = reinterpret_cast<const uint32_t*>(nw);
+#pragma unroll
+  for (int j = 0; j < NGW; ++j) {
+    const int i = threadIdx.x + j * SNT;
+    gw[j] = i < k / 2 ? g32[i] : 0u;
   }
 }
 
-// x as given (device-scope loads of another phase's output)
-template <int BM>
-__device__ __forceinline__ void plain_prologue(const bf16_t* src, int k, int kpad, bf16_t* xs) {
-  const int nch = k / 8;
-  for (int i = threadIdx.x; i < BM * nch; i += SNT) {
-    const int b = i / nch, c = i - b * nch;
-    *reinterpret_cast<uint4*>(xs + b * kpad + c * 8) = ld16_dev(src + (int64_t)b * k + c * 8);
-  }
-  zero_pad<BM>(xs, k, kpad);
-}
-
-// r = embed[token] (ra == nullptr) or bf16(ra + rb); r -> r_out (writer);
-// xs = bf16(w * bf16(r * rsqrt(mean(r^2) + eps)))     (ek_kernels.py:1025-1059, 1296-1304)
-template <int BM>
-__device__ __forceinline__ void norm_prologue(const StepArgs& a, const bf16_t* ra, const bf16_t* rb, const bf16_t* nw,
-                                              int k, int kpad, bf16_t* xs, bf16_t* r_out, float* red) {
-  constexpr int NCH = 2;   // chunks of 8 per thread: k <= 2 * 8 * SNT (checked by the plan)
+// rr = bf16(rr + x) over the words this thread owns (x pairs in xw, or no
+// add when xw is null); xs = bf16(w * bf16(rr * rsqrt(mean(rr^2) + eps)))
+// (ek_kernels.py:1025-1059, 1296-1304)
+__device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const uint32_t* gw, int k, int kpad,
+                                         float eps, bf16_t* xs, float* red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int nch = k / 8;
-  // the gain's chunks load with the activations (one memory round trip)
-  uint4 gw[NCH];
+  const int nw = k / 2;
+  float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c = tid + j * SNT;
-    gw[j] = c < nch ? ld16(nw + c * 8) : make_uint4(0, 0, 0, 0);
-  }
-  float ss[BM];
-#pragma unroll
-  for (int b = 0; b < BM; ++b) ss[b] = 0.f;
-#pragma unroll
-  for (int b = 0; b < BM; ++b) {
-    const bf16_t* erow = nullptr;
-    if (!ra) {
-      int64_t t = a.tokens[b];
-      t = t < 0 ? 0 : (t >= a.vocab ? a.vocab - 1 : t);
-      erow = a.embed + t * a.lde;
+  for (int j = 0; j < NGW; ++j) {
+    const int i = tid + j * SNT;
+    if (i >= nw) continue;
+    float r0 = rr[2 * i], r1 = rr[2 * i + 1];
+    if (xw) {
+      const uint32_t x = xw[i];
+      r0 = rbf(r0 + lo_bf(x));
+      r1 = rbf(r1 + hi_bf(x));
+      rr[2 * i] = r0;
+      rr[2 * i + 1] = r1;
     }
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = tid + j * SNT;
-      if (c >= nch) continue;
-      float r[8];
-      if (!ra) {
-        unpack8(ld16(erow + c * 8), r);
-      } else {
-        float x0[8], x1[8];
-        unpack8(ld16_dev(ra + (int64_t)b * k + c * 8), x0);
-        unpack8(ld16_dev(rb + (int64_t)b * k + c * 8), x1);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) r[q] = rbf(x0[q] + x1[q]);
-      }
-      const uint4 pk = make_uint4(pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7]));
-      *reinterpret_cast<uint4*>(xs + b * kpad + c * 8) = pk;
-      if (r_out) st16_dev(r_out + (int64_t)b * k + c * 8, pk);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) ss[b] = fmaf(r[q], r[q], ss[b]);
-    }
+    ss = fmaf(r0, r0, ss);
+    ss = fmaf(r1, r1, ss);
   }
-#pragma unroll
-  for (int b = 0; b < BM; ++b) {
-    const float v = wave_sum(ss[b]);
-    if (lane == 0) red[wave * BM + b] = v;
-  }
+  ss = wave_sum_dpp(ss);
+  if (lane == 0) red[wave] = ss;
   __syncthreads();
-  float rstd[BM];
+  float t = 0.f;
 #pragma unroll
-  for (int b = 0; b < BM; ++b) {
-    float t = 0.f;
+  for (int w = 0; w < SNW; ++w) t += red[w];
+  const float rstd = 1.0f / sqrtf(t / (float)k + eps);
+  uint32_t* xs32 = reinterpret_cast<uint32_t*>(xs);
 #pragma unroll
-    for (int w = 0; w < SNW; ++w) t += red[w * BM + b];
-    rstd[b] = 1.0f / sqrtf(t / (float)k + a.eps);
+  for (int j = 0; j < NGW; ++j) {
+    const int i = tid + j * SNT;
+    if (i >= nw) continue;
+    const float o0 = rbf(lo_bf(gw[j]) * rbf(rr[2 * i] * rstd));
+    const float o1 = rbf(hi_bf(gw[j]) * rbf(rr[2 * i + 1] * rstd));
+    xs32[i] = pack2(o0, o1);
   }
-#pragma unroll
-  for (int b = 0; b < BM; ++b) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = tid + j * SNT;
-      if (c >= nch) continue;
-      uint4* dst = reinterpret_cast<uint4*>(xs + b * kpad + c * 8);
-      float r[8], g[8], o[8];
-      unpack8(*dst, r);
-      unpack8(gw[j], g);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = rbf(g[q] * rbf(r[q] * rstd[b]));
-      *dst = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
-    }
-  }
-  zero_pad<BM>(xs, k, kpad);
+  zero_pad(xs, k, kpad);
 }
 
 // ---------------------------------------------------------------------------
-// attention phase: workgroup w < B * n_kv * D / 32 runs unit w
+// attention phase: workgroup w < n_kv * D / 32 runs unit w
 // ---------------------------------------------------------------------------
-template <int BM, int D, int G>
-__device__ __forceinline__ void attention_phase(const StepArgs& a, const int64_t* lw, const bf16_t* qkv, bf16_t* att, int64_t hi,
-                                unsigned char* smem) {
-  const int bhn = BM * a.nkv;
-  const int bh = blockIdx.x % bhn, c = blockIdx.x / bhn;
-  const int b = bh / a.nkv, h = bh - b * a.nkv;
-  const int qkvw = (a.nq + 2 * a.nkv) * D;
-  // this unit's q heads, new key and new value -> LDS
+template <int D, int G>
+__device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
+                                                int64_t hi, uint32_t ep, unsigned char* smem, int layer) {
+  (void)layer;
+  const int h = (int)blockIdx.x % a.nkv, c = (int)blockIdx.x / a.nkv;
+  // this unit's q heads, new key and new value -> LDS (bf16 pairs)
   bf16_t* qrow = reinterpret_cast<bf16_t*>(smem);
-  const bf16_t* src = qkv + (int64_t)b * qkvw;
-  for (int i = threadIdx.x; i < (G + 2) * D / 8; i += SNT) {
-    const int hh = i / (D / 8), c8 = i - hh * (D / 8);
-    const int64_t off = hh < G ? (int64_t)(h * G + hh) * D
-                               : (hh == G ? (int64_t)(a.nq + h) * D : (int64_t)(a.nq + a.nkv + h) * D);
-    *reinterpret_cast<uint4*>(qrow + hh * D + c8 * 8) = ld16_dev(src + off + c8 * 8);
-  }
-  __syncthreads();
+  const int hw = D / 2;   // words per head
+  const int qbase = h * G * hw, kbase = (a.nq + h) * hw, vbase = (a.nq + a.nkv + h) * hw;
+  struct Src {
+    const llw_t* p; int hw, g, qbase, kbase, vbase;
+    __device__ const llw_t* operator()(int i) const {
+      return p + (i < g * hw ? qbase + i : (i < (g + 1) * hw ? kbase + i - g * hw : vbase + i - (g + 1) * hw));
+    }
+  } src{qkv, hw, G, qbase, kbase, vbase};
+  // the q/k norm gains and this position's cos/sin rows, copied to LDS while
+  // the unit waits, so that the RoPE work after the wait reads only LDS
+  bf16_t* rope_lds = qrow + (G + 2) * D;   // [q gain | k gain | cos | sin] x D
+  const bf16_t* qn = reinterpret_cast<const bf16_t*>(lw[LW_QN]);
+  const bf16_t* kn = reinterpret_cast<const bf16_t*>(lw[LW_KN]);
+  int64_t crow = a.positions[0];
+  crow = crow < 0 ? 0 : (crow >= a.rope_len ? a.rope_len - 1 : crow);
+  const bf16_t* cr = a.cos + crow * a.ld_cs;
+  const bf16_t* sr = a.sin + crow * a.ld_cs;
   eka::AttnUnit u;
   u.qh = qrow; u.q_stride = D;
   u.kh = qrow + G * D; u.vh = qrow + (G + 1) * D;
   u.rope = 1;
-  u.qn = reinterpret_cast<const bf16_t*>(lw[LW_QN]);
-  u.kn = reinterpret_cast<const bf16_t*>(lw[LW_KN]);
-  int64_t crow = a.positions[b];
-  crow = crow < 0 ? 0 : (crow >= a.rope_len ? a.rope_len - 1 : crow);
-  u.cr = a.cos + crow * a.ld_cs;
-  u.sr = a.sin + crow * a.ld_cs;
+  u.qn = rope_lds;
+  u.kn = rope_lds + D;
+  u.cr = rope_lds + 2 * D;
+  u.sr = rope_lds + 3 * D;
   u.eps = a.eps; u.sm_scale = a.sm_scale;
-  u.kc = reinterpret_cast<bf16_t*>(lw[LW_KC]) + b * a.csb + h * a.csh;
-  u.vc = reinterpret_cast<bf16_t*>(lw[LW_VC]) + b * a.csb + h * a.csh;
+  u.kc = reinterpret_cast<bf16_t*>(lw[LW_KC]) + h * a.csh;
+  u.vc = reinterpret_cast<bf16_t*>(lw[LW_VC]) + h * a.csh;
   u.css = a.css;
   u.cap = a.s_cap;
-  int64_t lo = a.start_t[b];
+  int64_t lo = a.start_t[0];
   u.lo = lo < 0 ? 0 : lo;
   u.hi = hi;
   u.writer = c == 0;
   u.d0 = c * eka::FDC;
-  u.out = att + (int64_t)b * a.nq * D + (int64_t)h * G * D;
+  u.out = nullptr;
   u.out_stride = D;
-  u.coherent_out = true;
-  eka::attn_unit<D, G, STU, SPT>(u, smem + eka::align16((size_t)(G + 2) * D * 2));
+  u.ll_out = att + (int64_t)h * G * hw;
+  u.ll_ep = ep;
+#ifdef EK_STEP_TRACE
+  u.trace_row = a.bar->trace ? a.bar->trace + ((int64_t)blockIdx.x * 40 + layer) * 24 : nullptr;
+#endif
+  // the cached keys/values are already loading when the unit waits for its heads
+  auto wait_heads = [&]() -> bool {
+    for (int i = threadIdx.x; i < 4 * D; i += SNT) {
+      const int t = i / D, d = i - t * D;
+      rope_lds[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
+    }
+    const bool ok = ll_read<2>(src, (G + 2) * hw, ep, reinterpret_cast<uint32_t*>(qrow), a.err, a.spin);
+    return __syncthreads_and(ok) != 0;
+  };
+  return eka::attn_unit<D, G, ATU, APT>(u, smem + eka::align16((size_t)(G + 6) * D * 2), wait_heads);
 }
 
 // ---------------------------------------------------------------------------
 // the step
 // ---------------------------------------------------------------------------
-template <int BM, int D, int G>
+// the step
+// ---------------------------------------------------------------------------
+// Workgroups [0, n_attn) run only attention, one unit (kv head, 32 head dims)
+// each, layer after layer: they enter a layer's unit as soon as the previous
+// one is done, so its cached keys and values (up to ATU * 8 * 16 keys) load
+// into registers while the projections of the layer before run elsewhere,
+// and only QK-norm/RoPE, the two MFMA products and the softmax remain once
+// the layer's q/k/v arrive. The other workgroups run every projection and
+// the lm_head. The two roles share no state, so neither's registers are
+// live in the other's code.
+// LDS of a projection workgroup: [residual row, fp32 x h][activation row][wave partials][staged o_proj rows]
+__host__ __device__ inline size_t step_rr_bytes(int h) { return eka::align16((size_t)h * 4); }
+
+template <int D, int G>
+__device__ __forceinline__ void attention_loop(const StepArgs& a, uint32_t ep, int64_t hi, unsigned char* smem) {
+  const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
+  const int64_t lwords = arena_layer_words(a.h, a.inter, qkvw, qw);
+#ifdef EK_STEP_TRACE
+  int64_t* trace = a.bar->trace;
+#endif
+  for (int l = 0; l < a.nl; ++l) {
+    const int tl = l;
+    (void)tl;
+    const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
+    const llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
+    llw_t* att_ll = a.arena + (int64_t)l * lwords + qkvw / 2;
+    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, ep, smem, l)) return;
+    EK_TS(5);
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ Gp on_gemv_wgs(Gp g, int n_attn) {
+  g.wg0 = n_attn;
+  g.nwg = (int)gridDim.x - n_attn;
+  return g;
+}
+
+template <int D, int G>
 __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int s_ok;
-  __shared__ float s_red[SNW * BM];
-  __shared__ int s_redi[SNW * BM];
+  __shared__ float s_red[SNW];
+  __shared__ int s_redi[SNW];
+  __shared__ unsigned s_ep;
 
   const int tid = threadIdx.x;
-  unsigned gen = 0;
-  if (tid == 0) gen = __hip_atomic_load(&a.bar->gen[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    const unsigned e = __hip_atomic_load(&a.bar->ep[blockIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    __hip_atomic_store(&a.bar->ep[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ep = e;
+  }
+#ifdef EK_STEP_TRACE
+  int64_t* trace = a.bar->trace;
+#endif
+  __syncthreads();
+  const uint32_t ep = s_ep;
 
   const int h = a.h, inter = a.inter;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
-  const int64_t ls = arena_layer_elems(BM, h, inter, qkvw, qw);
+  const int64_t lwords = arena_layer_words(h, inter, qkvw, qw);
   const int64_t len_old = *a.len_t;
   int64_t hi = len_old + 1;
   hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
+  const int n_attn = a.nkv * (D / eka::FDC);   // attention units = workgroups [0, n_attn)
+  if ((int)blockIdx.x < n_attn) {
+    attention_loop<D, G>(a, ep, hi, smem);
+    return;
+  }
 
-  bf16_t* xs = reinterpret_cast<bf16_t*>(smem);
-  float* part = reinterpret_cast<float*>(smem + eka::align16((size_t)BM * a.kpad_max * 2));
-  const int part_n = a.part_max * SNW * BM;
-  bf16_t* wl = reinterpret_cast<bf16_t*>(smem + eka::align16((size_t)BM * a.kpad_max * 2) +
+  float* rr = reinterpret_cast<float*>(smem);
+  unsigned char* ph = smem + step_rr_bytes(h);
+  bf16_t* xs = reinterpret_cast<bf16_t*>(ph);
+  uint32_t* xs32 = reinterpret_cast<uint32_t*>(ph);
+  float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)a.kpad_max * 2));
+  const int part_n = a.part_max * SNW;
+  bf16_t* wl = reinterpret_cast<bf16_t*>(ph + eka::align16((size_t)a.kpad_max * 2) +
                                          eka::align16((size_t)part_n * 4));   // staged o_proj rows
 
   Ring ring;
   ring.ready = false;
 #pragma unroll
   for (int u = 0; u < NB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
+  uint32_t gw[NGW];
 
-  const bf16_t* prev_mid = nullptr;
-  const bf16_t* prev_dn = nullptr;
+  const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
+    const int tl = l;
+    (void)tl;
+    EK_TS(0);
     const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
-    bf16_t* base = a.arena + (int64_t)l * ls;
-    bf16_t* r_in = base;
-    bf16_t* r_mid = r_in + BM * h;
-    bf16_t* qkv = r_mid + BM * h;
-    bf16_t* att = qkv + BM * qkvw;
-    bf16_t* o = att + BM * qw;
-    bf16_t* act = o + BM * h;
-    bf16_t* dn = act + BM * inter;
-    const int n_attn = BM * a.nkv * (D / eka::FDC);   // attention units = workgroups [0, n_attn)
-    const Gp gq = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0);
-    Gp go = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0);
-    go.wg0 = n_attn;                                 // o_proj rows go to the other workgroups,
-    go.nwg = (int)gridDim.x - n_attn;                //   which stage them in LDS during attention
-    const Gp gg = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1);
-    const Gp gd = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_DOWN]), inter, h, 0);
-    Gp gnext;
-    if (l + 1 < a.nl) gnext = make_gp(reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw, 0);
-    else gnext = make_gp(a.lm_head, h, a.vocab, 0);
+    llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
+    llw_t* att_ll = qkv_ll + qkvw / 2;
+    llw_t* o_ll = att_ll + qw / 2;
+    llw_t* act_ll = o_ll + h / 2;
+    llw_t* dn_ll = act_ll + inter / 2;
+    const Gp gq = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 2), n_attn);
+    const Gp go = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 2), n_attn);
+    const Gp gg = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 2), n_attn);
+    const Gp gd = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_DOWN]), inter, h, 0, 2), n_attn);
 
-    // ---- r = (layer 0) embed[token] | r_mid(l-1) + down(l-1); norm; qkv
-    zero_part<BM>(part, part_n);
-    norm_prologue<BM>(a, prev_mid, prev_dn, reinterpret_cast<const bf16_t*>(lw[LW_LN1]), h, kpad_of(h), xs,
-                      blockIdx.x == 0 ? r_in : nullptr, s_red);
+    // ---- r = (layer 0) embed[token] | r + down(l-1); norm; qkv
+    zero_part(part, part_n);
+    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN1]), h, gw);
+    if (l == 0) {
+      int64_t t = a.tokens[0];
+      t = t < 0 ? 0 : (t >= a.vocab ? a.vocab - 1 : t);
+      const uint32_t* e32 = reinterpret_cast<const uint32_t*>(a.embed + t * a.lde);
+      for (int i = tid; i < h / 2; i += SNT) {
+        const uint32_t x = e32[i];
+        rr[2 * i] = lo_bf(x);
+        rr[2 * i + 1] = hi_bf(x);
+      }
+      add_norm(rr, nullptr, gw, h, kpad_of(h), a.eps, xs, s_red);
+    } else {
+      const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
+      if (!__syncthreads_and(ok)) return;
+      add_norm(rr, xs32, gw, h, kpad_of(h), a.eps, xs, s_red);
+    }
     __syncthreads();
-    gemv_phase<BM>(gq, ring, xs, kpad_of(h), part);
+    EK_TS(1);
+    gemv_phase(gq, ring, xs, part);
     __syncthreads();
-    epilogue_bf16<BM>(gq, part, qkv, qkvw);
-    const bool attn_wg = (int)blockIdx.x < n_attn;
-    drain();
-    if (!grid_sync(a.bar, gen, a.err, a.spin, true, &s_ok)) return;
+    EK_TS(2);
+    epilogue_ll(gq, part, qkv_ll, ep);
+    EK_TS(3);
+    __syncthreads();
 
-    // ---- attention (QK-norm, RoPE, KV write, softmax, PV) on workgroups
-    //      [0, n_attn); meanwhile the others copy their o_proj rows to LDS
-    if (attn_wg) attention_phase<BM, D, G>(a, lw, qkv, att, hi, smem);
-    else stage_rows_lds(go, wl);
-    drain();
-    if (!grid_sync(a.bar, gen, a.err, a.spin, true, &s_ok)) return;
-
+    // ---- while attention runs: this workgroup's o_proj rows into LDS, the
+    //      first gate/up chunks into the ring and the next ones into L2
+    stage_rows_lds(go, wl);
+    EK_TS(4);
+    prefetch_phase(gg, ring);
+    uint32_t sink = 0;
+    l2_touch(gg, sink);
     // ---- o projection (weights from LDS)
-    zero_part<BM>(part, part_n);
-    plain_prologue<BM>(att, qw, kpad_of(qw), xs);
+    zero_part(part, part_n);
+    {
+      const bool ok = ll_read(LinSrc{att_ll}, qw / 2, ep, xs32, a.err, a.spin);
+      if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
+      if (!__syncthreads_and(ok)) return;
+    }
+    zero_pad(xs, qw, kpad_of(qw));
+    EK_TS(6);
     __syncthreads();
-    gemv_lds_phase<BM>(go, wl, xs, kpad_of(qw), part);
+    gemv_lds_phase(go, wl, xs, part);
     __syncthreads();
-    epilogue_bf16<BM>(go, part, o, h);
-    drain();
-    prefetch_phase(&gg, ring);
-    if (!grid_sync(a.bar, gen, a.err, a.spin, true, &s_ok)) return;
+    EK_TS(7);
+    epilogue_ll(go, part, o_ll, ep);
+    EK_TS(8);
 
-    // ---- r' = r + o; norm; gate/up; SwiGLU
-    zero_part<BM>(part, part_n);
-    norm_prologue<BM>(a, r_in, o, reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, kpad_of(h), xs,
-                      blockIdx.x == 0 ? r_mid : nullptr, s_red);
+    // ---- r = r + o; norm; gate/up; SwiGLU
     __syncthreads();
-    gemv_phase<BM>(gg, ring, xs, kpad_of(h), part);
+    zero_part(part, part_n);
+    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw);
+    {
+      const bool ok = ll_read(LinSrc{o_ll}, h / 2, ep, xs32, a.err, a.spin);
+      if (!__syncthreads_and(ok)) return;
+    }
+    add_norm(rr, xs32, gw, h, kpad_of(h), a.eps, xs, s_red);
     __syncthreads();
-    epilogue_swiglu<BM>(gg, part, act, inter);
-    drain();
-    prefetch_phase(&gd, ring);
-    if (!grid_sync(a.bar, gen, a.err, a.spin, true, &s_ok)) return;
+    EK_TS(9);
+    gemv_phase(gg, ring, xs, part);
+    __syncthreads();
+    EK_TS(10);
+    epilogue_swiglu_ll(gg, part, act_ll, ep);
+    EK_TS(11);
+    prefetch_phase(gd, ring);
 
     // ---- down projection
-    zero_part<BM>(part, part_n);
-    plain_prologue<BM>(act, inter, kpad_of(inter), xs);
     __syncthreads();
-    gemv_phase<BM>(gd, ring, xs, kpad_of(inter), part);
+    zero_part(part, part_n);
+    {
+      const bool ok = ll_read(LinSrc{act_ll}, inter / 2, ep, xs32, a.err, a.spin);
+      if (!__syncthreads_and(ok)) return;
+    }
+    zero_pad(xs, inter, kpad_of(inter));
     __syncthreads();
-    epilogue_bf16<BM>(gd, part, dn, h);
-    drain();
-    prefetch_phase(&gnext, ring);
-    if (!grid_sync(a.bar, gen, a.err, a.spin, true, &s_ok)) return;
-    prev_mid = r_mid;
-    prev_dn = dn;
+    EK_TS(12);
+    gemv_phase(gd, ring, xs, part);
+    __syncthreads();
+    EK_TS(13);
+    epilogue_ll(gd, part, dn_ll, ep);
+    EK_TS(14);
+    if (l + 1 < a.nl)
+      prefetch_phase(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_QKV]),
+                                         h, qkvw, 0, 2), n_attn), ring);
+    else
+      prefetch_phase(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
+    dn_prev = dn_ll;
+    __syncthreads();
   }
 
   // ---- final add + norm, lm_head, per-workgroup argmax
-  zero_part<BM>(part, part_n);
-  norm_prologue<BM>(a, prev_mid, prev_dn, a.fnorm, h, kpad_of(h), xs, nullptr, s_red);
-  __syncthreads();
-  const Gp gl = make_gp(a.lm_head, h, a.vocab, 0);
-  gemv_phase<BM>(gl, ring, xs, kpad_of(h), part);
-  __syncthreads();
-  epilogue_argmax<BM>(gl, part, s_red, s_redi, a.am_val, a.am_idx);
-  drain();
-  // every workgroup arrives; only workgroup 0 waits and finishes the step
-  if (!grid_sync(a.bar, gen, a.err, a.spin, blockIdx.x == 0, &s_ok) || blockIdx.x != 0) return;
-
-  // ---- token = first-index argmax over the partials; step bookkeeping
-  //      (engine.py:289-292; slot/len advance of ek_model.py:375-388)
-  const int lane = tid & 63, wave = wave_id();
-#pragma unroll
-  for (int b = 0; b < BM; ++b) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int w = tid; w < (int)gridDim.x; w += SNT) {
-      const float v = __hip_atomic_load(a.am_val + w * BM + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int i = __hip_atomic_load(a.am_idx + w * BM + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float v = __shfl_xor(bv, o, EK_WAVE);
-      const int i = __shfl_xor(bi, o, EK_WAVE);
-      if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
-    }
-    if (lane == 0) { s_red[wave * BM + b] = bv; s_redi[wave * BM + b] = bi; }
+  const int tl = a.nl;
+  (void)tl;
+  EK_TS(0);
+  llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
+  zero_part(part, part_n);
+  load_gain(a.fnorm, h, gw);
+  {
+    const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
+    if (!__syncthreads_and(ok)) return;
   }
+  add_norm(rr, xs32, gw, h, kpad_of(h), a.eps, xs, s_red);
   __syncthreads();
+  EK_TS(1);
+  const Gp gl = on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn);
+  gemv_phase(gl, ring, xs, part);
+  __syncthreads();
+  EK_TS(2);
+  epilogue_argmax_ll(gl, part, s_red, s_redi, am_ll, ep);
+  EK_TS(3);
+  if ((int)blockIdx.x != n_attn) return;
+
+  // ---- token = first-index argmax over the projection workgroups'
+  //      partials; step bookkeeping (engine.py:289-292; slot/len advance of
+  //      ek_model.py:375-388)
+  __syncthreads();
+  uint32_t* amw = reinterpret_cast<uint32_t*>(part);
+  const int n_gemv = (int)gridDim.x - n_attn;
+  {
+    const bool ok = ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, ep, amw, a.err, a.spin);
+    if (!__syncthreads_and(ok)) return;
+  }
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int w = tid; w < n_gemv; w += SNT) {
+    const float v = __uint_as_float(amw[2 * w]);
+    const int i = (int)amw[2 * w + 1];
+    if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+  float ov;
+  int oi;
+  wg_argmax(bv, bi, s_red, s_redi, ov, oi);
+  EK_TS(4);
   if (tid == 0) {
     const int64_t step = *a.step_idx;
-    for (int b = 0; b < BM; ++b) {
-      float v = s_red[b];
-      int i = s_redi[b];
-      for (int w = 1; w < SNW; ++w)
-        if (am_better(s_red[w * BM + b], s_redi[w * BM + b], v, i)) { v = s_red[w * BM + b]; i = s_redi[w * BM + b]; }
-      const int64_t tok = i == 0x7fffffff ? 0 : i;
-      if (a.out_tok) a.out_tok[b] = tok;
-      a.tokens[b] = tok;
-      a.positions[b] += 1;
-      a.slot_t[b] = len_old;
-      if (step >= 0 && step < a.max_steps) a.out_buf[step * BM + b] = (int32_t)tok;
-    }
+    const int64_t tok = oi == 0x7fffffff ? 0 : oi;
+    if (a.out_tok) a.out_tok[0] = tok;
+    a.tokens[0] = tok;
+    a.positions[0] += 1;
+    a.slot_t[0] = len_old;
+    if (step >= 0 && step < a.max_steps) a.out_buf[step] = (int32_t)tok;
     *a.len_t = len_old + 1;
     *a.step_idx = step + 1;
   }
 }
 
-// LDS bytes of step_kernel<BM, D, G> (o_rows: the most o_proj rows of one workgroup, qw = n_q * D)
-template <int BM, int D, int G>
-inline size_t step_lds_bytes(int kpad_max, int part_max, int64_t s_cap, int o_rows, int qw) {
-  const size_t gemv = eka::align16((size_t)BM * kpad_max * 2) + eka::align16((size_t)part_max * SNW * BM * 4) +
-                      (size_t)o_rows * qw * 2;
-  const size_t attn = eka::align16((size_t)(G + 2) * D * 2) + eka::AttnLds<D, G>::bytes(s_cap);
+// LDS bytes of step_kernel<D, G> (o_rows: the most o_proj rows of one workgroup, qw = n_q * D)
+template <int D, int G>
+inline size_t step_lds_bytes(int h, int kpad_max, int part_max, int64_t s_cap, int o_rows, int qw) {
+  const size_t gemv = step_rr_bytes(h) + eka::align16((size_t)kpad_max * 2) +
+                      eka::align16((size_t)part_max * SNW * 4) + (size_t)o_rows * qw * 2;
+  const size_t attn = eka::align16((size_t)(G + 6) * D * 2) + eka::AttnLds<D, G>::bytes(s_cap);
   return gemv > attn ? gemv : attn;
 }
 
-// launch of one (BM, D) instantiation for any G (ek_step_inst.hip)
-template <int BM, int D>
+// launch of one head-dim instantiation for any G (ek_step_inst.hip)
+template <int D>
 hipError_t launch_step(const StepArgs& a, int g, int nwg, hipStream_t st);
 
 }  // namespace eks

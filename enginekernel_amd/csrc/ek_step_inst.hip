@@ -10,34 +10,29 @@
 
 namespace eks {
 
-template <int BM, int D, int G>
+template <int D, int G>
 static hipError_t launch_one(const StepArgs& a, int nwg, hipStream_t st) {
-  const size_t lds = step_lds_bytes<BM, D, G>(a.kpad_max, a.part_max, a.s_cap, a.o_rows, a.nq * D);
+  const size_t lds = step_lds_bytes<D, G>(a.h, a.kpad_max, a.part_max, a.s_cap, a.o_rows, a.nq * D);
   static bool attr_done = false;   // allow more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU)
   if (!attr_done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<BM, D, G>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<D, G>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
     if (e != hipSuccess) return e;
     attr_done = true;
   }
-  hipLaunchKernelGGL((step_kernel<BM, D, G>), dim3(nwg), dim3(SNT), lds, st, a);
+  hipLaunchKernelGGL((step_kernel<D, G>), dim3(nwg), dim3(SNT), lds, st, a);
   return hipGetLastError();
 }
 
-template <int BM>
-static hipError_t launch_g(const StepArgs& a, int g, int nwg, hipStream_t st) {
+template <>
+hipError_t launch_step<EK_STEP_D>(const StepArgs& a, int g, int nwg, hipStream_t st) {
   switch (g) {
-    case 1: return launch_one<BM, EK_STEP_D, 1>(a, nwg, st);
-    case 2: return launch_one<BM, EK_STEP_D, 2>(a, nwg, st);
-    case 4: return launch_one<BM, EK_STEP_D, 4>(a, nwg, st);
-    case 8: return launch_one<BM, EK_STEP_D, 8>(a, nwg, st);
+    case 1: return launch_one<EK_STEP_D, 1>(a, nwg, st);
+    case 2: return launch_one<EK_STEP_D, 2>(a, nwg, st);
+    case 4: return launch_one<EK_STEP_D, 4>(a, nwg, st);
+    case 8: return launch_one<EK_STEP_D, 8>(a, nwg, st);
     default: return hipErrorInvalidValue;
   }
-}
-
-template <>
-hipError_t launch_step<1, EK_STEP_D>(const StepArgs& a, int g, int nwg, hipStream_t st) {
-  return launch_g<1>(a, g, nwg, st);
 }
 
 }  // namespace eks

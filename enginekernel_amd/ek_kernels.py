@@ -394,44 +394,30 @@ def decode_step_plan(hidden: int, inter: int, n_q: int, n_kv: int, head_dim: int
 
 
 class StepScratch:
-    """Device state of the persistent decode step: the activation arena, the
-    argmax partials, the barrier block and the error word, sized by
-    decode_step_plan. One per (model, batch); launches sharing it must not
-    overlap."""
+    """Device state of the persistent decode step: the hand-over arena, the
+    launch-state block and the error word, sized by decode_step_plan and
+    zeroed once (the kernel keeps a launch epoch in them). One per (model,
+    batch); launches sharing it must not overlap."""
 
     def __init__(self, sizes, device):
-        arena_bytes, am, bar_bytes, grid = sizes
-        self.arena = torch.empty((arena_bytes + 1) // 2, dtype=_BF16, device=device)
-        self.am_val = torch.empty(am, dtype=torch.float32, device=device)
-        self.am_idx = torch.empty(am, dtype=torch.int32, device=device)
+        arena_bytes, _, bar_bytes, grid = sizes
+        self.arena = torch.zeros((arena_bytes + 7) // 8, dtype=torch.int64, device=device)
         self.barrier = torch.zeros((bar_bytes + 3) // 4, dtype=torch.int32, device=device)
         self.err = torch.zeros(1, dtype=torch.int32, device=device)
-        self.arena_bytes, self.am_cap, self.grid = arena_bytes, am, grid
+        self.arena_bytes, self.grid = arena_bytes, grid
 
-    def layer_views(self, cfg, m: int = 1):
-        """The arena's per-layer activations of the last launch, as views:
-        r_in (residual entering the layer), r_mid (after attention), qkv,
-        att (attention output), o, act (SwiGLU output), dn (down output)."""
-        h, inter = cfg.hidden_size, cfg.intermediate_size
-        qw, qkvw = cfg.num_heads * cfg.head_dim, (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim
-        ls = m * (4 * h + qkvw + qw + inter)
-        out = []
-        for l in range(cfg.num_layers):
-            o = l * ls
-            d = {}
-            for name, w in (("r_in", h), ("r_mid", h), ("qkv", qkvw), ("att", qw), ("o", h), ("act", inter),
-                            ("dn", h)):
-                d[name] = self.arena[o:o + m * w].view(m, w)
-                o += m * w
-            out.append(d)
-        return out
+    def reset(self) -> None:
+        """Zero the arena, the launch state and the error word (after an
+        abandoned launch)."""
+        self.arena.zero_()
+        self.barrier.zero_()
+        self.err.zero_()
 
     def check(self) -> None:
-        """Raise if a launch abandoned a barrier wait (and re-arm the state)."""
-        if int(self.err.item()):
-            self.err.zero_()
-            self.barrier.zero_()
-            raise RuntimeError("decode_step: a grid barrier wait timed out; the step's outputs are invalid")
+        """Raise if a launch abandoned a hand-over wait (its outputs are invalid)."""
+        if int(self.err.item()) != 0:
+            self.reset()
+            raise RuntimeError("decode_step: a hand-over wait timed out; the step's outputs are invalid")
 
 
 def layer_table(layers, k_cache, v_cache, device) -> torch.Tensor:
@@ -460,8 +446,8 @@ def decode_step(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_ca
          ptr(embed), embed.stride(0), ptr(lm_head), ptr(final_norm), ptr(cos), ptr(sin), cos.stride(0),
          cos.shape[0], k_cache0.stride(0), k_cache0.stride(1), k_cache0.stride(2), s_cap,
          ptr(tokens), ptr(positions), ptr(len_t), ptr(slot_t), ptr(start_t), ptr(out_buf), ptr(step_idx),
-         out_buf.shape[0], ptr(out_tok), ptr(scratch.arena), scratch.arena_bytes, ptr(scratch.am_val),
-         ptr(scratch.am_idx), scratch.am_cap, ptr(scratch.barrier), ptr(scratch.err), stream())
+         out_buf.shape[0], ptr(out_tok), ptr(scratch.arena), scratch.arena_bytes, ptr(scratch.barrier),
+         ptr(scratch.err), stream())
     return tokens
 
 

@@ -152,11 +152,11 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
                       int64_t* st_step, int64_t max_steps, int64_t rpw, int64_t blocks, void* stream);
 
 /* decode_step_plan: whether the persistent decode-step kernel handles this
- * shape (returns 0) and, in sizes[4], the bytes of the activation arena, the
- * entries of each argmax scratch array, the bytes of the barrier block and
- * the grid (one workgroup per CU). It handles batch 1, head_dim 32/64/128,
- * n_q / n_kv in {1, 2, 4, 8}, hidden, intermediate and n_q * head_dim
- * multiples of 512, and n_q / n_kv * s_cap * 4 <= 32 KiB.
+ * shape (returns 0) and, in sizes[4], the bytes of the hand-over arena, 0
+ * (unused), the bytes of the launch-state block and the grid (one workgroup
+ * per CU). It handles batch 1, head_dim 32/64/128, n_q / n_kv in {1, 2, 4, 8},
+ * hidden (<= 4096), intermediate and n_q * head_dim multiples of 512, and
+ * n_q / n_kv * s_cap * 4 <= 32 KiB.
  * Plans engine/engine.py:273-282 (_make_ws) for the step below. */
 int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
                         int64_t m, int64_t s_cap, int64_t n_layers, int64_t* sizes);
@@ -167,17 +167,18 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
  * first-index argmax and the step bookkeeping (tokens[b] = token,
  * positions[b] += 1, slot_t[b] = *len_t, *len_t += 1, out_buf[*step_idx * m +
  * b] = token if *step_idx < max_steps, *step_idx += 1, out_tok[b] = token if
- * out_tok). One workgroup per CU, grid barriers between the phases, each
- * workgroup loading the next phase's weights before it waits.
+ * out_tok). One workgroup per CU; workgroups hand activations to each other
+ * through the arena as {data, epoch} words that the consumer polls, with no
+ * grid barrier.
  * layer_ptrs: device int64 [n_layers][10] = addresses of qkv [(n_q + 2 n_kv) D,
  * hidden], o [hidden, n_q D], gate/up [2 inter, hidden], down [hidden, inter],
  * ln1, ln2 [hidden], q_norm, k_norm [D], k_cache, v_cache [B, n_kv, S, D] of
  * each layer (bf16, all caches with strides csb/csh/css). arena: the
- * activation arena (decode_step_plan sizes[0] bytes; contents not
- * preserved); am_val/am_idx: argmax scratch (sizes[1] entries); barrier:
- * sizes[2] bytes, zero before the first launch, left zero by every launch
- * that completes; err: set to 1 (and the launch abandoned) if a barrier wait
- * exceeds its bound -- then clear err and the barrier before the next launch.
+ * hand-over arena (decode_step_plan sizes[0] bytes) and barrier: the
+ * launch-state block (sizes[2] bytes), both zero before the first launch and
+ * kept between launches (they hold the launch epoch); err: set to 1 (and the
+ * launch abandoned) if a hand-over wait exceeds its bound -- then zero err,
+ * the arena and the barrier block before the next launch.
  * Launches that overlap on one device race on the arena and the barrier.
  * Replaces engine/ek_model.py:360-416 (decode) + :490-493 (argmax_token) and
  * the bookkeeping of engine/engine.py:288-292, i.e. the whole captured step
@@ -188,8 +189,7 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
                    const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb, int64_t csh, int64_t css,
                    int64_t s_cap, int64_t* tokens, int64_t* positions, int64_t* len_t, int64_t* slot_t,
                    const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
-                   void* arena, int64_t arena_bytes, float* am_val, int32_t* am_idx, int64_t am_cap, void* barrier,
-                   int* err, void* stream);
+                   void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream);
 
 #ifdef __cplusplus
 }
