@@ -14,10 +14,14 @@ bytes). W untimed replays, then exactly K timed replays bracketed by
 synchronisation; ms_per_step = time / K.
 
 Also reported, on the same JSON line:
-  roofline      the dominant kernel (fused add + RMSNorm + gate_up + SwiGLU),
-                launched over all 36 layers' weights (3.6 GB, beyond the
-                256 MB Infinity Cache) and timed with HIP events on its stream;
-                achieved = algorithmic bytes per launch / average launch time.
+  roofline      the dominant kernel. On the default batch-1 path the whole
+                step is ONE persistent kernel (eks::step_kernel), so the
+                replay time is its launch time: achieved = the step's
+                algorithmic bytes (weights, the KV rows it reads and writes,
+                norm gains, the embedding row) / average replay time, HIP
+                events on the replay stream. With ENGINE_PERSISTENT=0 (the
+                per-kernel graph) it is the fused add + RMSNorm + gate_up +
+                SwiGLU launch over all 36 layers' weights instead.
   cpu_baseline  the CPU oracle (the reference's torch fallback restated) decoding
                 a bounded sample of the same workload on this host's cores,
                 from the GPU's prefill KV cache and the same weights.
@@ -36,12 +40,15 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 
-# HBM bytes per fused gate_up launch at batch 1, from two rocprofv3 PMC runs of
-# `bench.py --probe-traffic` (FETCH_SIZE, then WRITE_SIZE), each scaled by what
-# the same counter reads for a 256 MiB device copy (FETCH 0.50007, WRITE 1.0):
-# 48,795.5 KiB / 0.50007 fetched + 81.2 KiB written. Measured on
-# gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1>; re-measure when that kernel changes.
+# HBM bytes per launch, from two rocprofv3 PMC runs of `bench.py --probe-traffic`
+# (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same counter reads for a
+# 256 MiB device copy (FETCH 0.50007, WRITE 1.0). Re-measure when the kernel changes.
+#   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
 GATE_UP_TRAFFIC_B1 = 100_003_000
+#   the persistent step kernel (step_kernel<128, 4>) at batch 1, context 137..146:
+#   4,106,889 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.043x its
+#   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
+STEP_TRAFFIC_B1 = 8_413_008_000
 
 
 def log(msg: str) -> None:
@@ -53,6 +60,18 @@ def gate_up_bytes(b: int, h: int, inter: int, sk: int) -> int:
     prologue's fp32 partials + bf16 residual + gain, the bf16 residual it
     writes, and the [B, I] bf16 activation out."""
     return 2 * (2 * inter) * h + b * h * (4 * sk + 2 + 2) + 2 * h + 2 * b * inter
+
+
+def step_bytes(cfg: dict, ctx_avg: float) -> int:
+    """Algorithmic bytes of one batch-1 decode step: every weight once
+    (8,044,544,000 at the Qwen3-4B shape), the cached K and V rows attended
+    (2 x layers x kv heads x head dim x 2 B per key) and the new row written,
+    the norm gains, the embedding row and the cos/sin rows."""
+    from enginekernel_amd import checkpoint as C
+    h, d, nl = cfg["hidden_size"], cfg["head_dim"], cfg["num_hidden_layers"]
+    kv_row = 2 * nl * cfg["num_key_value_heads"] * d * 2
+    gains = nl * (2 * h + 2 * d) * 2 + h * 2
+    return int(C.weight_bytes_per_token(cfg) + kv_row * (ctx_avg + 1) + gains + 2 * h + 2 * 2 * d)
 
 
 def time_dominant_kernel(model, b: int, reps: int = 3):
@@ -90,9 +109,11 @@ def time_dominant_kernel(model, b: int, reps: int = 3):
 def probe_traffic(b: int = 1, layers: int = 36) -> None:
     """The launches a `rocprofv3 --pmc FETCH_SIZE` (then `WRITE_SIZE`) run
     counts: one plain device copy of 256 MiB (the calibration: its
-    algorithmic traffic is 256 MiB read + 256 MiB written), then the fused
-    gate_up launch once over each of `layers` distinct weight copies (3.6 GB
-    at 36, beyond the 256 MB Infinity Cache), at the Qwen3-4B shape."""
+    algorithmic traffic is 256 MiB read + 256 MiB written), then 10 eager
+    launches of the persistent decode step at the Qwen3-4B shape (batch 1,
+    context 137..146; 8 GB of weights per launch, beyond the 256 MB Infinity
+    Cache); with ENGINE_PERSISTENT=0, the fused gate_up launch over 36
+    distinct weight copies instead."""
     import torch
     from enginekernel_amd import checkpoint as C
     from enginekernel_amd import ek_kernels as K
@@ -104,6 +125,31 @@ def probe_traffic(b: int = 1, layers: int = 36) -> None:
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
+    if os.environ.get("ENGINE_PERSISTENT", "1") != "0":
+        from enginekernel_amd.ek_model import Qwen3
+        from enginekernel_amd.engine import _FastEngine
+        cfg = dict(C.QWEN3_4B)
+        model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+        eng = _FastEngine(model=model)
+        s, steps = 136, 10
+        with torch.inference_mode():
+            eng._ensure_cache(1, s + steps + 1)
+            g = eng._get_graph(1, s + steps + 1)
+            g.tokens.fill_(1)
+            g.positions.fill_(s)
+            g.start_t.zero_()
+            g.len_t.fill_(s)
+            g.step_idx.zero_()
+            kv = ([t[:1] for t in eng.k_cache], [t[:1] for t in eng.v_cache])
+            torch.cuda.synchronize()
+            for _ in range(steps):
+                eng._step_body(g, kv)
+            torch.cuda.synchronize()
+        model.check_step_error()
+        print(json.dumps({"probe": "traffic", "copy_bytes": 2 * src.numel(), "step_launches": steps,
+                          "step_bytes": step_bytes(cfg, s + (steps + 1) / 2), "context": [s + 1, s + steps]}),
+              flush=True)
+        return
     g = torch.Generator(device=dev).manual_seed(0)
     ws = [torch.empty(2 * inter, h, dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g)
           for _ in range(layers)]
@@ -251,8 +297,18 @@ def main():
         if graph.step_idx.item() != W + K_steps:
             raise RuntimeError("graph step counter out of step with the replays")
 
-        dom_s, dom_bytes, dom_n = time_dominant_kernel(model, b)
-        log(f"gate_up kernel: {dom_s * 1e6:.2f} us over {dom_n} launches")
+        persistent = model.buffers(b).step is not None
+        model.check_step_error()
+        if persistent:
+            # one kernel per replay: its launch time is the replay time
+            ctx_avg = s + W + 1 + (K_steps - 1) / 2
+            dom_s, dom_bytes, dom_n = step_s, step_bytes(cfg, ctx_avg), K_steps
+            dom_name, dom_traffic = "eks::step_kernel<128,4> (the whole decode step, one launch)", STEP_TRAFFIC_B1
+        else:
+            dom_s, dom_bytes, dom_n = time_dominant_kernel(model, b)
+            dom_name = "gemv_kernel<PRO_PARTS,EPI_SWIGLU> (add+RMSNorm+gate_up+SwiGLU)"
+            dom_traffic = GATE_UP_TRAFFIC_B1 if b == 1 else None
+            log(f"gate_up kernel: {dom_s * 1e6:.2f} us over {dom_n} launches")
 
         cpu = None
         if not args.no_cpu:
@@ -283,7 +339,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (random-init weights ~N(0,0.02) seed 0, random prompt ids seed 1)",
         "config": {
-            "workload": "config 4: Qwen3-4B-architecture bf16 greedy decode, one hipGraph replay per token",
+            "workload": ("config 4: Qwen3-4B-architecture bf16 greedy decode, one hipGraph replay per token"
+                         + (" (one persistent kernel per step)" if persistent else " (per-kernel graph)")),
             "batch": b, "prompt_len": s, "context_at_timed_steps": [s + W + 1, s + W + K_steps],
             "layers": cfg["num_hidden_layers"], "hidden": cfg["hidden_size"],
             "intermediate": cfg["intermediate_size"], "heads": [cfg["num_attention_heads"], cfg["num_key_value_heads"]],
@@ -293,9 +350,9 @@ def main():
         "weight_bytes_per_token": w_bytes,
         "hbm_roofline_frac": round(w_bytes / step_s / PEAK_HBM, 4),
         "roofline": {
-            "bound": "hbm", "kernel": "gemv_kernel<PRO_PARTS,EPI_SWIGLU> (add+RMSNorm+gate_up+SwiGLU)",
+            "bound": "hbm", "kernel": dom_name,
             "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM, 4), "traffic": GATE_UP_TRAFFIC_B1 if b == 1 else None,
+            "frac": round(achieved / PEAK_HBM, 4), "traffic": dom_traffic,
             "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_s * 1e6, 3), "launches": dom_n,
         },
         "cpu_baseline": cpu,

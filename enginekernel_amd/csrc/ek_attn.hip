@@ -351,7 +351,7 @@ __global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
   u.ll_out = nullptr;
   u.ll_ep = 0;
 #ifdef EK_STEP_TRACE
-  u.trace_row = nullptr;
+  u.trace_lds = nullptr;
 #endif
   eka::attn_unit<D, G>(u, lds);
 }

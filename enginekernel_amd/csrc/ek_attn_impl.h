@@ -22,7 +22,7 @@
 //
 // In rope mode the unit norms/rotates its query heads and the new key (which
 // stands in for the cache row at the new slot), takes the raw new value
-// (likewise), and the writer unit also stores both in the cache. The first K
+// (likewise), and the writer unit stores both in the cache at its end. The first K
 // and V tiles are loaded on entry, before the q/k/v heads are awaited and
 // before the QK-norm/RoPE work, so both overlap the work before their use.
 //
@@ -54,7 +54,7 @@ __device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w,
     xp[i] = ok ? bf2f(x[pd]) : 0.f;
     ss = fmaf(xv[i], xv[i], ss);
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float rstd = 1.0f / sqrtf(ss / (float)D + eps);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -113,12 +113,12 @@ struct AttnUnit {
   // workgroups of the same launch, which poll for the epoch)
   unsigned long long* ll_out; uint32_t ll_ep;
 #ifdef EK_STEP_TRACE
-  int64_t* trace_row;                    // per-stage timestamps of this unit (trace builds)
+  int64_t* trace_lds;                    // per-stage timestamps of this unit, in LDS (trace builds)
 #endif
 };
 
 #ifdef EK_STEP_TRACE
-#define EK_ATTN_MARK(ev) do { if (threadIdx.x == 0 && a.trace_row) a.trace_row[ev] = wall_clock64(); } while (0)
+#define EK_ATTN_MARK(ev) do { if (threadIdx.x == 0 && a.trace_lds) a.trace_lds[ev] = wall_clock64(); } while (0)
 #else
 #define EK_ATTN_MARK(ev) do { } while (0)
 #endif
@@ -135,8 +135,9 @@ struct AttnLds {
   static constexpr size_t ST = align16((size_t)FNW * 8 * 4);
   static constexpr size_t VT = align16((size_t)FNW * 32 * VTS * 2);
   static constexpr size_t OUTP = align16((size_t)FNW * G * FDC * 4);
+  static constexpr size_t KNB = align16((size_t)D * 2);
   static __host__ __device__ constexpr size_t bytes(int64_t cap) {
-    return scores(cap) + QS + KNEW + VNEW + 2 * ST + VT + OUTP;
+    return scores(cap) + QS + KNEW + VNEW + 2 * ST + VT + OUTP + KNB;
   }
 };
 
@@ -161,6 +162,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
   float (*stl)[8] = reinterpret_cast<float (*)[8]>(fx + L::QS + L::KNEW + L::VNEW + L::ST);
   uint16_t (*vt)[32][VTS] = reinterpret_cast<uint16_t (*)[32][VTS]>(fx + L::QS + L::KNEW + L::VNEW + 2 * L::ST);
   float (*outp)[G][FDC] = reinterpret_cast<float (*)[G][FDC]>(fx + L::QS + L::KNEW + L::VNEW + 2 * L::ST + L::VT);
+  bf16_t* knew_bf = reinterpret_cast<bf16_t*>(fx + L::QS + L::KNEW + L::VNEW + 2 * L::ST + L::VT + L::OUTP);
 
   // the thread index is made opaque here so that the per-lane offsets below
   // are computed per call rather than hoisted out of a caller's loop (where
@@ -204,6 +206,19 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
       vreg[u][m] = (rel < nrel && !(fresh && rel == srel)) ? ld16(vb + (lo + rel) * a.css) : make_uint4(0, 0, 0, 0);
     }
   }
+  // the writer unit stores the new key (normed, rotated) and value at the
+  // new slot once its own work is done: a store issued earlier would hold up
+  // the memory waits that follow it
+  auto store_new_row = [&]() {
+    if (a.rope && a.writer && slot >= 0 && wave == FNW - 1) {
+      bf16_t* kdst = a.kc + slot * a.css;
+      bf16_t* vdst = a.vc + slot * a.css;
+      for (int d = lane; d < D; d += EK_WAVE) {
+        kdst[d] = knew_bf[d];
+        vdst[d] = a.vh[d];
+      }
+    }
+  };
   if (!pre()) return false;
   EK_ATTN_MARK(15);
 
@@ -214,13 +229,8 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
       if (u < G) {
         head_norm_rope<D>(a.qh + u * a.q_stride, a.qn, a.cr, a.sr, a.eps, qs[u], nullptr);
       } else {
-        bf16_t* kdst = writer ? a.kc + slot * a.css : nullptr;
-        head_norm_rope<D>(a.kh, a.kn, a.cr, a.sr, a.eps, knew, kdst);
+        head_norm_rope<D>(a.kh, a.kn, a.cr, a.sr, a.eps, knew, knew_bf);
       }
-    }
-    if (writer && wave == FNW - 1) {
-      bf16_t* vdst = a.vc + slot * a.css;
-      for (int d = lane; d < D; d += EK_WAVE) vdst[d] = a.vh[d];
     }
     if (fresh && tid < FDC) vnew[tid] = a.vh[d0 + tid];
   } else {
@@ -231,7 +241,10 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
   EK_ATTN_MARK(16);
 
   // ---- scores. B operand = Q^T: q[g = r16][32 i + 8 q4 .. +7], zero for g >= G
+  // (every lane reads a valid row and masks afterwards: a read under a lane
+  // condition becomes a branch with its own wait, serialising the reads)
   uint4 qb[KS];
+  const uint32_t qmask = r16 < G ? 0xffffffffu : 0u;
 #pragma unroll
   for (int i = 0; i < KS; ++i) {
     const int g = r16 < G ? r16 : 0;
@@ -239,10 +252,12 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int dd = 32 * i + 8 * q4 + 2 * e;
-      w[e] = r16 < G ? (f2bf(qs[g][dd]) | (f2bf(qs[g][dd + 1]) << 16)) : 0u;
+      const float2 v = *reinterpret_cast<const float2*>(&qs[g][dd]);
+      w[e] = (f2bf(v.x) | (f2bf(v.y) << 16)) & qmask;
     }
     qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
   }
+  EK_ATTN_MARK(20);
   float mrun = -1e30f, lrun = 0.f;   // this lane's scores: head r16, running max / exp-sum
   for (int64_t t0 = wave; t0 < ntile; t0 += (int64_t)FNW * FTU) {
     if (t0 != wave) {
@@ -258,17 +273,9 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
     for (int u = 0; u < FTU; ++u) {
       const int64_t tb = (t0 + u * FNW) << 4;
       if (tb >= nrel) break;
-      if (fresh && tb + r16 == srel) {   // the new key, not the cache row
+      if (fresh && tb + r16 == srel) {   // the new key (packed bf16 in LDS), not the cache row
 #pragma unroll
-        for (int i = 0; i < KS; ++i) {
-          uint32_t w[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int dd = 32 * i + 8 * q4 + 2 * e;
-            w[e] = f2bf(knew[dd]) | (f2bf(knew[dd + 1]) << 16);
-          }
-          kt[u][i] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
+        for (int i = 0; i < KS; ++i) kt[u][i] = *reinterpret_cast<const uint4*>(&knew_bf[32 * i + 8 * q4]);
       }
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -294,6 +301,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
       }
     }
   }
+  EK_ATTN_MARK(21);
   // merge over the four lane rows of a head, then over the waves
 #pragma unroll
   for (int o = 16; o < EK_WAVE; o <<= 1) {
@@ -301,6 +309,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
     const float l2 = __shfl_xor(lrun, o, EK_WAVE);
     merge_ml(mrun, lrun, m2, l2);
   }
+  EK_ATTN_MARK(22);
   if (q4 == 0 && r16 < G) {
     stm[wave][r16] = mrun;
     stl[wave][r16] = lrun;
@@ -354,10 +363,13 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
       uint32_t pw[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
+        // p values are exact bf16; reads are clamped to the last key and masked
         const int64_t ra = rel0 + 2 * e;
-        const float pa = (r16 < G && ra < nrel) ? prow[ra] : 0.f;        // exact bf16 values
-        const float pb = (r16 < G && ra + 1 < nrel) ? prow[ra + 1] : 0.f;
-        pw[e] = (__float_as_uint(pa) >> 16) | (__float_as_uint(pb) & 0xffff0000u);
+        const float pa = prow[ra < nrel ? ra : nrel - 1];
+        const float pb = prow[ra + 1 < nrel ? ra + 1 : nrel - 1];
+        const uint32_t ma = (r16 < G && ra < nrel) ? 0xffffu : 0u;
+        const uint32_t mb = (r16 < G && ra + 1 < nrel) ? 0xffff0000u : 0u;
+        pw[e] = ((__float_as_uint(pa) >> 16) & ma) | (__float_as_uint(pb) & mb);
       }
       const uint4 pa4 = make_uint4(pw[0], pw[1], pw[2], pw[3]);
 #pragma unroll
@@ -390,6 +402,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
       const unsigned long long word = ((unsigned long long)a.ll_ep << 32) | pack2(t0, t1);
       __hip_atomic_store(a.ll_out + (g * a.out_stride + d0 + d) / 2, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    store_new_row();
     return true;
   }
   for (int i = tid; i < G * FDC; i += FNT) {
@@ -399,6 +412,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
     for (int w = 0; w < FNW; ++w) t += outp[w][g][d];
     a.out[g * a.out_stride + d0 + d] = (bf16_t)f2bf(t);
   }
+  store_new_row();
   return true;
 }
 

@@ -37,7 +37,7 @@ size_t attn_lds(int d, int g, int64_t s_cap) {
   size_t attn = eka::align16((size_t)(g + 6) * d * 2) + eka::align16((size_t)g * s_cap * 4);
   attn += eka::align16((size_t)g * d * 4) + eka::align16((size_t)d * 4) + eka::align16((size_t)eka::FDC * 2) +
           2 * eka::align16((size_t)eka::FNW * 8 * 4) + eka::align16((size_t)eka::FNW * 32 * eka::VTS * 2) +
-          eka::align16((size_t)eka::FNW * g * eka::FDC * 4);
+          eka::align16((size_t)eka::FNW * g * eka::FDC * 4) + eka::align16((size_t)d * 2);
   return attn;
 }
 
@@ -73,7 +73,7 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   p.o_rows = 2 * eks::cdiv_i((int)hidden / 2, n_gemv);
   p.part_max = eks::part_rows_max((int)hidden, (int)inter, qkvw, (int)vocab, n_gemv, p.o_rows);
   const size_t gemv = eks::step_rr_bytes((int)hidden) + eka::align16((size_t)p.kpad_max * 2) +
-                      eka::align16((size_t)p.part_max * eks::SNW * 4) + (size_t)p.o_rows * qw * 2;
+                      eka::align16((size_t)p.part_max * eks::SNW * 4);
   const size_t attn = attn_lds((int)head_dim, (int)g, s_cap);
   p.lds = gemv > attn ? gemv : attn;
   if (p.lds > kLdsLimit) return ek_fail(hipErrorInvalidValue, "decode_step: LDS plan exceeds the workgroup limit");

@@ -22,9 +22,10 @@
 // wait.
 //
 // Weights never depend on activations: before each wait a workgroup's waves
-// load the first weight chunks of the coming phase into a register ring, and
-// the workgroups without attention work copy their o_proj rows into LDS while
-// attention runs, so the HBM stream keeps going across the hand-overs.
+// load the first weight chunks of the coming phase into a register ring
+// (which holds a workgroup's whole o_proj share at the Qwen3-4B shape), and
+// while attention runs they also pull their first gate/up chunks into L2, so
+// the HBM stream keeps going across the hand-overs.
 //
 // Projections: a phase's output rows (gate/up row pairs for SwiGLU) are split
 // evenly over the workgroups in pairs (so that every output word is produced
@@ -49,6 +50,8 @@ namespace eks {
 constexpr int SNT = eka::FNT;          // 512 threads
 constexpr int SNW = SNT / EK_WAVE;     // 8 waves
 constexpr int NB = 8;                  // weight chunks in flight per wave
+constexpr int PF = 8;                  // chunks per wave prefetched ahead of a hand-over wait
+constexpr int OB = 12;                 // o_proj chunks per wave held in registers through attention
 constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
 constexpr int LW_FIELDS = 10;          // per-layer pointer table row
 constexpr int ATU = 6;                 // attention: 16-key score tiles per wave held in registers
@@ -107,10 +110,18 @@ __host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int voc
   return r;
 }
 
+// -DEK_STEP_TRACE builds stamp phase events into LDS (a global store would
+// delay the memory waits that follow it) and copy one layer's stamps to
+// bar->trace[wg][layer][24] at the layer's end.
 #ifdef EK_STEP_TRACE
-#define EK_TS(ev) do { if (threadIdx.x == 0 && trace) trace[((int64_t)blockIdx.x * 40 + (tl)) * 24 + (ev)] = wall_clock64(); } while (0)
+#define EK_TS(ev) do { if (threadIdx.x == 0) ts_lds[ev] = wall_clock64(); } while (0)
+#define EK_TS_FLUSH(layer) do { if (a.bar->trace && threadIdx.x < 24) \
+    a.bar->trace[((int64_t)blockIdx.x * 40 + (layer)) * 24 + threadIdx.x] = ts_lds[threadIdx.x]; } while (0)
+#define EK_TS_FLUSH_SYNC(layer) do { __syncthreads(); EK_TS_FLUSH(layer); } while (0)
 #else
+#define EK_TS_FLUSH_SYNC(layer) do { } while (0)
 #define EK_TS(ev) do { } while (0)
+#define EK_TS_FLUSH(layer) do { } while (0)
 #endif
 
 // ---------------------------------------------------------------------------
@@ -240,33 +251,77 @@ __device__ __forceinline__ const bf16_t* span_item(const Span& s, int i) {
   return i < s.half ? s.base + (int64_t)i * CH : s.up + (int64_t)(i - s.half) * CH;
 }
 
-// The wave's ring: when `ready`, r[u] holds item u of the coming phase.
+// The wave's ring: slots [0, nready) hold items 0 .. nready-1 of the coming
+// phase (loaded ahead by prefetch_phase).
 struct Ring {
   uint4 r[NB];
-  bool ready;
+  int nready;
 };
 
-// The first NB items of phase `pn` into this wave's ring, issued ahead of a
-// wait so that they load while the workgroup waits for its inputs.
+// The first `cnt` items of phase `pn` into this wave's ring, issued ahead of
+// a wait so that they load while the workgroup waits for its inputs. Loads
+// retire in order, so every item prefetched here is also a load the wait's
+// own polls queue behind: ahead of a short hand-over only a few are worth it.
+template <int CNT>
 __device__ __forceinline__ void prefetch_phase(const Gp& pn, Ring& ring) {
   const Span sn = make_span(pn, wave_id());
   const int loff = (threadIdx.x & 63) * 8;
 #pragma unroll
-  for (int u = 0; u < NB; ++u) ring.r[u] = ld16(span_item(sn, sn.i0 + (u < sn.n ? u : 0)) + loff);
-  ring.ready = true;
+  for (int u = 0; u < CNT; ++u) ring.r[u] = ld16(span_item(sn, sn.i0 + (u < sn.n ? u : 0)) + loff);
+  ring.nready = CNT;
 }
 
-// Bring items [NB, NB + L2T) of this wave's share of phase `pn` into the L2
-// (one 4-byte load per 64-byte sector), so that the phase later reads them
-// from L2 instead of HBM. The loaded words are folded into `sink`, which the
-// caller consumes where it waits anyway.
+// The o projection's chunks: a wave's first OB items (all of them at the
+// Qwen3-4B shape), loaded into registers while attention runs and consumed
+// once its output arrives; items past OB (larger shapes) load one by one.
+__device__ __forceinline__ void hold_phase(const Gp& P, uint4* ob) {
+  const Span sn = make_span(P, wave_id());
+  const int loff = (threadIdx.x & 63) * 8;
+#pragma unroll
+  for (int u = 0; u < OB; ++u) ob[u] = ld16(span_item(sn, sn.i0 + (u < sn.n ? u : 0)) + loff);
+}
+
+__device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, const bf16_t* xs, float* part) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const Span sp = make_span(P, wave);
+  const int n = sp.n;
+  const int loff = lane * 8;
+  int r = sp.i0 / P.C, ch = sp.i0 - (sp.i0 / P.C) * P.C;
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < OB; ++u) {
+    if (u < n) {
+      acc = dot8_acc(ob[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+      if (ch == P.C - 1 || u == n - 1) {
+        const float sum = wave_sum_dpp(acc);
+        if (lane == 0) part[r * SNW + wave] = sum;
+        acc = 0.f;
+      }
+      if (++ch == P.C) { ch = 0; ++r; }
+    }
+  }
+  for (int k = OB; k < n; ++k) {
+    acc = dot8_acc(ld16(span_item(sp, sp.i0 + k) + loff), *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+    if (ch == P.C - 1 || k == n - 1) {
+      const float sum = wave_sum_dpp(acc);
+      if (lane == 0) part[r * SNW + wave] = sum;
+      acc = 0.f;
+    }
+    if (++ch == P.C) { ch = 0; ++r; }
+  }
+}
+
+// Bring items [PF, PF + L2T) of this wave's share of phase `pn` (the ones
+// after its ring prefetch) into the L2 (one 4-byte load per 64-byte sector),
+// so that the phase later reads them from L2 instead of HBM. The loaded words are
+// folded into `sink`, which the caller consumes where it waits anyway.
 constexpr int L2T = 12;
 __device__ __forceinline__ void l2_touch(const Gp& pn, uint32_t& sink) {
   const Span sn = make_span(pn, wave_id());
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < L2T / 4; ++j) {
-    const int i = NB + 4 * j + (lane >> 4);
+    const int i = PF + 4 * j + (lane >> 4);
     if (i < sn.n) sink ^= *reinterpret_cast<const uint32_t*>(span_item(sn, sn.i0 + i) + (lane & 15) * 32);
   }
 }
@@ -283,10 +338,9 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
   const Span sp = make_span(P, wave);
   const int n = sp.n;
   const int loff = lane * 8;
-  if (!ring.ready) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) ring.r[u] = ld16(span_item(sp, sp.i0 + (u < n ? u : 0)) + loff);
-  }
+  for (int u = 0; u < NB; ++u)
+    if (u >= ring.nready) ring.r[u] = ld16(span_item(sp, sp.i0 + (u < n ? u : 0)) + loff);
   int r = sp.i0 / P.C, ch = sp.i0 - (sp.i0 / P.C) * P.C;   // consume position (row-local, chunk)
   float acc = 0.f;
   int k0 = 0;
@@ -320,68 +374,7 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
     const float sum = wave_sum_dpp(acc);
     if (lane == 0) part[r * SNW + wave] = sum;
   }
-  ring.ready = false;
-}
-
-// Copy this workgroup's rows of a plain phase into LDS (row-major, K per row):
-// 8 chunks of 16 B per thread in flight per round.
-__device__ __forceinline__ void stage_rows_lds(const Gp& P, bf16_t* wl) {
-  int u0, u1;
-  unit_range(P, u0, u1);
-  const int n16 = (u1 - u0) * P.K / 8;
-  const bf16_t* src = P.w + (int64_t)u0 * P.K;
-  for (int i0 = threadIdx.x; i0 < n16; i0 += 8 * SNT) {
-    uint4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = i0 + j * SNT;
-      v[j] = ld16(src + (int64_t)(i < n16 ? i : 0) * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = i0 + j * SNT;
-      if (i < n16) *reinterpret_cast<uint4*>(wl + (int64_t)i * 8) = v[j];
-    }
-  }
-}
-
-// A plain projection phase whose rows stage_rows_lds put in LDS: same item
-// split and partials as gemv_phase, weights read from LDS, LB items' reads
-// issued before any is consumed.
-constexpr int LB = 4;
-__device__ __forceinline__ void gemv_lds_phase(const Gp& P, const bf16_t* wl, const bf16_t* xs, float* part) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
-  int u0, u1;
-  unit_range(P, u0, u1);
-  const WaveItems wr = wave_items(P, u1 - u0, wave);
-  const int loff = lane * 8;
-  int r = wr.i0 / P.C, ch = wr.i0 - (wr.i0 / P.C) * P.C;
-  float acc = 0.f;
-  for (int k0 = 0; k0 < wr.n; k0 += LB) {
-    uint4 wv[LB], xv[LB];
-    int rl = r, cl = ch;
-#pragma unroll
-    for (int u = 0; u < LB; ++u) {
-      if (k0 + u < wr.n) {
-        wv[u] = *reinterpret_cast<const uint4*>(wl + (int64_t)rl * P.K + cl * CH + loff);
-        xv[u] = *reinterpret_cast<const uint4*>(xs + cl * CH + loff);
-      }
-      if (++cl == P.C) { cl = 0; ++rl; }
-    }
-#pragma unroll
-    for (int u = 0; u < LB; ++u) {
-      const int k = k0 + u;
-      if (k < wr.n) {
-        acc = dot8_acc(wv[u], xv[u], acc);
-        if (ch == P.C - 1 || k == wr.n - 1) {
-          const float sum = wave_sum_dpp(acc);
-          if (lane == 0) part[r * SNW + wave] = sum;
-          acc = 0.f;
-        }
-        if (++ch == P.C) { ch = 0; ++r; }
-      }
-    }
-  }
+  ring.nready = 0;
 }
 
 // sum of the waves' partials of row_local r, fixed order
@@ -487,20 +480,31 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int nw = k / 2;
   float ss = 0.f;
+  float r0v[NGW], r1v[NGW];
+  // reads at clamped indices, then masked use (no read under a lane condition)
 #pragma unroll
   for (int j = 0; j < NGW; ++j) {
     const int i = tid + j * SNT;
-    if (i >= nw) continue;
-    float r0 = rr[2 * i], r1 = rr[2 * i + 1];
+    const int ic = i < nw ? i : 0;
+    float r0 = rr[2 * ic], r1 = rr[2 * ic + 1];
     if (xw) {
-      const uint32_t x = xw[i];
+      const uint32_t x = xw[ic];
       r0 = rbf(r0 + lo_bf(x));
       r1 = rbf(r1 + hi_bf(x));
-      rr[2 * i] = r0;
-      rr[2 * i + 1] = r1;
     }
-    ss = fmaf(r0, r0, ss);
-    ss = fmaf(r1, r1, ss);
+    r0v[j] = r0;
+    r1v[j] = r1;
+    const float m = i < nw ? 1.f : 0.f;
+    ss = fmaf(r0 * m, r0, ss);
+    ss = fmaf(r1 * m, r1, ss);
+  }
+#pragma unroll
+  for (int j = 0; j < NGW; ++j) {
+    const int i = tid + j * SNT;
+    if (xw && i < nw) {
+      rr[2 * i] = r0v[j];
+      rr[2 * i + 1] = r1v[j];
+    }
   }
   ss = wave_sum_dpp(ss);
   if (lane == 0) red[wave] = ss;
@@ -513,10 +517,9 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
 #pragma unroll
   for (int j = 0; j < NGW; ++j) {
     const int i = tid + j * SNT;
-    if (i >= nw) continue;
-    const float o0 = rbf(lo_bf(gw[j]) * rbf(rr[2 * i] * rstd));
-    const float o1 = rbf(hi_bf(gw[j]) * rbf(rr[2 * i + 1] * rstd));
-    xs32[i] = pack2(o0, o1);
+    const float o0 = rbf(lo_bf(gw[j]) * rbf(r0v[j] * rstd));
+    const float o1 = rbf(hi_bf(gw[j]) * rbf(r1v[j] * rstd));
+    if (i < nw) xs32[i] = pack2(o0, o1);
   }
   zero_pad(xs, k, kpad);
 }
@@ -526,7 +529,11 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
 // ---------------------------------------------------------------------------
 template <int D, int G>
 __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
-                                                int64_t hi, uint32_t ep, unsigned char* smem, int layer) {
+                                                int64_t hi, uint32_t ep, unsigned char* smem, int layer
+#ifdef EK_STEP_TRACE
+                                                , int64_t* ts_lds
+#endif
+                                                ) {
   (void)layer;
   const int h = (int)blockIdx.x % a.nkv, c = (int)blockIdx.x / a.nkv;
   // this unit's q heads, new key and new value -> LDS (bf16 pairs)
@@ -571,7 +578,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
   u.ll_out = att + (int64_t)h * G * hw;
   u.ll_ep = ep;
 #ifdef EK_STEP_TRACE
-  u.trace_row = a.bar->trace ? a.bar->trace + ((int64_t)blockIdx.x * 40 + layer) * 24 : nullptr;
+  u.trace_lds = ts_lds;
 #endif
   // the cached keys/values are already loading when the unit waits for its heads
   auto wait_heads = [&]() -> bool {
@@ -598,25 +605,29 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 // the layer's q/k/v arrive. The other workgroups run every projection and
 // the lm_head. The two roles share no state, so neither's registers are
 // live in the other's code.
-// LDS of a projection workgroup: [residual row, fp32 x h][activation row][wave partials][staged o_proj rows]
+// LDS of a projection workgroup: [residual row, fp32 x h][activation row][wave partials]
 __host__ __device__ inline size_t step_rr_bytes(int h) { return eka::align16((size_t)h * 4); }
 
 template <int D, int G>
-__device__ __forceinline__ void attention_loop(const StepArgs& a, uint32_t ep, int64_t hi, unsigned char* smem) {
+__device__ __forceinline__ void attention_loop(const StepArgs& a, uint32_t ep, int64_t hi, unsigned char* smem
+#ifdef EK_STEP_TRACE
+                                               , int64_t* ts_lds
+#endif
+                                               ) {
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = arena_layer_words(a.h, a.inter, qkvw, qw);
-#ifdef EK_STEP_TRACE
-  int64_t* trace = a.bar->trace;
-#endif
   for (int l = 0; l < a.nl; ++l) {
-    const int tl = l;
-    (void)tl;
     const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
     const llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
     llw_t* att_ll = a.arena + (int64_t)l * lwords + qkvw / 2;
-    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, ep, smem, l)) return;
+    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, ep, smem, l
+#ifdef EK_STEP_TRACE
+                                , ts_lds
+#endif
+                                )) return;
     EK_TS(5);
     __syncthreads();
+    EK_TS_FLUSH(l);
   }
 }
 
@@ -640,7 +651,8 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     s_ep = e;
   }
 #ifdef EK_STEP_TRACE
-  int64_t* trace = a.bar->trace;
+  __shared__ int64_t s_ts[24];
+  int64_t* ts_lds = s_ts;
 #endif
   __syncthreads();
   const uint32_t ep = s_ep;
@@ -653,7 +665,11 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
   const int n_attn = a.nkv * (D / eka::FDC);   // attention units = workgroups [0, n_attn)
   if ((int)blockIdx.x < n_attn) {
-    attention_loop<D, G>(a, ep, hi, smem);
+    attention_loop<D, G>(a, ep, hi, smem
+#ifdef EK_STEP_TRACE
+                         , ts_lds
+#endif
+                         );
     return;
   }
 
@@ -663,19 +679,15 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   uint32_t* xs32 = reinterpret_cast<uint32_t*>(ph);
   float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)a.kpad_max * 2));
   const int part_n = a.part_max * SNW;
-  bf16_t* wl = reinterpret_cast<bf16_t*>(ph + eka::align16((size_t)a.kpad_max * 2) +
-                                         eka::align16((size_t)part_n * 4));   // staged o_proj rows
 
   Ring ring;
-  ring.ready = false;
+  ring.nready = 0;
 #pragma unroll
   for (int u = 0; u < NB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
   uint32_t gw[NGW];
 
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
-    const int tl = l;
-    (void)tl;
     EK_TS(0);
     const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
     llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
@@ -715,14 +727,15 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     EK_TS(3);
     __syncthreads();
 
-    // ---- while attention runs: this workgroup's o_proj rows into LDS, the
-    //      first gate/up chunks into the ring and the next ones into L2
-    stage_rows_lds(go, wl);
-    EK_TS(4);
-    prefetch_phase(gg, ring);
+    // ---- while attention runs: this workgroup's o_proj rows into registers
+    //      (all of them at the Qwen3-4B shape) and its first gate/up rows into L2
+    uint4 ob[OB];
+    hold_phase(go, ob);
+    prefetch_phase<PF>(gg, ring);
     uint32_t sink = 0;
     l2_touch(gg, sink);
-    // ---- o projection (weights from LDS)
+    EK_TS(4);
+    // ---- o projection
     zero_part(part, part_n);
     {
       const bool ok = ll_read(LinSrc{att_ll}, qw / 2, ep, xs32, a.err, a.spin);
@@ -732,7 +745,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     zero_pad(xs, qw, kpad_of(qw));
     EK_TS(6);
     __syncthreads();
-    gemv_lds_phase(go, wl, xs, part);
+    gemv_held_phase(go, ob, xs, part);
     __syncthreads();
     EK_TS(7);
     epilogue_ll(go, part, o_ll, ep);
@@ -754,7 +767,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     EK_TS(10);
     epilogue_swiglu_ll(gg, part, act_ll, ep);
     EK_TS(11);
-    prefetch_phase(gd, ring);
+    prefetch_phase<PF>(gd, ring);
 
     // ---- down projection
     __syncthreads();
@@ -772,17 +785,16 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     epilogue_ll(gd, part, dn_ll, ep);
     EK_TS(14);
     if (l + 1 < a.nl)
-      prefetch_phase(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_QKV]),
+      prefetch_phase<PF>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_QKV]),
                                          h, qkvw, 0, 2), n_attn), ring);
     else
-      prefetch_phase(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
+      prefetch_phase<PF>(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
     dn_prev = dn_ll;
     __syncthreads();
+    EK_TS_FLUSH(l);
   }
 
   // ---- final add + norm, lm_head, per-workgroup argmax
-  const int tl = a.nl;
-  (void)tl;
   EK_TS(0);
   llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
   zero_part(part, part_n);
@@ -800,6 +812,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   EK_TS(2);
   epilogue_argmax_ll(gl, part, s_red, s_redi, am_ll, ep);
   EK_TS(3);
+  EK_TS_FLUSH_SYNC(a.nl);
   if ((int)blockIdx.x != n_attn) return;
 
   // ---- token = first-index argmax over the projection workgroups'
@@ -823,6 +836,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   int oi;
   wg_argmax(bv, bi, s_red, s_redi, ov, oi);
   EK_TS(4);
+  EK_TS_FLUSH_SYNC(a.nl);
   if (tid == 0) {
     const int64_t step = *a.step_idx;
     const int64_t tok = oi == 0x7fffffff ? 0 : oi;
@@ -839,8 +853,8 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
 // LDS bytes of step_kernel<D, G> (o_rows: the most o_proj rows of one workgroup, qw = n_q * D)
 template <int D, int G>
 inline size_t step_lds_bytes(int h, int kpad_max, int part_max, int64_t s_cap, int o_rows, int qw) {
-  const size_t gemv = step_rr_bytes(h) + eka::align16((size_t)kpad_max * 2) +
-                      eka::align16((size_t)part_max * SNW * 4) + (size_t)o_rows * qw * 2;
+  (void)o_rows; (void)qw;
+  const size_t gemv = step_rr_bytes(h) + eka::align16((size_t)kpad_max * 2) + eka::align16((size_t)part_max * SNW * 4);
   const size_t attn = eka::align16((size_t)(G + 6) * D * 2) + eka::AttnLds<D, G>::bytes(s_cap);
   return gemv > attn ? gemv : attn;
 }

@@ -166,9 +166,9 @@ class Qwen3(torch.nn.Module):
         self._bufs: dict = {}
         self._plans: dict = {}
         self._tables: dict = {}
-        # the whole step as one persistent launch where its plan allows (opt-in:
-        # ENGINE_PERSISTENT=1; the per-kernel graph step is the default)
-        self.persistent = os.environ.get("ENGINE_PERSISTENT", "0") == "1"
+        # the whole batch-1 step as one persistent launch where its plan allows
+        # (ENGINE_PERSISTENT=0 selects the per-kernel graph step everywhere)
+        self.persistent = os.environ.get("ENGINE_PERSISTENT", "1") != "0"
         # the prefill's hipBLASLt projections: no reduced-precision bf16 reductions
         torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
 
@@ -334,7 +334,7 @@ class Qwen3(torch.nn.Module):
         return tab
 
     def check_step_error(self) -> None:
-        """Raise if a persistent step abandoned a barrier wait."""
+        """Raise if a persistent step abandoned a hand-over wait."""
         for bufs in self._bufs.values():
             if bufs.step is not None:
                 bufs.step.check()

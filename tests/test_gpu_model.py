@@ -142,6 +142,7 @@ def test_engine_4b_shapes_tokens(dev):
     cfg = dict(MID_4B)
     tensors = C.random_weights(cfg, seed=0)
     model = Qwen3(None, dev, tensors=tensors, config=cfg)
+    model.persistent = False     # the per-kernel graph step (the one-launch step has its own tests)
     eng = Engine(model=model)
     om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
     g = torch.Generator().manual_seed(2)
@@ -214,7 +215,7 @@ def test_decode_parity_full_depth_against_the_noise_floor(dev):
 
 
 # ---------------------------------------------------------------------------
-# the one-launch decode step (ek_decode_step, ENGINE_PERSISTENT=1)
+# the one-launch decode step (ek_decode_step; the default batch-1 step)
 # ---------------------------------------------------------------------------
 def _persistent(cfg, tensors, dev):
     model = Qwen3(None, dev, tensors=tensors, config=cfg)
