@@ -7,12 +7,11 @@
 //   scores   per tile of 16 keys, S^T[16 x 16] = K_tile[16 x D] . Q^T[D x 16]
 //            on the matrix cores (v_mfma_f32_16x16x32_bf16: bf16 products are
 //            exact in fp32, sums are fp32), the G query heads in the first G
-//            columns; scaled into an LDS row per head. Each lane also keeps
-//            the running max and exp-sum of the scores it produced; the lanes
-//            and waves merge them into the row's M and L.
-//   softmax  p = bf16(exp(s - M) / L) in place, one exp per score, spread
-//            over all threads (the reference fallback's rounding point,
-//            engine/ek_model.py:475-488).
+//            columns; scaled into an LDS row per head, with each lane's
+//            running max; the lanes and waves merge the maxima into M.
+//   softmax  e = exp(s - M) in place, L = sum of e (fixed order), then
+//            p = bf16(e / L): one exp per score, spread over all threads
+//            (the reference fallback's rounding point, engine/ek_model.py:475-488).
 //   PV       per tile of 32 keys, O[16 x 16] += P[16 x 32] . V[32 x 16] per
 //            16 head dims, the heads in the first G rows. V arrives as 16 B
 //            per lane and is re-laid through a per-wave LDS tile into the B
@@ -84,13 +83,6 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) { return __builtin_bit_ca
 
 __device__ __forceinline__ f32x4_t mfma16x16x32(const uint4& a, const uint4& b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
-}
-
-// merge a (max, sum of exp(s - max)) pair into another
-__device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2) {
-  const float mn = fmaxf(m, m2);
-  l = l * expf(m - mn) + l2 * expf(m2 - mn);
-  m = mn;
 }
 
 struct AttnUnit {
@@ -258,7 +250,9 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
     qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
   }
   EK_ATTN_MARK(20);
-  float mrun = -1e30f, lrun = 0.f;   // this lane's scores: head r16, running max / exp-sum
+  // pass 1: scores into the LDS rows and each lane's running max (no
+  // exponentials yet, no read under a lane condition)
+  float mrun = -INFINITY;            // this lane's scores: head r16
   for (int64_t t0 = wave; t0 < ntile; t0 += (int64_t)FNW * FTU) {
     if (t0 != wave) {
 #pragma unroll
@@ -280,50 +274,48 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
       f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KS; ++i) c = mfma16x16x32(kt[u][i], qb[i], c);
-      if (r16 < G) {
-        float sv[4];
-        float mx = mrun;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t rel = tb + 4 * q4 + e;
-          sv[e] = c[e] * a.sm_scale;
-          if (rel < nrel) {
-            sc_lds[(int64_t)r16 * cap + rel] = sv[e];
-            mx = fmaxf(mx, sv[e]);
-          }
-        }
-        float add = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (tb + 4 * q4 + e < nrel) add += expf(sv[e] - mx);
-        lrun = lrun * expf(mrun - mx) + add;
-        mrun = mx;
+      for (int e = 0; e < 4; ++e) {
+        const int64_t rel = tb + 4 * q4 + e;
+        const float sv = c[e] * a.sm_scale;
+        const bool ok = r16 < G && rel < nrel;
+        if (ok) sc_lds[(int64_t)r16 * cap + rel] = sv;
+        mrun = ok ? fmaxf(mrun, sv) : mrun;
       }
     }
   }
   EK_ATTN_MARK(21);
-  // merge over the four lane rows of a head, then over the waves
-#pragma unroll
-  for (int o = 16; o < EK_WAVE; o <<= 1) {
-    const float m2 = __shfl_xor(mrun, o, EK_WAVE);
-    const float l2 = __shfl_xor(lrun, o, EK_WAVE);
-    merge_ml(mrun, lrun, m2, l2);
-  }
+  // row max: over the four lane rows of a head, then over the waves
+  mrun = fmaxf(mrun, __shfl_xor(mrun, 16, EK_WAVE));
+  mrun = fmaxf(mrun, __shfl_xor(mrun, 32, EK_WAVE));
   EK_ATTN_MARK(22);
-  if (q4 == 0 && r16 < G) {
-    stm[wave][r16] = mrun;
-    stl[wave][r16] = lrun;
-  }
+  if (q4 == 0 && r16 < G) stm[wave][r16] = mrun;
   __syncthreads();
   EK_ATTN_MARK(17);
-  // p = bf16(exp(s - M) / L) in place, once per score: thread -> head tid % G
+  // pass 2: e = exp(s - M) in place and its sum L (thread -> head tid % G,
+  // keys tid / G + k FNT / G; the sum in a fixed order), then
+  // p = bf16(e / L) -- the reference fallback's rounding point
   {
     const int g = tid % G;
-    float M = stm[0][g], Lsum = stl[0][g];
+    float M = stm[0][g];
 #pragma unroll
-    for (int w = 1; w < FNW; ++w) merge_ml(M, Lsum, stm[w][g], stl[w][g]);
+    for (int w = 1; w < FNW; ++w) M = fmaxf(M, stm[w][g]);
     float* row = sc_lds + (int64_t)g * cap;
-    for (int64_t n = tid / G; n < nrel; n += FNT / G) row[n] = rbf(expf(row[n] - M) / Lsum);
+    float lsum = 0.f;
+    for (int64_t n = tid / G; n < nrel; n += FNT / G) {
+      const float ev = expf(row[n] - M);
+      row[n] = ev;
+      lsum += ev;
+    }
+    // threads with the same head: lanes l, l + G, l + 2G, ... of each wave
+#pragma unroll
+    for (int o = G; o < EK_WAVE; o <<= 1) lsum += __shfl_xor(lsum, o, EK_WAVE);
+    if (lane < G) stl[wave][lane] = lsum;
+    __syncthreads();
+    float Lsum = stl[0][g];
+#pragma unroll
+    for (int w = 1; w < FNW; ++w) Lsum += stl[w][g];
+    for (int64_t n = tid / G; n < nrel; n += FNT / G) row[n] = rbf(row[n] / Lsum);
   }
   __syncthreads();
   EK_ATTN_MARK(18);
