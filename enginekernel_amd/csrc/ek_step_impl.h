@@ -331,8 +331,9 @@ __device__ __forceinline__ void l2_touch(const Gp& pn, uint32_t& sink) {
 // is refilled, right after its chunk is consumed, with the item NB places
 // ahead, so NB chunks stay in flight and a refill never waits for anything
 // but its own slot's previous load. The ring holds items 0 .. NB-1 on entry
-// when prefetch_phase loaded them. Loads past the end re-read item 0 (never
-// consumed).
+// when prefetch_phase loaded them. Refills past the wave's last item (every
+// slot is refilled, so that the loads stay countable at compile time and NB
+// stay in flight) re-read that last item, which the L2 has just fetched.
 __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t* xs, float* part) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const Span sp = make_span(P, wave);
@@ -349,7 +350,7 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
     for (int u = 0; u < NB; ++u) {
       acc = dot8_acc(ring.r[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
       const int kn = k0 + u + NB;
-      ring.r[u] = ld16(span_item(sp, sp.i0 + (kn < n ? kn : 0)) + loff);
+      ring.r[u] = ld16(span_item(sp, sp.i0 + (kn < n ? kn : n - 1)) + loff);
       if (ch == P.C - 1) {
         const float sum = wave_sum_dpp(acc);
         if (lane == 0) part[r * SNW + wave] = sum;
@@ -684,7 +685,10 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   ring.nready = 0;
 #pragma unroll
   for (int u = 0; u < NB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
-  uint32_t gw[NGW];
+  // norm gains, loaded a phase ahead of their use: gw1 = input norm of the
+  // coming layer (the final norm after the last), gw2 = post-attention norm
+  uint32_t gw1[NGW], gw2[NGW];
+  load_gain(reinterpret_cast<const bf16_t*>(a.lw[LW_LN1]), h, gw1);
 
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
@@ -702,7 +706,6 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
 
     // ---- r = (layer 0) embed[token] | r + down(l-1); norm; qkv
     zero_part(part, part_n);
-    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN1]), h, gw);
     if (l == 0) {
       int64_t t = a.tokens[0];
       t = t < 0 ? 0 : (t >= a.vocab ? a.vocab - 1 : t);
@@ -712,11 +715,11 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
         rr[2 * i] = lo_bf(x);
         rr[2 * i + 1] = hi_bf(x);
       }
-      add_norm(rr, nullptr, gw, h, kpad_of(h), a.eps, xs, s_red);
+      add_norm(rr, nullptr, gw1, h, kpad_of(h), a.eps, xs, s_red);
     } else {
       const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
       if (!__syncthreads_and(ok)) return;
-      add_norm(rr, xs32, gw, h, kpad_of(h), a.eps, xs, s_red);
+      add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
     }
     __syncthreads();
     EK_TS(1);
@@ -734,6 +737,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     prefetch_phase<PF>(gg, ring);
     uint32_t sink = 0;
     l2_touch(gg, sink);
+    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
     EK_TS(4);
     // ---- o projection
     zero_part(part, part_n);
@@ -754,12 +758,14 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     // ---- r = r + o; norm; gate/up; SwiGLU
     __syncthreads();
     zero_part(part, part_n);
-    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw);
     {
       const bool ok = ll_read(LinSrc{o_ll}, h / 2, ep, xs32, a.err, a.spin);
       if (!__syncthreads_and(ok)) return;
     }
-    add_norm(rr, xs32, gw, h, kpad_of(h), a.eps, xs, s_red);
+    add_norm(rr, xs32, gw2, h, kpad_of(h), a.eps, xs, s_red);
+    // the next input norm's gain loads with the gate/up stream
+    load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm,
+              h, gw1);
     __syncthreads();
     EK_TS(9);
     gemv_phase(gg, ring, xs, part);
@@ -798,12 +804,11 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   EK_TS(0);
   llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
   zero_part(part, part_n);
-  load_gain(a.fnorm, h, gw);
   {
     const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
     if (!__syncthreads_and(ok)) return;
   }
-  add_norm(rr, xs32, gw, h, kpad_of(h), a.eps, xs, s_red);
+  add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
   __syncthreads();
   EK_TS(1);
   const Gp gl = on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn);

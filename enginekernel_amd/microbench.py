@@ -1,0 +1,258 @@
+"""Per-kernel measurements of the decode path on one MI355X, beside the
+batch-1 end-to-end figure of bench.py:
+
+  config 2  the decode projections one launch at a time: each weight shape
+            of the Qwen3-4B decode at batch 1 and 4, through the entry point
+            the per-kernel decode uses for it (gemv, gemv_swiglu, gemv_parts),
+            over enough distinct weight copies that every timed round reads
+            at least 512 MB (the 256 MB Infinity Cache holds nothing of it).
+  config 3  decode attention over one layer's cache: q [1, 32, 128], K/V
+            [1, 8, L, 128] bf16 ~N(0, 1), L in {512, 4096, 16384, 32768},
+            swept over the split count, again over copies that defeat the
+            Infinity Cache.
+  config 5  batch 8, left-padded prompts of U[64, 2048] random ids (seed 2),
+            256 greedy tokens through the per-kernel captured graph, cache
+            capacity 8192.
+
+Every figure is HIP-event time on the launching stream divided by the
+launches inside the timed region; bytes are algorithmic (each weight, key,
+value, activation and output byte once)."""
+
+from __future__ import annotations
+
+import math
+import os
+import time
+
+PEAK_HBM = 8.0e12
+CACHE_DEFEAT = 512 << 20   # bytes each timed round touches (> the 256 MB Infinity Cache)
+
+# (name, N, K, kind, copies): kind "gemv" = bf16 out, "swiglu" = the fused
+# gate/up with SiLU*up epilogue (N counts gate+up rows), "parts" = fp32 split-K
+# partials. Copies as in the reference's sweep (gemv_sweep.py:94 analogue).
+GEMV_SHAPES = (
+    ("qkv", 6144, 2560, "gemv", 17),
+    ("gate_up", 19456, 2560, "swiglu", 6),
+    ("o", 2560, 4096, "parts", 25),
+    ("down", 2560, 9728, "parts", 11),
+    ("lm_head", 151936, 2560, "gemv", 1),
+)
+ATTN_LENGTHS = (512, 4096, 16384, 32768)
+ATTN_SPLITS = (1, 2, 4, 8, 16, 32, 64, 128)
+
+
+def gemv_bytes(kind: str, n: int, k: int, b: int, sk: int = 1) -> int:
+    """Algorithmic bytes of one launch: W once (2NK), x (2BK) and the output
+    (bf16 [B, N], bf16 [B, N/2] after SwiGLU, or fp32 [sk, B, N] partials)."""
+    out = {"gemv": 2 * b * n, "swiglu": 2 * b * (n // 2), "parts": 4 * sk * b * n}[kind]
+    return 2 * n * k + 2 * b * k + out
+
+
+def gemv_floor_us(n: int, k: int) -> float:
+    """The weight stream alone at the 8 TB/s spec peak."""
+    return 2 * n * k / PEAK_HBM * 1e6
+
+
+def attn_bytes(length: int, n_q: int = 32, n_kv: int = 8, d: int = 128) -> int:
+    """K and V rows of the attended keys plus q in and the output out."""
+    return 2 * n_kv * d * 2 * length + 2 * (2 * n_q * d)
+
+
+def _timed(fn, reps: int) -> float:
+    """Seconds per call of fn: fn (a round of launches) is captured once as
+    a HIP graph, so host launch overhead stays out of the figure, and the
+    graph is replayed `reps` times between HIP events on the replay stream."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def gemv_sweep(batches=(1, 4), rounds: int = 10, log=print):
+    """Config 2. Returns one record per (shape, batch)."""
+    import torch
+    from enginekernel_amd import ek_kernels as K
+
+    dev = torch.device("cuda:0")
+    out = []
+    for name, n, k, kind, copies in GEMV_SHAPES:
+        g = torch.Generator(device=dev).manual_seed(0)
+        ws = [torch.empty(n, k, dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g)
+              for _ in range(copies)]
+        for b in batches:
+            x = torch.empty(b, k, dtype=torch.bfloat16, device=dev).normal_(0, 0.02, generator=g)
+            sk = K.parts_splits(b, k) if kind == "parts" else 1
+            if kind == "gemv":
+                y = torch.empty(b, n, dtype=torch.bfloat16, device=dev)
+                call = lambda w: K.gemv(x, w, out=y)
+            elif kind == "swiglu":
+                call = lambda w: K.gemv_swiglu(x, w)
+            else:
+                p = torch.empty(sk, b, n, dtype=torch.float32, device=dev)
+                call = lambda w: K.gemv_parts(x, w, sk=sk, out=p)
+
+            def one_round():
+                for w in ws:
+                    call(w)
+
+            t = _timed(one_round, rounds) / copies
+            nbytes = gemv_bytes(kind, n, k, b, sk)
+            rec = {"proj": name, "w": [n, k], "batch": b, "entry": {"gemv": "ek_gemv", "swiglu": "ek_gemv_swiglu",
+                                                                    "parts": "ek_gemv_parts"}[kind],
+                   "splits": sk, "copies": copies, "us": round(t * 1e6, 2),
+                   "floor_us": round(gemv_floor_us(n, k), 2), "bytes": nbytes,
+                   "GBps": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / PEAK_HBM, 4)}
+            log(f"gemv {name:8s} B={b} {rec['us']:8.2f} us  {rec['GBps']:7.1f} GB/s  ({rec['frac']:.1%})")
+            out.append(rec)
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
+def attn_sweep(lengths=ATTN_LENGTHS, splits=ATTN_SPLITS, reps: int = 20, log=print):
+    """Config 3. One record per (L, splits); rows of the fused single-launch
+    path (L <= 2048, where the split count is unused) are timed once."""
+    import torch
+    from enginekernel_amd import ek_kernels as K
+
+    dev = torch.device("cuda:0")
+    n_q, n_kv, d = 32, 8, 128
+    scale = d ** -0.5
+    out = []
+    for length in lengths:
+        per = attn_bytes(length)
+        copies = max(4, math.ceil(CACHE_DEFEAT / per))
+        g = torch.Generator(device=dev).manual_seed(0)
+        caches = [(torch.empty(1, n_kv, length, d, dtype=torch.bfloat16, device=dev).normal_(generator=g),
+                   torch.empty(1, n_kv, length, d, dtype=torch.bfloat16, device=dev).normal_(generator=g))
+                  for _ in range(copies)]
+        q = torch.empty(1, n_q, d, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        seq = torch.full((1,), length, dtype=torch.int64, device=dev)
+        start = torch.zeros(1, dtype=torch.int32, device=dev)
+        fused = 4 * length * 4 <= 32 * 1024
+        for sp in (splits[:1] if fused else splits):
+            chunk = K._cdiv(length, sp)
+            ws = K.make_workspace(1, n_q, n_kv, d, length, dev, splits=sp, chunk=chunk)
+
+            def one_round():
+                for kc, vc in caches:
+                    K.flash_decode(q, kc, vc, seq, start, ws, scale)
+
+            t = _timed(one_round, reps) / copies
+            rec = {"L": length, "splits": 0 if fused else sp, "path": "fused" if fused else "scores+pv",
+                   "copies": copies, "us": round(t * 1e6, 2), "floor_us": round(per / PEAK_HBM * 1e6, 2),
+                   "bytes": per, "GBps": round(per / t / 1e9, 1), "frac": round(per / t / PEAK_HBM, 4)}
+            log(f"attn L={length:6d} splits={rec['splits']:4d} {rec['us']:8.2f} us  {rec['GBps']:7.1f} GB/s")
+            out.append(rec)
+        del caches
+        torch.cuda.empty_cache()
+    return out
+
+
+def batch8_prompts(vocab: int, b: int = 8, seed: int = 2, lo: int = 64, hi: int = 2048):
+    """Config 5's prompts: lengths U[lo, hi], ids U[0, vocab), one generator."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (b,), generator=g).tolist()
+    return [torch.randint(0, vocab, (n,), generator=g).tolist() for n in lens]
+
+
+def batch8_bytes(w_bytes: int, kv_row: int, attended: int) -> int:
+    """Algorithmic bytes of one batch step: every weight once, plus the K/V
+    rows of every attended key of every row (kv_row bytes per key)."""
+    return w_bytes + kv_row * attended
+
+
+def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
+    """Config 5 on the Qwen3-4B architecture. Returns one record."""
+    import torch
+    from enginekernel_amd import checkpoint as C
+    from enginekernel_amd.ek_model import Qwen3
+    from enginekernel_amd.engine import _FastEngine
+
+    dev = torch.device("cuda:0")
+    cfg = dict(C.QWEN3_4B)
+    t0 = time.perf_counter()
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+    torch.cuda.synchronize()
+    log(f"config 5: weights ready in {time.perf_counter() - t0:.1f}s")
+    eng = _FastEngine(model=model)
+    prompts = batch8_prompts(cfg["vocab_size"])
+    b = len(prompts)
+    steps = tokens - 1
+    with torch.inference_mode():
+        ids, pos, pad, s, bias = eng._pack(prompts)
+        eng._ensure_cache(b, cap)
+        graph = eng._get_graph(b, s + tokens)
+        first = eng._first_token(ids, pos, b, s, bias)
+        pad_t = torch.as_tensor(pad, dtype=torch.int32)
+        graph.tokens.copy_(first)
+        graph.positions.copy_((s - pad_t).to(torch.int64))
+        graph.start_t.copy_(pad_t)
+        graph.len_t.fill_(s)
+        graph.step_idx.zero_()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            graph.graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        step_s = e0.elapsed_time(e1) / 1e3 / steps
+        model.check_step_error()
+        if graph.step_idx.item() != steps:
+            raise RuntimeError("graph step counter out of step with the replays")
+    w_bytes = C.weight_bytes_per_token(cfg)
+    kv_row = 2 * cfg["num_hidden_layers"] * cfg["num_key_value_heads"] * cfg["head_dim"] * 2
+    # step j (1-based) attends keys [pad_b, s + j) of row b
+    attended = sum(sum(s + j - p for p in pad) for j in range(1, steps + 1)) / steps
+    nbytes = batch8_bytes(w_bytes, kv_row, attended)
+    rec = {"batch": b, "prompt_lens": [len(p) for p in prompts], "padded_len": s, "cache_cap": eng.cache_s,
+           "graph_bucket": graph.bucket, "tokens": tokens, "timed_replays": steps,
+           "ms_per_step": round(step_s * 1e3, 4), "tokens_per_s": round(b / step_s, 1),
+           "bytes_per_step": int(nbytes), "weight_frac": round(w_bytes / step_s / PEAK_HBM, 4),
+           "weight_kv_frac": round(nbytes / step_s / PEAK_HBM, 4)}
+    log(f"config 5: {step_s * 1e3:.4f} ms/step, {rec['tokens_per_s']} tok/s, "
+        f"weights {rec['weight_frac']:.1%} / weights+KV {rec['weight_kv_frac']:.1%} of 8 TB/s")
+    return rec
+
+
+def run(config: int, log=print) -> dict:
+    """One JSON-ready record for config 2, 3 or 5."""
+    import torch
+    if not torch.cuda.is_available():
+        raise RuntimeError("the microbenchmarks need a GPU")
+    if config == 2:
+        return {"metric": "decode GEMV per-launch time and HBM fraction (config 2)", "unit": "us",
+                "higher_is_better": False, "dtype": "bf16", "data": "synthetic ~N(0,0.02), seed 0",
+                "config": {"workload": "config 2: Qwen3-4B decode projections, B in {1, 4}"},
+                "results": gemv_sweep(log=log)}
+    if config == 3:
+        return {"metric": "decode attention per-launch time and HBM fraction (config 3)", "unit": "us",
+                "higher_is_better": False, "dtype": "bf16", "data": "synthetic q, K, V ~N(0,1), seed 0",
+                "config": {"workload": "config 3: one layer, 32/8 heads, D 128, L swept, splits swept"},
+                "results": attn_sweep(log=log)}
+    if config == 5:
+        return {"metric": "batch-8 decode tokens/s and % of HBM roofline (config 5)", "unit": "tokens/s",
+                "higher_is_better": True, "dtype": "bf16",
+                "data": "synthetic (random-init weights seed 0, prompts seed 2)",
+                "config": {"workload": "config 5: Qwen3-4B architecture, batch 8 ragged, per-kernel graph"},
+                "results": [batch8_decode(log=log)]}
+    raise ValueError(f"no microbenchmark for config {config}")

@@ -135,6 +135,19 @@ def test_decode_parity_4b_shapes(dev):
         assert max(e for e, _ in res) <= 2e-2, res
 
 
+def test_decode_parity_4b_shapes_batch8_ragged(dev):
+    """The batch of config 5 (eight left-padded rows, the kernels' widest
+    batch tile) at every Qwen3-4B shape with two layers: prompt lengths
+    U[16, 300] (seed 2), 6 teacher-forced steps."""
+    from enginekernel_amd.microbench import batch8_prompts
+    cfg = dict(MID_4B)
+    tensors = C.random_weights(cfg, seed=0)
+    prompts = batch8_prompts(cfg["vocab_size"], lo=16, hi=300)
+    assert len({len(p) for p in prompts}) > 1
+    res = _decode_parity(cfg, tensors, prompts, 6, dev)
+    assert max(e for e, _ in res) <= 2e-2, res
+
+
 def test_engine_4b_shapes_tokens(dev):
     """Free-running greedy through the captured graph at the 4B shapes vs the
     oracle loop; a divergence is accepted only at a near-tie, and the
