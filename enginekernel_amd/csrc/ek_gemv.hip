@@ -4,7 +4,11 @@
 // Every entry point takes two tuning arguments: rpw (output rows per wave,
 // 1, 2 or 4; 0 = default) and blocks (the grid cap: workgroups loop over row
 // groups, so a grid of a few workgroups per CU streams any height; 0 =
-// default of 4 per CU). Neither changes results.
+// default of 4 per CU). Both apply to the FMA kernel. Launches of 2..8 batch
+// rows whose per-split K is a multiple of 128 take the matrix-core kernel
+// (own tiles and grid; the tuning arguments are ignored) unless rpw < 0,
+// which forces the FMA kernel. Neither changes results beyond fp32 summation
+// order.
 
 #include <cstring>
 
@@ -42,6 +46,28 @@ int cu_count() {
   return cache[dev];
 }
 
+// The matrix-core kernel's grid: one 512-thread workgroup per CU at most,
+// every wave the same number of 4-row tiles.
+int64_t mfma_grid(int64_t n) {
+  const int64_t ntiles = (n + MT - 1) / MT;
+  const int64_t cap = (int64_t)cu_count() * MNW;   // waves
+  const int64_t per = (ntiles + cap - 1) / cap;    // tiles per wave
+  return (ntiles + per * MNW - 1) / (per * MNW);
+}
+
+// whether a launch takes the matrix-core kernel
+bool use_mfma(int m, int64_t ks, int64_t rpw) { return m >= 2 && rpw >= 0 && ks % MCH == 0; }
+
+// ring depth of the matrix-core kernel: the deepest that divides the chunks
+// per tile, at most 20 loads in flight per wave (10 per row tile for the
+// gate/up pairs)
+int mfma_nb(int64_t chunks, bool pair) {
+  static const int deep[] = {20, 19, 16, 10, 8, 5, 4};
+  for (int nb : deep)
+    if ((!pair || nb <= 10) && chunks % nb == 0) return nb;
+  return 1;
+}
+
 // Launch one GEMV-family kernel. sk > 1 splits the reduction over
 // blockIdx.y (EPI_PARTS only). The grid width used goes to *gx_out.
 hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int64_t rpw, int64_t blocks,
@@ -61,7 +87,31 @@ hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int64
   const size_t lds = (size_t)bm * p.ks * sizeof(bf16_t);
   if (lds > kMaxLds)
     return ek_fail(hipErrorInvalidValue, "gemv: batch rows x K exceed the 48 KiB activation stage (split K)");
-  if (rpw <= 0) rpw = (epi == EPI_ARGMAX) ? 4 : 1;
+  if (use_mfma(p.m, p.ks, rpw)) {
+    const int64_t gx = mfma_grid(p.n);
+    if (gx_out) *gx_out = gx;
+    const int nb = mfma_nb(p.ks / MCH, epi == EPI_SWIGLU);
+    const size_t mlds = (size_t)bm * mfma_xld(p.ks) * sizeof(bf16_t);
+    dim3 grid((unsigned)gx, (unsigned)sk);
+#define EK_CASE(PR, EP) \
+  if (pro == PR && epi == EP) return launch_mfma_pair<PR, EP>(p, bm, nb, grid, mlds, st);
+    EK_CASE(PRO_X, EPI_BF16)
+    EK_CASE(PRO_X, EPI_PARTS)
+    EK_CASE(PRO_X, EPI_SWIGLU)
+    EK_CASE(PRO_X, EPI_ARGMAX)
+    EK_CASE(PRO_NORM, EPI_BF16)
+    EK_CASE(PRO_NORM, EPI_SWIGLU)
+    EK_CASE(PRO_ADD_NORM, EPI_BF16)
+    EK_CASE(PRO_ADD_NORM, EPI_SWIGLU)
+    EK_CASE(PRO_PARTS, EPI_BF16)
+    EK_CASE(PRO_PARTS, EPI_SWIGLU)
+    EK_CASE(PRO_PARTS, EPI_ARGMAX)
+    EK_CASE(PRO_EMBED, EPI_BF16)
+#undef EK_CASE
+    return ek_fail(hipErrorInvalidValue, "gemv: unsupported prologue/epilogue pair");
+  }
+  if (rpw < 0) rpw = -rpw;   // -r: the FMA kernel forced, r rows per wave
+  if (rpw == 0) rpw = (epi == EPI_ARGMAX) ? 4 : 1;
   if (rpw != 1 && rpw != 2 && rpw != 4) return ek_fail(hipErrorInvalidValue, "gemv: rows per wave must be 1, 2 or 4");
   const int64_t rows_per_grp = (int64_t)NWAVE * rpw;
   const int64_t ngroups = (p.n + rows_per_grp - 1) / rows_per_grp;
@@ -252,11 +302,12 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
   if (m < 1 || m > 8 || vocab < 1) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: m must be 1..8");
   if (st_tokens && (!st_positions || !st_out || !st_step))
     return ek_fail(hipErrorInvalidValue, "lm_head_argmax: step state needs tokens, positions, out and step");
-  if (rpw <= 0) rpw = 4;
-  if (rpw != 1 && rpw != 2 && rpw != 4) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: rpw must be 1, 2 or 4");
+  const bool force_fma = rpw < 0;
+  int64_t r = rpw < 0 ? -rpw : rpw == 0 ? 4 : rpw;
+  if (r != 1 && r != 2 && r != 4) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: rpw must be 1, 2 or 4");
   if (blocks <= 0) blocks = 4 * (int64_t)cu_count();
-  const int64_t groups = (vocab + NWAVE * rpw - 1) / (NWAVE * rpw);
-  const int64_t gx = groups < blocks ? groups : blocks;
+  const int64_t groups = (vocab + NWAVE * r - 1) / (NWAVE * r);
+  const int64_t gx = use_mfma((int)m, k, force_fma ? -r : r) ? mfma_grid(vocab) : groups < blocks ? groups : blocks;
   if (gx * m > am_cap) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: partial buffer too small");
   GemvParams p = zero_params();
   p.w = (const bf16_t*)w; p.ldw = ldw; p.n = vocab; p.m = (int)m;
@@ -269,7 +320,7 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
   const int pro = parts ? PRO_PARTS : PRO_X;
   hipStream_t st = (hipStream_t)stream;
   int64_t used = 0;
-  hipError_t e = run_gemv(pro, EPI_ARGMAX, p, k, 1, rpw, blocks, st, &used);
+  hipError_t e = run_gemv(pro, EPI_ARGMAX, p, k, 1, force_fma ? -r : r, blocks, st, &used);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(NTHR), 0, st, (const float*)am_val,
                      (const int32_t*)am_idx, used, (int)m, out_tok, st_tokens, st_positions, st_out, st_step,

@@ -63,115 +63,177 @@ struct GemvParams {
 };
 
 // ----------------------------------------------------------------------------
-// prologue: xs[b][e] (bf16) for b < BM, e < ks
+// prologue: xs[b * xld + e] (bf16) for b < BM, e < ks
+//
+// The BM x ks/8 chunks of 8 elements are dealt out flat over the threads
+// (job j -> row j / nch, chunk j % nch) and taken GJ jobs at a time with
+// every load of the group issued before any is used, so a whole stage costs
+// a few memory round trips rather than one per row. Addresses of jobs past
+// the end are clamped to a valid chunk (read, never stored), so no load sits
+// under a lane condition. The norm variants store the pre-norm row r first,
+// then take each row's sum of squares from the stage (one wave per row) and
+// normalise in place.
 // ----------------------------------------------------------------------------
-template <int PRO, int BM>
-__device__ __forceinline__ void prologue(const GemvParams& p, bf16_t* xs, float (*red)[BM]) {
+constexpr int GJ = 4;   // jobs per thread in flight
+
+template <int PRO, int BM, int NT = NTHR>
+__device__ __forceinline__ void prologue(const GemvParams& p, bf16_t* xs, int64_t xld, float (*red)[BM]) {
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int64_t ks = p.ks;
   const int64_t nch = ks >> 3;
   const int64_t kbase = (int64_t)blockIdx.y * ks;
-  if constexpr (PRO == PRO_X) {
-    for (int b = 0; b < BM; ++b) {
-      for (int64_t c = tid; c < nch; c += NTHR) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (b < p.m) v = ld16(p.x + b * p.ldx + kbase + c * 8);
-        *reinterpret_cast<uint4*>(xs + b * ks + c * 8) = v;
-      }
+  const int64_t jobs = (int64_t)BM * nch;
+  const bool writer = (blockIdx.x == 0 && blockIdx.y == 0);
+
+  // pass 1: x (PRO_X) or the pre-norm row r into the stage
+  for (int64_t j0 = tid; j0 < jobs; j0 += (int64_t)GJ * NT) {
+    int bj[GJ];
+    int64_t cj[GJ];
+    bool ok[GJ];
+#pragma unroll
+    for (int g = 0; g < GJ; ++g) {
+      int64_t j = j0 + (int64_t)g * NT;
+      ok[g] = j < jobs;
+      j = ok[g] ? j : jobs - 1;
+      bj[g] = (int)(j / nch);
+      cj[g] = j - (int64_t)bj[g] * nch;
+      ok[g] = ok[g] && bj[g] < p.m;
     }
-    return;
-  } else {
-    // pass 1: r (the pre-norm row, bf16) into xs, sum of squares per row
-    const bool writer = (blockIdx.x == 0 && blockIdx.y == 0);
-    float ss[BM];
+    // rows >= m read row 0 (zeroed below)
+    int br[GJ];
 #pragma unroll
-    for (int b = 0; b < BM; ++b) ss[b] = 0.f;
+    for (int g = 0; g < GJ; ++g) br[g] = bj[g] < p.m ? bj[g] : 0;
+    uint4 out[GJ];
+    if constexpr (PRO == PRO_X) {
+      uint4 v[GJ];
 #pragma unroll
-    for (int b = 0; b < BM; ++b) {
-      if (b >= p.m) continue;
-      const bf16_t* src = nullptr;
-      if constexpr (PRO == PRO_EMBED) {
-        int64_t t = p.tokens[b];
-        t = t < 0 ? 0 : (t >= p.vocab ? p.vocab - 1 : t);
-        src = p.embed + t * p.lde;
-      }
-      for (int64_t c = tid; c < nch; c += NTHR) {
-        float r[8];
+      for (int g = 0; g < GJ; ++g) v[g] = ld16(p.x + br[g] * p.ldx + kbase + cj[g] * 8);
+#pragma unroll
+      for (int g = 0; g < GJ; ++g) out[g] = ok[g] ? v[g] : make_uint4(0, 0, 0, 0);
+    } else if constexpr (PRO == PRO_NORM || PRO == PRO_EMBED) {
+      uint4 v[GJ];
+#pragma unroll
+      for (int g = 0; g < GJ; ++g) {
+        const bf16_t* src;
         if constexpr (PRO == PRO_EMBED) {
-          unpack8(ld16(src + c * 8), r);
-        } else if constexpr (PRO == PRO_NORM) {
-          unpack8(ld16(p.x + b * p.ldx + c * 8), r);
-        } else if constexpr (PRO == PRO_ADD_NORM) {
-          float xv[8], rv[8];
-          unpack8(ld16(p.x + b * p.ldx + c * 8), xv);
-          unpack8(ld16(p.res + b * p.ldr + c * 8), rv);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) r[j] = rbf(rv[j] + xv[j]);
-        } else {  // PRO_PARTS
-          float sum[8];
-          const float* pp = p.parts + b * ks + c * 8;
-          float4 a0 = *reinterpret_cast<const float4*>(pp);
-          float4 a1 = *reinterpret_cast<const float4*>(pp + 4);
-          sum[0] = a0.x; sum[1] = a0.y; sum[2] = a0.z; sum[3] = a0.w;
-          sum[4] = a1.x; sum[5] = a1.y; sum[6] = a1.z; sum[7] = a1.w;
-          for (int s = 1; s < p.sk_in; ++s) {
-            const float* q = pp + s * p.parts_ss;
-            float4 b0 = *reinterpret_cast<const float4*>(q);
-            float4 b1 = *reinterpret_cast<const float4*>(q + 4);
-            sum[0] += b0.x; sum[1] += b0.y; sum[2] += b0.z; sum[3] += b0.w;
-            sum[4] += b1.x; sum[5] += b1.y; sum[6] += b1.z; sum[7] += b1.w;
-          }
-          float rv[8];
-          unpack8(ld16(p.res + b * p.ldr + c * 8), rv);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) r[j] = rbf(rv[j] + rbf(sum[j]));
+          int64_t t = p.tokens[br[g]];
+          t = t < 0 ? 0 : (t >= p.vocab ? p.vocab - 1 : t);
+          src = p.embed + t * p.lde;
+        } else {
+          src = p.x + br[g] * p.ldx;
         }
-        uint4 pk = make_uint4(pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7]));
-        *reinterpret_cast<uint4*>(xs + b * ks + c * 8) = pk;
-        if (PRO != PRO_NORM && writer && p.res_out)
-          *reinterpret_cast<uint4*>(p.res_out + b * p.ldro + c * 8) = pk;
+        v[g] = ld16(src + cj[g] * 8);
+      }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss[b] = fmaf(r[j], r[j], ss[b]);
+      for (int g = 0; g < GJ; ++g) out[g] = ok[g] ? v[g] : make_uint4(0, 0, 0, 0);
+    } else if constexpr (PRO == PRO_ADD_NORM) {
+      uint4 xv[GJ], rv[GJ];
+#pragma unroll
+      for (int g = 0; g < GJ; ++g) {
+        xv[g] = ld16(p.x + br[g] * p.ldx + cj[g] * 8);
+        rv[g] = ld16(p.res + br[g] * p.ldr + cj[g] * 8);
+      }
+#pragma unroll
+      for (int g = 0; g < GJ; ++g) {
+        float a[8], r[8], o[8];
+        unpack8(xv[g], a);
+        unpack8(rv[g], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = rbf(r[e] + a[e]);
+        out[g] = ok[g] ? make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]))
+                       : make_uint4(0, 0, 0, 0);
+      }
+    } else {  // PRO_PARTS: r = bf16(res + bf16(sum_s parts_s)), two splits per round trip
+      float sum[GJ][8];
+      uint4 rv[GJ];
+#pragma unroll
+      for (int g = 0; g < GJ; ++g) {
+        rv[g] = ld16(p.res + br[g] * p.ldr + cj[g] * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum[g][e] = 0.f;
+      }
+      for (int s0 = 0; s0 < p.sk_in; s0 += 2) {
+        const bool two = s0 + 1 < p.sk_in;
+        float4 a[GJ][2], b2[GJ][2];
+#pragma unroll
+        for (int g = 0; g < GJ; ++g) {
+          const float* pp = p.parts + (int64_t)s0 * p.parts_ss + br[g] * ks + cj[g] * 8;
+          const float* pq = two ? pp + p.parts_ss : pp;
+          a[g][0] = *reinterpret_cast<const float4*>(pp);
+          a[g][1] = *reinterpret_cast<const float4*>(pp + 4);
+          b2[g][0] = *reinterpret_cast<const float4*>(pq);
+          b2[g][1] = *reinterpret_cast<const float4*>(pq + 4);
+        }
+#pragma unroll
+        for (int g = 0; g < GJ; ++g) {
+          sum[g][0] += a[g][0].x; sum[g][1] += a[g][0].y; sum[g][2] += a[g][0].z; sum[g][3] += a[g][0].w;
+          sum[g][4] += a[g][1].x; sum[g][5] += a[g][1].y; sum[g][6] += a[g][1].z; sum[g][7] += a[g][1].w;
+          if (two) {
+            sum[g][0] += b2[g][0].x; sum[g][1] += b2[g][0].y; sum[g][2] += b2[g][0].z; sum[g][3] += b2[g][0].w;
+            sum[g][4] += b2[g][1].x; sum[g][5] += b2[g][1].y; sum[g][6] += b2[g][1].z; sum[g][7] += b2[g][1].w;
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < GJ; ++g) {
+        float r[8], o[8];
+        unpack8(rv[g], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = rbf(r[e] + rbf(sum[g][e]));
+        out[g] = ok[g] ? make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]))
+                       : make_uint4(0, 0, 0, 0);
       }
     }
-    if constexpr (PRO == PRO_EMBED) {
-      if (writer && tid == 0 && p.len_t) {
-        int64_t len = *p.len_t;
-        for (int b = 0; b < p.m; ++b) p.slot_t[b] = len;
-        *p.len_t = len + 1;
-      }
+#pragma unroll
+    for (int g = 0; g < GJ; ++g) {
+      if (j0 + (int64_t)g * NT >= jobs) continue;
+      *reinterpret_cast<uint4*>(xs + bj[g] * xld + cj[g] * 8) = out[g];
+      if (PRO != PRO_X && PRO != PRO_NORM && writer && p.res_out && ok[g])
+        *reinterpret_cast<uint4*>(p.res_out + bj[g] * p.ldro + cj[g] * 8) = out[g];
     }
-    const int lane = tid & 63, wave = tid >> 6;
-#pragma unroll
-    for (int b = 0; b < BM; ++b) {
-      float v = wave_sum(ss[b]);
-      if (lane == 0) red[wave][b] = v;
+  }
+  if constexpr (PRO == PRO_X) return;
+
+  if constexpr (PRO == PRO_EMBED) {
+    if (writer && tid == 0 && p.len_t) {
+      int64_t len = *p.len_t;
+      for (int b = 0; b < p.m; ++b) p.slot_t[b] = len;
+      *p.len_t = len + 1;
     }
-    __syncthreads();
-    float rstd[BM];
+  }
+  __syncthreads();
+  // row statistics from the stage: wave w takes rows w, w + NT/64, ...
+  for (int b = wave; b < BM; b += NT / EK_WAVE) {
+    float ss = 0.f;
+    for (int64_t c = lane; c < nch; c += EK_WAVE) {
+      float r[8];
+      unpack8(*reinterpret_cast<const uint4*>(xs + b * xld + c * 8), r);
 #pragma unroll
-    for (int b = 0; b < BM; ++b) {
-      float t = 0.f;
-#pragma unroll
-      for (int w = 0; w < NWAVE; ++w) t += red[w][b];
-      float mean = t / (float)ks;
-      rstd[b] = 1.0f / sqrtf(mean + p.eps);
+      for (int e = 0; e < 8; ++e) ss = fmaf(r[e], r[e], ss);
     }
-    // pass 2: xn = bf16(w * bf16(r * rstd)); zero rows >= m
+    ss = wave_sum(ss);
+    if (lane == 0) red[0][b] = ss;
+  }
+  __syncthreads();
+  float rstd[BM];
 #pragma unroll
-    for (int b = 0; b < BM; ++b) {
-      for (int64_t c = tid; c < nch; c += NTHR) {
-        uint4* dst = reinterpret_cast<uint4*>(xs + b * ks + c * 8);
-        if (b >= p.m) { *dst = make_uint4(0, 0, 0, 0); continue; }
-        float r[8], g[8];
-        unpack8(*dst, r);
-        unpack8(ld16(p.nw + c * 8), g);
-        float o[8];
+  for (int b = 0; b < BM; ++b) rstd[b] = 1.0f / sqrtf(red[0][b] / (float)ks + p.eps);
+  // pass 2: xn = bf16(w * bf16(r * rstd)); rows >= m stay zero
+  for (int64_t j = tid; j < jobs; j += NT) {
+    const int b = (int)(j / nch);
+    const int64_t c = j - (int64_t)b * nch;
+    if (b >= p.m) continue;
+    uint4* dst = reinterpret_cast<uint4*>(xs + b * xld + c * 8);
+    float r[8], g[8], o[8];
+    unpack8(*dst, r);
+    unpack8(ld16(p.nw + c * 8), g);
+    float rs = rstd[0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = rbf(g[j] * rbf(r[j] * rstd[b]));
-        *dst = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
-      }
-    }
+    for (int bb = 1; bb < BM; ++bb) rs = b == bb ? rstd[bb] : rs;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = rbf(g[e] * rbf(r[e] * rs));
+    *dst = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
   }
 }
 
@@ -225,7 +287,7 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams p) {
       for (int r = 0; r < R2; ++r) wv[r][j] = (c < nch) ? ld16(wrow(g, r) + c * 8) : make_uint4(0, 0, 0, 0);
     }
   }
-  prologue<PRO, BM>(p, xs, red);
+  prologue<PRO, BM>(p, xs, ks, red);
   __syncthreads();
 
   for (; g < ngroups; g += gridDim.x) {
@@ -336,18 +398,246 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams p) {
 }
 
 // ----------------------------------------------------------------------------
+// the matrix-core kernel, for 2..8 batch rows
+//
+// At 2..8 rows the FMA kernel above runs out of issue slots (each weight
+// element costs a conversion and BM FMAs, each x element an LDS read per
+// row). Here v_mfma_f32_4x4x4_16b_bf16 does the products. Its 64 lanes are
+// 16 blocks of 4: lane l = 4 blk + j holds A[blk][row j][4 k], B[blk][4 k]
+// [column j] and C[blk][rows 0..3][column j]. A tile is 4 weight rows; lane
+// l loads 16 B of row j at k offset 8 blk of each 128-wide chunk, so one
+// load instruction reads 256 contiguous bytes of each of the 4 rows (a
+// pattern that streams HBM as well as whole 1 KiB rows do, where the 16x16
+// MFMA layout's 64-byte row pieces reach only about 60% of that), and two
+// MFMAs take its two halves. Block blk accumulates the k offsets 8 blk .. 8
+// blk + 7 of every chunk; at the tile's end the 16 blocks are added with
+// DPP row rotations and two cross-row shuffles, and lane (blk = e, j) holds
+// output row e of column j. The B operand is the batch rows' 16 bytes at the
+// same k from the LDS stage: columns 0..3 per MFMA, so 8 rows take two
+// column groups. Batch columns >= BM repeat a real row; their outputs are
+// dropped.
+//
+// The loads themselves are lane-contiguous (lanes 16 r .. 16 r + 15 read the
+// 256 B of row r, the pattern the memory pipeline coalesces best: with rows
+// interleaved over neighbouring lanes, as the MFMA layout has them, the
+// same bytes stream markedly slower), and four ds_bpermute per load move
+// piece blk of row j to lane 4 blk + j.
+//
+// Each wave streams whole tiles (no cross-wave reduction, no barrier after
+// the prologue): tiles gw, gw + W, ... for wave gw of W. A ring of NB loads
+// (per row tile) stays in flight: a slot is refilled right after its MFMAs
+// with the chunk NB places ahead in the wave's sequence (the next tile's
+// once this one runs out). NB divides the chunks per tile, so a tile always
+// ends at the last slot of a ring round. The norm prologues run before the
+// ring is filled (their loads would otherwise retire behind the weight
+// loads, which complete in order); the plain-x stage runs after it.
+// ----------------------------------------------------------------------------
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int MNT = 512;                 // threads of a matrix-core workgroup
+constexpr int MNW = MNT / EK_WAVE;
+constexpr int MT = 4;                    // weight rows per tile
+constexpr int MCH = 128;                 // K per chunk (one load instruction)
+
+__device__ __forceinline__ f32x4_t mfma4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
+  const s16x4_t a = __builtin_bit_cast(s16x4_t, make_uint2(a0, a1));
+  const s16x4_t b = __builtin_bit_cast(s16x4_t, make_uint2(b0, b1));
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// the stage's row stride (elements): rows 64 B apart modulo 256 B, so the
+// lanes of one k offset and different rows hit different banks
+__host__ __device__ inline int64_t mfma_xld(int64_t ks) { return ks + 32; }
+
+// sum over the 16 blocks of a wave (lanes with equal l % 4); every lane
+// gets the total of its column
+__device__ __forceinline__ float block_sum(float v) {
+  v = dpp_plus<0x128>(v);   // row_ror:8
+  v = dpp_plus<0x124>(v);   // row_ror:4
+  v += __shfl_xor(v, 16, EK_WAVE);
+  v += __shfl_xor(v, 32, EK_WAVE);
+  return v;
+}
+
+template <int PRO, int EPI, int BM, int NB, int NT = MNT>
+__global__ __launch_bounds__(NT) void gemv_mfma_kernel(GemvParams p) {
+  constexpr int NWV = NT / EK_WAVE;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  bf16_t* xs = reinterpret_cast<bf16_t*>(smem_raw);
+  constexpr int RT = (EPI == EPI_SWIGLU) ? 2 : 1;   // gate and up tiles side by side
+  constexpr int CG = BM > 4 ? 2 : 1;                // column groups of 4 batch rows
+  __shared__ float red[NWV][BM];
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int blk = lane >> 2, j4 = lane & 3;
+  const int lrow = lane >> 4, lpc = lane & 15;      // row and 16-byte piece this lane loads
+  const int src = (16 * j4 + blk) * 4;              // ds_bpermute source: row j4, piece blk
+  const int64_t ks = p.ks;
+  const int64_t xld = mfma_xld(ks);
+  const int C = (int)(ks / MCH);                    // chunks per tile
+  const int64_t ntiles = (p.n + MT - 1) / MT;
+  const int64_t W = (int64_t)gridDim.x * NWV;
+  const int64_t gw = (int64_t)blockIdx.x * NWV + wave;
+  const int64_t my_tiles = gw < ntiles ? (ntiles - 1 - gw) / W + 1 : 0;
+  const int64_t rounds = my_tiles * (C / NB);
+  const bf16_t* wbase = p.w + (int64_t)blockIdx.y * ks + lpc * 8;
+
+  // the weight row this lane loads in tile j (of this wave) and row tile t;
+  // rows past the end re-read the last row (their outputs are dropped)
+  auto wrow = [&](int64_t j, int t) -> const bf16_t* {
+    int64_t n = (gw + j * W) * MT + lrow;
+    n = n < p.n ? n : p.n - 1;
+    if (t == 1) n += p.up_off;
+    return wbase + n * p.ldw;
+  };
+
+  if constexpr (PRO != PRO_X) prologue<PRO, BM, NT>(p, xs, xld, red);
+  // the first round in the order the ring refills it (slot-major), so each
+  // slot's wait counts the same loads behind it as in every later round
+  uint4 ring[RT][NB];
+  if (rounds > 0) {
+    const bf16_t* w0[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) w0[t] = wrow(0, t);
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+#pragma unroll
+      for (int t = 0; t < RT; ++t) ring[t][u] = ld16(w0[t] + u * MCH);
+  }
+  if constexpr (PRO == PRO_X) prologue<PRO, BM, NT>(p, xs, xld, red);
+  __syncthreads();
+
+  const bf16_t* xr[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) xr[c] = xs + ((4 * c + j4) & (BM - 1)) * xld + blk * 8;
+  float best_v[CG];
+  int best_i[CG];
+#pragma unroll
+  for (int c = 0; c < CG; ++c) { best_v[c] = -INFINITY; best_i[c] = 0x7fffffff; }
+  f32x4_t acc[RT][CG];
+#pragma unroll
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int c = 0; c < CG; ++c) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int R = C / NB;   // ring rounds per tile
+  for (int64_t rd = 0; rd < rounds; ++rd) {
+    const int64_t j = rd / R;
+    const int c0 = (int)(rd - j * R) * NB;
+    const int64_t rn = rd + 1 < rounds ? rd + 1 : rd;   // the last round re-reads itself
+    const int64_t jn = rn / R;
+    const int cn0 = (int)(rn - jn * R) * NB;
+    const bf16_t* wn[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) wn[t] = wrow(jn, t) + cn0 * MCH;
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      uint4 xv[CG];
+#pragma unroll
+      for (int c = 0; c < CG; ++c) xv[c] = *reinterpret_cast<const uint4*>(xr[c] + (c0 + u) * MCH);
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        const uint4 g = ring[t][u];
+        uint4 w;
+        w.x = __builtin_amdgcn_ds_bpermute(src, (int)g.x);
+        w.y = __builtin_amdgcn_ds_bpermute(src, (int)g.y);
+        w.z = __builtin_amdgcn_ds_bpermute(src, (int)g.z);
+        w.w = __builtin_amdgcn_ds_bpermute(src, (int)g.w);
+        ring[t][u] = ld16(wn[t] + u * MCH);
+#pragma unroll
+        for (int c = 0; c < CG; ++c) {
+          acc[t][c] = mfma4(w.x, w.y, xv[c].x, xv[c].y, acc[t][c]);
+          acc[t][c] = mfma4(w.z, w.w, xv[c].z, xv[c].w, acc[t][c]);
+        }
+      }
+      // keep each slot's refill where it is: the scheduler would otherwise
+      // sink all refills below the round's MFMAs and drain the ring
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (c0 + NB < C) continue;
+
+    // ---- tile end: lane (blk = e < 4, j) takes row e of batch columns j, 4 + j
+    const int64_t n0 = (gw + j * W) * MT;
+#pragma unroll
+    for (int c = 0; c < CG; ++c) {
+      float v[RT];
+#pragma unroll
+      for (int t = 0; t < RT; ++t) {
+        float mine = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float tot = block_sum(acc[t][c][e]);
+          mine = blk == e ? tot : mine;
+        }
+        v[t] = mine;
+        acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      const int64_t n = n0 + blk;
+      const int b = 4 * c + j4;
+      if (blk < 4 && n < p.n && b < p.m) {
+        if constexpr (EPI == EPI_BF16) {
+          p.y[b * p.ldy + n] = (bf16_t)f2bf(v[0]);
+        } else if constexpr (EPI == EPI_PARTS) {
+          p.p_out[((int64_t)blockIdx.y * p.m + b) * p.n + n] = v[0];
+        } else if constexpr (EPI == EPI_SWIGLU) {
+          const float gt = rbf(v[0]);
+          const float u = rbf(v[RT - 1]);
+          const float sl = rbf(gt / (1.0f + expf(-gt)));
+          p.y[b * p.ldy + n] = (bf16_t)f2bf(sl * u);
+        } else {   // EPI_ARGMAX: this lane's rows of batch row b arrive in increasing order
+          const float lv = rbf(v[0]);
+          if (p.y) p.y[b * p.ldy + n] = (bf16_t)f2bf(lv);
+          if (lv > best_v[c] || best_i[c] == 0x7fffffff) { best_v[c] = lv; best_i[c] = (int)n; }
+        }
+      }
+    }
+  }
+
+  if constexpr (EPI == EPI_ARGMAX) {
+    // per-workgroup (value, index) partials: batch row b's candidates are
+    // lanes blk < 4, j = b % 4, column group b / 4 of every wave;
+    // ek_argmax_reduce finishes
+    __shared__ float abv[NWV][16][CG];
+    __shared__ int abi[NWV][16][CG];
+    if (lane < 16) {
+#pragma unroll
+      for (int c = 0; c < CG; ++c) { abv[wave][lane][c] = best_v[c]; abi[wave][lane][c] = best_i[c]; }
+    }
+    __syncthreads();
+    if (threadIdx.x < (unsigned)p.m) {
+      const int b = threadIdx.x;
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int w = 0; w < NWV; ++w)
+        for (int e = 0; e < 4; ++e) {
+          const float vv = abv[w][4 * e + (b & 3)][b >> 2];
+          const int ii = abi[w][4 * e + (b & 3)][b >> 2];
+          if (ii != 0x7fffffff && (bi == 0x7fffffff || vv > bv || (vv == bv && ii < bi))) { bv = vv; bi = ii; }
+        }
+      p.am_val[(int64_t)blockIdx.x * p.m + b] = bv;
+      p.am_idx[(int64_t)blockIdx.x * p.m + b] = bi;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // per-(prologue, epilogue) launchers, each defined in its own translation unit
 // (ek_gemv_inst.hip compiled once per pair)
 // ----------------------------------------------------------------------------
 template <int PRO, int EPI>
 hipError_t launch_pair(const GemvParams& p, int bm, int kpl, int rpw, dim3 grid, size_t lds, hipStream_t st);
+template <int PRO, int EPI>
+hipError_t launch_mfma_pair(const GemvParams& p, int bm, int nb, dim3 grid, size_t lds, hipStream_t st);
 
 // the pairs that exist (the build compiles ek_gemv_inst.hip once for each)
 #define EK_GEMV_PAIRS(X) \
   X(0, 0) X(0, 1) X(0, 2) X(0, 3) X(1, 0) X(1, 2) X(2, 0) X(2, 2) X(3, 0) X(3, 2) X(3, 3) X(4, 0)
-#define EK_DECL_PAIR(PR, EP) \
-  template <>              \
-  hipError_t launch_pair<PR, EP>(const GemvParams&, int, int, int, dim3, size_t, hipStream_t);
+#define EK_DECL_PAIR(PR, EP)                                                                \
+  template <>                                                                               \
+  hipError_t launch_pair<PR, EP>(const GemvParams&, int, int, int, dim3, size_t, hipStream_t); \
+  template <>                                                                               \
+  hipError_t launch_mfma_pair<PR, EP>(const GemvParams&, int, int, dim3, size_t, hipStream_t);
 EK_GEMV_PAIRS(EK_DECL_PAIR)
 #undef EK_DECL_PAIR
 

@@ -1,5 +1,6 @@
-// One (prologue, epilogue) pair of the GEMV family, instantiated over batch
-// tiles, chunks per lane and rows per wave. The build compiles this file
+// One (prologue, epilogue) pair of the GEMV family: the FMA kernel
+// instantiated over batch tiles, chunks per lane and rows per wave, and the
+// matrix-core kernel over batch tiles and ring depths. The build compiles this file
 // once per pair with -DEK_PRO=<prologue> -DEK_EPI=<epilogue> so that the
 // instantiations compile in parallel.
 
@@ -46,7 +47,45 @@ hipError_t launch_b(const GemvParams& p, int bm, int kpl, int rpw, dim3 grid, si
   }
 }
 
+template <int PRO, int EPI, int BM, int NB>
+hipError_t launch_m(const GemvParams& p, dim3 grid, size_t lds, hipStream_t st) {
+  hipLaunchKernelGGL((gemv_mfma_kernel<PRO, EPI, BM, NB>), grid, dim3(MNT), lds, st, p);
+  return hipGetLastError();
+}
+
+// ring depths (mfma_nb in ek_gemv.hip): up to 20 for single row tiles, up
+// to 10 for the gate/up pairs
+template <int PRO, int EPI, int BM>
+hipError_t launch_mn(const GemvParams& p, int nb, dim3 grid, size_t lds, hipStream_t st) {
+  if constexpr (EPI != EPI_SWIGLU) {
+    switch (nb) {
+      case 20: return launch_m<PRO, EPI, BM, 20>(p, grid, lds, st);
+      case 19: return launch_m<PRO, EPI, BM, 19>(p, grid, lds, st);
+      case 16: return launch_m<PRO, EPI, BM, 16>(p, grid, lds, st);
+      default: break;
+    }
+  }
+  switch (nb) {
+    case 10: return launch_m<PRO, EPI, BM, 10>(p, grid, lds, st);
+    case 8: return launch_m<PRO, EPI, BM, 8>(p, grid, lds, st);
+    case 5: return launch_m<PRO, EPI, BM, 5>(p, grid, lds, st);
+    case 4: return launch_m<PRO, EPI, BM, 4>(p, grid, lds, st);
+    case 1: return launch_m<PRO, EPI, BM, 1>(p, grid, lds, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
+
+template <>
+hipError_t launch_mfma_pair<EK_PRO, EK_EPI>(const GemvParams& p, int bm, int nb, dim3 grid, size_t lds,
+                                            hipStream_t st) {
+  switch (bm) {
+    case 2: return launch_mn<EK_PRO, EK_EPI, 2>(p, nb, grid, lds, st);
+    case 4: return launch_mn<EK_PRO, EK_EPI, 4>(p, nb, grid, lds, st);
+    default: return launch_mn<EK_PRO, EK_EPI, 8>(p, nb, grid, lds, st);
+  }
+}
 
 template <>
 hipError_t launch_pair<EK_PRO, EK_EPI>(const GemvParams& p, int bm, int kpl, int rpw, dim3 grid, size_t lds,

@@ -60,9 +60,13 @@ int ek_qk_norm_rope_kv(void* qkv, const void* qn, const void* kn, const void* co
                        int64_t ld_cs, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t csb, int64_t csh,
                        int64_t css, int64_t s_cap, int64_t m_per_batch, float eps, void* stream);
 
-/* GEMV-family tuning arguments (results do not depend on them): rpw =
- * output rows per wave (1, 2 or 4; 0 = default), blocks = grid cap (0 =
- * four workgroups per CU; workgroups loop over row groups). */
+/* GEMV-family tuning arguments (results do not depend on them beyond the
+ * fp32 summation order): rpw = output rows per wave of the FMA kernel (1, 2
+ * or 4; 0 = default), blocks = its grid cap (0 = four workgroups per CU;
+ * workgroups loop over row groups). Launches of 2..8 batch rows whose
+ * per-split K is a multiple of 128 run on the matrix cores (16-row MFMA
+ * tiles, their own grid) and ignore both, unless rpw is negative: -r forces
+ * the FMA kernel with r rows per wave. */
 
 /* gemv: y[m, n] = bf16(sum_k x[m, k] * w[n, k]) with fp32 accumulation.
  * Replaces engine/ek_kernels.py:1322-1347 (gemv, kernel :281-308). */

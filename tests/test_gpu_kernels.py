@@ -215,6 +215,48 @@ def test_norm_gemv_fused_prologues(dev, m):
     assert_rounded(y, O.rms_norm(emb[tok], nw, 1e-6), w, name="embed", min_equal=0.98)
 
 
+@pytest.mark.parametrize("m,n,k", [(2, 1001, 128), (5, 4099, 384), (7, 777, 640), (8, 2560, 2432),
+                                   (3, 2048, 2560), (6, 333, 3072), (2, 515, 4864)])
+def test_matrix_core_gemv_matches_fma_kernel(dev, m, n, k):
+    """The matrix-core GEMV (2..8 rows) against the exact product and the
+    FMA kernel (forced with a negative rows-per-wave argument): ragged tile
+    counts (N % 4 != 0), odd batch rows, one and two column groups, K / 128
+    chunks per tile of 1, 3, 5, 19, 20, 24 and 38 (ring depths 1, 5, 8, 10,
+    19, 20) and the bf16, SwiGLU, partials and argmax epilogues."""
+    g = _gen(m * 7 + n)
+    x = (torch.randn(m, k, generator=g) * 0.05).to(BF)
+    w = (torch.randn(2 * n, k, generator=g) * 0.05).to(BF)
+    xd, wd = x.to(dev), w.to(dev)
+    ys = {}
+    for rpw in (0, -1):                              # 0: matrix cores, -1: FMA kernel
+        y = torch.empty(m, n, dtype=BF, device=dev)
+        K.call("ek_gemv", K.ptr(xd), K.ptr(wd), K.ptr(y), m, n, k, k, k, n, rpw, 0, K.stream())
+        a = torch.empty(m, n, dtype=BF, device=dev)
+        K.call("ek_gemv_swiglu", K.ptr(xd), K.ptr(wd), K.ptr(a), m, n, k, k, k, n, rpw, 0, K.stream())
+        sk = 2 if k % 256 == 0 else 1
+        pt = torch.empty(sk, m, 2 * n, dtype=torch.float32, device=dev)
+        K.call("ek_gemv_parts", K.ptr(xd), K.ptr(wd), K.ptr(pt), m, 2 * n, k, k, k, sk, rpw, 0, K.stream())
+        scratch = K.ArgmaxScratch(m, 2 * n, dev)
+        tok = torch.empty(m, dtype=torch.int64, device=dev)
+        lg = torch.empty(m, 2 * n, dtype=BF, device=dev)
+        K.call("ek_lm_head_argmax", K.ptr(xd), None, 0, None, None, 1e-6, K.ptr(wd), m, 2 * n, k, k, 0, k,
+               K.ptr(lg), 2 * n, K.ptr(scratch.val), K.ptr(scratch.idx), scratch.cap, K.ptr(tok),
+               None, None, None, None, 0, rpw, 0, K.stream())
+        ys[rpw] = (y.cpu(), a.cpu(), pt.cpu(), tok.cpu(), lg.cpu())
+    y, a, pt, tok, lg = ys[0]
+    assert_rounded(y, x, w[:n], name=f"mfma gemv m={m} n={n} k={k}")
+    want = O.silu_mul(_proj_ref(x, w))
+    assert_close_ulps(a, want, min_equal=0.99, name="mfma swiglu", abs_tol=2.0 ** -20 * want.abs().max().item())
+    exact = x.double() @ w.double().t()
+    assert (pt.sum(0).double() - exact).abs().max() <= 1e-5 * exact.abs().max() + 1e-7
+    assert_rounded(lg, x, w, name="mfma logits")
+    assert tok.tolist() == torch.argmax(lg, -1).tolist()
+    # the FMA kernel sums in another order: the same values up to fp32 rounding
+    fy, fa, fpt, ftok, flg = ys[-1]
+    assert_close_ulps(y, fy, ulps=2, min_equal=0.99, name="mfma vs fma")   # 1 ulp at a binade edge is 2 below it
+    assert (pt.sum(0) - fpt.sum(0)).abs().max() <= 1e-5 * exact.abs().max() + 1e-7
+
+
 # ----------------------------------------------------------------------------
 # lm_head + argmax
 # ----------------------------------------------------------------------------
