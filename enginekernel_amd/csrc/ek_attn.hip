@@ -1,40 +1,45 @@
-// Decode attention over the static KV cache, for gfx950. Rows whose scores
-// fit in LDS take a single launch (attn_fused_kernel, below); longer rows the
-// two-phase split-K pair described here.
+// Decode attention over the static KV cache, for gfx950: a two-launch
+// split-K pair over a (split, kv head, batch row) grid for any length, and a
+// single-launch variant for rows whose scores fit in LDS (attn_fused_kernel,
+// below) when the plan asks for one split.
 //
 // The reference's fallback (engine/ek_model.py:475-488) rounds the softmax
 // probabilities to bf16 before the PV product: p = bf16(exp(s - M) / L) with
 // M, L the max and sum over ALL keys of the row. A one-pass flash-decode
-// cannot round there (it only knows M and L at the end), so the build splits
-// the work into two launches over the same (split, kv-head, batch) grid:
+// cannot round there (it only knows M and L at the end), so the split path
+// takes two launches over the same grid:
 //
-//   phase 1  [rope_attn_decode's prologue] QK-norm + RoPE of the G query
+//   scores   [rope_attn_decode's prologue] QK-norm + RoPE of the G query
 //            heads of this kv head (and, in the split owning the new slot,
 //            of the new key, which is written to the cache with the raw
-//            value), then fp32 scores s_n = (q . k_n) * scale for the
-//            split's keys -> a score scratch row, plus the split's running
-//            max m and sum l = sum exp(s - m).
-//   phase 2  one workgroup per (batch, kv head, chunk of DC head dims) over
-//            ALL keys: M = max_s m_s, L = sum_s l_s exp(m_s - M) from the
-//            splits' statistics; p_n = bf16(exp(s_n - M) / L); out =
-//            bf16(sum_n p_n v_n[chunk]) (fp32 sum). Splitting the head
-//            dimension instead of the keys leaves nothing to combine, so no
-//            workgroup waits on another: the eight L2s of the chip are not
-//            coherent, and a cross-workgroup handoff inside a kernel would
-//            need a full L2 write-back per workgroup.
+//            value); then S^T[16 keys x 16] = K_tile . Q^T on the matrix
+//            cores (v_mfma_f32_16x16x32_bf16, the G heads in the first G
+//            columns) for the split's keys -> fp32 scores in a scratch row,
+//            plus the split's max m and sum l = sum exp(s - m) per head.
+//   pv       M = max_s m_s, L = sum_s l_s exp(m_s - M) from the statistics;
+//            p_n = bf16(exp(s_n - M) / L) for the split's keys into LDS;
+//            the split's partial out = sum_n p_n v_n (fp32, all head dims)
+//            with FMAs on lane-contiguous value rows; then the splits'
+//            partials are added in split order by the last workgroup of the
+//            (batch row, kv head) to start, and rounded to bf16 once.
 //
-// Bytes: K is read once (phase 1), V once (phase 2); the score scratch adds
-// 4 bytes per key per query head written, and read once per dim chunk (at
-// G = 4, D = 128, DC = 32: 16 B written + 64 B read per key, against 512 B
-// of K+V). Lane layout: a key row's chunk of 16 B per lane, so a wave reads
-// 64/(D/8) keys per load instruction in phase 1 (4 keys, 1 KiB at D = 128)
-// and 64/(DC/8) keys in phase 2 (16 keys at DC = 32); dot products are
-// folded over the lanes of a key with a butterfly.
+// The split combine needs no third launch and no memory fence: a
+// workgroup takes an arrival ticket (atomic add at agent scope) when it
+// starts and writes its partial as 64-bit words {fp32 value, launch tag},
+// where the tag is one more than the (batch row, kv head)'s epoch word that
+// the previous launch left. The workgroup with the last ticket reads every
+// split's words until their tags match (all other workgroups of its row
+// have started, so they are resident and finish), sums them, then resets
+// the ticket counter and advances the epoch for the next launch. Launches
+// on one workspace are stream-ordered, so the epoch and counter always
+// describe the previous launch.
 //
-// Keys below start[b] (left padding) are never read. The owner split uses
-// the new key from LDS rather than re-reading the slot it just wrote. The
-// first key loads are issued before the QK-norm/RoPE work so that their
-// latency overlaps it.
+// Streaming: key and value rows are loaded lane-contiguously (lanes
+// (D / 8) r .. (D / 8) r + D / 8 - 1 read row r), the layout the memory
+// pipeline coalesces best; the scores kernel re-lays each 16-key tile
+// through a per-wave LDS tile into the MFMA operand layout. Keys below
+// start[b] (left padding) are never read. The owner split uses the new key
+// from LDS rather than re-reading the slot it just wrote.
 
 #include "ek_common.h"
 #include "ek_abi_internal.h"
@@ -45,7 +50,6 @@ namespace {
 
 constexpr int NT = 256;
 constexpr int NW = NT / EK_WAVE;
-constexpr int UNR = 4;   // key steps in flight per lane
 
 struct AttnParams {
   const bf16_t* q; int64_t ldq_b; int64_t ldq_h;
@@ -59,6 +63,8 @@ struct AttnParams {
   bf16_t* out; int64_t ldo_b, ldo_h;
   int nq, nkv, splits; int64_t chunk;
   float sm_scale, eps;
+  unsigned long long* part;   // [B, nkv, splits, G, D] {fp32 bits, tag} words
+  uint32_t* ticket;           // [B * nkv][2]: arrivals of this launch, epoch
 };
 
 struct Range { int64_t lo, hi, len; };
@@ -77,18 +83,39 @@ __device__ __forceinline__ Range key_range(const AttnParams& p, int s, int b) {
   return r;
 }
 
+// ---------------------------------------------------------------------------
+// launch 1: scores and the split's statistics
+// ---------------------------------------------------------------------------
+constexpr int KT = 16;   // keys per MFMA tile
+constexpr int UT = 4;    // key tiles in flight per wave
+
+template <int D>
+struct RowShape {
+  static constexpr int LPK = D / 8;          // lanes per key row (16 B each)
+  static constexpr int KPI = EK_WAVE / LPK;  // keys per load instruction
+  static constexpr int TL = KT / KPI;        // load instructions per 16-key tile
+  static constexpr int DS = D / 32;          // MFMA steps per tile
+  static constexpr int ROWB = 2 * D + 16;    // LDS tile row stride (bytes): conflict-free operand reads
+};
+
+// merge of two (max, sum-of-exp) statistics
+__device__ __forceinline__ void ml_merge(float& m, float& l, float m2, float l2) {
+  const float mn = fmaxf(m, m2);
+  l = l * expf(m - mn) + l2 * expf(m2 - mn);
+  m = mn;
+}
+
 template <int D, int G>
-__global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
-  constexpr int LPK = D / 8;         // lanes per key row
-  constexpr int KPW = EK_WAVE / LPK; // keys per wave per load
-  constexpr int KPB = NW * KPW;      // keys per workgroup per load
+__global__ __launch_bounds__(NT) void attn_qk_kernel(AttnParams p) {
+  using S = RowShape<D>;
   __shared__ float qs[G][D];
   __shared__ float knew[D];
-  __shared__ float stm[NW * KPW][G];
-  __shared__ float stl[NW * KPW][G];
+  __shared__ __align__(16) unsigned char ktile[NW][KT * S::ROWB];
+  __shared__ float stm[NW][G], stl[NW][G];
 
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, q4 = lane >> 4;
   const Range rg = key_range(p, s, b);
   const int64_t slot = rg.len - 1;
   const bool owns = p.rope && slot >= rg.lo && slot < rg.hi;
@@ -96,17 +123,23 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
   st = st < 0 ? 0 : st;
   const int64_t lo = rg.lo > st ? rg.lo : st;
   const int64_t hi = rg.hi;
+  const int64_t ntile = hi > lo ? (hi - lo + KT - 1) / KT : 0;
 
-  const int sub = lane % LPK, grp = lane / LPK;
-  const bf16_t* kb = p.kc + b * p.csb + h * p.csh + sub * 8;
-  // first key tiles in flight before the QK-norm/RoPE work
-  uint4 kv[UNR];
-  const int64_t first = lo + wave * KPW + grp;
+  // the first key tiles in flight before the QK-norm/RoPE work; rows past
+  // the split's end re-read its last row (their scores are dropped)
+  const int lrow = lane / S::LPK, lpc = lane % S::LPK;
+  const bf16_t* kb = p.kc + b * p.csb + h * p.csh + lpc * 8;
+  auto krow = [&](int64_t t, int i) -> const bf16_t* {
+    int64_t n = lo + t * KT + i * S::KPI + lrow;
+    n = n < hi ? n : hi - 1;
+    n = n < 0 ? 0 : n;
+    return kb + n * p.css;
+  };
+  uint4 ring[UT][S::TL];
 #pragma unroll
-  for (int u = 0; u < UNR; ++u) {
-    const int64_t n = first + (int64_t)u * KPB;
-    kv[u] = (n < hi) ? ld16(kb + n * p.css) : make_uint4(0, 0, 0, 0);
-  }
+  for (int u = 0; u < UT; ++u)
+#pragma unroll
+    for (int i = 0; i < S::TL; ++i) ring[u][i] = ld16(krow(wave + (int64_t)u * NW, i));
 
   if (p.rope) {
     const bf16_t* row = p.q + b * p.ldq_b;
@@ -133,177 +166,290 @@ __global__ __launch_bounds__(NT) void attn_scores_kernel(AttnParams p) {
   }
   __syncthreads();
 
-  float qr[G][8];
+  // B operand: the G query heads in columns 0..G-1 (bf16, zero elsewhere)
+  uint4 qb[S::DS];
+  {
+    const int g = r16 < G ? r16 : 0;
+    const float keep = r16 < G ? 1.f : 0.f;
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qr[g][j] = qs[g][sub * 8 + j];
-  float kn8[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kn8[j] = owns ? knew[sub * 8 + j] : 0.f;
-
-  float mr[G], lr[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) { mr[g] = -1e30f; lr[g] = 0.f; }
-
-  float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
-  for (int64_t n0 = first; n0 < hi; n0 += (int64_t)KPB * UNR) {
-    if (n0 != first) {
-#pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const int64_t n = n0 + (int64_t)u * KPB;
-        kv[u] = (n < hi) ? ld16(kb + n * p.css) : make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int64_t n = n0 + (int64_t)u * KPB;
-      const bool valid = n < hi;
-      float kf[8];
-      unpack8(kv[u], kf);
-      if (owns && n == slot) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) kf[j] = kn8[j];
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float d = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) d = fmaf(qr[g][j], kf[j], d);
-        d = group_sum<LPK>(d);
-        const float sc = d * p.sm_scale;
-        if (valid) {
-          if (sub == (g % LPK)) scb[(int64_t)g * p.score_ss + n] = sc;
-          const float mn = fmaxf(mr[g], sc);
-          lr[g] = lr[g] * expf(mr[g] - mn) + expf(sc - mn);
-          mr[g] = mn;
-        }
-      }
+    for (int i = 0; i < S::DS; ++i) {
+      const float* q = &qs[g][32 * i + 8 * q4];
+      qb[i] = make_uint4(pack2(keep * q[0], keep * q[1]), pack2(keep * q[2], keep * q[3]),
+                         pack2(keep * q[4], keep * q[5]), pack2(keep * q[6], keep * q[7]));
     }
   }
-  if (sub == 0) {
+  // the new key's row as four 16-byte pieces per lane group (owner split)
+  uint4 kn16 = make_uint4(0, 0, 0, 0);
+  if (owns) {
+    const float* k = &knew[lpc * 8];
+    kn16 = make_uint4(pack2(k[0], k[1]), pack2(k[2], k[3]), pack2(k[4], k[5]), pack2(k[6], k[7]));
+  }
+
+  unsigned char* tile = ktile[wave];
+  float* scb = p.scores + ((int64_t)b * p.nq + h * G + (r16 < G ? r16 : 0)) * p.score_ss;
+  float m_run = -1e30f, l_run = 0.f;
+  // this wave's tiles: wave, wave + NW, ...; a round takes UT of them (tiles
+  // past the split's end are re-reads of its last row, fully masked)
+  const int64_t nt_w = ntile > wave ? (ntile - wave + NW - 1) / NW : 0;
+  for (int64_t k0 = 0; k0 < nt_w; k0 += UT) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      stm[wave * KPW + grp][g] = mr[g];
-      stl[wave * KPW + grp][g] = lr[g];
+    for (int u = 0; u < UT; ++u) {
+      const int64_t t = wave + (k0 + u) * NW;
+      const int64_t tb = lo + t * KT;
+      // stage the tile row-major (lane-contiguous), the new key in its slot
+#pragma unroll
+      for (int i = 0; i < S::TL; ++i) {
+        const int r = i * S::KPI + lrow;
+        // a bitwise blend: a select of the two would become a load through a
+        // lane-dependent pointer and move the ring to scratch memory
+        const uint32_t nm = (owns && tb + r == slot) ? 0xffffffffu : 0u;
+        const uint4 v = ring[u][i];
+        *reinterpret_cast<uint4*>(tile + r * S::ROWB + lpc * 16) =
+            make_uint4((v.x & ~nm) | (kn16.x & nm), (v.y & ~nm) | (kn16.y & nm), (v.z & ~nm) | (kn16.z & nm),
+                       (v.w & ~nm) | (kn16.w & nm));
+      }
+#pragma unroll
+      for (int i = 0; i < S::TL; ++i) ring[u][i] = ld16(krow(t + (int64_t)UT * NW, i));
+      __builtin_amdgcn_sched_barrier(0);
+      eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < S::DS; ++i) {
+        const uint4 a = *reinterpret_cast<const uint4*>(tile + r16 * S::ROWB + (32 * i + 8 * q4) * 2);
+        c = eka::mfma16x16x32(a, qb[i], c);
+      }
+      // lanes r16 < G hold keys tb + 4 q4 + e of head r16
+      float sc[4], mt = -1e30f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = tb + 4 * q4 + e;
+        const bool ok = r16 < G && n < hi;
+        sc[e] = c[e] * p.sm_scale;
+        if (ok) scb[n] = sc[e];
+        sc[e] = ok ? sc[e] : -1e30f;
+        mt = fmaxf(mt, sc[e]);
+      }
+      const float mn = fmaxf(m_run, mt);
+      float lt = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lt += sc[e] > -1e29f ? expf(sc[e] - mn) : 0.f;
+      l_run = l_run * expf(m_run - mn) + lt;
+      m_run = mn;
     }
+  }
+  // merge the four lane groups of a head, then the waves
+#pragma unroll
+  for (int o = 16; o < EK_WAVE; o <<= 1) {
+    const float m2 = __shfl_xor(m_run, o, EK_WAVE), l2 = __shfl_xor(l_run, o, EK_WAVE);
+    ml_merge(m_run, l_run, m2, l2);
+  }
+  if (q4 == 0 && r16 < G) {
+    stm[wave][r16] = m_run;
+    stl[wave][r16] = l_run;
   }
   __syncthreads();
   if (tid < G) {
-    float M = -1e30f;
-    for (int i = 0; i < NW * KPW; ++i) M = fmaxf(M, stm[i][tid]);
-    float L = 0.f;
-    for (int i = 0; i < NW * KPW; ++i) L += stl[i][tid] * expf(stm[i][tid] - M);
+    float m = stm[0][tid], l = stl[0][tid];
+    for (int w = 1; w < NW; ++w) ml_merge(m, l, stm[w][tid], stl[w][tid]);
     const int64_t o = (((int64_t)b * p.nkv + h) * p.sp + s) * p.gp + tid;
-    p.mmax[o] = M;
-    p.lsum[o] = L;
+    p.mmax[o] = m;
+    p.lsum[o] = l;
   }
 }
 
-template <int D, int G, int DC>
-__global__ __launch_bounds__(NT) void attn_pv_kernel(AttnParams p) {
-  constexpr int LPK = DC / 8;          // lanes per key (16 B of the chunk each)
-  constexpr int KPW = EK_WAVE / LPK;   // keys per wave per load
-  constexpr int KPB = NW * KPW;
+// ---------------------------------------------------------------------------
+// launch 2: the softmax-weighted value sum of a split, and the combine
+// ---------------------------------------------------------------------------
+constexpr int PB = 256;   // keys per probability block (one per thread)
+
+__device__ __forceinline__ unsigned long long tagged(float v, uint32_t tag) {
+  return ((unsigned long long)tag << 32) | __float_as_uint(v);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(NT) void attn_pvs_kernel(AttnParams p) {
+  using S = RowShape<D>;
+  constexpr int KPW = PB / NW;                 // keys per wave per block
+  constexpr int VL = KPW / S::KPI;             // value loads per lane per block
   __shared__ float Ms[G], Ls[G];
-  __shared__ float red[NW][G][DC];
+  __shared__ float wm[NW][G], wl[NW][G];
+  __shared__ __align__(16) float pl[PB][G];
+  __shared__ float red[NW][G][D];
+  __shared__ uint32_t s_tag;
+  __shared__ int s_last;
 
-  const int bh = blockIdx.x;
-  const int b = bh / p.nkv, h = bh % p.nkv;
-  const int d0 = blockIdx.y * DC;
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int64_t len = *p.seq_len;
-  len = len < 0 ? 0 : (len > p.s_cap ? p.s_cap : len);
-  int64_t lo = p.start[b];
-  lo = lo < 0 ? 0 : lo;
-  const int64_t hi = len;
-
-  const int sub = lane % LPK, grp = lane / LPK;
-  const bf16_t* vb = p.vc + b * p.csb + h * p.csh + d0 + sub * 8;
+  const int64_t bh = (int64_t)b * p.nkv + h;
+  // the arrival ticket and the epoch, taken now; their values are first
+  // needed at the end, so the round trip overlaps the work
+  uint32_t t_old = 0, t_ep = 0;
+  if (tid == 0) {
+    t_old = __hip_atomic_fetch_add(p.ticket + 2 * bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    t_ep = __hip_atomic_load(p.ticket + 2 * bh + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const Range rg = key_range(p, s, b);
+  int64_t st = p.start[b];
+  st = st < 0 ? 0 : st;
+  const int64_t lo = rg.lo > st ? rg.lo : st;
+  const int64_t hi = rg.hi;
+  const int lrow = lane / S::LPK, lpc = lane % S::LPK;
+  const bf16_t* vb = p.vc + b * p.csb + h * p.csh + lpc * 8;
   const float* scb = p.scores + ((int64_t)b * p.nq + h * G) * p.score_ss;
-  const int64_t first = lo + wave * KPW + grp;
-  uint4 vv[UNR];
-  float sv[UNR][G];
-#pragma unroll
-  for (int u = 0; u < UNR; ++u) {
-    const int64_t n = first + (int64_t)u * KPB;
-    const bool valid = n < hi;
-    vv[u] = valid ? ld16(vb + n * p.css) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int g = 0; g < G; ++g) sv[u][g] = valid ? scb[(int64_t)g * p.score_ss + n] : 0.f;
-  }
 
-  const int64_t hbase = ((int64_t)b * p.nkv + h) * p.sp;
-  if (tid < G) {
-    float M = -1e30f;
-    for (int s2 = 0; s2 < p.splits; ++s2) M = fmaxf(M, p.mmax[(hbase + s2) * p.gp + tid]);
-    float L = 0.f;
-    for (int s2 = 0; s2 < p.splits; ++s2) {
-      const int64_t o = (hbase + s2) * p.gp + tid;
-      L += p.lsum[o] * expf(p.mmax[o] - M);
+  // one block of PB keys: this thread's key's scores (issued first: loads
+  // retire in order, so the probabilities wait only for them), then this
+  // wave's value rows (rows past the end re-read the split's last row and
+  // get p = 0). Blocks are double-buffered: the next block's loads are in
+  // flight while the current one is consumed.
+  auto load_blk = [&](int64_t kb, float (&sv)[G], uint4 (&vv)[VL]) {
+    int64_t n = kb + tid;
+    n = n < hi ? n : hi - 1;
+    n = n < 0 ? 0 : n;
+#pragma unroll
+    for (int g = 0; g < G; ++g) sv[g] = scb[(int64_t)g * p.score_ss + n];
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      int64_t nv = kb + wave * KPW + i * S::KPI + lrow;
+      nv = nv < hi ? nv : hi - 1;
+      nv = nv < 0 ? 0 : nv;
+      vv[i] = ld16(vb + nv * p.css);
     }
-    Ms[tid] = M;
-    Ls[tid] = L;
-  }
-  __syncthreads();
-  float Mr[G], Lr[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) { Mr[g] = Ms[g]; Lr[g] = Ls[g]; }
-
+  };
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.f;
-
-  for (int64_t n0 = first; n0 < hi; n0 += (int64_t)KPB * UNR) {
-    if (n0 != first) {
+  auto use_blk = [&](int64_t kb, const float (&sv)[G], const uint4 (&vv)[VL]) {
+    const bool ok = kb + tid < hi;
 #pragma unroll
-      for (int u = 0; u < UNR; ++u) {
-        const int64_t n = n0 + (int64_t)u * KPB;
-        const bool valid = n < hi;
-        vv[u] = valid ? ld16(vb + n * p.css) : make_uint4(0, 0, 0, 0);
+    for (int g = 0; g < G; ++g) pl[tid][g] = ok ? rbf(expf(sv[g] - Ms[g]) / Ls[g]) : 0.f;
+    __syncthreads();
 #pragma unroll
-        for (int g = 0; g < G; ++g) sv[u][g] = valid ? scb[(int64_t)g * p.score_ss + n] : 0.f;
-      }
-    }
+    for (int i = 0; i < VL; ++i) {
+      const int kl = wave * KPW + i * S::KPI + lrow;
+      float pv[G];
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const int64_t n = n0 + (int64_t)u * KPB;
-      if (n >= hi) continue;
+      for (int g = 0; g < G; ++g) pv[g] = pl[kl][g];
       float vf[8];
-      unpack8(vv[u], vf);
+      unpack8(vv[i], vf);
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pr = rbf(expf(sv[u][g] - Mr[g]) / Lr[g]);
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pr, vf[j], acc[g][j]);
-      }
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pv[g], vf[j], acc[g][j]);
+    }
+    __syncthreads();
+  };
+
+  // M and L of each head over all splits: thread t merges splits t, t + NT,
+  // ..., then the lanes and the waves merge in a fixed order. The first
+  // round's statistics are loaded before the first block's rows, which then
+  // stay in flight while the statistics are merged.
+  const int64_t base = bh * p.sp;
+  float m[G], l[G];
+  {
+    const int s2 = tid < p.splits ? tid : 0;
+    const float keep = tid < p.splits ? 0.f : -1e30f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = p.mmax[(base + s2) * p.gp + g];
+      l[g] = p.lsum[(base + s2) * p.gp + g];
+      m[g] = keep < 0.f ? -1e30f : m[g];
+      l[g] = keep < 0.f ? 0.f : l[g];
     }
   }
-  // fold the key groups of the wave (lanes with equal `sub`), then the waves
+  float s0[G], s1[G];
+  uint4 v0[VL], v1[VL];
+  load_blk(lo, s0, v0);
+  for (int s2 = tid + NT; s2 < p.splits; s2 += NT)
+#pragma unroll
+    for (int g = 0; g < G; ++g) ml_merge(m[g], l[g], p.mmax[(base + s2) * p.gp + g], p.lsum[(base + s2) * p.gp + g]);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int o = 1; o < EK_WAVE; o <<= 1)
+      ml_merge(m[g], l[g], __shfl_xor(m[g], o, EK_WAVE), __shfl_xor(l[g], o, EK_WAVE));
+    if (lane == 0) { wm[wave][g] = m[g]; wl[wave][g] = l[g]; }
+  }
+  __syncthreads();
+  if (tid < G) {
+    float mm = wm[0][tid], ll = wl[0][tid];
+    for (int w = 1; w < NW; ++w) ml_merge(mm, ll, wm[w][tid], wl[w][tid]);
+    Ms[tid] = mm;
+    Ls[tid] = ll;
+  }
+  __syncthreads();
+
+  for (int64_t kb = lo; kb < hi; kb += 2 * PB) {
+    load_blk(kb + PB, s1, v1);
+    use_blk(kb, s0, v0);
+    if (kb + PB >= hi) break;
+    load_blk(kb + 2 * PB, s0, v0);
+    use_blk(kb + PB, s1, v1);
+  }
+  // fold the key rows of the wave (lanes with equal lpc), then the waves
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       float v = acc[g][j];
 #pragma unroll
-      for (int o = LPK; o < EK_WAVE; o <<= 1) v += __shfl_xor(v, o, EK_WAVE);
+      for (int o = S::LPK; o < EK_WAVE; o <<= 1) v += __shfl_xor(v, o, EK_WAVE);
       acc[g][j] = v;
     }
-  if (grp == 0) {
+  if (lrow == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) red[wave][g][sub * 8 + j] = acc[g][j];
+      for (int j = 0; j < 8; ++j) red[wave][g][lpc * 8 + j] = acc[g][j];
+  }
+  if (tid == 0) {
+    s_tag = t_ep + 1;
+    s_last = t_old == (uint32_t)(p.splits - 1);
   }
   __syncthreads();
-  for (int i = tid; i < G * DC; i += NT) {
-    const int g = i / DC, d = i % DC;
-    float t = 0.f;
+  const uint32_t tag = s_tag;
+  unsigned long long* part = p.part + (bh * p.splits) * (int64_t)(G * D);
+  for (int i = tid; i < G * D; i += NT) {
+    float t = red[0][i / D][i % D];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) t += red[w][g][d];
-    p.out[b * p.ldo_b + (int64_t)(h * G + g) * p.ldo_h + d0 + d] = (bf16_t)f2bf(t);
+    for (int w = 1; w < NW; ++w) t += red[w][i / D][i % D];
+    __hip_atomic_store(part + (int64_t)s * G * D + i, tagged(t, tag), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!s_last) return;
+
+  // the last workgroup to start: every split's partial, added in split
+  // order; the words are read CB splits at a time with all loads in flight,
+  // and a word whose tag is not yet this launch's is polled on its own
+  constexpr int CB = 16;
+  for (int i = tid; i < G * D; i += NT) {
+    float t = 0.f;
+    for (int s0 = 0; s0 < p.splits; s0 += CB) {
+      unsigned long long v[CB];
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        const int s2 = s0 + k < p.splits ? s0 + k : p.splits - 1;
+        v[k] = __hip_atomic_load(part + (int64_t)s2 * G * D + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int k = 0; k < CB; ++k) {
+        if (s0 + k < p.splits) {
+          unsigned long long x = v[k];
+          unsigned long long* w = part + (int64_t)(s0 + k) * G * D + i;
+          for (int spin = 0; (uint32_t)(x >> 32) != tag && spin < (1 << 22); ++spin) {
+            __builtin_amdgcn_s_sleep(1);
+            x = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          t += __uint_as_float((uint32_t)x);
+        }
+      }
+    }
+    p.out[b * p.ldo_b + (int64_t)(h * G + i / D) * p.ldo_h + i % D] = (bf16_t)f2bf(t);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    __hip_atomic_store(p.ticket + 2 * bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.ticket + 2 * bh + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -357,27 +503,23 @@ __global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
 }
 
 // Score rows up to this many bytes per workgroup take the single-launch path
-// (with the kernel's static LDS, at most 64 KiB per workgroup).
+// (with the kernel's static LDS, at most 64 KiB per workgroup) when the plan
+// asks for one split.
 constexpr size_t kFusedScoreLds = 32 * 1024;
 
 template <int D, int G>
 hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
-  constexpr int DC = D >= 32 ? 32 : D;
-  // short rows: one fused launch (the whole score row of a head in LDS)
-  if ((size_t)G * p.s_cap * sizeof(float) <= kFusedScoreLds) {
+  if (p.splits == 1 && (size_t)G * p.s_cap * sizeof(float) <= kFusedScoreLds) {
     dim3 grid((unsigned)(b * p.nkv), (unsigned)(D / eka::FDC));
     const size_t lds = eka::AttnLds<D, G>::bytes(p.s_cap);
     hipLaunchKernelGGL((attn_fused_kernel<D, G>), grid, dim3(eka::FNT), lds, st, p);
     return hipGetLastError();
   }
-  dim3 grid1((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);
-  hipLaunchKernelGGL((attn_scores_kernel<D, G>), grid1, dim3(NT), 0, st, p);
+  dim3 grid((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);
+  hipLaunchKernelGGL((attn_qk_kernel<D, G>), grid, dim3(NT), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // (b, kv head) in x: the D/DC chunk workgroups of one head share an XCD
-  // (workgroups are dealt round-robin over the 8 XCDs by linear id)
-  dim3 grid2((unsigned)(b * p.nkv), (unsigned)(D / DC));
-  hipLaunchKernelGGL((attn_pv_kernel<D, G, DC>), grid2, dim3(NT), 0, st, p);
+  hipLaunchKernelGGL((attn_pvs_kernel<D, G>), grid, dim3(NT), 0, st, p);
   return hipGetLastError();
 }
 
@@ -402,7 +544,8 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
                    const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* lsum,
                    float* mmax, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
                    int64_t ldo_h, int64_t b, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits,
-                   int64_t chunk, float sm_scale, float eps, void* stream) {
+                   int64_t chunk, float sm_scale, float eps, void* part, int64_t part_words, uint32_t* ticket,
+                   void* stream) {
   EK_GUARD();
   if (b < 1 || b * n_kv > 0x7fffffff || n_kv < 1 || n_q < n_kv || n_q % n_kv || b > 65535)
     return ek_fail(hipErrorInvalidValue, "attn: bad batch or head counts");
@@ -410,6 +553,10 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
   if (splits < 1 || splits > sp || chunk < 1 || g > gp)
     return ek_fail(hipErrorInvalidValue, "attn: splits/chunk exceed the workspace");
   if (score_ss < s_cap) return ek_fail(hipErrorInvalidValue, "attn: score scratch shorter than the cache");
+  const bool fused = splits == 1 && (size_t)g * s_cap * sizeof(float) <= kFusedScoreLds;
+  if (!fused && (!part || !ticket || part_words < b * n_kv * splits * g * head_dim))
+    return ek_fail(hipErrorInvalidValue, "attn: the split path needs the partial words and the ticket block");
+  if (splits > 65535) return ek_fail(hipErrorInvalidValue, "attn: too many splits");
   if (rope && (!qn || !kn || !cos || !sin || rope_len < 1))
     return ek_fail(hipErrorInvalidValue, "attn: rope mode needs qn, kn, cos, sin");
   if (css % 8 || csh % 8 || csb % 8 || (reinterpret_cast<uintptr_t>(k_cache) & 15) ||
@@ -428,6 +575,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
   p.out = (bf16_t*)out; p.ldo_b = ldo_b; p.ldo_h = ldo_h;
   p.nq = (int)n_q; p.nkv = (int)n_kv; p.splits = (int)splits; p.chunk = chunk;
   p.sm_scale = sm_scale; p.eps = eps;
+  p.part = (unsigned long long*)part; p.ticket = ticket;
   hipStream_t st = (hipStream_t)stream;
   switch (head_dim) {
     case 32: return launch_attn_g<32>(p, (int)g, (int)b, st);

@@ -466,6 +466,10 @@ def _sm_count() -> int:
     return _SMS
 
 
+MIN_SPLIT_KEYS = 256    # keys per split at least (plan_splits)
+FUSED_BUCKET = 1024     # buckets taking one split, the single-launch kernel
+
+
 def group_pad(n_heads: int, n_kv: int) -> int:
     """ek_kernels.py:1350-1352 (the padded query-group size of the workspace)."""
     return max(16, _next_pow2(n_heads // n_kv))
@@ -480,14 +484,19 @@ def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta
     """ek_kernels.py:1355-1381: (splits, chunk, block_n). Aims for two
     workgroups per compute unit across (batch x kv heads x splits); one
     split when batch x kv heads already covers 0.8 of the CUs; chunk is a
-    multiple of block_n with splits * chunk >= bucket."""
+    multiple of block_n with splits * chunk >= bucket. On MI355X two rules
+    are added from the split sweep of the attention kernels (32/8 heads,
+    D 128): a split gets at least MIN_SPLIT_KEYS keys (the split combine
+    costs more than the parallelism gains below that), and buckets up to
+    FUSED_BUCKET take one split (the single-launch kernel, which keeps the
+    scores in LDS)."""
     sms = _sm_count()
     target_cta = target_cta or int(os.environ.get("ENGINE_ATTN_CTA", "0")) or 2 * sms
     base = batch * n_kv
-    if base >= sms * float(os.environ.get("ENGINE_ATTN_FILL", "0.8")):
+    if base >= sms * float(os.environ.get("ENGINE_ATTN_FILL", "0.8")) or bucket <= FUSED_BUCKET:
         splits = 1
     else:
-        splits = max(1, min(32, _cdiv(target_cta, base)))
+        splits = max(1, min(32, _cdiv(target_cta, base), bucket // MIN_SPLIT_KEYS))
     if not block_n:
         block_n = int(os.environ.get("ENGINE_ATTN_BLOCK", "0"))
     if not block_n:
@@ -500,8 +509,11 @@ def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta
 def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, device, splits=None, chunk=None):
     """The attention workspace: the reference's 7-tuple (acc, lsum, mmax, out,
     splits, chunk, block_n) of engine.py:273-282, extended with the score
-    scratch [B, n_q, bucket] fp32. `acc` is kept for callers that index the
-    tuple; the kernels need no per-split output partials."""
+    scratch [B, n_q, bucket] fp32 and the split combine's ticket block
+    (int32 [B, n_kv, 2], zeroed; the kernels keep an arrival count and an
+    epoch in it). `acc` ([B, n_kv, SP, GP, D] fp32, as in the reference)
+    holds the splits' partial outputs as 64-bit {value, tag} words, which
+    fit because GP >= 2 * (n_q / n_kv)."""
     s, c, bn = plan_splits(b, n_kv, bucket)
     if splits is not None:
         s = splits
@@ -513,20 +525,22 @@ def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, devi
     mmax = torch.full((b, n_kv, sp, gp), -1e30, dtype=torch.float32, device=device)
     out = torch.empty((b, n_q, head_dim), dtype=_BF16, device=device)
     scores = torch.empty((b, n_q, bucket), dtype=torch.float32, device=device)
-    return (acc, lsum, mmax, out, s, c, bn, scores)
+    ticket = torch.zeros((b, n_kv, 2), dtype=torch.int32, device=device)
+    return (acc, lsum, mmax, out, s, c, bn, scores, ticket)
 
 
 _SCRATCH: dict = {}
 
 
-def _attn_scratch(ws, b, n_q, s_cap, device):
-    """The score scratch; for a reference-style 7-tuple workspace it is
-    allocated once per shape (eager callers only)."""
-    if len(ws) >= 8:
-        return ws[7]
-    key = (device, b, n_q, s_cap)
+def _attn_scratch(ws, b, n_q, n_kv, s_cap, device):
+    """The score scratch and the ticket block; for a reference-style 7-tuple
+    workspace they are allocated once per shape (eager callers only)."""
+    if len(ws) >= 9:
+        return ws[7], ws[8]
+    key = (device, b, n_q, n_kv, s_cap)
     if key not in _SCRATCH:
-        _SCRATCH[key] = torch.empty((b, n_q, s_cap), dtype=torch.float32, device=device)
+        _SCRATCH[key] = (ws[7] if len(ws) >= 8 else torch.empty((b, n_q, s_cap), dtype=torch.float32, device=device),
+                         torch.zeros((b, n_kv, 2), dtype=torch.int32, device=device))
     return _SCRATCH[key]
 
 
@@ -542,8 +556,10 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
           and lsum.is_contiguous() and mmax.shape == lsum.shape and mmax.is_contiguous(), "lsum/mmax workspace")
     _need(splits * chunk >= 1, "splits/chunk")
     _need(seq_len_t.dtype == torch.int64 and start_t.dtype == torch.int32 and start_t.numel() >= b, "len/start")
-    scores = _attn_scratch(workspace, b, n_q, s_cap, out.device)
+    scores, ticket = _attn_scratch(workspace, b, n_q, n_kv, s_cap, out.device)
     _need(scores.shape[0] >= b and scores.shape[1] == n_q and scores.is_contiguous(), "score scratch")
+    _need(ticket.dtype == torch.int32 and ticket.is_contiguous() and ticket.numel() >= 2 * b * n_kv, "ticket block")
+    _need(acc.dtype == torch.float32 and acc.is_contiguous(), "acc (the splits' partial words)")
     # the workspace bounds the attended length, as the reference's chunk plan does
     s_cap = min(s_cap, scores.shape[2])
     ld_cs = cos.stride(0) if cos is not None else 0
@@ -552,7 +568,8 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
          ptr(positions), rope_len, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
          k_cache.stride(2), s_cap, ptr(seq_len_t), ptr(start_t), ptr(scores), scores.stride(1),
          ptr(lsum), ptr(mmax), lsum.shape[2], lsum.shape[3], ptr(out), out.stride(0),
-         out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), stream())
+         out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), ptr(acc), acc.numel() // 2,
+         ptr(ticket), stream())
     return out
 
 

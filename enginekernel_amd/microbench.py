@@ -7,9 +7,9 @@ batch-1 end-to-end figure of bench.py:
             over enough distinct weight copies that every timed round reads
             at least 512 MB (the 256 MB Infinity Cache holds nothing of it).
   config 3  decode attention over one layer's cache: q [1, 32, 128], K/V
-            [1, 8, L, 128] bf16 ~N(0, 1), L in {512, 4096, 16384, 32768},
-            swept over the split count, again over copies that defeat the
-            Infinity Cache.
+            bf16 ~N(0, 1) of capacity 32768 filled to L in {512, 4096,
+            16384, 32768}, swept over the split count, again over copies
+            that defeat the Infinity Cache.
   config 5  batch 8, left-padded prompts of U[64, 2048] random ids (seed 2),
             256 greedy tokens through the per-kernel captured graph, cache
             capacity 8192.
@@ -38,7 +38,7 @@ GEMV_SHAPES = (
     ("lm_head", 151936, 2560, "gemv", 1),
 )
 ATTN_LENGTHS = (512, 4096, 16384, 32768)
-ATTN_SPLITS = (1, 2, 4, 8, 16, 32, 64, 128)
+ATTN_SPLITS = (1, 2, 4, 8, 16, 32, 64, 128, 256)
 
 
 def gemv_bytes(kind: str, n: int, k: int, b: int, sk: int = 1) -> int:
@@ -125,9 +125,12 @@ def gemv_sweep(batches=(1, 4), rounds: int = 10, log=print):
     return out
 
 
-def attn_sweep(lengths=ATTN_LENGTHS, splits=ATTN_SPLITS, reps: int = 20, log=print):
-    """Config 3. One record per (L, splits); rows of the fused single-launch
-    path (L <= 2048, where the split count is unused) are timed once."""
+def attn_sweep(lengths=ATTN_LENGTHS, splits=ATTN_SPLITS, reps: int = 20, cap: int = 32768, log=print):
+    """Config 3. One record per (L, splits). The caches have the config's
+    capacity (head stride cap x 128): each copy is a [1, 8, L, 128] view of a
+    [1, 8, cap, 128] pool, cap // L copies per pool, enough copies that a
+    timed round reads at least 512 MB. splits = 1 at L <= 2048 takes the
+    single-launch kernel, every other point the split pair."""
     import torch
     from enginekernel_amd import ek_kernels as K
 
@@ -138,29 +141,35 @@ def attn_sweep(lengths=ATTN_LENGTHS, splits=ATTN_SPLITS, reps: int = 20, log=pri
     for length in lengths:
         per = attn_bytes(length)
         copies = max(4, math.ceil(CACHE_DEFEAT / per))
+        per_pool = cap // length
+        pools = math.ceil(copies / per_pool)
         g = torch.Generator(device=dev).manual_seed(0)
-        caches = [(torch.empty(1, n_kv, length, d, dtype=torch.bfloat16, device=dev).normal_(generator=g),
-                   torch.empty(1, n_kv, length, d, dtype=torch.bfloat16, device=dev).normal_(generator=g))
-                  for _ in range(copies)]
+        kp = [torch.empty(1, n_kv, cap, d, dtype=torch.bfloat16, device=dev).normal_(generator=g) for _ in range(pools)]
+        vp = [torch.empty(1, n_kv, cap, d, dtype=torch.bfloat16, device=dev).normal_(generator=g) for _ in range(pools)]
+        caches = [(kp[c // per_pool][:, :, (c % per_pool) * length:(c % per_pool + 1) * length],
+                   vp[c // per_pool][:, :, (c % per_pool) * length:(c % per_pool + 1) * length])
+                  for c in range(copies)]
         q = torch.empty(1, n_q, d, dtype=torch.bfloat16, device=dev).normal_(generator=g)
         seq = torch.full((1,), length, dtype=torch.int64, device=dev)
         start = torch.zeros(1, dtype=torch.int32, device=dev)
-        fused = 4 * length * 4 <= 32 * 1024
-        for sp in (splits[:1] if fused else splits):
+        for sp in splits:
+            if sp > length // 16:
+                continue
             chunk = K._cdiv(length, sp)
             ws = K.make_workspace(1, n_q, n_kv, d, length, dev, splits=sp, chunk=chunk)
+            fused = sp == 1 and 4 * length * 4 <= 32 * 1024
 
             def one_round():
                 for kc, vc in caches:
                     K.flash_decode(q, kc, vc, seq, start, ws, scale)
 
             t = _timed(one_round, reps) / copies
-            rec = {"L": length, "splits": 0 if fused else sp, "path": "fused" if fused else "scores+pv",
+            rec = {"L": length, "splits": sp, "path": "fused" if fused else "scores+pv",
                    "copies": copies, "us": round(t * 1e6, 2), "floor_us": round(per / PEAK_HBM * 1e6, 2),
                    "bytes": per, "GBps": round(per / t / 1e9, 1), "frac": round(per / t / PEAK_HBM, 4)}
-            log(f"attn L={length:6d} splits={rec['splits']:4d} {rec['us']:8.2f} us  {rec['GBps']:7.1f} GB/s")
+            log(f"attn L={length:6d} splits={sp:4d} {rec['path']:10s} {rec['us']:8.2f} us  {rec['GBps']:7.1f} GB/s")
             out.append(rec)
-        del caches
+        del caches, kp, vp
         torch.cuda.empty_cache()
     return out
 

@@ -120,14 +120,20 @@ int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, in
  * written at slot *seq_len - 1 -- rope_attn_decode, engine/ek_kernels.py:
  * 1476-1507 (kernel :678-780). rope == 0: q [B, n_q, D] is already rotated
  * -- flash_decode, engine/ek_kernels.py:1389-1416 (kernel :534-615).
- * When n_q / n_kv * s_cap * 4 <= 32 KiB, one launch per (b, kv head, 32 head
- * dims) keeps the row's scores in LDS (scores, lsum, mmax, splits and chunk
- * are then unused). Otherwise two launches: per-split scores into the scratch
- * [B, n_q, score_ss] with the split's max/sum in mmax/lsum [B, n_kv, sp, gp];
- * then the softmax-weighted value sum per (b, kv head, chunk of head dims).
- * Either way the reference's split combine (kernel :988-1019) has nothing
- * left to merge. Probabilities are rounded to bf16 before the PV product, as
- * in engine/ek_model.py:475-488.
+ * With splits == 1 and n_q / n_kv * s_cap * 4 <= 32 KiB, one launch per
+ * (b, kv head, 32 head dims) keeps the row's scores in LDS (scores, lsum,
+ * mmax, chunk, part and ticket are then unused). Otherwise two launches over
+ * (split, kv head, b), split s taking keys [s * chunk, (s + 1) * chunk) (the
+ * last split up to *seq_len): per-split scores into the scratch [B, n_q,
+ * score_ss] with the split's max/sum in mmax/lsum [B, n_kv, sp, gp]; then
+ * each split's softmax-weighted value sum, written as {fp32, tag} words to
+ * part (at least B * n_kv * splits * (n_q / n_kv) * D of them), which the
+ * last workgroup of each (b, kv head) adds in split order -- the reference's
+ * split combine (kernel :988-1019), deterministic. ticket holds two words
+ * per (b, kv head) (an arrival count and an epoch), zeroed once with the
+ * workspace and kept by the kernel; launches sharing a workspace must not
+ * overlap. Probabilities are rounded to bf16 before the PV product, as in
+ * engine/ek_model.py:475-488.
  * cos/sin rows: positions[b] when positions != NULL, else row b. */
 int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
                    const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
@@ -135,7 +141,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
                    const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* lsum,
                    float* mmax, int64_t sp, int64_t gp, void* out, int64_t ldo_b, int64_t ldo_h, int64_t b,
                    int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits, int64_t chunk, float sm_scale,
-                   float eps, void* stream);
+                   float eps, void* part, int64_t part_words, uint32_t* ticket, void* stream);
 
 /* lm_head_argmax: logits = bf16(h . w^T) over the vocabulary and the
  * first-index argmax per row -> out_tok[b] (int64). The hidden row h is x

@@ -93,7 +93,10 @@ def test_plan_splits_invariants(b, bucket):
     assert (splits - 1) * chunk < bucket                 # no split starts past the bucket
     ws = K.make_workspace(b, 32, 8, 128, bucket, "cpu")
     assert ws[0].shape == (b, 8, K._next_pow2(splits), K.group_pad(32, 8), 128)
-    assert ws[7].shape == (b, 32, bucket) and len(ws) == 8
+    assert ws[7].shape == (b, 32, bucket) and len(ws) == 9
+    # the ticket block, and room for every split's partial as 64-bit words
+    assert ws[8].shape == (b, 8, 2) and ws[8].dtype == torch.int32 and int(ws[8].abs().sum()) == 0
+    assert ws[0].numel() // 2 >= b * 8 * splits * (32 // 8) * 128
 
 
 def test_group_pad_and_helpers():

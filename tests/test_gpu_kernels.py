@@ -373,6 +373,33 @@ def test_attention_config3_lengths_and_split_sweep(dev, L):
         assert_close_ulps(outs[32], want, min_equal=0.99, name="vs oracle", abs_tol=2.0 ** -13 * vmax)
 
 
+def test_split_combine_tickets_across_launches(dev):
+    """The split combine's ticket block (arrival count + epoch per row and kv
+    head) carries from launch to launch: repeated launches on one workspace
+    are bitwise identical, the ticket ends each launch with zero arrivals and
+    an epoch equal to the launch count, and the same buffers then serve a
+    different split count."""
+    b, hq, hkv, d, cap, L = 3, 32, 8, 128, 4096, 3001
+    g = _gen(99)
+    q = torch.randn(b, hq, d, generator=g).to(BF).to(dev)
+    kc = torch.randn(b, hkv, cap, d, generator=g).to(BF).to(dev)
+    vc = torch.randn(b, hkv, cap, d, generator=g).to(BF).to(dev)
+    start = torch.tensor([0, 17, 900], dtype=torch.int32, device=dev)
+    ln = torch.tensor([L], device=dev)
+    ws = K.make_workspace(b, hq, hkv, d, cap, dev, splits=16, chunk=cap // 16)
+    outs = [K.flash_decode(q, kc, vc, ln, start, ws, d ** -0.5).clone() for _ in range(3)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    t = ws[8].cpu()
+    assert t[..., 0].eq(0).all() and t[..., 1].eq(3).all()
+    ws4 = ws[:4] + (4, cap // 4) + ws[6:]                       # same buffers, four splits
+    got4 = K.flash_decode(q, kc, vc, ln, start, ws4, d ** -0.5).clone()
+    vmax = vc.abs().max().item()
+    assert_close_ulps(got4, outs[0], min_equal=0.98, name="4 vs 16 splits", abs_tol=2.0 ** -13 * vmax)
+    want = O.decode_attn(q.cpu(), kc.cpu()[:, :, :L], vc.cpu()[:, :, :L], L, start.cpu(), d ** -0.5)
+    assert_close_ulps(outs[0], want, min_equal=0.99, name="vs oracle", abs_tol=2.0 ** -13 * vmax)
+    assert ws[8].cpu()[..., 1].eq(4).all()
+
+
 @pytest.mark.parametrize("b,d,nq,nkv,slen,pad,smax", [
     (1, 128, 32, 8, 129, 0, 1024), (3, 128, 32, 8, 300, 11, 1024), (3, 32, 4, 2, 17, 5, 1024),
     (8, 128, 32, 8, 700, 0, 1024), (1, 64, 16, 2, 333, 3, 1024), (1, 128, 32, 8, 1, 0, 256),

@@ -54,7 +54,7 @@ def test_graph_path_equals_eager_hip_path(dev, tiny_ckpt):
     assert list(eng.generate(prompts, 12)) == eager
 
 
-def _decode_parity(cfg, tensors, prompts, steps, dev):
+def _decode_parity(cfg, tensors, prompts, steps, dev, splits=None):
     """Both sides start from the oracle's prefill cache; the oracle's tokens
     are fed back to both. Returns per-step (rel logit error, tokens agree)."""
     om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
@@ -74,7 +74,7 @@ def _decode_parity(cfg, tensors, prompts, steps, dev):
         len_t = torch.full((1,), s, dtype=torch.int64, device=dev)
         start_t = torch.as_tensor(pad, dtype=torch.int32, device=dev)
         ws = K.make_workspace(b, cfg["num_attention_heads"], cfg["num_key_value_heads"],
-                              cfg.get("head_dim"), total, dev)
+                              cfg.get("head_dim"), total, dev, splits=splits)
         out = []
         for _ in range(steps):
             h_ref = om.decode(tok, st.positions, st.k, st.v, st.slot_t, st.len_t, st.start_t)
@@ -144,8 +144,9 @@ def test_decode_parity_4b_shapes_batch8_ragged(dev):
     tensors = C.random_weights(cfg, seed=0)
     prompts = batch8_prompts(cfg["vocab_size"], lo=16, hi=300)
     assert len({len(p) for p in prompts}) > 1
-    res = _decode_parity(cfg, tensors, prompts, 6, dev)
-    assert max(e for e, _ in res) <= 2e-2, res
+    for splits in (None, 3):           # the plan's (one split, the single-launch kernel), then the split pair
+        res = _decode_parity(cfg, tensors, prompts, 6, dev, splits=splits)
+        assert max(e for e, _ in res) <= 2e-2, res
 
 
 def test_engine_4b_shapes_tokens(dev):
