@@ -243,28 +243,32 @@ def parts_splits(m: int, k: int) -> int:
     return sk
 
 
-def add_rms_norm_parts(parts, residual, w, eps):
+def add_rms_norm_parts(parts, residual, w, eps, out=None):
     """ek_kernels.py:1296-1304: residual += bf16(sum(parts)) in place;
-    returns (norm * w, residual)."""
+    returns (norm * w, residual). `out` (optional, [M, N] bf16 rows)
+    receives the normed rows."""
     _gpu(parts, residual, w)
     sk, m, n = parts.shape
     _need(parts.dtype == torch.float32 and parts.is_contiguous(), "parts: contiguous fp32 [sk, M, N]")
     _rows(residual, "residual")
     _need(residual.shape == (m, n), "residual shape")
-    y = torch.empty(m, n, device=parts.device, dtype=residual.dtype)
+    y = torch.empty(m, n, device=parts.device, dtype=residual.dtype) if out is None else out
+    _need(y.shape == (m, n) and y.stride(-1) == 1 and y.dtype == residual.dtype, "add_rms_norm_parts: out")
     call("ek_add_rms_norm_parts", ptr(parts), ptr(residual), ptr(w), ptr(y), sk, m, n, residual.stride(0),
          y.stride(0), float(eps), stream())
     return y, residual
 
 
-def gemv_swiglu(x, w):
+def gemv_swiglu(x, w, out=None):
     """ek_kernels.py:1247-1261: w is the fused [2I, K] gate/up matrix ->
-    bf16(silu(bf16 gate)) (x) bf16(up), [M, I] (M <= 8)."""
+    bf16(silu(bf16 gate)) (x) bf16(up), [M, I] (M <= 8). `out` (optional)
+    receives the [M, I] rows."""
     _check_proj(x, w, "gemv_swiglu")
     m, k = x.shape
     i = w.shape[0] // 2
     _need(1 <= m <= 8, "gemv_swiglu: M must be 1..8")
-    y = torch.empty(m, i, device=x.device, dtype=x.dtype)
+    y = torch.empty(m, i, device=x.device, dtype=x.dtype) if out is None else out
+    _need(y.shape == (m, i) and y.stride(-1) == 1, "gemv_swiglu: out")
     call("ek_gemv_swiglu", ptr(x), ptr(w), ptr(y), m, i, k, x.stride(0), w.stride(0), y.stride(0),
          *_tune("swiglu", i, k, m), stream())
     return y

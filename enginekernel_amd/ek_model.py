@@ -136,6 +136,7 @@ class _StepBuffers:
         self.act = torch.empty(b, cfg.intermediate_size, dtype=bf, device=device)
         self.down_parts = torch.empty(self.sk_down, b, h, dtype=torch.float32, device=device)
         self.hidden = torch.empty(b, h, dtype=bf, device=device)
+        self.xn = torch.empty(b, h, dtype=bf, device=device)       # normed rows (2..8-row path)
         self.argmax = K.ArgmaxScratch(b, cfg.vocab_size, device)
         self.next_tok = torch.empty(b, dtype=torch.int64, device=device)
         self.step = None   # K.StepScratch of the persistent step, made on first use
@@ -275,10 +276,19 @@ class Qwen3(torch.nn.Module):
             raise ValueError(f"decode batch {b} exceeds {self.MAX_ROWS} rows per launch")
         bufs = self.buffers(b)
         res_a, res_b = bufs.res
+        # 1 row: the add + RMSNorm runs fused in each projection's prologue
+        # (ping-pong residual rows); 2..8 rows: once per layer boundary in
+        # add_rms_norm_parts (residual in res_a, in place), since the
+        # matrix-core projections' workgroups would each repeat it over the
+        # split-K partials
+        split = b >= 2
         for i, layer in enumerate(self.layers):
             if i == 0:
-                K.embed_norm_gemv(tokens, self.embed, res_b, layer["ln1"], layer["qkv"], c.rms_eps,
-                                  slot_t=slot_t, len_t=len_t, out=bufs.qkv)
+                K.embed_norm_gemv(tokens, self.embed, res_a if split else res_b, layer["ln1"], layer["qkv"],
+                                  c.rms_eps, slot_t=slot_t, len_t=len_t, out=bufs.qkv)
+            elif split:
+                K.add_rms_norm_parts(bufs.down_parts, res_a, layer["ln1"], c.rms_eps, out=bufs.xn)
+                K.gemv(bufs.xn, layer["qkv"], out=bufs.qkv)
             else:
                 K.parts_norm_gemv(bufs.down_parts, res_a, res_b, layer["ln1"], layer["qkv"], c.rms_eps,
                                   out=bufs.qkv)
@@ -286,8 +296,12 @@ class Qwen3(torch.nn.Module):
                                    v_cache[i], len_t, start_t, ws, self.sm_scale, c.num_heads, c.rms_eps,
                                    positions=positions)
             K.gemv_parts(o.view(b, c.q_size), layer["o"], sk=bufs.sk_o, out=bufs.o_parts)
-            K.parts_norm_gemv(bufs.o_parts, res_b, res_a, layer["ln2"], layer["gu"], c.rms_eps, silu=True,
-                              out=bufs.act)
+            if split:
+                K.add_rms_norm_parts(bufs.o_parts, res_a, layer["ln2"], c.rms_eps, out=bufs.xn)
+                K.gemv_swiglu(bufs.xn, layer["gu"], out=bufs.act)
+            else:
+                K.parts_norm_gemv(bufs.o_parts, res_b, res_a, layer["ln2"], layer["gu"], c.rms_eps, silu=True,
+                                  out=bufs.act)
             K.gemv_parts(bufs.act, layer["down"], sk=bufs.sk_down, out=bufs.down_parts)
         return bufs
 
@@ -360,6 +374,11 @@ class Qwen3(torch.nn.Module):
                           out_buf, step_idx, bufs.step, out_tok=bufs.next_tok)
             return bufs.next_tok
         bufs = self._layers(tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws)
+        state = (tokens, positions, out_buf, step_idx)
+        if b >= 2:
+            K.add_rms_norm_parts(bufs.down_parts, bufs.res[0], self.final_norm, self.cfg.rms_eps, out=bufs.hidden)
+            return K.lm_head_argmax(bufs.hidden, self.lm_head, bufs.argmax, out_tok=bufs.next_tok, logits=logits,
+                                    state=state)
         return K.lm_head_argmax(None, self.lm_head, bufs.argmax, out_tok=bufs.next_tok, logits=logits,
                                 parts=bufs.down_parts, residual=bufs.res[0], norm_w=self.final_norm,
-                                eps=self.cfg.rms_eps, state=(tokens, positions, out_buf, step_idx))
+                                eps=self.cfg.rms_eps, state=state)
