@@ -19,22 +19,35 @@ hipError_t launch_t(const GemvParams& p, dim3 grid, size_t lds, hipStream_t st) 
   return hipGetLastError();
 }
 
+// Whole-row register blocks (KPL 8 and 19, K = 4096 and 9728) exist for one
+// row per wave only: at 2 or 4 rows per wave they would not fit the register
+// file (the compiler spills them), so those launches take the generic
+// 4-chunk block loop, which is correct for any K.
 template <int PRO, int EPI, int BM, int RPW>
 hipError_t launch_k(const GemvParams& p, int kpl, dim3 grid, size_t lds, hipStream_t st) {
   switch (kpl) {
     case 1: return launch_t<PRO, EPI, BM, 1, RPW>(p, grid, lds, st);
     case 5: return launch_t<PRO, EPI, BM, 5, RPW>(p, grid, lds, st);
-    case 8: return launch_t<PRO, EPI, BM, 8, RPW>(p, grid, lds, st);
-    case 19: return launch_t<PRO, EPI, BM, 19, RPW>(p, grid, lds, st);
-    default: return launch_t<PRO, EPI, BM, 4, RPW>(p, grid, lds, st);
+    default: break;
   }
+  if constexpr (RPW == 1) {
+    if (kpl == 8) return launch_t<PRO, EPI, BM, 8, RPW>(p, grid, lds, st);
+    if (kpl == 19) return launch_t<PRO, EPI, BM, 19, RPW>(p, grid, lds, st);
+  }
+  return launch_t<PRO, EPI, BM, 4, RPW>(p, grid, lds, st);
 }
 
+// 8 batch rows x 4 rows per wave (x2 for the gate/up pairs) is more
+// accumulators than the register file holds: such launches run 2 rows per wave
 template <int PRO, int EPI, int BM>
 hipError_t launch_r(const GemvParams& p, int kpl, int rpw, dim3 grid, size_t lds, hipStream_t st) {
   if (rpw == 1) return launch_k<PRO, EPI, BM, 1>(p, kpl, grid, lds, st);
-  if (rpw == 2) return launch_k<PRO, EPI, BM, 2>(p, kpl, grid, lds, st);
-  return launch_k<PRO, EPI, BM, 4>(p, kpl, grid, lds, st);
+  if constexpr (BM == 8) {
+    return launch_k<PRO, EPI, BM, 2>(p, kpl, grid, lds, st);
+  } else {
+    if (rpw == 2) return launch_k<PRO, EPI, BM, 2>(p, kpl, grid, lds, st);
+    return launch_k<PRO, EPI, BM, 4>(p, kpl, grid, lds, st);
+  }
 }
 
 template <int PRO, int EPI>

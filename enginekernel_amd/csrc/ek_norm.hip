@@ -15,7 +15,14 @@ namespace {
 
 constexpr int NT = 256;
 
-// one workgroup per row; MODE 0 = norm, 1 = add+norm, 2 = parts-sum+add+norm
+// one workgroup per row; MODE 0 = norm, 1 = add+norm, 2 = parts-sum+add+norm.
+// A thread owns chunks tid, tid + NT, ... (8 elements each, at most CPT of
+// them: rows up to CPT * NT * 8 elements). Every load of the row -- inputs,
+// residual, partials, gain -- is issued before any is used, and the row
+// stays in registers between the statistics and the output, so the launch
+// costs about two memory round trips.
+constexpr int CPT = 4;
+
 template <int MODE>
 __global__ __launch_bounds__(NT) void row_norm_kernel(const bf16_t* __restrict__ x, int64_t ldx,
                                                       const float* __restrict__ parts, int sk, int64_t parts_ss,
@@ -26,30 +33,74 @@ __global__ __launch_bounds__(NT) void row_norm_kernel(const bf16_t* __restrict__
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t nch = n >> 3;
-  float ss = 0.f;
-  for (int64_t c = tid; c < nch; c += NT) {
-    float r[8];
-    if (MODE == 0) {
-      unpack8(ld16(x + row * ldx + c * 8), r);
-    } else {
-      float a[8], rv[8];
-      if (MODE == 1) {
-        unpack8(ld16(x + row * ldx + c * 8), a);
-      } else {
-        for (int j = 0; j < 8; ++j) a[j] = 0.f;
-        for (int s = 0; s < sk; ++s) {
-          const float* pp = parts + s * parts_ss + row * n + c * 8;
-          for (int j = 0; j < 8; ++j) a[j] += pp[j];
-        }
-        for (int j = 0; j < 8; ++j) a[j] = rbf(a[j]);
+  // chunk i of this thread, clamped (reads of a missing chunk are dropped)
+  int64_t cc[CPT];
+  bool ok[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int64_t c = tid + (int64_t)i * NT;
+    ok[i] = c < nch;
+    cc[i] = ok[i] ? c : nch - 1;
+  }
+  uint4 gv[CPT], xv[CPT], rv[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    gv[i] = ld16(w + cc[i] * 8);
+    if (MODE != 2) xv[i] = ld16(((MODE == 0) ? x : x) + row * ldx + cc[i] * 8);
+    if (MODE != 0) rv[i] = ld16(residual + row * ldr + cc[i] * 8);
+  }
+  float r[CPT][8];
+  if (MODE == 2) {
+    float a[CPT][8];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[i][j] = 0.f;
+#pragma unroll 2
+    for (int s = 0; s < sk; ++s) {
+      float4 p0[CPT], p1[CPT];
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const float* pp = parts + s * parts_ss + row * n + cc[i] * 8;
+        p0[i] = *reinterpret_cast<const float4*>(pp);
+        p1[i] = *reinterpret_cast<const float4*>(pp + 4);
       }
-      unpack8(ld16(residual + row * ldr + c * 8), rv);
-      for (int j = 0; j < 8; ++j) r[j] = rbf(rv[j] + a[j]);
-      // the row is read (above) and written (here) by this thread only
-      *reinterpret_cast<uint4*>(residual + row * ldr + c * 8) =
-          make_uint4(pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7]));
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        a[i][0] += p0[i].x; a[i][1] += p0[i].y; a[i][2] += p0[i].z; a[i][3] += p0[i].w;
+        a[i][4] += p1[i].x; a[i][5] += p1[i].y; a[i][6] += p1[i].z; a[i][7] += p1[i].w;
+      }
     }
-    for (int j = 0; j < 8; ++j) ss = fmaf(r[j], r[j], ss);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      float rr[8];
+      unpack8(rv[i], rr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[i][j] = rbf(rr[j] + rbf(a[i][j]));
+    }
+  } else if (MODE == 1) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      float aa[8], rr[8];
+      unpack8(xv[i], aa);
+      unpack8(rv[i], rr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[i][j] = rbf(rr[j] + aa[j]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) unpack8(xv[i], r[i]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    if (!ok[i]) continue;
+    if (MODE != 0)   // the row is read (above) and written (here) by this thread only
+      *reinterpret_cast<uint4*>(residual + row * ldr + cc[i] * 8) =
+          make_uint4(pack2(r[i][0], r[i][1]), pack2(r[i][2], r[i][3]), pack2(r[i][4], r[i][5]),
+                     pack2(r[i][6], r[i][7]));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = fmaf(r[i][j], r[i][j], ss);
   }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -57,13 +108,14 @@ __global__ __launch_bounds__(NT) void row_norm_kernel(const bf16_t* __restrict__
   float t = 0.f;
   for (int i = 0; i < NT / EK_WAVE; ++i) t += red[i];
   const float rstd = 1.0f / sqrtf(t / (float)n + eps);
-  for (int64_t c = tid; c < nch; c += NT) {
-    float r[8], g[8], o[8];
-    if (MODE == 0) unpack8(ld16(x + row * ldx + c * 8), r);
-    else unpack8(ld16(residual + row * ldr + c * 8), r);
-    unpack8(ld16(w + c * 8), g);
-    for (int j = 0; j < 8; ++j) o[j] = rbf(g[j] * rbf(r[j] * rstd));
-    *reinterpret_cast<uint4*>(y + row * ldy + c * 8) =
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    if (!ok[i]) continue;
+    float g[8], o[8];
+    unpack8(gv[i], g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = rbf(g[j] * rbf(r[i][j] * rstd));
+    *reinterpret_cast<uint4*>(y + row * ldy + cc[i] * 8) =
         make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
   }
 }
@@ -164,6 +216,7 @@ int ek_rms_norm(const void* x, const void* w, void* y, int64_t m, int64_t n, int
   EK_GUARD();
   if (m < 1 || m > 0x7fffffff || bad_row(n, x) || ldx % 8 || ldy % 8)
     return ek_fail(hipErrorInvalidValue, "rms_norm: rows must be a multiple of 8 elements, 16-byte aligned");
+  if (n > (int64_t)CPT * NT * 8) return ek_fail(hipErrorInvalidValue, "rms_norm: row longer than 8192 elements");
   hipLaunchKernelGGL((row_norm_kernel<0>), dim3((unsigned)m), dim3(NT), 0, (hipStream_t)stream,
                      (const bf16_t*)x, ldx, (const float*)nullptr, 0, (int64_t)0, (bf16_t*)nullptr, (int64_t)0,
                      (const bf16_t*)w, (bf16_t*)y, ldy, n, eps);
@@ -175,6 +228,7 @@ int ek_add_rms_norm(const void* x, void* residual, const void* w, void* y, int64
   EK_GUARD();
   if (m < 1 || m > 0x7fffffff || bad_row(n, x) || bad_row(n, residual) || ldx % 8 || ldr % 8 || ldy % 8)
     return ek_fail(hipErrorInvalidValue, "add_rms_norm: rows must be a multiple of 8 elements, 16-byte aligned");
+  if (n > (int64_t)CPT * NT * 8) return ek_fail(hipErrorInvalidValue, "add_rms_norm: row longer than 8192 elements");
   hipLaunchKernelGGL((row_norm_kernel<1>), dim3((unsigned)m), dim3(NT), 0, (hipStream_t)stream,
                      (const bf16_t*)x, ldx, (const float*)nullptr, 0, (int64_t)0, (bf16_t*)residual, ldr,
                      (const bf16_t*)w, (bf16_t*)y, ldy, n, eps);
@@ -184,8 +238,8 @@ int ek_add_rms_norm(const void* x, void* residual, const void* w, void* y, int64
 int ek_add_rms_norm_parts(const float* parts, void* residual, const void* w, void* y, int64_t sk, int64_t m,
                           int64_t n, int64_t ldr, int64_t ldy, float eps, void* stream) {
   EK_GUARD();
-  if (m < 1 || m > 0x7fffffff || sk < 1 || bad_row(n, residual) || ldr % 8 || ldy % 8)
-    return ek_fail(hipErrorInvalidValue, "add_rms_norm_parts: bad shape");
+  if (m < 1 || m > 0x7fffffff || sk < 1 || bad_row(n, residual) || ldr % 8 || ldy % 8 || n > (int64_t)CPT * NT * 8)
+    return ek_fail(hipErrorInvalidValue, "add_rms_norm_parts: bad shape (rows up to 8192 elements)");
   hipLaunchKernelGGL((row_norm_kernel<2>), dim3((unsigned)m), dim3(NT), 0, (hipStream_t)stream,
                      (const bf16_t*)nullptr, (int64_t)0, parts, (int)sk, m * n, (bf16_t*)residual, ldr,
                      (const bf16_t*)w, (bf16_t*)y, ldy, n, eps);
