@@ -46,13 +46,14 @@ int cu_count() {
   return cache[dev];
 }
 
-// The matrix-core kernel's grid: one 512-thread workgroup per CU at most,
-// every wave the same number of 4-row tiles.
-int64_t mfma_grid(int64_t n) {
+// The matrix-core kernel's grid: at most eight waves per CU (all
+// co-resident), every wave the same number of 4-row tiles.
+int64_t mfma_grid(int64_t n, int epi) {
   const int64_t ntiles = (n + MT - 1) / MT;
-  const int64_t cap = (int64_t)cu_count() * MNW;   // waves
+  const int64_t cap = (int64_t)cu_count() * 8;     // waves
   const int64_t per = (ntiles + cap - 1) / cap;    // tiles per wave
-  return (ntiles + per * MNW - 1) / (per * MNW);
+  const int64_t wpg = mfma_threads(epi) / EK_WAVE;
+  return (ntiles + per * wpg - 1) / (per * wpg);
 }
 
 // whether a launch takes the matrix-core kernel
@@ -88,7 +89,7 @@ hipError_t run_gemv(int pro, int epi, GemvParams p, int64_t k, int64_t sk, int64
   if (lds > kMaxLds)
     return ek_fail(hipErrorInvalidValue, "gemv: batch rows x K exceed the 48 KiB activation stage (split K)");
   if (use_mfma(p.m, p.ks, rpw)) {
-    const int64_t gx = mfma_grid(p.n);
+    const int64_t gx = mfma_grid(p.n, epi);
     if (gx_out) *gx_out = gx;
     const int nb = mfma_nb(p.ks / MCH, epi == EPI_SWIGLU);
     const size_t mlds = (size_t)bm * mfma_xld(p.ks) * sizeof(bf16_t);
@@ -307,7 +308,8 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
   if (r != 1 && r != 2 && r != 4) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: rpw must be 1, 2 or 4");
   if (blocks <= 0) blocks = 4 * (int64_t)cu_count();
   const int64_t groups = (vocab + NWAVE * r - 1) / (NWAVE * r);
-  const int64_t gx = use_mfma((int)m, k, force_fma ? -r : r) ? mfma_grid(vocab) : groups < blocks ? groups : blocks;
+  const int64_t gx =
+      use_mfma((int)m, k, force_fma ? -r : r) ? mfma_grid(vocab, EPI_ARGMAX) : groups < blocks ? groups : blocks;
   if (gx * m > am_cap) return ek_fail(hipErrorInvalidValue, "lm_head_argmax: partial buffer too small");
   GemvParams p = zero_params();
   p.w = (const bf16_t*)w; p.ldw = ldw; p.n = vocab; p.m = (int)m;

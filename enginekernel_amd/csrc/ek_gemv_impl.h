@@ -435,8 +435,10 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams p) {
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int MNT = 512;                 // threads of a matrix-core workgroup
-constexpr int MNW = MNT / EK_WAVE;
+// threads of a matrix-core workgroup: 256 for the split-K partials (whose
+// launches have the most tiles per CU: smaller workgroups stay co-resident),
+// 512 otherwise (one stage of x serves more tiles)
+__host__ __device__ constexpr int mfma_threads(int epi) { return epi == EPI_PARTS ? 256 : 512; }
 constexpr int MT = 4;                    // weight rows per tile
 constexpr int MCH = 128;                 // K per chunk (one load instruction)
 
@@ -460,7 +462,7 @@ __device__ __forceinline__ float block_sum(float v) {
   return v;
 }
 
-template <int PRO, int EPI, int BM, int NB, int NT = MNT>
+template <int PRO, int EPI, int BM, int NB, int NT = mfma_threads(EPI)>
 __global__ __launch_bounds__(NT) void gemv_mfma_kernel(GemvParams p) {
   constexpr int NWV = NT / EK_WAVE;
   extern __shared__ __align__(16) unsigned char smem_raw[];

@@ -62,7 +62,7 @@ hipError_t launch_b(const GemvParams& p, int bm, int kpl, int rpw, dim3 grid, si
 
 template <int PRO, int EPI, int BM, int NB>
 hipError_t launch_m(const GemvParams& p, dim3 grid, size_t lds, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_mfma_kernel<PRO, EPI, BM, NB>), grid, dim3(MNT), lds, st, p);
+  hipLaunchKernelGGL((gemv_mfma_kernel<PRO, EPI, BM, NB>), grid, dim3(mfma_threads(EPI)), lds, st, p);
   return hipGetLastError();
 }
 
