@@ -46,6 +46,7 @@ SIGNATURES = {
     "ek_attn_decode": [_P, _I64, _I64, _I, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64,
                        _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
                        _I64, _I64, _I64, _I64, _F, _F, _P, _I64, _P, _P],
+    "ek_attn_prefill": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "ek_lm_head_argmax": [_P, _P, _I64, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                           _P, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "ek_decode_step_plan": [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],

@@ -1,0 +1,247 @@
+// Prefill attention for gfx950: causal GQA flash attention over the prompt's
+// keys, on the matrix cores. The reference runs torch SDPA here
+// (engine/ek_model.py:315-323) with the prompt's additive mask: key <= query
+// and key >= start[b] (left padding, engine.py:541-570); query rows with no
+// visible key (the padding rows) attend to themselves, as this build's torch
+// path does, so that their K/V rows stay finite (no decode step reads them).
+//
+// One workgroup per (batch row, kv head, block of 16 query tokens), one wave
+// per query head of the group (G waves), so the G heads share each K/V tile:
+//
+//   S[16 tokens x 32 keys] = Q . K^T      two v_mfma_f32_16x16x32_bf16 chains
+//                                         of D/32 steps (16 keys each)
+//   online softmax per token row in fp32  (max, rescale, sum of exp)
+//   O[16 x D] += P . V                    D/16 MFMAs, P rounded to bf16
+//
+// Operand layouts (lane l = r + 16 q): A[row r][k 8q..8q+7], B[k 8q..8q+7]
+// [col r], C[rows 4q..4q+3][col r]. Q rows stay in registers (A operand);
+// K tiles are stored row-major in LDS (the B operand of QK^T is 16 B of a key
+// row); V tiles are stored transposed ([dim][key], so the B operand of PV is
+// 16 B of one dim over 8 keys); P goes from the C layout of S to the A layout
+// through a per-wave LDS tile. The next K/V tile is loaded into registers
+// while the current one is consumed. O is divided by the row sum and rounded
+// to bf16 once.
+
+#include <cstring>
+
+#include "ek_abi_internal.h"
+#include "ek_attn_impl.h"
+#include "ek_common.h"
+#include "ek_hip.h"
+
+namespace {
+
+constexpr int QT = 16;   // query tokens per workgroup
+constexpr int KB = 32;   // keys per tile
+
+struct PrefillParams {
+  const bf16_t* q; int64_t ldq;       // q of token t, head j: q + (b * S + t) * ldq + j * D
+  const bf16_t* kc; const bf16_t* vc; int64_t csb, csh, css;
+  const int32_t* start;               // [B] first visible key (left padding)
+  bf16_t* out; int64_t ldo;           // out row (b * S + t), head j at j * D
+  int64_t s;                          // prompt length (padded)
+  int nkv;
+  float scale;
+};
+
+template <int D, int G>
+struct PfLds {
+  static constexpr int KROW = D + 8;       // bf16 per K tile row (16 B pad)
+  static constexpr int VROW = KB + 8;      // bf16 per transposed V row
+  static constexpr int PROW = KB + 8;      // bf16 per P tile row
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
+  using L = PfLds<D, G>;
+  constexpr int NTH = 64 * G;
+  constexpr int DS = D / 32;               // MFMA steps of QK^T
+  constexpr int DB = D / 16;               // 16-dim blocks of O
+  constexpr int TCH = KB * D / 8;          // 16-byte chunks of one K (or V) tile
+  constexpr int CPT = (TCH + NTH - 1) / NTH;
+  __shared__ __align__(16) bf16_t ks[KB * L::KROW];
+  __shared__ __align__(16) bf16_t vt[D * L::VROW];
+  __shared__ __align__(16) bf16_t ps[G][QT * L::PROW];
+
+  const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
+  const int r16 = lane & 15, q4 = lane >> 4;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t t0 = (int64_t)blockIdx.x * QT;
+  int64_t pad = p.start[b];
+  pad = pad < 0 ? 0 : (pad > p.s ? p.s : pad);
+  const int64_t tend = t0 + QT < p.s ? t0 + QT : p.s;   // tokens [t0, tend)
+  // keys [k0, tend): padding rows see only themselves, the others keys >= pad
+  const int64_t k0 = (t0 < pad ? t0 : pad) & ~(int64_t)(KB - 1);
+  const int64_t ntile = (tend - k0 + KB - 1) / KB;
+
+  const bf16_t* kb = p.kc + b * p.csb + h * p.csh;
+  const bf16_t* vb = p.vc + b * p.csb + h * p.csh;
+  // tile chunk c: key c / (D / 8), 16-byte piece c % (D / 8); keys past the
+  // prompt re-read its last key (masked below)
+  auto tile_ld = [&](int64_t kt, uint4 (&kr)[CPT], uint4 (&vr)[CPT]) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      int c = tid + i * NTH;
+      c = c < TCH ? c : TCH - 1;
+      int64_t key = kt + c / (D / 8);
+      key = key < p.s ? key : p.s - 1;
+      kr[i] = ld16(kb + key * p.css + (c % (D / 8)) * 8);
+      vr[i] = ld16(vb + key * p.css + (c % (D / 8)) * 8);
+    }
+  };
+
+  // this wave's query rows (head h * G + g), A operand of QK^T
+  uint4 qa[DS];
+  {
+    int64_t t = t0 + r16;
+    t = t < p.s ? t : p.s - 1;
+    const bf16_t* qrow = p.q + ((int64_t)b * p.s + t) * p.ldq + (int64_t)(h * G + g) * D;
+#pragma unroll
+    for (int i = 0; i < DS; ++i) qa[i] = ld16(qrow + 32 * i + 8 * q4);
+  }
+  uint4 kr[CPT], vr[CPT];
+  tile_ld(k0, kr, vr);
+
+  eka::f32x4_t o[DB];
+#pragma unroll
+  for (int j = 0; j < DB; ++j) o[j] = eka::f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_row[4], l_row[4];                // rows 4 q4 + e of this lane group
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { m_row[e] = -1e30f; l_row[e] = 0.f; }
+  bf16_t* pw = ps[g];
+
+  for (int64_t it = 0; it < ntile; ++it) {
+    const int64_t kt = k0 + it * KB;
+    __syncthreads();   // the previous tile is no longer read
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * NTH;
+      if (c >= TCH) continue;
+      const int key = c / (D / 8), pc = c % (D / 8);
+      *reinterpret_cast<uint4*>(ks + key * L::KROW + pc * 8) = kr[i];
+      const uint32_t w4[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt[(pc * 8 + 2 * e) * L::VROW + key] = (bf16_t)(w4[e] & 0xffffu);
+        vt[(pc * 8 + 2 * e + 1) * L::VROW + key] = (bf16_t)(w4[e] >> 16);
+      }
+    }
+    __syncthreads();
+    if (it + 1 < ntile) tile_ld(kt + KB, kr, vr);   // in flight while this tile is consumed
+
+    // S for keys kt + 16 kb + r16 (two blocks), rows 4 q4 + e
+    float sv[2][4];
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk) {
+      eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < DS; ++i) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(ks + (16 * kbk + r16) * L::KROW + 32 * i + 8 * q4);
+        c = eka::mfma16x16x32(qa[i], kf, c);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t tok = t0 + 4 * q4 + e;
+        const int64_t key = kt + 16 * kbk + r16;
+        const bool ok = (key <= tok && key >= pad) || (tok < pad && key == tok);
+        sv[kbk][e] = ok ? c[e] * p.scale : -1e30f;
+      }
+    }
+    // online softmax: rows are spread over the 16 lanes of a lane group
+    float scale_o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float mt = fmaxf(sv[0][e], sv[1][e]);
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) mt = fmaxf(mt, __shfl_xor(mt, o2, EK_WAVE));
+      const float mn = fmaxf(m_row[e], mt);
+      float ls = 0.f;
+#pragma unroll
+      for (int kbk = 0; kbk < 2; ++kbk) {
+        const float pv = sv[kbk][e] > -1e29f ? expf(sv[kbk][e] - mn) : 0.f;
+        sv[kbk][e] = pv;
+        ls += pv;
+      }
+#pragma unroll
+      for (int o2 = 1; o2 < 16; o2 <<= 1) ls += __shfl_xor(ls, o2, EK_WAVE);
+      scale_o[e] = expf(m_row[e] - mn);
+      l_row[e] = l_row[e] * scale_o[e] + ls;
+      m_row[e] = mn;
+    }
+#pragma unroll
+    for (int j = 0; j < DB; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[j][e] *= scale_o[e];
+    // P (bf16) from the C layout to the A layout through this wave's tile
+#pragma unroll
+    for (int kbk = 0; kbk < 2; ++kbk)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pw[(4 * q4 + e) * L::PROW + 16 * kbk + r16] = (bf16_t)f2bf(sv[kbk][e]);
+    const uint4 pa = *reinterpret_cast<const uint4*>(pw + r16 * L::PROW + 8 * q4);
+#pragma unroll
+    for (int j = 0; j < DB; ++j) {
+      const uint4 vf = *reinterpret_cast<const uint4*>(vt + (16 * j + r16) * L::VROW + 8 * q4);
+      o[j] = eka::mfma16x16x32(pa, vf, o[j]);
+    }
+  }
+  // out rows 4 q4 + e, dims 16 j + r16
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t tok = t0 + 4 * q4 + e;
+    if (tok >= p.s) continue;
+    const float inv = l_row[e] > 0.f ? 1.f / l_row[e] : 0.f;
+    bf16_t* orow = p.out + ((int64_t)b * p.s + tok) * p.ldo + (int64_t)(h * G + g) * D;
+#pragma unroll
+    for (int j = 0; j < DB; ++j) orow[16 * j + r16] = (bf16_t)f2bf(o[j][e] * inv);
+  }
+}
+
+template <int D, int G>
+hipError_t launch_prefill(const PrefillParams& p, int64_t b, hipStream_t st) {
+  dim3 grid((unsigned)((p.s + QT - 1) / QT), (unsigned)p.nkv, (unsigned)b);
+  hipLaunchKernelGGL((attn_prefill_kernel<D, G>), grid, dim3(64 * G), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int D>
+hipError_t launch_prefill_g(const PrefillParams& p, int g, int64_t b, hipStream_t st) {
+  switch (g) {
+    case 1: return launch_prefill<D, 1>(p, b, st);
+    case 2: return launch_prefill<D, 2>(p, b, st);
+    case 4: return launch_prefill<D, 4>(p, b, st);
+    case 8: return launch_prefill<D, 8>(p, b, st);
+    default: return ek_fail(hipErrorInvalidValue, "attn_prefill: query heads per kv head must be 1, 2, 4 or 8");
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
+                    int64_t css, int64_t s_cap, const int32_t* start, void* out, int64_t ldo, int64_t b, int64_t s,
+                    int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale, void* stream) {
+  EK_GUARD();
+  if (b < 1 || b > 65535 || s < 1 || s > s_cap || n_kv < 1 || n_kv > 65535 || n_q % n_kv)
+    return ek_fail(hipErrorInvalidValue, "attn_prefill: bad batch, length or head counts");
+  if (ldq % 8 || ldo % 8 || css % 8 || csh % 8 || csb % 8 || (reinterpret_cast<uintptr_t>(q) & 15) ||
+      (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
+    return ek_fail(hipErrorInvalidValue, "attn_prefill: rows must be 16-byte aligned");
+  PrefillParams p;
+  memset(&p, 0, sizeof(p));
+  p.q = (const bf16_t*)q; p.ldq = ldq;
+  p.kc = (const bf16_t*)k_cache; p.vc = (const bf16_t*)v_cache; p.csb = csb; p.csh = csh; p.css = css;
+  p.start = start;
+  p.out = (bf16_t*)out; p.ldo = ldo;
+  p.s = s; p.nkv = (int)n_kv; p.scale = sm_scale;
+  hipStream_t st = (hipStream_t)stream;
+  const int g = (int)(n_q / n_kv);
+  switch (head_dim) {
+    case 32: return launch_prefill_g<32>(p, g, b, st);
+    case 64: return launch_prefill_g<64>(p, g, b, st);
+    case 128: return launch_prefill_g<128>(p, g, b, st);
+    default: return ek_fail(hipErrorInvalidValue, "attn_prefill: head_dim must be 32, 64 or 128");
+  }
+}
+
+}  // extern "C"

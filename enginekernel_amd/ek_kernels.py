@@ -577,6 +577,27 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
     return out
 
 
+def attn_prefill(qkv, k_cache, v_cache, start_t, s, n_q, sm_scale, out=None):
+    """The prompt's causal GQA attention, ek_model.py:315-323 (SDPA with the
+    _pack mask, engine.py:541-570): query heads from the fused rows qkv
+    [B*S, (n_q + 2 n_kv) D] (already QK-normed and rotated), keys/values from
+    the caches' slots [start_t[b], t] (written by qk_norm_rope_kv); padding
+    tokens (t < start_t[b]) attend to themselves. Returns [B*S, n_q*D] bf16."""
+    _gpu(qkv, k_cache, v_cache, start_t)
+    _rows(qkv, "qkv")
+    b, n_kv, s_cap, d = k_cache.shape
+    _need(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(), "k/v cache layouts differ")
+    _need(k_cache.dtype == _BF16 and k_cache.stride(-1) == 1, "cache")
+    _need(qkv.shape[0] == b * s and qkv.shape[1] >= (n_q + 2 * n_kv) * d, "qkv rows [B*S, (n_q + 2 n_kv) D]")
+    _need(start_t.dtype == torch.int32 and start_t.numel() >= b and start_t.is_contiguous(), "start_t: int32 [B]")
+    y = torch.empty(b * s, n_q * d, device=qkv.device, dtype=_BF16) if out is None else out
+    _need(y.shape == (b * s, n_q * d) and y.stride(-1) == 1, "attn_prefill: out")
+    call("ek_attn_prefill", ptr(qkv), qkv.stride(0), ptr(k_cache), ptr(v_cache), k_cache.stride(0),
+         k_cache.stride(1), k_cache.stride(2), s_cap, ptr(start_t), ptr(y), y.stride(0), b, s, n_q, n_kv, d,
+         float(sm_scale), stream())
+    return y
+
+
 def flash_decode(q, k_cache, v_cache, seq_len_t, start_t, workspace, sm_scale):
     """ek_kernels.py:1389-1416: q [B, HQ, D] (already rotated); caches
     [B, HKV, S, D]; seq_len_t (int64 [1]) / start_t (int32 [B]) on device.

@@ -216,30 +216,12 @@ class Qwen3(torch.nn.Module):
         return self._bufs[b]
 
     # ------------------------------------------------------------------
-    def _prefill_attn(self, q, k, v, attn_bias):
-        """Causal GQA attention of the prompt in fp32 (q [B, HQ, S, D] bf16,
-        k/v [B, HKV, S, D]); the stand-in for the reference's SDPA call
-        (ek_model.py:315-323). Query rows with no visible key (left padding)
-        attend to themselves so that their K/V stay finite."""
-        b, hq, s, d = q.shape
-        rep = hq // k.shape[1]
-        qf = q.float().contiguous()
-        kf = k.float().repeat_interleave(rep, 1).transpose(-1, -2).contiguous()
-        vf = v.float().repeat_interleave(rep, 1).contiguous()
-        scores = torch.matmul(qf, kf) * self.sm_scale
-        if attn_bias is None:
-            allow = torch.ones((s, s), dtype=torch.bool, device=q.device).tril()[None, None]
-        else:
-            allow = attn_bias == 0
-        allow = allow | (~allow.any(-1, keepdim=True)
-                         & torch.eye(s, dtype=torch.bool, device=q.device)[None, None])
-        scores = scores.masked_fill(~allow, float("-inf"))
-        p = torch.softmax(scores, dim=-1)
-        return torch.matmul(p, vf).to(q.dtype)
-
     def prefill(self, input_ids, positions, k_cache, v_cache, attn_bias=None):
         """ek_model.py:280-334: input_ids/positions [B, S]; writes cache slots
-        [0, S); returns the final-normed hidden of each row's last position."""
+        [0, S); returns the final-normed hidden of each row's last position.
+        attn_bias is the prompt mask of engine._pack (causal, keys from each
+        row's first real token) or None (causal); the attention is the HIP
+        flash kernel (K.attn_prefill), the projections torch (hipBLASLt)."""
         c = self.cfg
         b, s = input_ids.shape
         cos = self.cos.index_select(0, positions.reshape(-1))
@@ -247,6 +229,12 @@ class Qwen3(torch.nn.Module):
         zero_slot = self.zero_slot[:b] if b <= self.zero_slot.numel() else torch.zeros(
             b, dtype=torch.int64, device=self.device)
         residual = F.embedding(input_ids, self.embed).reshape(b * s, c.hidden_size)
+        # the first visible key of each row: with the prompt mask (left
+        # padding) it is S - len, read off the last position (len - 1)
+        if attn_bias is None:
+            start = torch.zeros(b, dtype=torch.int32, device=self.device)
+        else:
+            start = (s - 1 - positions[:, -1]).to(torch.int32).contiguous()
         x = None
         for i, layer in enumerate(self.layers):
             if i == 0:
@@ -256,9 +244,7 @@ class Qwen3(torch.nn.Module):
             qkv = torch.matmul(x, layer["qkv_t"])
             K.qk_norm_rope_kv(qkv, layer["qn"], layer["kn"], cos, sin, k_cache[i], v_cache[i], zero_slot,
                               c.num_heads, c.num_kv_heads, c.rms_eps, s)
-            q = qkv[:, : c.q_size].view(b, s, c.num_heads, c.head_dim).transpose(1, 2)
-            o = self._prefill_attn(q, k_cache[i][:, :, :s], v_cache[i][:, :, :s], attn_bias)
-            o = o.transpose(1, 2).reshape(b * s, c.q_size)
+            o = K.attn_prefill(qkv, k_cache[i], v_cache[i], start, s, c.num_heads, self.sm_scale)
             x = torch.matmul(o, layer["o_t"])
             x, residual = K.add_rms_norm(x, residual, layer["ln2"], c.rms_eps)
             x = torch.matmul(K.silu_mul(torch.matmul(x, layer["gu_t"])), layer["down_t"])

@@ -143,6 +143,19 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
                    int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits, int64_t chunk, float sm_scale,
                    float eps, void* part, int64_t part_words, uint32_t* ticket, void* stream);
 
+/* attn_prefill: the prompt's causal GQA attention, engine/ek_model.py:315-323
+ * (torch SDPA with the prompt mask of engine/engine.py:541-570): for each
+ * row b and token t < s, query head j (q at q + (b * s + t) * ldq + j * D),
+ * keys/values of kv head j / (n_q / n_kv) at cache slots [start[b], t]
+ * (caches [B, n_kv, s_cap, D], strides csb/csh/css); a padding token
+ * (t < start[b]) attends to itself only. out row (b * s + t), head j at
+ * j * D, bf16. Flash attention on the matrix cores (fp32 online softmax,
+ * probabilities rounded to bf16 for the value product). D in {32, 64, 128},
+ * n_q / n_kv in {1, 2, 4, 8}. */
+int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
+                    int64_t css, int64_t s_cap, const int32_t* start, void* out, int64_t ldo, int64_t b, int64_t s,
+                    int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale, void* stream);
+
 /* lm_head_argmax: logits = bf16(h . w^T) over the vocabulary and the
  * first-index argmax per row -> out_tok[b] (int64). The hidden row h is x
  * (parts == NULL) or, fused, rms_norm(bf16(residual + bf16(sum_s parts[s])))

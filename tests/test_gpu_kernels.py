@@ -437,6 +437,56 @@ def test_rope_attn_decode(dev, b, d, nq, nkv, slen, pad, smax):
 
 
 # ----------------------------------------------------------------------------
+# prefill attention (ek_model.py:315-323, SDPA with the _pack mask)
+# ----------------------------------------------------------------------------
+def _ref_prefill64(qkv, kc, vc, start, s, nq, d):
+    """Causal GQA softmax attention in float64 over keys [start_b, t]; a
+    padding token (t < start_b) attends to itself."""
+    b, nkv = kc.shape[0], kc.shape[1]
+    g = nq // nkv
+    q = qkv[:, : nq * d].double().view(b, s, nq, d).transpose(1, 2)             # [b, nq, s, d]
+    k = kc[:, :, :s].double().repeat_interleave(g, 1)
+    v = vc[:, :, :s].double().repeat_interleave(g, 1)
+    sc = q @ k.transpose(-1, -2) * d ** -0.5
+    t = torch.arange(s)
+    out = torch.empty(b, nq, s, d, dtype=torch.float64)
+    for i in range(b):
+        st = int(start[i])
+        allow = (t[None, :] <= t[:, None]) & (t[None, :] >= st)
+        allow |= (t[:, None] < st) & (t[None, :] == t[:, None])
+        si = sc[i].masked_fill(~allow, float("-inf"))
+        out[i] = torch.softmax(si, -1) @ v[i]
+    return out.transpose(1, 2).reshape(b * s, nq * d)
+
+
+@pytest.mark.parametrize("b,s,d,nq,nkv,pads,cap", [
+    (1, 17, 128, 32, 8, [0], 32), (3, 100, 128, 32, 8, [0, 37, 99], 256), (2, 300, 64, 16, 2, [5, 0], 512),
+    (2, 33, 32, 4, 2, [0, 10], 64), (1, 70, 128, 8, 8, [3], 96), (1, 2048, 128, 32, 8, [0], 4096)])
+def test_attn_prefill_flash(dev, b, s, d, nq, nkv, pads, cap):
+    """The prompt's causal GQA flash attention against a float64 softmax:
+    ragged left padding (a row with one real token included), every group
+    size G = 1, 2, 4, 8, head dims 32/64/128, partial 16-token blocks and a
+    cache capacity above the prompt. Padding rows return their own value
+    row exactly."""
+    g = _gen(s + b + d)
+    qkv = torch.randn(b * s, (nq + 2 * nkv) * d, generator=g).to(BF)
+    kc = torch.randn(b, nkv, cap, d, generator=g).to(BF)
+    vc = torch.randn(b, nkv, cap, d, generator=g).to(BF)
+    start = torch.tensor(pads, dtype=torch.int32)
+    got = K.attn_prefill(qkv.to(dev), kc.to(dev), vc.to(dev), start.to(dev), s, nq, d ** -0.5).cpu()
+    want = _ref_prefill64(qkv, kc, vc, start, s, nq, d)
+    check_scale(got, want, 1e-2, "vs float64 softmax")
+    # elementwise: probabilities are rounded to bf16 (2^-9 relative) before the value sum
+    bound = 2.0 ** -7 * want.abs() + 2.0 ** -8 * vc.float().abs().max().item()
+    assert ((got.double() - want).abs() <= bound).float().mean().item() >= 0.999
+    gg = nq // nkv
+    for i, st in enumerate(pads):
+        for t in range(min(st, s)):
+            row = got.view(b, s, nq, d)[i, t]
+            assert torch.equal(row, vc[i, :, t].repeat_interleave(gg, 0)), (i, t)
+
+
+# ----------------------------------------------------------------------------
 # graph capture of C-ABI launches
 # ----------------------------------------------------------------------------
 def test_graph_replay_matches_eager(dev):

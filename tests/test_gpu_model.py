@@ -151,8 +151,8 @@ def test_decode_parity_4b_shapes_batch8_ragged(dev):
 
 def test_engine_4b_shapes_tokens(dev):
     """Free-running greedy through the captured graph at the 4B shapes vs the
-    oracle loop; a divergence is accepted only at a near-tie, and the
-    teacher-forced test above pins every step's logits."""
+    oracle loop fed the same tokens: a different token is accepted only at a
+    near-tie (the teacher-forced test above pins every step's logits)."""
     cfg = dict(MID_4B)
     tensors = C.random_weights(cfg, seed=0)
     model = Qwen3(None, dev, tensors=tensors, config=cfg)
@@ -162,9 +162,20 @@ def test_engine_4b_shapes_tokens(dev):
     g = torch.Generator().manual_seed(2)
     prompts = [torch.randint(0, 151936, (32,), generator=g).tolist()]
     got = list(eng.generate(prompts, 16))
-    want = list(O.generate_eager(om, prompts, 16))
-    assert got[0] == want[0]              # the prefill's first token
-    assert got == want
+    # the oracle fed the GPU's own tokens (bench/check_exact.py's rule): at
+    # every step the GPU's token is the oracle's argmax for the same history,
+    # or within 2 bf16 ulps of the oracle's top logit
+    ref = list(O.generate_eager(om, prompts, 16, record_logits=True, force=got[:-1]))
+    agree = 0
+    for j, (toks, logits) in enumerate(ref):
+        top = int(torch.argmax(logits[0]))
+        if got[j][0] == top:
+            agree += 1
+            continue
+        lr = logits[0].float()
+        assert float(lr[top] - lr[got[j][0]]) <= 2 * _ulp(logits[0, top].double()).item(), (j, got[j], toks)
+    assert got[0] == ref[0][0]            # the prefill's first token
+    assert agree >= 14, agree
 
 
 def test_decode_parity_full_depth_against_the_noise_floor(dev):
