@@ -23,6 +23,9 @@
 //            partials are added in split order by the last workgroup of the
 //            (batch row, kv head) to start, and rounded to bf16 once.
 //
+// Cached keys and values are read once per launch: their loads are marked
+// non-temporal (ld16_nt), which measurably shortens the split launches.
+//
 // The split combine needs no third launch and no memory fence: a
 // workgroup takes an arrival ticket (atomic add at agent scope) when it
 // starts and writes its partial as 64-bit words {fp32 value, launch tag},
@@ -139,7 +142,7 @@ __global__ __launch_bounds__(NT) void attn_qk_kernel(AttnParams p) {
 #pragma unroll
   for (int u = 0; u < UT; ++u)
 #pragma unroll
-    for (int i = 0; i < S::TL; ++i) ring[u][i] = ld16(krow(wave + (int64_t)u * NW, i));
+    for (int i = 0; i < S::TL; ++i) ring[u][i] = ld16_nt(krow(wave + (int64_t)u * NW, i));
 
   if (p.rope) {
     const bf16_t* row = p.q + b * p.ldq_b;
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(NT) void attn_qk_kernel(AttnParams p) {
                        (v.w & ~nm) | (kn16.w & nm));
       }
 #pragma unroll
-      for (int i = 0; i < S::TL; ++i) ring[u][i] = ld16(krow(t + (int64_t)UT * NW, i));
+      for (int i = 0; i < S::TL; ++i) ring[u][i] = ld16_nt(krow(t + (int64_t)UT * NW, i));
       __builtin_amdgcn_sched_barrier(0);
       eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(NT) void attn_pvs_kernel(AttnParams p) {
       int64_t nv = kb + wave * KPW + i * S::KPI + lrow;
       nv = nv < hi ? nv : hi - 1;
       nv = nv < 0 ? 0 : nv;
-      vv[i] = ld16(vb + nv * p.css);
+      vv[i] = ld16_nt(vb + nv * p.css);
     }
   };
   float acc[G][8];

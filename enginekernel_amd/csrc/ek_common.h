@@ -104,6 +104,13 @@ __device__ __forceinline__ uint4 ld16(const bf16_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// The same load marked non-temporal, for data read once per pass (weights,
+// cached keys and values): the L2 then keeps the lines that are reused.
+__device__ __forceinline__ uint4 ld16_nt(const bf16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load((global_u32x4_t*)(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Release this workgroup's global writes and count it in; returns true in
 // the last workgroup to arrive (which then observes every other
 // workgroup's writes). The counter is reset by that last workgroup, so it
