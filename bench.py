@@ -3,7 +3,8 @@ fraction of the HBM roofline.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
     python bench.py --probe-traffic     (the launches the PMC traffic profile counts)
-    python bench.py --config 2|3|5      (GEMV sweep, attention sweep, batch-8 decode)
+    python bench.py --config 2|3|5|6    (GEMV sweep, attention sweep, batch-8 decode,
+                                         batch-1 speculative decode vs plain)
 
 Workload: a random-init bf16 model of the Qwen3-4B
 architecture (36 layers, hidden 2560, intermediate 9728, 32/8 heads, head
@@ -229,9 +230,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--probe-traffic", action="store_true", help="run only the launches of the PMC traffic profile")
-    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5),
-                    help="4 (default): the batch-1 decode line; 2 / 3 / 5: the GEMV sweep, the attention "
-                         "sweep or the batch-8 decode, one JSON line each (enginekernel_amd.microbench)")
+    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5, 6),
+                    help="4 (default): the batch-1 decode line; 2 / 3 / 5 / 6: the GEMV sweep, the attention "
+                         "sweep, the batch-8 decode or batch-1 speculative vs plain decode, one JSON line each "
+                         "(enginekernel_amd.microbench)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}).",

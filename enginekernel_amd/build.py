@@ -22,7 +22,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libek_hip.so")
-SOURCES = ["ek_abi.hip", "ek_norm.hip", "ek_gemv.hip", "ek_attn.hip", "ek_prefill.hip", "ek_step.hip"]
+SOURCES = ["ek_abi.hip", "ek_norm.hip", "ek_gemv.hip", "ek_attn.hip", "ek_prefill.hip", "ek_spec.hip", "ek_step.hip"]
 # head dims of the persistent decode-step kernel; ek_step_inst.hip is compiled once per head dim
 STEP_HEAD_DIMS = [32, 64, 128]
 # (prologue, epilogue) pairs of the GEMV family; ek_gemv_inst.hip is compiled

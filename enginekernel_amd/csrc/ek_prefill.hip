@@ -5,6 +5,12 @@
 // visible key (the padding rows) attend to themselves, as this build's torch
 // path does, so that their K/V rows stay finite (no decode step reads them).
 //
+// The same kernel scores a speculative verify step (ek_attn_verify; the
+// reference's flash_verify, engine/ek_kernels.py:1419, restated by its torch
+// fallback attn_torch, :1451): the row's S query tokens then sit at cache
+// positions q0[b] .. q0[b] + S - 1 (after the row's cached keys), query j
+// sees keys [start[b], q0[b] + j].
+//
 // One workgroup per (batch row, kv head, block of 16 query tokens), one wave
 // per query head of the group (G waves), so the G heads share each K/V tile:
 //
@@ -38,8 +44,10 @@ struct PrefillParams {
   const bf16_t* q; int64_t ldq;       // q of token t, head j: q + (b * S + t) * ldq + j * D
   const bf16_t* kc; const bf16_t* vc; int64_t csb, csh, css;
   const int32_t* start;               // [B] first visible key (left padding)
+  const int64_t* q0;                  // [B] cache position of query token 0 (verify), or null (prefill: 0)
   bf16_t* out; int64_t ldo;           // out row (b * S + t), head j at j * D
-  int64_t s;                          // prompt length (padded)
+  int64_t s;                          // query tokens per row (prefill: the padded prompt length)
+  int64_t s_cap;                      // cache rows per (batch row, kv head)
   int nkv;
   float scale;
 };
@@ -66,25 +74,29 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
   const int tid = threadIdx.x, lane = tid & 63, g = tid >> 6;
   const int r16 = lane & 15, q4 = lane >> 4;
   const int h = blockIdx.y, b = blockIdx.z;
+  // query token t of this row sits at cache position qb + t; keys [0, kend)
+  int64_t qb = p.q0 ? p.q0[b] : 0;
+  qb = qb < 0 ? 0 : (qb > p.s_cap - p.s ? p.s_cap - p.s : qb);
+  const int64_t kend = qb + p.s;
   const int64_t t0 = (int64_t)blockIdx.x * QT;
   int64_t pad = p.start[b];
-  pad = pad < 0 ? 0 : (pad > p.s ? p.s : pad);
+  pad = pad < 0 ? 0 : (pad > kend ? kend : pad);
   const int64_t tend = t0 + QT < p.s ? t0 + QT : p.s;   // tokens [t0, tend)
-  // keys [k0, tend): padding rows see only themselves, the others keys >= pad
-  const int64_t k0 = (t0 < pad ? t0 : pad) & ~(int64_t)(KB - 1);
-  const int64_t ntile = (tend - k0 + KB - 1) / KB;
+  // keys [k0, qb + tend): padding rows see only themselves, the others keys >= pad
+  const int64_t k0 = (qb + t0 < pad ? qb + t0 : pad) & ~(int64_t)(KB - 1);
+  const int64_t ntile = (qb + tend - k0 + KB - 1) / KB;
 
   const bf16_t* kb = p.kc + b * p.csb + h * p.csh;
   const bf16_t* vb = p.vc + b * p.csb + h * p.csh;
   // tile chunk c: key c / (D / 8), 16-byte piece c % (D / 8); keys past the
-  // prompt re-read its last key (masked below)
+  // last query's position re-read that key (masked below)
   auto tile_ld = [&](int64_t kt, uint4 (&kr)[CPT], uint4 (&vr)[CPT]) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       int c = tid + i * NTH;
       c = c < TCH ? c : TCH - 1;
       int64_t key = kt + c / (D / 8);
-      key = key < p.s ? key : p.s - 1;
+      key = key < kend ? key : kend - 1;
       kr[i] = ld16(kb + key * p.css + (c % (D / 8)) * 8);
       vr[i] = ld16(vb + key * p.css + (c % (D / 8)) * 8);
     }
@@ -141,7 +153,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t tok = t0 + 4 * q4 + e;
+        const int64_t tok = qb + t0 + 4 * q4 + e;   // the query's cache position
         const int64_t key = kt + 16 * kbk + r16;
         const bool ok = (key <= tok && key >= pad) || (tok < pad && key == tok);
         sv[kbk][e] = ok ? c[e] * p.scale : -1e30f;
@@ -216,32 +228,54 @@ hipError_t launch_prefill_g(const PrefillParams& p, int g, int64_t b, hipStream_
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
-                    int64_t css, int64_t s_cap, const int32_t* start, void* out, int64_t ldo, int64_t b, int64_t s,
-                    int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale, void* stream) {
-  EK_GUARD();
+hipError_t attn_flash(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
+                      int64_t css, int64_t s_cap, const int32_t* start, const int64_t* q0, void* out, int64_t ldo,
+                      int64_t b, int64_t s, int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale,
+                      void* stream) {
   if (b < 1 || b > 65535 || s < 1 || s > s_cap || n_kv < 1 || n_kv > 65535 || n_q % n_kv)
-    return ek_fail(hipErrorInvalidValue, "attn_prefill: bad batch, length or head counts");
+    return ek_fail(hipErrorInvalidValue, "attn_prefill/attn_verify: bad batch, length or head counts");
   if (ldq % 8 || ldo % 8 || css % 8 || csh % 8 || csb % 8 || (reinterpret_cast<uintptr_t>(q) & 15) ||
       (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
-    return ek_fail(hipErrorInvalidValue, "attn_prefill: rows must be 16-byte aligned");
+    return ek_fail(hipErrorInvalidValue, "attn_prefill/attn_verify: rows must be 16-byte aligned");
   PrefillParams p;
   memset(&p, 0, sizeof(p));
   p.q = (const bf16_t*)q; p.ldq = ldq;
   p.kc = (const bf16_t*)k_cache; p.vc = (const bf16_t*)v_cache; p.csb = csb; p.csh = csh; p.css = css;
-  p.start = start;
+  p.start = start; p.q0 = q0;
   p.out = (bf16_t*)out; p.ldo = ldo;
-  p.s = s; p.nkv = (int)n_kv; p.scale = sm_scale;
+  p.s = s; p.s_cap = s_cap; p.nkv = (int)n_kv; p.scale = sm_scale;
   hipStream_t st = (hipStream_t)stream;
   const int g = (int)(n_q / n_kv);
   switch (head_dim) {
     case 32: return launch_prefill_g<32>(p, g, b, st);
     case 64: return launch_prefill_g<64>(p, g, b, st);
     case 128: return launch_prefill_g<128>(p, g, b, st);
-    default: return ek_fail(hipErrorInvalidValue, "attn_prefill: head_dim must be 32, 64 or 128");
+    default: return ek_fail(hipErrorInvalidValue, "attn_prefill/attn_verify: head_dim must be 32, 64 or 128");
   }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
+                    int64_t css, int64_t s_cap, const int32_t* start, void* out, int64_t ldo, int64_t b, int64_t s,
+                    int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale, void* stream) {
+  EK_GUARD();
+  return attn_flash(q, ldq, k_cache, v_cache, csb, csh, css, s_cap, start, nullptr, out, ldo, b, s, n_q, n_kv,
+                    head_dim, sm_scale, stream);
+}
+
+int ek_attn_verify(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
+                   int64_t css, int64_t s_cap, const int32_t* start, const int64_t* len_b, void* out, int64_t ldo,
+                   int64_t b, int64_t nq, int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale,
+                   void* stream) {
+  EK_GUARD();
+  if (!len_b) return ek_fail(hipErrorInvalidValue, "attn_verify: len_b is required");
+  return attn_flash(q, ldq, k_cache, v_cache, csb, csh, css, s_cap, start, len_b, out, ldo, b, nq, n_q, n_kv,
+                    head_dim, sm_scale, stream);
 }
 
 }  // extern "C"

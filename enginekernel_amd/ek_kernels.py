@@ -599,6 +599,61 @@ def attn_prefill(qkv, k_cache, v_cache, start_t, s, n_q, sm_scale, out=None):
     return y
 
 
+def attn_verify(qkv, k_cache, v_cache, start_t, len_b, nq, n_q, sm_scale, out=None):
+    """The attention of a speculative verify step, ek_kernels.py:1419
+    (flash_verify; torch form attn_torch, :1451): row b's nq query tokens
+    (rows b*nq + j of the fused qkv [B*nq, (n_q + 2 n_kv) D], already
+    QK-normed and rotated, their keys/values written at cache slots
+    len_b[b] + j by qk_norm_rope_kv) see the keys at slots
+    [start_t[b], len_b[b] + j]. Returns [B*nq, n_q*D] bf16."""
+    _gpu(qkv, k_cache, v_cache, start_t, len_b)
+    _rows(qkv, "qkv")
+    b, n_kv, s_cap, d = k_cache.shape
+    _need(k_cache.shape == v_cache.shape and k_cache.stride() == v_cache.stride(), "k/v cache layouts differ")
+    _need(k_cache.dtype == _BF16 and k_cache.stride(-1) == 1, "cache")
+    _need(qkv.shape[0] == b * nq and qkv.shape[1] >= (n_q + 2 * n_kv) * d, "qkv rows [B*nq, (n_q + 2 n_kv) D]")
+    _need(start_t.dtype == torch.int32 and start_t.numel() >= b and start_t.is_contiguous(), "start_t: int32 [B]")
+    _need(len_b.dtype == torch.int64 and len_b.numel() >= b and len_b.is_contiguous(), "len_b: int64 [B]")
+    y = torch.empty(b * nq, n_q * d, device=qkv.device, dtype=_BF16) if out is None else out
+    _need(y.shape == (b * nq, n_q * d) and y.stride(-1) == 1, "attn_verify: out")
+    call("ek_attn_verify", ptr(qkv), qkv.stride(0), ptr(k_cache), ptr(v_cache), k_cache.stride(0),
+         k_cache.stride(1), k_cache.stride(2), s_cap, ptr(start_t), ptr(len_b), ptr(y), y.stride(0), b, nq, n_q,
+         n_kv, d, float(sm_scale), stream())
+    return y
+
+
+def ngram_draft(hist, hist_len, tokens):
+    """ek_kernels.py:1510: tokens[B, Q] <- [last token, Q-1 n-gram drafts]
+    per row of hist [B, H] (int64, first hist_len[b] entries valid)."""
+    _gpu(hist, hist_len, tokens)
+    _need(hist.dtype == torch.int64 and hist.dim() == 2 and hist.is_contiguous(), "hist: int64 [B, H]")
+    b, h = hist.shape
+    _need(hist_len.dtype == torch.int64 and hist_len.numel() >= b and hist_len.is_contiguous(), "hist_len")
+    _need(tokens.dtype == torch.int64 and tokens.dim() == 2 and tokens.shape[0] == b and tokens.is_contiguous(),
+          "tokens: int64 [B, Q]")
+    call("ek_ngram_draft", ptr(hist), ptr(hist_len), ptr(tokens), b, h, tokens.shape[1], stream())
+    return tokens
+
+
+def spec_accept(tokens, am, hist, hist_len, len_b, pos_b, remaining, out_tok, out_adv, step_idx):
+    """ek_kernels.py:1519: accept the longest draft prefix the model agrees
+    with and do the step's bookkeeping (outputs at out_tok/out_adv[step_idx],
+    history, lengths, positions, budget). step_idx is not advanced."""
+    _gpu(tokens, am, hist, hist_len, len_b, pos_b, remaining, out_tok, out_adv, step_idx)
+    b, q = tokens.shape
+    for t, nm in ((tokens, "tokens"), (am, "am"), (hist, "hist"), (hist_len, "hist_len"), (len_b, "len_b"),
+                  (pos_b, "pos_b"), (remaining, "remaining"), (step_idx, "step_idx")):
+        _need(t.dtype == torch.int64 and t.is_contiguous(), f"spec_accept: {nm} must be contiguous int64")
+    _need(am.shape == (b, q) and hist.dim() == 2 and hist.shape[0] == b, "spec_accept: am [B, Q], hist [B, H]")
+    _need(out_tok.dtype == torch.int32 and out_tok.dim() == 3 and out_tok.shape[1:] == (b, q)
+          and out_tok.is_contiguous(), "spec_accept: out_tok int32 [steps, B, Q]")
+    _need(out_adv.dtype == torch.int32 and out_adv.shape == (out_tok.shape[0], b) and out_adv.is_contiguous(),
+          "spec_accept: out_adv int32 [steps, B]")
+    call("ek_spec_accept", ptr(tokens), ptr(am), ptr(hist), ptr(hist_len), ptr(len_b), ptr(pos_b),
+         ptr(remaining), ptr(out_tok), ptr(out_adv), ptr(step_idx), b, hist.shape[1], q, out_tok.shape[0],
+         stream())
+
+
 def flash_decode(q, k_cache, v_cache, seq_len_t, start_t, workspace, sm_scale):
     """ek_kernels.py:1389-1416: q [B, HQ, D] (already rotated); caches
     [B, HKV, S, D]; seq_len_t (int64 [1]) / start_t (int32 [B]) on device.

@@ -137,6 +137,7 @@ class _StepBuffers:
         self.down_parts = torch.empty(self.sk_down, b, h, dtype=torch.float32, device=device)
         self.hidden = torch.empty(b, h, dtype=bf, device=device)
         self.xn = torch.empty(b, h, dtype=bf, device=device)       # normed rows (2..8-row path)
+        self.att = torch.empty(b, cfg.q_size, dtype=bf, device=device)   # verify attention rows
         self.argmax = K.ArgmaxScratch(b, cfg.vocab_size, device)
         self.next_tok = torch.empty(b, dtype=torch.int64, device=device)
         self.step = None   # K.StepScratch of the persistent step, made on first use
@@ -164,6 +165,7 @@ class Qwen3(torch.nn.Module):
         self._build_rope(self.cfg.max_position if self.cfg.max_position <= 16384 else 16384)
         self.sm_scale = self.cfg.head_dim ** -0.5
         self.zero_slot = torch.zeros(1024, dtype=torch.int64, device=device)
+        self.arange_q = torch.arange(16, dtype=torch.int64, device=device)   # verify positions (<= 16 per row)
         self._bufs: dict = {}
         self._plans: dict = {}
         self._tables: dict = {}
@@ -302,6 +304,44 @@ class Qwen3(torch.nn.Module):
         res_a = bufs.res[0]
         hidden, _ = K.add_rms_norm_parts(bufs.down_parts, res_a, self.final_norm, self.cfg.rms_eps)
         return hidden
+
+    def verify(self, tokens, pos_b, k_cache, v_cache, len_b, start_t, ws=None):
+        """ek_model.py:418-472: score NQ tokens per sequence in one pass (the
+        speculative verify). tokens [B, NQ] = the last emitted token and NQ-1
+        drafts at positions pos_b[b] + j; their keys/values go to cache slots
+        len_b[b] + j (what follows a rejected draft is overwritten by the next
+        step). Returns the greedy token after each position, [B, NQ] int64.
+        The HIP kernels of the 2..8-row decode at B*NQ rows, with the verify
+        attention (K.attn_verify) in place of the decode attention; ws is
+        accepted for the reference's signature and not used."""
+        c = self.cfg
+        b, nq = tokens.shape
+        rows = b * nq
+        if not self.use_gemv_for(rows):
+            raise ValueError(f"verify: {rows} rows exceed {self.MAX_ROWS} rows per launch")
+        positions = (pos_b[:, None] + self.arange_q[None, :nq]).reshape(-1).clamp(max=self.rope_len - 1)
+        cos = self.cos.index_select(0, positions)
+        sin = self.sin.index_select(0, positions)
+        bufs = self.buffers(rows)
+        res = bufs.res[0]
+        tok = tokens.reshape(-1).contiguous()
+        for i, layer in enumerate(self.layers):
+            if i == 0:
+                K.embed_norm_gemv(tok, self.embed, res, layer["ln1"], layer["qkv"], c.rms_eps, out=bufs.qkv)
+            else:
+                K.add_rms_norm_parts(bufs.down_parts, res, layer["ln1"], c.rms_eps, out=bufs.xn)
+                K.gemv(bufs.xn, layer["qkv"], out=bufs.qkv)
+            K.qk_norm_rope_kv(bufs.qkv, layer["qn"], layer["kn"], cos, sin, k_cache[i], v_cache[i], len_b,
+                              c.num_heads, c.num_kv_heads, c.rms_eps, nq)
+            o = K.attn_verify(bufs.qkv, k_cache[i], v_cache[i], start_t, len_b, nq, c.num_heads, self.sm_scale,
+                              out=bufs.att)
+            K.gemv_parts(o, layer["o"], sk=bufs.sk_o, out=bufs.o_parts)
+            K.add_rms_norm_parts(bufs.o_parts, res, layer["ln2"], c.rms_eps, out=bufs.xn)
+            K.gemv_swiglu(bufs.xn, layer["gu"], out=bufs.act)
+            K.gemv_parts(bufs.act, layer["down"], sk=bufs.sk_down, out=bufs.down_parts)
+        hidden, _ = K.add_rms_norm_parts(bufs.down_parts, res, self.final_norm, c.rms_eps, out=bufs.hidden)
+        am = K.lm_head_argmax(hidden, self.lm_head, bufs.argmax, out_tok=bufs.next_tok)
+        return am.view(b, nq)
 
     def argmax_token(self, hidden, logits=None):
         """ek_model.py:490-493: first index of the max bf16 logit, [B] int64."""

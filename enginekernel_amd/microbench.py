@@ -254,8 +254,68 @@ def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
     return rec
 
 
+def spec_decode(tokens: int = 256, log=print):
+    """Batch-1 greedy decode at the Qwen3-4B shape (random-init weights,
+    seed 0) through the engine, plain (one persistent step per token) and
+    speculative (ENGINE_SPEC_Q tokens scored per verify step), on a random
+    prompt and on a prompt that repeats a 16-token phrase. Time from the
+    first token's arrival to the last (prefill excluded). Records where the
+    two greedy sequences first differ, if they do (near-ties: the exact
+    equality is tested on the tiny model and the verify pass position by
+    position against the oracle)."""
+    import time
+
+    import torch
+
+    from . import checkpoint as C
+    from .ek_model import Qwen3
+    from .engine import _FastEngine, _spec_q
+
+    cfg = dict(C.QWEN3_4B)
+    dev = torch.device("cuda:0")
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+    eng = _FastEngine(model=model)
+    g = torch.Generator().manual_seed(1)
+    phrase = torch.randint(0, cfg["vocab_size"], (16,), generator=g).tolist()
+    prompts = {"random": torch.randint(0, cfg["vocab_size"], (128,), generator=g).tolist(),
+               "repeating": phrase * 8}
+    out = []
+    for name, prompt in prompts.items():
+        rec = {"prompt": name, "prompt_len": len(prompt), "tokens": tokens, "q": _spec_q(1)}
+        toks = {}
+        for spec in (False, True):
+            eng.spec = spec
+            list(eng.generate([prompt], 16))          # capture the graphs outside the timing
+            it = eng.generate([prompt], tokens)
+            first = next(it)
+            t0 = time.perf_counter()
+            rest = list(it)
+            dt = time.perf_counter() - t0
+            toks[spec] = [first] + rest
+            key = "spec" if spec else "plain"
+            rec[key + "_ms_per_token"] = round(dt * 1e3 / (tokens - 1), 4)
+            rec[key + "_tokens_per_s"] = round((tokens - 1) / dt, 1)
+            if spec:
+                steps, target = eng.last_stats
+                rec["verify_steps"] = steps
+                rec["tokens_per_verify"] = round(target / steps, 3)
+                rec["ms_per_verify"] = round(dt * 1e3 / steps, 4)
+        # greedy ties: the verify pass (3-row kernels, flash attention) and the
+        # one-launch step round differently, and on a random-init model, whose
+        # logits are flat, a near-tie flip makes the two sequences part ways
+        div = next((i for i, (a, b) in enumerate(zip(toks[True], toks[False])) if a != b), None)
+        rec["first_divergence"] = div
+        rec["speedup"] = round(rec["plain_ms_per_token"] / rec["spec_ms_per_token"], 3)
+        log(f"[bench] spec {name}: plain {rec['plain_ms_per_token']} ms/token, spec {rec['spec_ms_per_token']} "
+            f"ms/token ({rec['tokens_per_verify']} tokens per {rec['ms_per_verify']} ms verify), "
+            f"first divergence {rec['first_divergence']}")
+        out.append(rec)
+    eng.spec = False
+    return out
+
+
 def run(config: int, log=print) -> dict:
-    """One JSON-ready record for config 2, 3 or 5."""
+    """One JSON-ready record for config 2, 3, 5 or 6."""
     import torch
     if not torch.cuda.is_available():
         raise RuntimeError("the microbenchmarks need a GPU")
@@ -275,4 +335,10 @@ def run(config: int, log=print) -> dict:
                 "data": "synthetic (random-init weights seed 0, prompts seed 2)",
                 "config": {"workload": "config 5: Qwen3-4B architecture, batch 8 ragged, per-kernel graph"},
                 "results": [batch8_decode(log=log)]}
+    if config == 6:
+        return {"metric": "batch-1 speculative decode tokens/s vs plain (config 6)", "unit": "tokens/s",
+                "higher_is_better": True, "dtype": "bf16",
+                "data": "synthetic (random-init weights seed 0; random and repeating prompts, seed 1)",
+                "config": {"workload": "config 6: Qwen3-4B architecture, batch 1, n-gram draft + verify"},
+                "results": spec_decode(log=log)}
     raise ValueError(f"no microbenchmark for config {config}")

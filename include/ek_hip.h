@@ -156,6 +156,37 @@ int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void*
                     int64_t css, int64_t s_cap, const int32_t* start, void* out, int64_t ldo, int64_t b, int64_t s,
                     int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale, void* stream);
 
+/* attn_verify: the attention of a speculative verify step, engine/ek_kernels.py:1419
+ * (flash_verify; its torch form attn_torch, :1451): row b's nq query tokens
+ * (q rows b * nq + j, as in attn_prefill) sit at cache slots len_b[b] + j
+ * (their keys/values already written there), and query j sees the keys at
+ * slots [start[b], len_b[b] + j]. Same kernel, layouts and arithmetic as
+ * attn_prefill; len_b is a device int64 [B], clamped to [0, s_cap - nq]. */
+int ek_attn_verify(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
+                   int64_t css, int64_t s_cap, const int32_t* start, const int64_t* len_b, void* out, int64_t ldo,
+                   int64_t b, int64_t nq, int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale,
+                   void* stream);
+
+/* ngram_draft: engine/ek_kernels.py:1510 (ngram_draft, its kernel :618):
+ * per row b, tokens[b][0..q) = [hist[b][hl - 1], q - 1 drafts] with hl =
+ * hist_len[b]: the drafts continue the most recent earlier occurrence of the
+ * trailing 3-gram of hist[b][0..hl) (else 2-gram, else token), wrapping around
+ * a short cycle (see csrc/ek_spec.hip). hist [B, h] int64 (h < 2^20),
+ * hist_len [B], tokens [B, q] int64 (q <= 256). */
+int ek_ngram_draft(const int64_t* hist, const int64_t* hist_len, int64_t* tokens, int64_t b, int64_t h, int64_t q,
+                   void* stream);
+
+/* spec_accept: engine/ek_kernels.py:1519 (spec_accept, its kernel :652):
+ * per row b, with am [B, q] the model's argmax after each of tokens[b]:
+ * adv = min(1 + the number of leading drafts tokens[b][j + 1] == am[b][j],
+ * remaining[b]); out_tok[step][b][0..q) = am[b] (int32), out_adv[step][b] =
+ * adv (step = *step_idx, stores skipped unless 0 <= step < max_steps);
+ * hist[b][hist_len[b] + j] = am[b][j] (j < q, inside the row); hist_len,
+ * len_b, pos_b += adv; remaining -= adv. *step_idx is not advanced. q <= 64. */
+int ek_spec_accept(const int64_t* tokens, const int64_t* am, int64_t* hist, int64_t* hist_len, int64_t* len_b,
+                   int64_t* pos_b, int64_t* remaining, int32_t* out_tok, int32_t* out_adv, const int64_t* step_idx,
+                   int64_t b, int64_t h, int64_t q, int64_t max_steps, void* stream);
+
 /* lm_head_argmax: logits = bf16(h . w^T) over the vocabulary and the
  * first-index argmax per row -> out_tok[b] (int64). The hidden row h is x
  * (parts == NULL) or, fused, rms_norm(bf16(residual + bf16(sum_s parts[s])))

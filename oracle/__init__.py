@@ -15,5 +15,9 @@ transposed operand fails a test) is listed in `tests/test_oracle.py`:
 transformers' own Qwen3ForCausalLM greedy decode (token-exact, the
 reference's `bench/test_equivalence.py` check), float64 closed forms for the
 norms, RoPE and attention, the HF rotary formula, brute-force softmax on
-tiny inputs, and attention special cases (one key, constant keys).
+tiny inputs, and attention special cases (one key, constant keys). The
+speculative draft is pinned against a search by n-gram order then position
+(an independent statement of its score), the accept step against hand-worked
+cases, and the verify attention against the single-query decode attention
+(each verify query equals a decode at its own length).
 """

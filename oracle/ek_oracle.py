@@ -337,3 +337,84 @@ def bf16_ulp(x: float) -> float:
     if x == 0:
         return 2.0 ** -133
     return 2.0 ** (math.floor(math.log2(x)) - 7)
+
+
+# ----------------------------------------------------------------------------
+# speculative decoding -- engine/engine.py:345-383 (the torch form of the
+# draft/verify/accept step) and engine/ek_kernels.py:618-680 (the integer
+# kernels that replace its draft and accept parts; where the two differ, at a
+# full history, the kernels' behaviour is restated: no store past the row)
+# ----------------------------------------------------------------------------
+def ngram_draft(hist, hist_len, q: int):
+    """engine.py:357-376 / ek_kernels.py:618-649: per row, [last token,
+    q-1 drafts continuing the most recent earlier occurrence of the trailing
+    3-gram (else 2-gram, else token), wrapping around a short cycle].
+    hist [B, H] int64, hist_len [B] -> tokens [B, q] int64."""
+    hist = torch.as_tensor(hist, dtype=torch.int64)
+    b, h = hist.shape
+    big = 1 << 20
+    out = torch.empty((b, q), dtype=torch.int64)
+    for r in range(b):
+        hl = int(hist_len[r])
+        row = hist[r].tolist()
+        k_last, k_prev, k_pp = row[hl - 1], row[max(hl - 2, 0)], row[max(hl - 3, 0)]
+        best = 0
+        for j in range(0, hl - 1):                     # j <= hl - 2
+            m1 = row[j] == k_last
+            m2 = m1 and j >= 1 and row[j - 1] == k_prev
+            m3 = m2 and j >= 2 and row[j - 2] == k_pp
+            best = max(best, (j + 1 if m1 else 0) + (big if m2 else 0) + (2 * big if m3 else 0))
+        p = best % big
+        span = max(hl - p, 1)
+        out[r, 0] = k_last
+        for i in range(q - 1):
+            out[r, i + 1] = row[min(p + i % span, h - 1)]
+    return out
+
+
+def spec_accept(tokens, am, hist, hist_len, len_b, pos_b, remaining, out_tok, out_adv, step: int):
+    """engine.py:377-383 / ek_kernels.py:652-680, in place on CPU tensors:
+    adv = min(1 + leading drafts equal to the argmax before them, remaining);
+    outputs at out_tok/out_adv[step]; all q argmax tokens into hist[hl ..]
+    inside the row; hist_len, len_b, pos_b += adv; remaining -= adv."""
+    b, q = tokens.shape
+    h = hist.shape[1]
+    for r in range(b):
+        nacc = 0
+        while nacc < q - 1 and int(tokens[r, nacc + 1]) == int(am[r, nacc]):
+            nacc += 1
+        rem = int(remaining[r])
+        adv = min(nacc + 1, rem)
+        if 0 <= step < out_tok.shape[0]:
+            out_tok[step, r] = am[r].to(torch.int32)
+            out_adv[step, r] = adv
+        hl = int(hist_len[r])
+        for j in range(q):
+            if hl + j < h:
+                hist[r, hl + j] = am[r, j]
+        hist_len[r] += adv
+        len_b[r] += adv
+        pos_b[r] += adv
+        remaining[r] = rem - adv
+
+
+def verify_attn(q, kc, vc, len_b, start_t, sm_scale: float, nq: int):
+    """ek_kernels.py:1451-1475 (attn_torch, the verify attention's torch
+    form): q [B*nq, HQ, D]; caches [B, HKV, S, D]; query j of row b sees
+    keys [start_t[b], len_b[b] + j]; fp32 softmax, p rounded to bf16."""
+    bq, hq, d = q.shape
+    b = bq // nq
+    hkv = kc.shape[1]
+    g = hq // hkv
+    bucket = kc.shape[2]
+    qg = q.view(b, nq, hkv, g, d).permute(0, 2, 1, 3, 4).reshape(b, hkv, nq * g, d)
+    scores = torch.matmul(qg, kc.transpose(-1, -2)).float() * sm_scale
+    ar = torch.arange(bucket)
+    qlen = torch.as_tensor(len_b, dtype=torch.int64)[:, None] + torch.arange(nq)[None, :] + 1
+    qlen = qlen.repeat_interleave(g, dim=1)
+    start = torch.as_tensor(start_t, dtype=torch.int64)
+    ok = (ar[None, None, :] < qlen[:, :, None]) & (ar[None, None, :] >= start[:, None, None])
+    scores = scores.masked_fill(~ok[:, None, :, :], float("-inf"))
+    p = torch.softmax(scores, dim=-1).to(q.dtype)
+    out = torch.matmul(p, vc)
+    return out.view(b, hkv, nq, g, d).permute(0, 2, 1, 3, 4).reshape(bq, hq, d)
