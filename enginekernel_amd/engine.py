@@ -19,6 +19,8 @@ from __future__ import annotations
 
 import gc
 import os
+import subprocess
+import sys
 
 import torch
 
@@ -36,6 +38,26 @@ LOOKAHEAD = int(os.environ.get("ENGINE_LOOKAHEAD", "2"))
 SPEC = os.environ.get("ENGINE_SPEC", "0") == "1"
 SPEC_Q = int(os.environ.get("ENGINE_SPEC_Q", "3"))
 SPEC_MAX_BATCH = int(os.environ.get("ENGINE_SPEC_MAX_BATCH", "1"))
+
+
+# Out-of-process probes (engine.py:47-77, 439-470): with ENGINE_PROBE_CHILD=1
+# the engine first loads and runs the library in a child process, and runs
+# each new graph shape's attention launches there before capturing it. Off by
+# default: the kernels are compiled ahead of time (no JIT that can abort the
+# process), and a child costs seconds of start-up.
+PROBE_CHILD = os.environ.get("ENGINE_PROBE_CHILD", "0") == "1"
+
+
+def _child_ok(args, timeout=None) -> bool:
+    """engine.py:47-61: run ek_probe with args in a child; True only on a clean exit."""
+    try:
+        r = subprocess.run([sys.executable, "-m", "enginekernel_amd.ek_probe"] + [str(a) for a in args],
+                           stdin=subprocess.DEVNULL, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                           cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                           timeout=timeout or float(os.environ.get("ENGINE_PROBE_TIMEOUT", "150")))
+        return r.returncode == 0
+    except Exception:
+        return False
 
 
 def _spec_q(b: int) -> int:
@@ -82,6 +104,9 @@ class _FastEngine:
         if not torch.cuda.is_available():
             raise K.HipUnavailable("no GPU visible: the HIP engine cannot run")
         self.device = torch.device(f"cuda:{torch.cuda.current_device()}")
+        self.probe_child = PROBE_CHILD
+        if self.probe_child and not _child_ok(["basic"]):
+            raise K.HipUnavailable("libek_hip.so failed its load-and-run probe in a child process")
         if not K.probe_hip():
             raise K.HipUnavailable("libek_hip.so failed its load-and-run probe")
         self.hip = True
@@ -199,6 +224,7 @@ class _FastEngine:
         bucket = self._bucket(total)
         key = (b, bucket)
         if key not in self.graphs:
+            self._shape_ok(b, 0, bucket)
             self.graphs[key] = self._capture(b, bucket)
         return self.graphs[key]
 
@@ -254,11 +280,20 @@ class _FastEngine:
         torch.cuda.synchronize()
         return g
 
+    def _shape_ok(self, b: int, q: int, bucket: int) -> None:
+        """engine.py:444-452: run this shape's attention launches in a child
+        before capturing it here (with ENGINE_PROBE_CHILD=1)."""
+        if self.probe_child and not _child_ok(["shape", b, q, bucket, self.n_kv, self.model.cfg.num_heads,
+                                               self.head_dim]):
+            raise K.HipUnavailable(f"the attention launches of shape (b={b}, q={q}, bucket={bucket}) "
+                                   "failed their probe in a child process")
+
     def _get_spec_graph(self, b: int, need: int) -> _SpecGraph:
-        """engine.py:440-470 (without the child-process shape probe)."""
+        """engine.py:440-455."""
         bucket = self._bucket(need)
         key = ("spec", b, bucket)
         if key not in self.graphs:
+            self._shape_ok(b, _spec_q(b), bucket)
             self.graphs[key] = self._capture_spec(b, bucket)
         return self.graphs[key]
 

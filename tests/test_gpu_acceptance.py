@@ -42,3 +42,20 @@ def test_engine_output_passes_acceptance(dev, cfg_name):
     gen = list(eng.generate(prompts, 8))
     v = A.verdict(A.margins(fn, prompts, gen))
     assert v["pass"] and v["positions"] == 24, v
+
+
+def test_child_probes_and_probed_engine(dev, monkeypatch):
+    """ek_probe in a child: the load-and-run probe and the attention launches
+    of a decode and a verify shape; an engine that probes every new shape in
+    a child before capturing it still generates the same tokens."""
+    from enginekernel_amd import engine as E
+    assert E._child_ok(["basic"])
+    assert E._child_ok(["shape", 1, 3, 1024, 8, 32, 128])
+    assert E._child_ok(["shape", 4, 0, 2048, 8, 32, 128])
+    cfg = dict(C.QWEN3_TINY)
+    tensors = C.random_weights(cfg, seed=0)
+    plain = list(Engine(model=Qwen3(None, dev, tensors=tensors, config=cfg)).generate([[1, 2, 3, 4, 5]], 6))
+    monkeypatch.setattr(E, "PROBE_CHILD", True)
+    eng = Engine(model=Qwen3(None, dev, tensors=tensors, config=cfg))
+    assert eng._impl.probe_child
+    assert list(eng.generate([[1, 2, 3, 4, 5]], 6)) == plain
