@@ -46,7 +46,7 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 # (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same counter reads for a
 # 256 MiB device copy (FETCH 0.50007, WRITE 1.0). Re-measure when the kernel changes.
 #   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
-GATE_UP_TRAFFIC_B1 = 100_003_000
+GATE_UP_TRAFFIC_B1 = 100_153_865
 #   the persistent step kernel (step_kernel<128, 4>) at batch 1, context 137..146:
 #   3,977,284 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.010x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)

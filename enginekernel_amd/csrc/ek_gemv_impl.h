@@ -63,8 +63,126 @@ struct GemvParams {
   float* am_val; int32_t* am_idx;
 };
 
+// The FMA kernel's prologue (one workgroup of NTHR threads per group of
+// output rows, weights of a whole block already in flight): rows one after
+// another, each thread's sum of squares folded with one barrier. At batch 1
+// it is measured faster than the bulk form below (per-kernel batch-1 step
+// 2.46 against 2.96 ms: the bulk form's second barrier and one-wave row
+// statistics sit on the path after the weights land).
+template <int PRO, int BM>
+__device__ __forceinline__ void prologue_rows(const GemvParams& p, bf16_t* xs, float (*red)[BM]) {
+  const int tid = threadIdx.x;
+  const int64_t ks = p.ks;
+  const int64_t nch = ks >> 3;
+  const int64_t kbase = (int64_t)blockIdx.y * ks;
+  if constexpr (PRO == PRO_X) {
+    for (int b = 0; b < BM; ++b) {
+      for (int64_t c = tid; c < nch; c += NTHR) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (b < p.m) v = ld16(p.x + b * p.ldx + kbase + c * 8);
+        *reinterpret_cast<uint4*>(xs + b * ks + c * 8) = v;
+      }
+    }
+    return;
+  } else {
+    // pass 1: r (the pre-norm row, bf16) into xs, sum of squares per row
+    const bool writer = (blockIdx.x == 0 && blockIdx.y == 0);
+    float ss[BM];
+#pragma unroll
+    for (int b = 0; b < BM; ++b) ss[b] = 0.f;
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      if (b >= p.m) continue;
+      const bf16_t* src = nullptr;
+      if constexpr (PRO == PRO_EMBED) {
+        int64_t t = p.tokens[b];
+        t = t < 0 ? 0 : (t >= p.vocab ? p.vocab - 1 : t);
+        src = p.embed + t * p.lde;
+      }
+      for (int64_t c = tid; c < nch; c += NTHR) {
+        float r[8];
+        if constexpr (PRO == PRO_EMBED) {
+          unpack8(ld16(src + c * 8), r);
+        } else if constexpr (PRO == PRO_NORM) {
+          unpack8(ld16(p.x + b * p.ldx + c * 8), r);
+        } else if constexpr (PRO == PRO_ADD_NORM) {
+          float xv[8], rv[8];
+          unpack8(ld16(p.x + b * p.ldx + c * 8), xv);
+          unpack8(ld16(p.res + b * p.ldr + c * 8), rv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) r[j] = rbf(rv[j] + xv[j]);
+        } else {  // PRO_PARTS
+          float sum[8];
+          const float* pp = p.parts + b * ks + c * 8;
+          float4 a0 = *reinterpret_cast<const float4*>(pp);
+          float4 a1 = *reinterpret_cast<const float4*>(pp + 4);
+          sum[0] = a0.x; sum[1] = a0.y; sum[2] = a0.z; sum[3] = a0.w;
+          sum[4] = a1.x; sum[5] = a1.y; sum[6] = a1.z; sum[7] = a1.w;
+          for (int s = 1; s < p.sk_in; ++s) {
+            const float* q = pp + s * p.parts_ss;
+            float4 b0 = *reinterpret_cast<const float4*>(q);
+            float4 b1 = *reinterpret_cast<const float4*>(q + 4);
+            sum[0] += b0.x; sum[1] += b0.y; sum[2] += b0.z; sum[3] += b0.w;
+            sum[4] += b1.x; sum[5] += b1.y; sum[6] += b1.z; sum[7] += b1.w;
+          }
+          float rv[8];
+          unpack8(ld16(p.res + b * p.ldr + c * 8), rv);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) r[j] = rbf(rv[j] + rbf(sum[j]));
+        }
+        uint4 pk = make_uint4(pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7]));
+        *reinterpret_cast<uint4*>(xs + b * ks + c * 8) = pk;
+        if (PRO != PRO_NORM && writer && p.res_out)
+          *reinterpret_cast<uint4*>(p.res_out + b * p.ldro + c * 8) = pk;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss[b] = fmaf(r[j], r[j], ss[b]);
+      }
+    }
+    if constexpr (PRO == PRO_EMBED) {
+      if (writer && tid == 0 && p.len_t) {
+        int64_t len = *p.len_t;
+        for (int b = 0; b < p.m; ++b) p.slot_t[b] = len;
+        *p.len_t = len + 1;
+      }
+    }
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      float v = wave_sum(ss[b]);
+      if (lane == 0) red[wave][b] = v;
+    }
+    __syncthreads();
+    float rstd[BM];
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      float t = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWAVE; ++w) t += red[w][b];
+      float mean = t / (float)ks;
+      rstd[b] = 1.0f / sqrtf(mean + p.eps);
+    }
+    // pass 2: xn = bf16(w * bf16(r * rstd)); zero rows >= m
+#pragma unroll
+    for (int b = 0; b < BM; ++b) {
+      for (int64_t c = tid; c < nch; c += NTHR) {
+        uint4* dst = reinterpret_cast<uint4*>(xs + b * ks + c * 8);
+        if (b >= p.m) { *dst = make_uint4(0, 0, 0, 0); continue; }
+        float r[8], g[8];
+        unpack8(*dst, r);
+        unpack8(ld16(p.nw + c * 8), g);
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = rbf(g[j] * rbf(r[j] * rstd[b]));
+        *dst = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+      }
+    }
+  }
+}
+
+
 // ----------------------------------------------------------------------------
-// prologue: xs[b * xld + e] (bf16) for b < BM, e < ks
+// prologue: xs[b * xld + e] (bf16) for b < BM, e < ks -- the matrix-core
+// kernel's (2..8 rows; the FMA kernel takes prologue_rows above).
 //
 // The BM x ks/8 chunks of 8 elements are dealt out flat over the threads
 // (job j -> row j / nch, chunk j % nch) and taken GJ jobs at a time with
@@ -288,7 +406,7 @@ __global__ __launch_bounds__(NTHR) void gemv_kernel(GemvParams p) {
       for (int r = 0; r < R2; ++r) wv[r][j] = (c < nch) ? ld16_nt(wrow(g, r) + c * 8) : make_uint4(0, 0, 0, 0);
     }
   }
-  prologue<PRO, BM>(p, xs, ks, red);
+  prologue_rows<PRO, BM>(p, xs, red);
   __syncthreads();
 
   for (; g < ngroups; g += gridDim.x) {
