@@ -48,7 +48,7 @@ SIGNATURES = {
                        _I64, _I64, _I64, _I64, _F, _F, _P, _I64, _P, _P],
     "ek_attn_prefill": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "ek_attn_verify": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
-                       _P],
+                       _P, _I64, _I64, _P],
     "ek_ngram_draft": [_P, _P, _P, _I64, _I64, _I64, _P],
     "ek_spec_accept": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "ek_lm_head_argmax": [_P, _P, _I64, _P, _P, _F, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,

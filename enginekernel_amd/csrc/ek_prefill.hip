@@ -50,6 +50,13 @@ struct PrefillParams {
   int64_t s_cap;                      // cache rows per (batch row, kv head)
   int nkv;
   float scale;
+  // key splits (verify): split sp of a query block takes keys [k0 + sp * kchunk,
+  // + kchunk) and writes its unnormalised output and (max, sum) to po / pml
+  int nsplit;                         // 1: no split, the normalised output goes to out
+  int64_t kchunk;                     // keys per split (a multiple of KB)
+  float* po;                          // [nsplit][B*S][n_q][D]
+  float* pml;                         // [nsplit][B*S][n_q][2]
+  int nq;                             // query heads (n_kv * G)
 };
 
 template <int D, int G>
@@ -78,13 +85,18 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
   int64_t qb = p.q0 ? p.q0[b] : 0;
   qb = qb < 0 ? 0 : (qb > p.s_cap - p.s ? p.s_cap - p.s : qb);
   const int64_t kend = qb + p.s;
-  const int64_t t0 = (int64_t)blockIdx.x * QT;
+  const int qblk = (int)blockIdx.x / p.nsplit, sp = (int)blockIdx.x - qblk * p.nsplit;
+  const int64_t t0 = (int64_t)qblk * QT;
   int64_t pad = p.start[b];
   pad = pad < 0 ? 0 : (pad > kend ? kend : pad);
   const int64_t tend = t0 + QT < p.s ? t0 + QT : p.s;   // tokens [t0, tend)
   // keys [k0, qb + tend): padding rows see only themselves, the others keys >= pad
-  const int64_t k0 = (qb + t0 < pad ? qb + t0 : pad) & ~(int64_t)(KB - 1);
-  const int64_t ntile = (qb + tend - k0 + KB - 1) / KB;
+  const int64_t kb0 = (qb + t0 < pad ? qb + t0 : pad) & ~(int64_t)(KB - 1);
+  // this split's keys [k0, k1)
+  const int64_t k0 = p.nsplit == 1 ? kb0 : kb0 + sp * p.kchunk;
+  int64_t k1 = p.nsplit == 1 ? qb + tend : k0 + p.kchunk;
+  k1 = k1 < qb + tend ? k1 : qb + tend;
+  const int64_t ntile = k1 > k0 ? (k1 - k0 + KB - 1) / KB : 0;
 
   const bf16_t* kb = p.kc + b * p.csb + h * p.csh;
   const bf16_t* vb = p.vc + b * p.csb + h * p.csh;
@@ -155,7 +167,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
       for (int e = 0; e < 4; ++e) {
         const int64_t tok = qb + t0 + 4 * q4 + e;   // the query's cache position
         const int64_t key = kt + 16 * kbk + r16;
-        const bool ok = (key <= tok && key >= pad) || (tok < pad && key == tok);
+        const bool ok = key < k1 && ((key <= tok && key >= pad) || (tok < pad && key == tok));
         sv[kbk][e] = ok ? c[e] * p.scale : -1e30f;
       }
     }
@@ -197,6 +209,23 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
     }
   }
   // out rows 4 q4 + e, dims 16 j + r16
+  if (p.nsplit > 1) {   // this split's unnormalised rows and their (max, sum)
+    const int64_t rows = (int64_t)gridDim.z * p.s;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t tok = t0 + 4 * q4 + e;
+      if (tok >= p.s) continue;
+      const int64_t idx = ((int64_t)sp * rows + (int64_t)b * p.s + tok) * p.nq + (h * G + g);
+      float* prow = p.po + idx * D;
+#pragma unroll
+      for (int j = 0; j < DB; ++j) prow[16 * j + r16] = o[j][e];
+      if (r16 == 0) {
+        p.pml[2 * idx] = m_row[e];
+        p.pml[2 * idx + 1] = l_row[e];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int64_t tok = t0 + 4 * q4 + e;
@@ -208,10 +237,37 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillParams p) {
   }
 }
 
+// The key splits' rows combined: M = max m_s, out = sum_s o_s e^(m_s - M) /
+// sum_s l_s e^(m_s - M), rounded to bf16 once. One workgroup of D threads
+// per (query row, head).
+template <int D>
+__global__ __launch_bounds__(D) void attn_split_combine_kernel(PrefillParams p) {
+  const int64_t row = blockIdx.x, head = blockIdx.y;
+  const int64_t rows = (int64_t)gridDim.x;
+  const int d = threadIdx.x;
+  float mx = -1e30f;
+  for (int s = 0; s < p.nsplit; ++s) mx = fmaxf(mx, p.pml[2 * ((s * rows + row) * p.nq + head)]);
+  float l = 0.f, acc = 0.f;
+  for (int s = 0; s < p.nsplit; ++s) {
+    const int64_t idx = (s * rows + row) * p.nq + head;
+    const float ms = p.pml[2 * idx];
+    const float w = ms > -1e29f ? expf(ms - mx) : 0.f;
+    l += p.pml[2 * idx + 1] * w;
+    acc += p.po[idx * D + d] * w;
+  }
+  p.out[row * p.ldo + head * D + d] = (bf16_t)f2bf(l > 0.f ? acc / l : 0.f);
+}
+
 template <int D, int G>
 hipError_t launch_prefill(const PrefillParams& p, int64_t b, hipStream_t st) {
-  dim3 grid((unsigned)((p.s + QT - 1) / QT), (unsigned)p.nkv, (unsigned)b);
+  dim3 grid((unsigned)((p.s + QT - 1) / QT * p.nsplit), (unsigned)p.nkv, (unsigned)b);
   hipLaunchKernelGGL((attn_prefill_kernel<D, G>), grid, dim3(64 * G), 0, st, p);
+  if (p.nsplit > 1) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((attn_split_combine_kernel<D>), dim3((unsigned)(b * p.s), (unsigned)p.nq), dim3(D), 0, st,
+                       p);
+  }
   return hipGetLastError();
 }
 
@@ -233,9 +289,13 @@ namespace {
 hipError_t attn_flash(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
                       int64_t css, int64_t s_cap, const int32_t* start, const int64_t* q0, void* out, int64_t ldo,
                       int64_t b, int64_t s, int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale,
-                      void* stream) {
+                      void* stream, float* part = nullptr, int64_t part_floats = 0, int64_t splits = 1) {
   if (b < 1 || b > 65535 || s < 1 || s > s_cap || n_kv < 1 || n_kv > 65535 || n_q % n_kv)
     return ek_fail(hipErrorInvalidValue, "attn_prefill/attn_verify: bad batch, length or head counts");
+  if (splits < 1 || splits > 256 || (s + QT - 1) / QT * splits > 65535)
+    return ek_fail(hipErrorInvalidValue, "attn_verify: splits must be 1..256");
+  if (splits > 1 && (!part || part_floats < splits * b * s * n_q * (head_dim + 2)))
+    return ek_fail(hipErrorInvalidValue, "attn_verify: the split workspace is too small");
   if (ldq % 8 || ldo % 8 || css % 8 || csh % 8 || csb % 8 || (reinterpret_cast<uintptr_t>(q) & 15) ||
       (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
     return ek_fail(hipErrorInvalidValue, "attn_prefill/attn_verify: rows must be 16-byte aligned");
@@ -246,6 +306,12 @@ hipError_t attn_flash(const void* q, int64_t ldq, const void* k_cache, const voi
   p.start = start; p.q0 = q0;
   p.out = (bf16_t*)out; p.ldo = ldo;
   p.s = s; p.s_cap = s_cap; p.nkv = (int)n_kv; p.scale = sm_scale;
+  p.nq = (int)n_q;
+  p.nsplit = (int)splits;
+  // keys per split: the cache's rows spread evenly, in whole 32-key tiles
+  p.kchunk = ((s_cap + splits - 1) / splits + KB - 1) / KB * KB;
+  p.po = part;
+  p.pml = part ? part + splits * b * s * n_q * head_dim : nullptr;
   hipStream_t st = (hipStream_t)stream;
   const int g = (int)(n_q / n_kv);
   switch (head_dim) {
@@ -271,11 +337,11 @@ int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void*
 int ek_attn_verify(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
                    int64_t css, int64_t s_cap, const int32_t* start, const int64_t* len_b, void* out, int64_t ldo,
                    int64_t b, int64_t nq, int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale,
-                   void* stream) {
+                   float* part, int64_t part_floats, int64_t splits, void* stream) {
   EK_GUARD();
   if (!len_b) return ek_fail(hipErrorInvalidValue, "attn_verify: len_b is required");
   return attn_flash(q, ldq, k_cache, v_cache, csb, csh, css, s_cap, start, len_b, out, ldo, b, nq, n_q, n_kv,
-                    head_dim, sm_scale, stream);
+                    head_dim, sm_scale, stream, part, part_floats, splits);
 }
 
 }  // extern "C"

@@ -599,7 +599,18 @@ def attn_prefill(qkv, k_cache, v_cache, start_t, s, n_q, sm_scale, out=None):
     return y
 
 
-def attn_verify(qkv, k_cache, v_cache, start_t, len_b, nq, n_q, sm_scale, out=None):
+_VERIFY_PART: dict = {}
+
+
+def verify_splits(s_cap: int) -> int:
+    """Key splits of the verify attention: one per 64 cache rows (at most
+    32; measured at the Qwen3-4B shape, 512-row cache: 4 / 8 / 16 splits ->
+    3.49 / 3.33 / 3.37 ms per verify step); a split past a row's keys writes
+    an empty partial and leaves at once."""
+    return max(1, min(32, s_cap // 64))
+
+
+def attn_verify(qkv, k_cache, v_cache, start_t, len_b, nq, n_q, sm_scale, out=None, splits=None):
     """The attention of a speculative verify step, ek_kernels.py:1419
     (flash_verify; torch form attn_torch, :1451): row b's nq query tokens
     (rows b*nq + j of the fused qkv [B*nq, (n_q + 2 n_kv) D], already
@@ -616,9 +627,17 @@ def attn_verify(qkv, k_cache, v_cache, start_t, len_b, nq, n_q, sm_scale, out=No
     _need(len_b.dtype == torch.int64 and len_b.numel() >= b and len_b.is_contiguous(), "len_b: int64 [B]")
     y = torch.empty(b * nq, n_q * d, device=qkv.device, dtype=_BF16) if out is None else out
     _need(y.shape == (b * nq, n_q * d) and y.stride(-1) == 1, "attn_verify: out")
+    sp = verify_splits(s_cap) if splits is None else int(splits)
+    part = None
+    if sp > 1:
+        need = sp * b * nq * n_q * (d + 2)
+        key = (qkv.device, need)
+        part = _VERIFY_PART.get(key)
+        if part is None:   # allocated once per shape, before any graph capture records the launch
+            part = _VERIFY_PART[key] = torch.empty(need, dtype=torch.float32, device=qkv.device)
     call("ek_attn_verify", ptr(qkv), qkv.stride(0), ptr(k_cache), ptr(v_cache), k_cache.stride(0),
          k_cache.stride(1), k_cache.stride(2), s_cap, ptr(start_t), ptr(len_b), ptr(y), y.stride(0), b, nq, n_q,
-         n_kv, d, float(sm_scale), stream())
+         n_kv, d, float(sm_scale), ptr(part), part.numel() if part is not None else 0, sp, stream())
     return y
 
 

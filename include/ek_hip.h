@@ -161,11 +161,15 @@ int ek_attn_prefill(const void* q, int64_t ldq, const void* k_cache, const void*
  * (q rows b * nq + j, as in attn_prefill) sit at cache slots len_b[b] + j
  * (their keys/values already written there), and query j sees the keys at
  * slots [start[b], len_b[b] + j]. Same kernel, layouts and arithmetic as
- * attn_prefill; len_b is a device int64 [B], clamped to [0, s_cap - nq]. */
+ * attn_prefill; len_b is a device int64 [B], clamped to [0, s_cap - nq].
+ * splits > 1 spreads each row's keys over that many workgroups (s_cap / splits
+ * keys each, in 32-key tiles) whose unnormalised rows and (max, sum) go to
+ * part (fp32, at least splits * B * nq * n_q * (head_dim + 2) floats) and
+ * are combined by a second launch; splits = 1 needs no part. */
 int ek_attn_verify(const void* q, int64_t ldq, const void* k_cache, const void* v_cache, int64_t csb, int64_t csh,
                    int64_t css, int64_t s_cap, const int32_t* start, const int64_t* len_b, void* out, int64_t ldo,
                    int64_t b, int64_t nq, int64_t n_q, int64_t n_kv, int64_t head_dim, float sm_scale,
-                   void* stream);
+                   float* part, int64_t part_floats, int64_t splits, void* stream);
 
 /* ngram_draft: engine/ek_kernels.py:1510 (ngram_draft, its kernel :618):
  * per row b, tokens[b][0..q) = [hist[b][hl - 1], q - 1 drafts] with hl =

@@ -86,7 +86,9 @@ def test_attn_verify_matches_oracle(dev, d, g, lens, starts, nq):
     len_b = torch.tensor(lens, dtype=torch.int64)
     start = torch.tensor(starts, dtype=torch.int32)
     scale = d ** -0.5
-    got = K.attn_verify(qkv.to(dev), kc.to(dev), vc.to(dev), start.to(dev), len_b.to(dev), nq, n_q, scale).cpu()
+    outs = [K.attn_verify(qkv.to(dev), kc.to(dev), vc.to(dev), start.to(dev), len_b.to(dev), nq, n_q, scale,
+                          splits=sp).cpu() for sp in (1, 3, None, 32)]
+    got = outs[0]
     # float64 softmax attention over keys [start_b, len_b + j]
     want = torch.empty(b * nq, n_q * d, dtype=torch.float64)
     for r in range(b):
@@ -103,6 +105,10 @@ def test_attn_verify_matches_oracle(dev, d, g, lens, starts, nq):
     # and the oracle's restatement of the reference's torch form (bf16 scores)
     ref = O.verify_attn(q, kc, vc, len_b, start, scale, nq).float().reshape(b * nq, n_q * d)
     assert (got.float() - ref).abs().max().item() <= 2e-2 * ref.abs().max().item()
+    # key splits (3, the default plan's, 32): the same bound against float64
+    for o in outs[1:]:
+        err = (o.double() - want).abs()
+        assert (err <= bound).all(), err.max().item()
 
 
 def test_verify_equals_teacher_forced_decode(dev):
