@@ -48,9 +48,9 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 #   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
 GATE_UP_TRAFFIC_B1 = 100_153_865
 #   the persistent step kernel (step_kernel<128, 4>) at batch 1, context 137..146:
-#   3,977,284 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.010x its
+#   3,973,974 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.009x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_148_929_000
+STEP_TRAFFIC_B1 = 8_142_155_000
 
 
 def log(msg: str) -> None:
