@@ -120,7 +120,10 @@ __host__ __device__ constexpr size_t align16(size_t x) { return (x + 15) & ~(siz
 // LDS layout of one unit: the score rows, then the fixed-size arrays
 template <int D, int G>
 struct AttnLds {
-  static __host__ __device__ constexpr size_t scores(int64_t cap) { return align16((size_t)G * cap * 4); }
+  // score rows of an odd stride: with a stride that is a multiple of the 32
+  // LDS banks, the G rows' same-key entries would share a bank
+  static __host__ __device__ constexpr int64_t stride(int64_t cap) { return cap | 1; }
+  static __host__ __device__ constexpr size_t scores(int64_t cap) { return align16((size_t)G * stride(cap) * 4); }
   static constexpr size_t QS = align16((size_t)G * D * 4);
   static constexpr size_t KNEW = align16((size_t)D * 4);
   static constexpr size_t VNEW = align16((size_t)FDC * 2);
@@ -279,7 +282,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
         const int64_t rel = tb + 4 * q4 + e;
         const float sv = c[e] * a.sm_scale;
         const bool ok = r16 < G && rel < nrel;
-        if (ok) sc_lds[(int64_t)r16 * cap + rel] = sv;
+        if (ok) sc_lds[(int64_t)r16 * L::stride(cap) + rel] = sv;
         mrun = ok ? fmaxf(mrun, sv) : mrun;
       }
     }
@@ -300,7 +303,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
     float M = stm[0][g];
 #pragma unroll
     for (int w = 1; w < FNW; ++w) M = fmaxf(M, stm[w][g]);
-    float* row = sc_lds + (int64_t)g * cap;
+    float* row = sc_lds + (int64_t)g * L::stride(cap);
     float lsum = 0.f;
     for (int64_t n = tid / G; n < nrel; n += FNT / G) {
       const float ev = expf(row[n] - M);
@@ -325,7 +328,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
   f32x4_t acc[2];
   acc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   acc[1] = acc[0];
-  const float* prow = sc_lds + (int64_t)(r16 < G ? r16 : 0) * cap;
+  const float* prow = sc_lds + (int64_t)(r16 < G ? r16 : 0) * L::stride(cap);
   uint16_t (*vtw)[VTS] = vt[wave];
   for (int64_t t0 = wave; t0 < ntile32; t0 += (int64_t)FNW * FPT) {
     if (t0 != wave) {

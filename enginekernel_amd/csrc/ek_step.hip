@@ -34,7 +34,7 @@ struct Plan {
 };
 
 size_t attn_lds(int d, int g, int64_t s_cap) {
-  size_t attn = eka::align16((size_t)(g + 6) * d * 2) + eka::align16((size_t)g * s_cap * 4);
+  size_t attn = eka::align16((size_t)(g + 6) * d * 2) + eka::align16((size_t)g * (s_cap | 1) * 4);   // AttnLds
   attn += eka::align16((size_t)g * d * 4) + eka::align16((size_t)d * 4) + eka::align16((size_t)eka::FDC * 2) +
           2 * eka::align16((size_t)eka::FNW * 8 * 4) + eka::align16((size_t)eka::FNW * 32 * eka::VTS * 2) +
           eka::align16((size_t)eka::FNW * g * eka::FDC * 4) + eka::align16((size_t)d * 2);
