@@ -137,17 +137,13 @@ def probe_traffic(b: int = 1, layers: int = 36) -> None:
         with torch.inference_mode():
             eng._ensure_cache(1, s + steps + 1)
             g = eng._get_graph(1, s + steps + 1)
-            g.tokens.fill_(1)
-            g.positions.fill_(s)
-            g.start_t.zero_()
-            g.len_t.fill_(s)
-            g.step_idx.zero_()
+            g.begin(torch.ones(1, dtype=torch.int64, device=dev), [s], [0], s)
             kv = ([t[:1] for t in eng.k_cache], [t[:1] for t in eng.v_cache])
             torch.cuda.synchronize()
             for _ in range(steps):
                 eng._step_body(g, kv)
             torch.cuda.synchronize()
-        model.check_step_error()
+        K.check_error_word(g.err, "the profiled decode steps")
         print(json.dumps({"probe": "traffic", "copy_bytes": 2 * src.numel(), "step_launches": steps,
                           "step_bytes": step_bytes(cfg, s + (steps + 1) / 2), "context": [s + 1, s + steps]}),
               flush=True)
@@ -249,6 +245,7 @@ def main():
 
     import torch
     from enginekernel_amd import checkpoint as C
+    from enginekernel_amd import ek_kernels as K
     from enginekernel_amd.ek_model import Qwen3
     from enginekernel_amd.engine import MAX_STEPS, _FastEngine
 
@@ -284,11 +281,7 @@ def main():
         graph = eng._get_graph(b, total)
         log(f"graph captured in {time.perf_counter() - t0:.1f}s (bucket {graph.bucket})")
         first = eng._first_token(ids, pos, b, s, bias)
-        graph.tokens.copy_(first)
-        graph.positions.fill_(s)
-        graph.start_t.zero_()
-        graph.len_t.fill_(s)
-        graph.step_idx.zero_()
+        graph.begin(first, [s], [0], s)
         for _ in range(W):
             graph.graph.replay()
         torch.cuda.synchronize()
@@ -308,7 +301,7 @@ def main():
             raise RuntimeError("graph step counter out of step with the replays")
 
         persistent = model.buffers(b).step is not None
-        model.check_step_error()
+        K.check_error_word(graph.err, "the timed decode steps")
         if persistent:
             # one kernel per replay: its launch time is the replay time
             ctx_avg = s + W + 1 + (K_steps - 1) / 2

@@ -45,7 +45,7 @@ SIGNATURES = {
                            _P, _P, _I64, _I64, _P],
     "ek_attn_decode": [_P, _I64, _I64, _I, _P, _P, _P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64,
                        _I64, _P, _P, _P, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
-                       _I64, _I64, _I64, _I64, _F, _F, _P, _I64, _P, _P],
+                       _I64, _I64, _I64, _I64, _F, _F, _P, _I64, _P, _P, _P],
     "ek_attn_prefill": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "ek_attn_verify": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F,
                        _P, _I64, _I64, _P],
@@ -57,7 +57,7 @@ SIGNATURES = {
     "ek_decode_step": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _F,
                        _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                        _P, _P, _P, _P, _P, _P, _P, _I64, _P,
-                       _P, _I64, _P, _P, _P],
+                       _P, _P, _I64, _P, _P, _P],
 }
 
 
@@ -106,6 +106,8 @@ def load(path: str | None = None):
     lib.ek_last_error.restype = ctypes.c_char_p
     lib.ek_device_info.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_char_p, ctypes.c_int]
     lib.ek_device_info.restype = ctypes.c_int
+    lib.ek_set_wait_limit.argtypes = [ctypes.c_int64]
+    lib.ek_set_wait_limit.restype = ctypes.c_int64
     if path is None:
         _lib = lib
     return lib
@@ -136,6 +138,12 @@ def ptr(t) -> int | None:
 def stream() -> int:
     """The current torch stream as a hipStream_t value (captured by graphs)."""
     return torch.cuda.current_stream().cuda_stream
+
+
+def set_wait_limit(polls: int) -> int:
+    """Bound the device-side waits of later launches to `polls` polls (<= 0:
+    the kernels' defaults); returns the previous setting."""
+    return int(load().ek_set_wait_limit(int(polls)))
 
 
 def device_info() -> tuple[int, str]:

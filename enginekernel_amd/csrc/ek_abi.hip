@@ -7,8 +7,16 @@
 #include "ek_abi_internal.h"
 #include "ek_hip.h"
 
+#include <atomic>
+
 namespace {
 thread_local char g_err[256] = {0};
+std::atomic<int64_t> g_wait_limit{0};   // 0: each kernel's own default
+}
+
+int64_t ek_wait_limit(int64_t dflt) {
+  const int64_t v = g_wait_limit.load(std::memory_order_relaxed);
+  return v > 0 ? v : dflt;
 }
 
 hipError_t ek_fail(hipError_t code, const char* msg) {
@@ -22,7 +30,11 @@ extern "C" {
 
 const char* ek_last_error(void) { return g_err; }
 
-const char* ek_version(void) { return "enginekernel_amd 0.1 gfx950"; }
+const char* ek_version(void) { return "enginekernel_amd 0.2 gfx950"; }
+
+int64_t ek_set_wait_limit(int64_t polls) {
+  return g_wait_limit.exchange(polls > 0 ? polls : 0, std::memory_order_relaxed);
+}
 
 // Report the device the current HIP context targets: compute units and the
 // gfx architecture name (e.g. "gfx950"). Returns a hipError_t.

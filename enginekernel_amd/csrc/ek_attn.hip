@@ -68,6 +68,8 @@ struct AttnParams {
   float sm_scale, eps;
   unsigned long long* part;   // [B, nkv, splits, G, D] {fp32 bits, tag} words
   uint32_t* ticket;           // [B * nkv][2]: arrivals of this launch, epoch
+  int* err;                   // set to 1 when the combine's wait for a split gives up (may be null)
+  int64_t spin;               // polls of that wait before it gives up
 };
 
 struct Range { int64_t lo, hi, len; };
@@ -439,7 +441,11 @@ __global__ __launch_bounds__(NT) void attn_pvs_kernel(AttnParams p) {
         if (s0 + k < p.splits) {
           unsigned long long x = v[k];
           unsigned long long* w = part + (int64_t)(s0 + k) * G * D + i;
-          for (int spin = 0; (uint32_t)(x >> 32) != tag && spin < (1 << 22); ++spin) {
+          for (int64_t spin = 0; (uint32_t)(x >> 32) != tag; ++spin) {
+            if (spin >= p.spin) {   // a split never delivered: flag the output as invalid
+              if (p.err) __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              break;
+            }
             __builtin_amdgcn_s_sleep(1);
             x = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
@@ -548,7 +554,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
                    float* mmax, int64_t sp, int64_t gp, void* out, int64_t ldo_b,
                    int64_t ldo_h, int64_t b, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits,
                    int64_t chunk, float sm_scale, float eps, void* part, int64_t part_words, uint32_t* ticket,
-                   void* stream) {
+                   int* err, void* stream) {
   EK_GUARD();
   if (b < 1 || b * n_kv > 0x7fffffff || n_kv < 1 || n_q < n_kv || n_q % n_kv || b > 65535)
     return ek_fail(hipErrorInvalidValue, "attn: bad batch or head counts");
@@ -579,6 +585,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
   p.nq = (int)n_q; p.nkv = (int)n_kv; p.splits = (int)splits; p.chunk = chunk;
   p.sm_scale = sm_scale; p.eps = eps;
   p.part = (unsigned long long*)part; p.ticket = ticket;
+  p.err = err; p.spin = ek_wait_limit(int64_t(1) << 22);
   hipStream_t st = (hipStream_t)stream;
   switch (head_dim) {
     case 32: return launch_attn_g<32>(p, (int)g, (int)b, st);

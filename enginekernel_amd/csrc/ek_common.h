@@ -110,23 +110,3 @@ __device__ __forceinline__ uint4 ld16_nt(const bf16_t* p) {
   const u32x4_t v = __builtin_nontemporal_load((global_u32x4_t*)(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-
-// Release this workgroup's global writes and count it in; returns true in
-// the last workgroup to arrive (which then observes every other
-// workgroup's writes). The counter is reset by that last workgroup, so it
-// is zero again when the next launch that uses it starts. Every thread of
-// the workgroup must call this.
-__device__ __forceinline__ bool last_to_arrive(int* counter, int total, int* lds_flag) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    int last = (prev == total - 1);
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *lds_flag = last;
-  }
-  __syncthreads();
-  bool last = *lds_flag != 0;
-  if (last) __threadfence();
-  return last;
-}

@@ -5,15 +5,22 @@
 #include "ek_abi_internal.h"
 #include "ek_hip.h"
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 namespace eks {
 template <> hipError_t launch_step<32>(const StepArgs&, int, int, hipStream_t);
 template <> hipError_t launch_step<64>(const StepArgs&, int, int, hipStream_t);
 template <> hipError_t launch_step<128>(const StepArgs&, int, int, hipStream_t);
+template <> int step_occupancy<32>(int, size_t);
+template <> int step_occupancy<64>(int, size_t);
+template <> int step_occupancy<128>(int, size_t);
 }  // namespace eks
 
 namespace {
 
-constexpr int64_t kSpin = int64_t(1) << 20;           // polls of one hand-over wait before giving up (~1 s)
+constexpr int64_t kSpin = int64_t(1) << 20;           // default polls of one hand-over wait before giving up (~1 s)
 constexpr size_t kLdsLimit = 160 * 1024 - 1024;       // dynamic LDS per workgroup (static arrays aside)
 constexpr int64_t kFusedScoreLds = 32 * 1024;         // score row bytes per attention unit
 
@@ -39,6 +46,25 @@ size_t attn_lds(int d, int g, int64_t s_cap) {
           2 * eka::align16((size_t)eka::FNW * 8 * 4) + eka::align16((size_t)eka::FNW * 32 * eka::VTS * 2) +
           eka::align16((size_t)eka::FNW * g * eka::FDC * 4) + eka::align16((size_t)d * 2);
   return attn;
+}
+
+// Workgroups of step_kernel<d, g> with `lds` bytes of dynamic LDS that one CU
+// holds at once (the occupancy query, cached per instantiation and size).
+int resident_per_cu(int d, int g, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, size_t>, int> cache;
+  const auto key = std::make_tuple(d, g, lds);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  switch (d) {
+    case 32: n = eks::step_occupancy<32>(g, lds); break;
+    case 64: n = eks::step_occupancy<64>(g, lds); break;
+    default: n = eks::step_occupancy<128>(g, lds); break;
+  }
+  cache[key] = n;
+  return n;
 }
 
 // Returns an error (with a message) when the shape is outside what the kernel handles.
@@ -78,6 +104,11 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   p.lds = gemv > attn ? gemv : attn;
   if (p.lds > kLdsLimit) return ek_fail(hipErrorInvalidValue, "decode_step: LDS plan exceeds the workgroup limit");
   p.arena_bytes = 8 * eks::arena_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg);
+  // every workgroup must be resident at once (the hand-over waits of one
+  // need the others running): at least one workgroup of this instantiation,
+  // with this LDS, per CU -- registers, scratch and LDS all counted
+  if (resident_per_cu((int)head_dim, (int)g, p.lds) < 1)
+    return ek_fail(hipErrorInvalidValue, "decode_step: one workgroup per CU does not fit (registers or LDS)");
   return hipSuccess;
 }
 
@@ -106,7 +137,7 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
                    const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb, int64_t csh, int64_t css,
                    int64_t s_cap, int64_t* tokens, int64_t* positions, int64_t* len_t, int64_t* slot_t,
                    const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
-                   void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream) {
+                   void* logits, void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream) {
   EK_GUARD();
   Plan p;
   hipError_t e = make_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
@@ -128,8 +159,9 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
   a.ld_cs = ld_cs; a.rope_len = rope_len; a.csb = csb; a.csh = csh; a.css = css; a.s_cap = s_cap;
   a.tokens = tokens; a.positions = positions; a.len_t = len_t; a.slot_t = slot_t; a.start_t = start_t;
   a.out_buf = out_buf; a.step_idx = step_idx; a.max_steps = max_steps; a.out_tok = out_tok;
+  a.logits = (bf16_t*)logits;
   a.arena = (eks::llw_t*)arena;
-  a.bar = (eks::Bar*)barrier; a.err = err; a.spin = kSpin;
+  a.bar = (eks::Bar*)barrier; a.err = err; a.spin = ek_wait_limit(kSpin);
   a.kpad_max = p.kpad_max; a.part_max = p.part_max; a.o_rows = p.o_rows;
   const int g = (int)(n_q / n_kv);
   hipStream_t st = (hipStream_t)stream;

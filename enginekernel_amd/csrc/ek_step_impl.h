@@ -85,6 +85,7 @@ struct StepArgs {
   int64_t csb, csh, css, s_cap;
   int64_t* tokens; int64_t* positions; int64_t* len_t; int64_t* slot_t; const int32_t* start_t;
   int32_t* out_buf; int64_t* step_idx; int64_t max_steps; int64_t* out_tok;
+  bf16_t* logits;                      // optional [vocab] bf16 logits of the step (null on the hot path)
   llw_t* arena;
   Bar* bar; int* err; int64_t spin;
   int kpad_max, part_max, o_rows;      // LDS plan (host-computed, see make_plan in ek_step.hip)
@@ -436,7 +437,7 @@ __device__ __forceinline__ void wg_argmax(float bv, int bi, float* sv, int* si, 
 }
 
 __device__ __forceinline__ void epilogue_argmax_ll(const Gp& P, const float* part, float* sv, int* si, llw_t* am,
-                                                   uint32_t ep) {
+                                                   uint32_t ep, bf16_t* logits) {
   int u0, u1;
   unit_range(P, u0, u1);
   const int nu = u1 - u0;
@@ -444,6 +445,7 @@ __device__ __forceinline__ void epilogue_argmax_ll(const Gp& P, const float* par
   int bi = 0x7fffffff;
   for (int ul = threadIdx.x; ul < nu; ul += SNT) {
     const float v = rbf(row_sum(part, ul));
+    if (logits) logits[u0 + ul] = (bf16_t)f2bf(v);
     if (am_better(v, u0 + ul, bv, bi)) { bv = v; bi = u0 + ul; }
   }
   float ov;
@@ -641,41 +643,21 @@ __device__ __forceinline__ Gp on_gemv_wgs(Gp g, int n_attn) {
   return g;
 }
 
+// The projection workgroups' part of the step: every layer's projections,
+// then the final add + norm, lm_head and this workgroup's argmax words.
+// False when a hand-over wait gave up (the error word is then set).
 template <int D, int G>
-__global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float s_red[SNW];
-  __shared__ int s_redi[SNW];
-  __shared__ unsigned s_ep;
-
-  const int tid = threadIdx.x;
-  if (tid == 0) {
-    const unsigned e = __hip_atomic_load(&a.bar->ep[blockIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    __hip_atomic_store(&a.bar->ep[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_ep = e;
-  }
+__device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, unsigned char* smem, float* s_red,
+                                                int* s_redi
 #ifdef EK_STEP_TRACE
-  __shared__ int64_t s_ts[24];
-  int64_t* ts_lds = s_ts;
+                                                , int64_t* ts_lds
 #endif
-  __syncthreads();
-  const uint32_t ep = s_ep;
-
+                                                ) {
+  const int tid = threadIdx.x;
   const int h = a.h, inter = a.inter;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = arena_layer_words(h, inter, qkvw, qw);
-  const int64_t len_old = *a.len_t;
-  int64_t hi = len_old + 1;
-  hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
-  const int n_attn = a.nkv * (D / eka::FDC);   // attention units = workgroups [0, n_attn)
-  if ((int)blockIdx.x < n_attn) {
-    attention_loop<D, G>(a, ep, hi, smem
-#ifdef EK_STEP_TRACE
-                         , ts_lds
-#endif
-                         );
-    return;
-  }
+  const int n_attn = a.nkv * (D / eka::FDC);
 
   float* rr = reinterpret_cast<float*>(smem);
   unsigned char* ph = smem + step_rr_bytes(h);
@@ -721,7 +703,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
       add_norm(rr, nullptr, gw1, h, kpad_of(h), a.eps, xs, s_red);
     } else {
       const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
-      if (!__syncthreads_and(ok)) return;
+      if (!__syncthreads_and(ok)) return false;
       add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
     }
     __syncthreads();
@@ -747,7 +729,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     {
       const bool ok = ll_read(LinSrc{att_ll}, qw / 2, ep, xs32, a.err, a.spin);
       if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
-      if (!__syncthreads_and(ok)) return;
+      if (!__syncthreads_and(ok)) return false;
     }
     zero_pad(xs, qw, kpad_of(qw));
     EK_TS(6);
@@ -763,7 +745,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     zero_part(part, part_n);
     {
       const bool ok = ll_read(LinSrc{o_ll}, h / 2, ep, xs32, a.err, a.spin);
-      if (!__syncthreads_and(ok)) return;
+      if (!__syncthreads_and(ok)) return false;
     }
     add_norm(rr, xs32, gw2, h, kpad_of(h), a.eps, xs, s_red);
     // the next input norm's gain loads with the gate/up stream
@@ -783,7 +765,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     zero_part(part, part_n);
     {
       const bool ok = ll_read(LinSrc{act_ll}, inter / 2, ep, xs32, a.err, a.spin);
-      if (!__syncthreads_and(ok)) return;
+      if (!__syncthreads_and(ok)) return false;
     }
     zero_pad(xs, inter, kpad_of(inter));
     __syncthreads();
@@ -809,7 +791,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   zero_part(part, part_n);
   {
     const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
-    if (!__syncthreads_and(ok)) return;
+    if (!__syncthreads_and(ok)) return false;
   }
   add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
   __syncthreads();
@@ -818,44 +800,108 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   gemv_phase(gl, ring, xs, part);
   __syncthreads();
   EK_TS(2);
-  epilogue_argmax_ll(gl, part, s_red, s_redi, am_ll, ep);
+  epilogue_argmax_ll(gl, part, s_red, s_redi, am_ll, ep, a.logits);
   EK_TS(3);
   EK_TS_FLUSH_SYNC(a.nl);
-  if ((int)blockIdx.x != n_attn) return;
+  return true;
+}
 
-  // ---- token = first-index argmax over the projection workgroups'
-  //      partials; step bookkeeping (engine.py:289-292; slot/len advance of
-  //      ek_model.py:375-388)
-  __syncthreads();
-  uint32_t* amw = reinterpret_cast<uint32_t*>(part);
+// Workgroup n_attn's end of the step: the token = first-index argmax over
+// the projection workgroups' words, then the step's bookkeeping
+// (engine.py:289-292; the slot/len advance of ek_model.py:375-388). A step
+// that gave up (ok false, or a wait here runs out) still advances the step
+// counter and writes the sentinel -1 as its token (out_buf, out_tok), and
+// leaves tokens, positions, slot and length as they were, so the host reads
+// the failure at this step's own row and every later row stays aligned.
+template <int D>
+__device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool ok, int64_t len_old,
+                                            unsigned char* smem, float* s_red, int* s_redi) {
+  const int tid = threadIdx.x;
+  const int h = a.h;
+  const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
+  const int n_attn = a.nkv * (D / eka::FDC);
   const int n_gemv = (int)gridDim.x - n_attn;
-  {
-    const bool ok = ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, ep, amw, a.err, a.spin);
-    if (!__syncthreads_and(ok)) return;
+  const llw_t* am_ll = a.arena + (int64_t)a.nl * arena_layer_words(h, a.inter, qkvw, qw);
+  uint32_t* amw = reinterpret_cast<uint32_t*>(smem + step_rr_bytes(h) + eka::align16((size_t)a.kpad_max * 2));
+  __syncthreads();
+  if (ok) ok = __syncthreads_and(ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, ep, amw, a.err, a.spin)) != 0;
+  float ov = 0.f;
+  int oi = 0x7fffffff;
+  if (ok) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int w = tid; w < n_gemv; w += SNT) {
+      const float v = __uint_as_float(amw[2 * w]);
+      const int i = (int)amw[2 * w + 1];
+      if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    wg_argmax(bv, bi, s_red, s_redi, ov, oi);
   }
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int w = tid; w < n_gemv; w += SNT) {
-    const float v = __uint_as_float(amw[2 * w]);
-    const int i = (int)amw[2 * w + 1];
-    if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
-  }
-  float ov;
-  int oi;
-  wg_argmax(bv, bi, s_red, s_redi, ov, oi);
-  EK_TS(4);
-  EK_TS_FLUSH_SYNC(a.nl);
   if (tid == 0) {
     const int64_t step = *a.step_idx;
-    const int64_t tok = oi == 0x7fffffff ? 0 : oi;
+    const int64_t tok = !ok ? -1 : (oi == 0x7fffffff ? 0 : oi);
     if (a.out_tok) a.out_tok[0] = tok;
-    a.tokens[0] = tok;
-    a.positions[0] += 1;
-    a.slot_t[0] = len_old;
     if (step >= 0 && step < a.max_steps) a.out_buf[step] = (int32_t)tok;
-    *a.len_t = len_old + 1;
+    if (ok) {
+      a.tokens[0] = tok;
+      a.positions[0] += 1;
+      a.slot_t[0] = len_old;
+      *a.len_t = len_old + 1;
+    }
     *a.step_idx = step + 1;
   }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float s_red[SNW];
+  __shared__ int s_redi[SNW];
+  __shared__ unsigned s_ep;
+  __shared__ int s_abort;
+
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    const unsigned e = __hip_atomic_load(&a.bar->ep[blockIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    __hip_atomic_store(&a.bar->ep[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ep = e;
+    // the error word is sticky: once a launch gave up, later launches only
+    // advance the step counter (with the sentinel) until the host clears it
+    s_abort = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#ifdef EK_STEP_TRACE
+  __shared__ int64_t s_ts[24];
+  int64_t* ts_lds = s_ts;
+#endif
+  __syncthreads();
+  const uint32_t ep = s_ep;
+  const bool aborted = s_abort != 0;
+  const int64_t len_old = *a.len_t;
+  const int n_attn = a.nkv * (D / eka::FDC);   // attention units = workgroups [0, n_attn)
+  if ((int)blockIdx.x < n_attn) {
+    if (aborted) return;
+    int64_t hi = len_old + 1;
+    hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
+    attention_loop<D, G>(a, ep, hi, smem
+#ifdef EK_STEP_TRACE
+                         , ts_lds
+#endif
+                         );
+    return;
+  }
+  bool ok = !aborted;
+  if (ok)
+    ok = projection_pass<D, G>(a, ep, smem, s_red, s_redi
+#ifdef EK_STEP_TRACE
+                               , ts_lds
+#endif
+                               );
+  if ((int)blockIdx.x != n_attn) return;
+  finish_step<D>(a, ep, ok, len_old, smem, s_red, s_redi);
+#ifdef EK_STEP_TRACE
+  EK_TS(4);
+  EK_TS_FLUSH_SYNC(a.nl);
+#endif
 }
 
 // LDS bytes of step_kernel<D, G> (o_rows: the most o_proj rows of one workgroup, qw = n_q * D)
@@ -870,5 +916,8 @@ inline size_t step_lds_bytes(int h, int kpad_max, int part_max, int64_t s_cap, i
 // launch of one head-dim instantiation for any G (ek_step_inst.hip)
 template <int D>
 hipError_t launch_step(const StepArgs& a, int g, int nwg, hipStream_t st);
+// workgroups of step_kernel<D, g> with `lds` dynamic LDS bytes resident per CU
+template <int D>
+int step_occupancy(int g, size_t lds);
 
 }  // namespace eks

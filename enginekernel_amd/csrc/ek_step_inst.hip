@@ -24,6 +24,29 @@ static hipError_t launch_one(const StepArgs& a, int nwg, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int D, int G>
+static int occupancy_one(size_t lds) {
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<D, G>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024) != hipSuccess)
+    return 0;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&step_kernel<D, G>), SNT, lds) !=
+      hipSuccess)
+    return 0;
+  return n;
+}
+
+template <>
+int step_occupancy<EK_STEP_D>(int g, size_t lds) {
+  switch (g) {
+    case 1: return occupancy_one<EK_STEP_D, 1>(lds);
+    case 2: return occupancy_one<EK_STEP_D, 2>(lds);
+    case 4: return occupancy_one<EK_STEP_D, 4>(lds);
+    case 8: return occupancy_one<EK_STEP_D, 8>(lds);
+    default: return 0;
+  }
+}
+
 template <>
 hipError_t launch_step<EK_STEP_D>(const StepArgs& a, int g, int nwg, hipStream_t st) {
   switch (g) {

@@ -434,15 +434,24 @@ def layer_table(layers, k_cache, v_cache, device) -> torch.Tensor:
 
 
 def decode_step(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap, tokens, positions, len_t,
-                slot_t, start_t, out_buf, step_idx, scratch: StepScratch, out_tok=None):
+                slot_t, start_t, out_buf, step_idx, scratch: StepScratch, out_tok=None, logits=None, err=None):
     """ek_model.py:360-416 + :490-493 + engine.py:288-292 (the captured step
     body) as ONE persistent launch: every layer, the final norm, lm_head, the
     first-index argmax and the step bookkeeping (tokens <- next, positions +=
     1, slot_t <- len, len += 1, out_buf[step_idx] <- next, step_idx += 1).
-    Batch 1; `table` from layer_table; k_cache0 gives the cache strides."""
+    Batch 1; `table` from layer_table; k_cache0 gives the cache strides.
+    logits: optional bf16 tensor of vocab elements that receives the step's
+    logits. err: the error word to use (default: the scratch's own); a step
+    that gives up, and every step launched while the word is set, writes
+    token -1 and advances only step_idx."""
     _gpu(tokens, embed, lm_head, k_cache0)
     m = tokens.shape[0]
     _need(out_buf.dtype == torch.int32 and out_buf.shape[1] == m and out_buf.is_contiguous(), "out_buf")
+    if logits is not None:
+        _need(logits.dtype == _BF16 and logits.is_contiguous() and logits.numel() == cfg.vocab_size, "logits")
+    if err is None:
+        err = scratch.err
+    _need(err.dtype == torch.int32 and err.numel() >= 1 and err.device == tokens.device, "err")
     _need(table.dtype == torch.int64 and table.shape == (cfg.num_layers, 10) and table.is_contiguous(), "table")
     _need(embed.stride(-1) == 1 and lm_head.stride(-1) == 1 and cos.stride(0) == sin.stride(0), "weights")
     call("ek_decode_step", ptr(table), cfg.num_layers, cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
@@ -450,8 +459,8 @@ def decode_step(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_ca
          ptr(embed), embed.stride(0), ptr(lm_head), ptr(final_norm), ptr(cos), ptr(sin), cos.stride(0),
          cos.shape[0], k_cache0.stride(0), k_cache0.stride(1), k_cache0.stride(2), s_cap,
          ptr(tokens), ptr(positions), ptr(len_t), ptr(slot_t), ptr(start_t), ptr(out_buf), ptr(step_idx),
-         out_buf.shape[0], ptr(out_tok), ptr(scratch.arena), scratch.arena_bytes, ptr(scratch.barrier),
-         ptr(scratch.err), stream())
+         out_buf.shape[0], ptr(out_tok), ptr(logits), ptr(scratch.arena), scratch.arena_bytes,
+         ptr(scratch.barrier), ptr(err), stream())
     return tokens
 
 
@@ -514,11 +523,13 @@ def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta
 def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, device, splits=None, chunk=None):
     """The attention workspace: the reference's 7-tuple (acc, lsum, mmax, out,
     splits, chunk, block_n) of engine.py:273-282, extended with the score
-    scratch [B, n_q, bucket] fp32 and the split combine's ticket block
+    scratch [B, n_q, bucket] fp32, the split combine's ticket block
     (int32 [B, n_kv, 2], zeroed; the kernels keep an arrival count and an
-    epoch in it). `acc` ([B, n_kv, SP, GP, D] fp32, as in the reference)
-    holds the splits' partial outputs as 64-bit {value, tag} words, which
-    fit because GP >= 2 * (n_q / n_kv)."""
+    epoch in it) and an error word (int32 [1]: set by a device-side wait
+    that gave up, cleared by the caller; ws_error returns it). `acc`
+    ([B, n_kv, SP, GP, D] fp32, as in the reference) holds the splits'
+    partial outputs as 64-bit {value, tag} words, which fit because
+    GP >= 2 * (n_q / n_kv)."""
     s, c, bn = plan_splits(b, n_kv, bucket)
     if splits is not None:
         s = splits
@@ -531,7 +542,22 @@ def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, devi
     out = torch.empty((b, n_q, head_dim), dtype=_BF16, device=device)
     scores = torch.empty((b, n_q, bucket), dtype=torch.float32, device=device)
     ticket = torch.zeros((b, n_kv, 2), dtype=torch.int32, device=device)
-    return (acc, lsum, mmax, out, s, c, bn, scores, ticket)
+    err = torch.zeros(1, dtype=torch.int32, device=device)
+    return (acc, lsum, mmax, out, s, c, bn, scores, ticket, err)
+
+
+def ws_error(ws):
+    """The workspace's error word (a 1-element int32 device tensor), or None
+    for a reference-style workspace that has none."""
+    return ws[9] if ws is not None and len(ws) >= 10 else None
+
+
+def check_error_word(err, what: str = "a kernel") -> None:
+    """Raise HipKernelError if the error word `err` (device int32) is set,
+    i.e. a device-side wait of `what` gave up and its outputs are invalid.
+    Reads the word back (waits for the work queued before it)."""
+    if err is not None and int(err.reshape(-1)[0].item()) != 0:
+        raise HipKernelError(what, 1, "a device-side wait gave up; the outputs are invalid")
 
 
 _SCRATCH: dict = {}
@@ -574,7 +600,7 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
          k_cache.stride(2), s_cap, ptr(seq_len_t), ptr(start_t), ptr(scores), scores.stride(1),
          ptr(lsum), ptr(mmax), lsum.shape[2], lsum.shape[3], ptr(out), out.stride(0),
          out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), ptr(acc), acc.numel() // 2,
-         ptr(ticket), stream())
+         ptr(ticket), ptr(ws_error(workspace)), stream())
     return out
 
 

@@ -385,19 +385,23 @@ class Qwen3(torch.nn.Module):
         + lm_head + argmax, then tokens <- next, positions += 1, out_buf[step_idx]
         <- next, step_idx += 1. At batch 1 (and rows whose attention scores fit
         in LDS) it is one persistent launch (K.decode_step); otherwise HIP
-        launches per layer with the last three fused into one kernel."""
+        launches per layer with the last three fused into one kernel.
+        logits: optional bf16 [B, vocab] that receives the step's logits.
+        The device-side waits report a failure in the workspace's error word
+        (K.ws_error(ws)); the persistent step then emits token -1."""
         b = tokens.shape[0]
         s_cap = k_cache[0].shape[2]
         if ws is not None and len(ws) >= 8:
             s_cap = min(s_cap, ws[7].shape[2])
-        plan = self.persistent_plan(b, s_cap) if (self.persistent and logits is None) else None
+        plan = self.persistent_plan(b, s_cap) if self.persistent else None
         if plan is not None:
             bufs = self.buffers(b)
             if bufs.step is None:
                 bufs.step = K.StepScratch(plan, self.device)
             K.decode_step(self._layer_table(k_cache, v_cache), self.cfg, self.embed, self.lm_head, self.final_norm,
                           self.cos, self.sin, k_cache[0], s_cap, tokens, positions, len_t, slot_t, start_t,
-                          out_buf, step_idx, bufs.step, out_tok=bufs.next_tok)
+                          out_buf, step_idx, bufs.step, out_tok=bufs.next_tok, logits=logits,
+                          err=K.ws_error(ws))
             return bufs.next_tok
         bufs = self._layers(tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws)
         state = (tokens, positions, out_buf, step_idx)

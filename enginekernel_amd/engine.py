@@ -1,27 +1,47 @@
 """Greedy-decode engine over the gfx950 kernels: the reference's Engine API.
 
-Mirrors jeojdi1/EngineKernel `engine/engine.py`:
-`Engine(model_path).generate(input_ids, max_new_tokens)` yields one list of B
-token ids per step. The decode step is captured once per (batch, bucket) as a
-HIP graph (torch.cuda.graph over the C-ABI launches) that advances the
-device-resident token, position, length and output index itself, so N tokens
-are N graph replays with no host round trip; the host keeps LOOKAHEAD
-replays queued and reads tokens back through pinned memory and events.
+Surface of jeojdi1/EngineKernel `engine/engine.py`: Engine(model_path)
+.generate(input_ids, max_new_tokens) yields one list of B token ids per step;
+.tier, .model, .graphs, .cache_b, .cache_s, ._make_ws(b, bucket), .last_stats.
 
-Failure handling: the fast tier never degrades silently. If the HIP library
-or GPU is missing, construction raises. A caller may pass `fallback`, a
-factory of another engine (for example a CPU reference); then a failure at
-load or mid-stream switches to it, and the deterministic greedy sequence is
-replayed with the already-yielded steps skipped (engine.py:770-824).
+How this build runs a request:
+
+* KV cache (`_KVStore`): one bf16 tensor [layers, rows, n_kv, S, D] for the
+  keys and one for the values, so growing the cache is two allocations and
+  every per-layer view shares their strides. S is rounded up to 256 and the
+  store only grows (to the union of the requests seen), which invalidates the
+  captured graphs, since they hold its addresses.
+* Captured step (`_StepGraph`): one HIP graph per (batch, bucket). Its rows
+  are cut into tiles of at most Qwen3.MAX_ROWS rows (the kernels' batch
+  tile); each tile has its own slice of the device state and its own
+  attention workspace, and the graph runs the tiles' steps back to back, so
+  batches above 8 rows are captured too. The per-row state (token, position,
+  slot) lives in one int64 block, set for a request by one host-to-device
+  copy. All tiles share one error word, which a step's device-side waits set
+  when they give up.
+* Read-back (`_Readback`): a small ring of pinned rows, each holding a step's
+  B tokens and the error word, copied after each replay and marked by an
+  event. The consumer waits on the oldest event, and a set error word raises
+  before that step's tokens are yielded (the persistent step also writes -1
+  as the token of a step that gave up). At most LOOKAHEAD + 1 replays are in
+  flight, and never more than the request still needs.
+* Failure handling: no silent degradation. Construction raises if the HIP
+  library or the GPU is missing. `Engine(fallback=factory)` switches to the
+  factory's engine at load or mid-stream; greedy decoding is deterministic, so
+  the new tier's stream is replayed with the already-yielded steps skipped.
 """
 
 from __future__ import annotations
 
+import collections
+import contextlib
 import gc
+import itertools
 import os
 import subprocess
 import sys
 
+import numpy as np
 import torch
 
 from . import ek_kernels as K
@@ -38,6 +58,9 @@ LOOKAHEAD = int(os.environ.get("ENGINE_LOOKAHEAD", "2"))
 SPEC = os.environ.get("ENGINE_SPEC", "0") == "1"
 SPEC_Q = int(os.environ.get("ENGINE_SPEC_Q", "3"))
 SPEC_MAX_BATCH = int(os.environ.get("ENGINE_SPEC_MAX_BATCH", "1"))
+# The widest batch a captured step takes (tiles of Qwen3.MAX_ROWS rows).
+GRAPH_MAX_BATCH = int(os.environ.get("ENGINE_GRAPH_MAX_BATCH", "64"))
+CACHE_ALIGN = 256
 
 
 # Out-of-process probes (engine.py:47-77, 439-470): with ENGINE_PROBE_CHILD=1
@@ -70,31 +93,139 @@ def _spec_ok(b: int) -> bool:
     return 2 <= _spec_q(b) <= 16 and b <= SPEC_MAX_BATCH and b * _spec_q(b) <= Qwen3.MAX_ROWS
 
 
-def _pinned(shape, dtype):
-    """Pinned staging if page-locking is allowed, pageable otherwise (engine.py:105-110)."""
-    try:
+def _as_rows(input_ids) -> list[list[int]]:
+    """A batch of prompts (nested lists or tuples, a 2-D numpy array or
+    tensor, or a list of 1-D arrays) as plain lists of ints."""
+    if isinstance(input_ids, (torch.Tensor, np.ndarray)):
+        return [[int(t) for t in row] for row in input_ids.tolist()]
+    return [[int(t) for t in (row.tolist() if hasattr(row, "tolist") else row)] for row in input_ids]
+
+
+def _host_buffer(shape, dtype) -> torch.Tensor:
+    """Page-locked host memory where the runtime grants it (asynchronous
+    device-to-host copies need it); ordinary memory otherwise."""
+    with contextlib.suppress(RuntimeError):
         return torch.empty(shape, dtype=dtype, pin_memory=True)
-    except Exception:
-        return torch.empty(shape, dtype=dtype)
+    return torch.empty(shape, dtype=dtype)
 
 
-def _rows(input_ids):
-    """Lists, tuples, numpy arrays or tensors -> list[list[int]] (engine.py:113-117)."""
-    if hasattr(input_ids, "tolist"):
-        input_ids = input_ids.tolist()
-    return [r.tolist() if hasattr(r, "tolist") else [int(t) for t in r] for r in input_ids]
+def _tiles(b: int, width: int) -> list[tuple[int, int]]:
+    """Rows [0, b) cut into the fewest tiles of at most `width` rows, of
+    near-equal size (16 -> 8 + 8, 12 -> 6 + 6, 10 -> 5 + 5)."""
+    n = -(-b // width)
+    cuts = [b * i // n for i in range(n + 1)]
+    return list(zip(cuts[:-1], cuts[1:]))
+
+
+class _KVStore:
+    """The engine's KV cache: keys and values as one [layers, rows, n_kv, S, D]
+    bf16 tensor each (engine.py:239-263 keeps a list of per-layer tensors)."""
+
+    def __init__(self, n_layers: int, n_kv: int, head_dim: int, device):
+        self.shape_tail = (n_kv, head_dim)
+        self.n_layers = n_layers
+        self.device = device
+        self.keys = self.values = None
+        self.rows = self.slots = 0
+
+    def covers(self, b: int, s: int) -> bool:
+        return b <= self.rows and s <= self.slots
+
+    def allocate(self, b: int, s: int) -> None:
+        self.keys = self.values = None
+        n_kv, d = self.shape_tail
+        shape = (self.n_layers, b, n_kv, s, d)
+        self.keys = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+        self.values = torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
+        self.rows, self.slots = b, s
+
+    def release(self) -> None:
+        self.keys = self.values = None
+        self.rows = self.slots = 0
+
+    def layer_views(self, r0: int = 0, r1: int | None = None):
+        """Per-layer [r1 - r0, n_kv, S, D] views of rows [r0, r1)."""
+        r1 = self.rows if r1 is None else r1
+        if self.keys is None:
+            return [], []
+        return ([self.keys[i, r0:r1] for i in range(self.n_layers)],
+                [self.values[i, r0:r1] for i in range(self.n_layers)])
+
+
+class _Tile:
+    """Rows [r0, r1) of a captured step: views of the step's state block and
+    the tile's own attention workspace and output rows."""
+    __slots__ = ("r0", "r1", "tokens", "positions", "slot_t", "len_t", "step_idx", "start_t", "out_buf", "ws")
 
 
 class _Graph:
-    """engine.py:172-174: one captured decode step and its device state."""
-    __slots__ = ("graph", "tokens", "positions", "slot_t", "len_t", "start_t",
-                 "out_buf", "step_idx", "ws", "batch", "bucket")
+    """engine.py:172-174: one captured decode step (all its tiles) and its
+    device state. For a single tile, tokens/positions/slot_t/start_t/out_buf
+    are that tile's tensors ([B] and [MAX_STEPS, B]); len_t and step_idx hold
+    one entry per tile."""
+    __slots__ = ("graph", "tokens", "positions", "slot_t", "len_t", "start_t", "out_buf", "step_idx", "ws",
+                 "batch", "bucket", "tiles", "err", "state", "_seed64", "_seed32")
+
+    def begin(self, first_tokens, positions, start, length: int) -> None:
+        """Set the state for a new request: the first tokens (device [B]),
+        each row's next position and first real key, the shared length; the
+        step counters and the error word restart at zero."""
+        b, nt = self.batch, len(self.tiles)
+        seed = self._seed64
+        seed[:b] = 0
+        seed[b:2 * b] = torch.as_tensor(positions, dtype=torch.int64)
+        seed[2 * b:3 * b] = 0
+        seed[3 * b:3 * b + nt] = int(length)
+        seed[3 * b + nt:3 * b + 2 * nt] = 0
+        self._seed32[:b] = torch.as_tensor(start, dtype=torch.int32)
+        self.state.copy_(seed, non_blocking=True)
+        self.start_t.copy_(self._seed32[:b], non_blocking=True)
+        self.state[:b].copy_(first_tokens.reshape(-1))
+        self.err.zero_()
 
 
 class _SpecGraph:
     """engine.py:386-420: one captured draft -> verify -> accept step."""
     __slots__ = ("graph", "batch", "bucket", "q", "hist", "hist_len", "len_b", "pos_b", "remaining", "start_t",
                  "out_tok", "out_adv", "step_idx", "tokens")
+
+
+class _Readback:
+    """Pinned host rows for a pipeline of graph replays: after a replay the
+    step's output row and the error word are copied into the next slot and
+    an event is recorded; collect() waits for the oldest slot."""
+
+    def __init__(self, depth: int, width: int):
+        self.rows = _host_buffer((depth, width + 1), torch.int32)
+        self.events = [torch.cuda.Event() for _ in range(depth)]
+        self.depth, self.width = depth, width
+        self.head = self.count = 0
+
+    def fits(self, depth: int, width: int) -> bool:
+        return depth <= self.depth and width <= self.width
+
+    def reset(self) -> None:
+        self.head = self.count = 0
+
+    def post(self, sources, err) -> None:
+        """Queue the copies of one step: sources = [(device row, column offset)]."""
+        slot = (self.head + self.count) % self.depth
+        row = self.rows[slot]
+        for src, c0 in sources:
+            row[c0:c0 + src.numel()].copy_(src.reshape(-1), non_blocking=True)
+        row[self.width:self.width + 1].copy_(err, non_blocking=True)
+        self.events[slot].record(torch.cuda.current_stream())
+        self.count += 1
+
+    def collect(self, b: int) -> list[int]:
+        slot = self.head
+        self.events[slot].synchronize()
+        self.head = (self.head + 1) % self.depth
+        self.count -= 1
+        vals = self.rows[slot].tolist()
+        if vals[self.width] != 0 or min(vals[:b]) < 0:
+            raise K.HipKernelError("decode step", 1, "a device-side wait gave up; the step's tokens are invalid")
+        return vals[:b]
 
 
 class _FastEngine:
@@ -112,121 +243,213 @@ class _FastEngine:
         self.hip = True
         self.model = model if model is not None else Qwen3(model_path, self.device)
         cfg = self.model.cfg
-        self.n_kv = cfg.num_kv_heads
-        self.head_dim = cfg.head_dim
-        self.n_layers = cfg.num_layers
+        self.n_kv, self.head_dim, self.n_layers = cfg.num_kv_heads, cfg.head_dim, cfg.num_layers
+        self.store = _KVStore(self.n_layers, self.n_kv, self.head_dim, self.device)
         self.graphs: dict = {}
         self.pool = torch.cuda.graph_pool_handle()
-        self.k_cache: list = []
-        self.v_cache: list = []
-        self.cache_b = 0
-        self.cache_s = 0
-        self.host_buf = None
-        self.host_b = 0
+        self.readback = None
+        self.spec_rows = None
         self.last_stats = (0, 0)
         self.spec = SPEC
-        self.host_tok = None
-        self.host_adv = None
-        self.events = [torch.cuda.Event() for _ in range(LOOKAHEAD + 2)]
-        # graphs bake in the cos/sin pointers, so size the table once, here
+        # graphs hold the cos/sin table's address, so size it once, here
         self.model.ensure_rope(16384 + MAX_STEPS)
 
-    # -- memory ---------------------------------------------------------
-    def _release(self):
-        """engine.py:229-237."""
+    # -- the KV cache -----------------------------------------------------
+    @property
+    def cache_b(self) -> int:
+        return self.store.rows
+
+    @property
+    def cache_s(self) -> int:
+        return self.store.slots
+
+    @property
+    def k_cache(self) -> list:
+        return self.store.layer_views()[0]
+
+    @property
+    def v_cache(self) -> list:
+        return self.store.layer_views()[1]
+
+    def _drop_graphs(self) -> None:
         self.graphs.clear()
-        self.k_cache, self.v_cache = [], []
-        self.cache_b = self.cache_s = 0
-        self.pool = None
+        self.pool = torch.cuda.graph_pool_handle()
+
+    def _ensure_cache(self, b: int, s: int) -> None:
+        """engine.py:253-263: make the cache hold b rows of s slots (s rounded
+        up to 256), growing to the union of what was asked so far; if the
+        union does not fit, this request alone."""
+        s = -(-s // CACHE_ALIGN) * CACHE_ALIGN
+        if self.store.covers(b, s):
+            return
+        want = (max(b, self.store.rows), max(s, self.store.slots))
+        self.graphs.clear()
+        self.store.release()
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         self.pool = torch.cuda.graph_pool_handle()
+        for rows, slots in (want, (b, s)):
+            try:
+                self.store.allocate(rows, slots)
+                return
+            except torch.OutOfMemoryError:
+                self.store.release()
+                torch.cuda.empty_cache()
+        raise torch.OutOfMemoryError(f"KV cache of {b} rows x {s} slots does not fit")
 
-    def _alloc_cache(self, b: int, s: int):
-        """engine.py:239-251: one [B, n_kv, S, D] bf16 tensor per layer for K and V."""
-        shape = (b, self.n_kv, s, self.head_dim)
-        self.k_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
-                        for _ in range(self.n_layers)]
-        self.v_cache = [torch.zeros(shape, dtype=torch.bfloat16, device=self.device)
-                        for _ in range(self.n_layers)]
-        self.cache_b, self.cache_s = b, s
-
-    def _ensure_cache(self, b: int, s: int):
-        """engine.py:253-263: S rounded up to 256; grown to the union of requests."""
-        s = -(-s // 256) * 256
-        if b <= self.cache_b and s <= self.cache_s:
-            return
-        nb, ns = max(b, self.cache_b), max(s, self.cache_s)
-        self._release()
-        try:
-            self._alloc_cache(nb, ns)
-        except Exception:
-            self.k_cache = self.v_cache = []
-            torch.cuda.empty_cache()
-            self._alloc_cache(b, s)
-
-    def _ensure_host(self, b: int):
-        if self.host_buf is None or self.host_b < b:
-            self.host_buf = _pinned((MAX_STEPS, b), torch.int32)
-            self.host_b = b
-
-    # -- graph capture --------------------------------------------------
+    # -- captured steps --------------------------------------------------
     def _make_ws(self, b: int, bucket: int):
-        """engine.py:273-282 (plus the attention score scratch)."""
-        cfg = self.model.cfg
-        return K.make_workspace(b, cfg.num_heads, self.n_kv, self.head_dim, bucket, self.device)
+        """engine.py:273-282 (plus the score scratch, ticket block and error word)."""
+        return K.make_workspace(b, self.model.cfg.num_heads, self.n_kv, self.head_dim, bucket, self.device)
 
-    def _step_body(self, g: _Graph, kv):
-        """engine.py:284-292, as HIP launches only (argmax and bookkeeping fused)."""
-        k, v = kv
-        self.model.step(g.tokens, g.positions, k, v, g.slot_t, g.len_t, g.start_t, g.ws, g.out_buf, g.step_idx)
+    def _step_body(self, g: _Graph, kv=None) -> None:
+        """engine.py:284-292 for every tile: the model's step (decode, final
+        norm, lm_head, argmax and the state advance, all HIP launches)."""
+        for t in g.tiles:
+            if kv is None or len(g.tiles) > 1:
+                k, v = self.store.layer_views(t.r0, t.r1)
+            else:
+                k, v = kv
+            self.model.step(t.tokens, t.positions, k, v, t.slot_t, t.len_t, t.start_t, t.ws, t.out_buf, t.step_idx)
 
-    def _capture(self, b: int, bucket: int) -> _Graph:
-        """engine.py:294-330: warm up on a side stream, then capture one step."""
+    def _new_graph(self, b: int, bucket: int) -> _Graph:
         dev = self.device
+        tiles = _tiles(b, Qwen3.MAX_ROWS)
+        nt = len(tiles)
         g = _Graph()
         g.batch, g.bucket = b, bucket
-        g.tokens = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.positions = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.slot_t = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.len_t = torch.zeros(1, dtype=torch.int64, device=dev)
+        g.state = torch.zeros(3 * b + 2 * nt, dtype=torch.int64, device=dev)
         g.start_t = torch.zeros(b, dtype=torch.int32, device=dev)
-        g.out_buf = torch.zeros((MAX_STEPS, b), dtype=torch.int32, device=dev)
-        g.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
-        g.ws = self._make_ws(b, bucket)
-        kv = ([t[:b] for t in self.k_cache], [t[:b] for t in self.v_cache])
-        self.model.buffers(b)
-        warm = max(1, bucket // 2)
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for _ in range(3):
-                g.len_t.fill_(warm)
-                g.positions.fill_(warm)
-                g.step_idx.zero_()
-                self._step_body(g, kv)
-        torch.cuda.current_stream().wait_stream(s)
+        g.err = torch.zeros(1, dtype=torch.int32, device=dev)
+        g._seed64 = _host_buffer(3 * b + 2 * nt, torch.int64)
+        g._seed32 = _host_buffer(b, torch.int32)
+        g.tokens, g.positions, g.slot_t = g.state[:b], g.state[b:2 * b], g.state[2 * b:3 * b]
+        g.len_t, g.step_idx = g.state[3 * b:3 * b + nt], g.state[3 * b + nt:]
+        g.tiles = []
+        for i, (r0, r1) in enumerate(tiles):
+            t = _Tile()
+            t.r0, t.r1 = r0, r1
+            t.tokens, t.positions, t.slot_t = g.tokens[r0:r1], g.positions[r0:r1], g.slot_t[r0:r1]
+            t.start_t = g.start_t[r0:r1]
+            t.len_t, t.step_idx = g.len_t[i:i + 1], g.step_idx[i:i + 1]
+            t.out_buf = torch.zeros((MAX_STEPS, r1 - r0), dtype=torch.int32, device=dev)
+            t.ws = self._make_ws(r1 - r0, bucket)[:9] + (g.err,)
+            g.tiles.append(t)
+        g.out_buf = g.tiles[0].out_buf if nt == 1 else None
+        g.ws = g.tiles[0].ws if nt == 1 else None
+        return g
+
+    def _capture(self, b: int, bucket: int) -> _Graph:
+        """One eager step first (it builds what a capture cannot: the layer
+        pointer tables and the step buffers), from a mid-bucket state, then
+        the capture of the same step."""
+        g = self._new_graph(b, bucket)
+        for t in g.tiles:
+            self.model.buffers(t.r1 - t.r0)
+        mid = max(1, bucket // 2)
+        g.begin(torch.zeros(b, dtype=torch.int64, device=self.device), [mid] * b, [0] * b, mid)
+        self._step_body(g)
         torch.cuda.synchronize()
-        g.len_t.fill_(warm)
-        g.positions.fill_(warm)
-        g.step_idx.zero_()
+        K.check_error_word(g.err, "the warm-up step of a new graph")
+        g.begin(torch.zeros(b, dtype=torch.int64, device=self.device), [mid] * b, [0] * b, mid)
+        torch.cuda.synchronize()
         g.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g.graph, pool=self.pool):
-            self._step_body(g, kv)
+            self._step_body(g)
         torch.cuda.synchronize()
         return g
 
     def _bucket(self, need: int) -> int:
-        return -(-need // 256) * 256
+        return -(-need // CACHE_ALIGN) * CACHE_ALIGN
+
+    def _shape_ok(self, b: int, q: int, bucket: int) -> None:
+        """engine.py:444-452: run this shape's attention launches in a child
+        before capturing it here (with ENGINE_PROBE_CHILD=1)."""
+        if self.probe_child and not _child_ok(["shape", b, q, bucket, self.n_kv, self.model.cfg.num_heads,
+                                               self.head_dim]):
+            raise K.HipUnavailable(f"the attention launches of shape (b={b}, q={q}, bucket={bucket}) "
+                                   "failed their probe in a child process")
 
     def _get_graph(self, b: int, total: int) -> _Graph:
-        """engine.py:456-470."""
-        bucket = self._bucket(total)
-        key = (b, bucket)
+        """engine.py:456-470: the captured step for b rows and a bucket that
+        holds `total` slots (captured on first use)."""
+        key = (b, self._bucket(total))
         if key not in self.graphs:
-            self._shape_ok(b, 0, bucket)
-            self.graphs[key] = self._capture(b, bucket)
+            self._shape_ok(b, 0, key[1])
+            self.graphs[key] = self._capture(*key)
         return self.graphs[key]
+
+    # -- inputs ------------------------------------------------------------
+    def _pack(self, input_ids):
+        """engine.py:541-570: prompts left-padded to the longest (pad id 0, pad
+        position 0, real positions 0..len-1), one host-to-device copy each for
+        the ids and the positions, and for a ragged batch an additive bf16
+        mask [B, 1, S, S]: 0 where query i may see key j (j <= i and j at or
+        after the row's first real token), -inf elsewhere. Returns (ids,
+        positions, pads, S, mask or None)."""
+        lens = np.array([len(r) for r in input_ids], dtype=np.int64)
+        b, s = len(input_ids), int(lens.max())
+        pad = s - lens
+        col = np.arange(s, dtype=np.int64)[None, :]
+        real = col >= pad[:, None]
+        ids = np.zeros((b, s), dtype=np.int64)
+        ids[real] = np.concatenate([np.asarray(r, dtype=np.int64) for r in input_ids])
+        pos = np.where(real, col - pad[:, None], 0)
+        mask = None
+        if pad.max() > 0:
+            visible = (col.T >= col)[None] & real[:, None, :]          # [B, query, key]
+            mask = torch.from_numpy(np.where(visible, 0.0, -np.inf).astype(np.float32)).to(torch.bfloat16)
+            mask = mask.unsqueeze(1).to(self.device, non_blocking=True)
+        return (torch.from_numpy(ids).to(self.device, non_blocking=True),
+                torch.from_numpy(pos).to(self.device, non_blocking=True), pad.tolist(), s, mask)
+
+    def _first_token(self, ids, pos, b, s, bias):
+        """Prefill the cache's first b rows; the first greedy token of each row."""
+        k, v = self.store.layer_views(0, b)
+        return self.model.argmax_token(self.model.prefill(ids, pos, k, v, bias))
+
+    # -- public API ----------------------------------------------------------
+    @torch.inference_mode()
+    def generate(self, input_ids, max_new_tokens: int):
+        """engine.py:573-634: route the request, then stream its steps. The
+        captured graph takes up to GRAPH_MAX_BATCH rows and MAX_STEPS tokens;
+        with `spec` (ENGINE_SPEC=1) and a batch that fits, the speculative
+        path (engine.py:591-593); anything else runs the eager HIP loop."""
+        rows = _as_rows(input_ids)
+        n = int(max_new_tokens)
+        ids, pos, pad, s, bias = self._pack(rows)
+        b = len(rows)
+        if s + n + 1 > self.model.rope_len:
+            # a longer table is a new tensor, and every graph holds the old one's address
+            self.model.ensure_rope(s + n + 1)
+            self._drop_graphs()
+        if n > MAX_STEPS or b > GRAPH_MAX_BATCH:
+            yield from self._generate_eager(ids, pos, pad, s, bias, n)
+        elif self.spec and _spec_ok(b) and n > 1:
+            yield from self._generate_spec(ids, pos, pad, s, bias, n)
+        else:
+            yield from self._generate_graph(ids, pos, pad, s, bias, n)
+
+    def _generate_graph(self, ids, pos, pad, s, bias, n):
+        b = ids.shape[0]
+        self._ensure_cache(b, s + n)
+        g = self._get_graph(b, s + n)
+        first = self._first_token(ids, pos, b, s, bias)
+        g.begin(first, [s - p for p in pad], pad, s)
+        yield first.to(torch.int32).cpu().tolist()
+        if self.readback is None or not self.readback.fits(LOOKAHEAD + 1, b):
+            self.readback = _Readback(LOOKAHEAD + 1, max(b, 8))
+        rb = self.readback
+        rb.reset()
+        cols = [(t.out_buf, t.r0) for t in g.tiles]
+        issued = 0
+        for _ in range(n - 1):
+            while issued < n - 1 and rb.count < rb.depth:
+                g.graph.replay()
+                rb.post([(buf[issued], c0) for buf, c0 in cols], g.err)
+                issued += 1
+            yield rb.collect(b)
+        self.last_stats = (issued, n - 1)
 
     # -- speculative decoding --------------------------------------------
     def _spec_body(self, g: _SpecGraph, kv):
@@ -239,7 +462,8 @@ class _FastEngine:
         g.step_idx.add_(1)
 
     def _capture_spec(self, b: int, bucket: int) -> _SpecGraph:
-        """engine.py:386-438: device state, warm-up on a side stream, capture."""
+        """engine.py:386-438: the device state, one eager step from a
+        mid-bucket state, then the capture."""
         dev = self.device
         q = _spec_q(b)
         g = _SpecGraph()
@@ -254,39 +478,24 @@ class _FastEngine:
         g.out_adv = torch.zeros((MAX_STEPS, b), dtype=torch.int32, device=dev)
         g.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
         g.tokens = torch.zeros((b, q), dtype=torch.int64, device=dev)
-        kv = ([t[:b] for t in self.k_cache], [t[:b] for t in self.v_cache])
+        kv = self.store.layer_views(0, b)
         self.model.buffers(b * q)
-
-        def reset():
-            half = max(4, bucket // 2)
-            g.hist_len.fill_(half)
-            g.len_b.fill_(half - 1)
-            g.pos_b.fill_(half - 1)
+        mid = max(4, bucket // 2)
+        for phase in ("warm", "capture"):
+            g.hist_len.fill_(mid)
+            g.len_b.fill_(mid - 1)
+            g.pos_b.fill_(mid - 1)
             g.remaining.fill_(1 << 30)
             g.step_idx.zero_()
-
-        st = torch.cuda.Stream()
-        st.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(st):
-            for _ in range(3):
-                reset()
+            torch.cuda.synchronize()
+            if phase == "warm":
                 self._spec_body(g, kv)
-        torch.cuda.current_stream().wait_stream(st)
-        torch.cuda.synchronize()
-        reset()
-        g.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g.graph, pool=self.pool):
-            self._spec_body(g, kv)
+                continue
+            g.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g.graph, pool=self.pool):
+                self._spec_body(g, kv)
         torch.cuda.synchronize()
         return g
-
-    def _shape_ok(self, b: int, q: int, bucket: int) -> None:
-        """engine.py:444-452: run this shape's attention launches in a child
-        before capturing it here (with ENGINE_PROBE_CHILD=1)."""
-        if self.probe_child and not _child_ok(["shape", b, q, bucket, self.n_kv, self.model.cfg.num_heads,
-                                               self.head_dim]):
-            raise K.HipUnavailable(f"the attention launches of shape (b={b}, q={q}, bucket={bucket}) "
-                                   "failed their probe in a child process")
 
     def _get_spec_graph(self, b: int, need: int) -> _SpecGraph:
         """engine.py:440-455."""
@@ -297,251 +506,163 @@ class _FastEngine:
             self.graphs[key] = self._capture_spec(b, bucket)
         return self.graphs[key]
 
-    def _generate_spec(self, ids, pos, pad, s, bias, max_new_tokens):
-        """engine.py:636-718 without the pacing: the host keeps LOOKAHEAD
-        verify steps queued and emits each token once every row has it."""
+    def _generate_spec(self, ids, pos, pad, s, bias, n):
+        """engine.py:636-718 without the pacing. A verify step emits between 1
+        and Q tokens per row; a row's tokens wait in its own queue until every
+        row has the next one. Replays are issued while fewer than LOOKAHEAD
+        are in flight and fewer than the tokens still missing from the
+        slowest row (each replay yields at least one per row), so no replay
+        outlives the request. If the speculative graph cannot be built for
+        this shape, the request runs on the plain captured step instead
+        (engine.py:640-649)."""
         b = ids.shape[0]
         q = _spec_q(b)
-        need = s + max_new_tokens + q
-        self._ensure_cache(b, need)
-        if self.host_tok is None or self.host_tok.shape[1] < b or self.host_tok.shape[2] < q:
-            self.host_tok = _pinned((MAX_STEPS, b, q), torch.int32)
-            self.host_adv = _pinned((MAX_STEPS, b), torch.int32)
-        g = self._get_spec_graph(b, need)
+        try:
+            self._ensure_cache(b, s + n + q)
+            g = self._get_spec_graph(b, s + n + q)
+        except (RuntimeError, torch.OutOfMemoryError):
+            yield from self._generate_graph(ids, pos, pad, s, bias, n)
+            return
         first = self._first_token(ids, pos, b, s, bias)
-
-        pad_t = torch.as_tensor(pad, dtype=torch.int32)
+        pad_t = torch.as_tensor(pad, dtype=torch.int64)
         g.hist[:, :s].copy_(ids)
         g.hist[:, s].copy_(first)
         g.hist_len.fill_(s + 1)
         g.len_b.fill_(s)
-        g.pos_b.copy_((s - pad_t).to(torch.int64), non_blocking=True)
-        g.start_t.copy_(pad_t, non_blocking=True)
-        g.remaining.fill_(max_new_tokens - 1)
+        g.pos_b.copy_(s - pad_t, non_blocking=True)
+        g.start_t.copy_(pad_t.to(torch.int32), non_blocking=True)
+        g.remaining.fill_(n - 1)
         g.step_idx.zero_()
-
-        host_tok, host_adv, events = self.host_tok, self.host_adv, self.events
-        stream = torch.cuda.current_stream()
-        launched = 0
-        consumed = 0
-
-        def launch():
-            nonlocal launched
-            g.graph.replay()
-            host_tok[launched, :b, :q].copy_(g.out_tok[launched], non_blocking=True)
-            host_adv[launched, :b].copy_(g.out_adv[launched], non_blocking=True)
-            events[launched % len(events)].record(stream)
-            launched += 1
-
-        target = max_new_tokens - 1
         yield first.to(torch.int32).cpu().tolist()
-        for _ in range(min(LOOKAHEAD, target)):
-            launch()
-        queues = [[] for _ in range(b)]
-        out_i = 0
-        ready = 0
-        while out_i < target:
-            events[consumed % len(events)].synchronize()
-            toks = host_tok[consumed, :b, :q].tolist()
-            adv = host_adv[consumed, :b].tolist()
-            consumed += 1
+
+        if self.spec_rows is None or self.spec_rows[0].shape[1] < b * q + b:
+            self.spec_rows = (_host_buffer((MAX_STEPS, b * q + b), torch.int32),
+                              [torch.cuda.Event() for _ in range(LOOKAHEAD + 1)])
+        host, events = self.spec_rows
+        stream = torch.cuda.current_stream()
+        queues = [collections.deque() for _ in range(b)]
+        want = n - 1
+        issued = done = emitted = 0
+        while emitted < want:
+            missing = want - emitted - min(len(x) for x in queues)
+            while issued - done < LOOKAHEAD and issued - done < missing and issued < MAX_STEPS:
+                g.graph.replay()
+                host[issued, :b * q].copy_(g.out_tok[issued].reshape(-1), non_blocking=True)
+                host[issued, b * q:b * q + b].copy_(g.out_adv[issued], non_blocking=True)
+                events[issued % len(events)].record(stream)
+                issued += 1
+            if issued == done:
+                raise RuntimeError("speculative decode: no verify step in flight")
+            events[done % len(events)].synchronize()
+            row = host[done].tolist()
+            done += 1
             for r in range(b):
-                queues[r].extend(toks[r][: adv[r]])
-            ready = min(len(x) for x in queues)
-            # every queued step verifies at least one token, so never queue
-            # more than the unverified remainder
-            if ready < target and launched - consumed < min(LOOKAHEAD, target - ready) and launched < MAX_STEPS:
-                launch()
-            while out_i < min(ready, target):
-                yield [queues[r][out_i] for r in range(b)]
-                out_i += 1
-        self.last_stats = (consumed, target)
+                queues[r].extend(row[r * q:r * q + row[b * q + r]])
+            while emitted < want and all(queues):
+                yield [x.popleft() for x in queues]
+                emitted += 1
+        self.last_stats = (done, want)
 
-    def _first_token(self, ids, pos, b, s, bias):
-        kv_k = [t[:b] for t in self.k_cache]
-        kv_v = [t[:b] for t in self.v_cache]
-        return self.model.argmax_token(self.model.prefill(ids, pos, kv_k, kv_v, bias))
-
-    # -- inputs ---------------------------------------------------------
-    def _pack(self, input_ids):
-        """engine.py:541-570: left-pad to a rectangle, one H2D copy each for
-        ids and positions (pads at position 0), and an additive bf16 -inf
-        mask (causal and key >= pad) for ragged batches."""
-        b = len(input_ids)
-        lens = [len(x) for x in input_ids]
-        s = max(lens)
-        pad = [s - n for n in lens]
-        dev = self.device
-        if min(lens) == s:
-            ids_c = torch.as_tensor(input_ids, dtype=torch.int64)
-            pos_c = torch.arange(s, dtype=torch.int64).expand(b, s)
-        else:
-            ids_c = torch.zeros((b, s), dtype=torch.int64)
-            pos_c = torch.zeros((b, s), dtype=torch.int64)
-            for i, seq in enumerate(input_ids):
-                ids_c[i, pad[i]:] = torch.as_tensor(seq, dtype=torch.int64)
-                pos_c[i, pad[i]:] = torch.arange(lens[i], dtype=torch.int64)
-        ids = ids_c.to(dev, non_blocking=True)
-        pos = pos_c.to(dev, non_blocking=True)
-        bias = None
-        if max(pad) > 0:
-            key_ok = torch.zeros((b, s), dtype=torch.bool)
-            for i, p in enumerate(pad):
-                key_ok[i, p:] = True
-            allow = torch.ones((s, s), dtype=torch.bool).tril()[None] & key_ok[:, None, :]
-            bias = torch.zeros((b, 1, s, s), dtype=torch.bfloat16)
-            bias.masked_fill_(~allow.unsqueeze(1), float("-inf"))
-            bias = bias.to(dev, non_blocking=True)
-        return ids, pos, pad, s, bias
-
-    # -- public API -----------------------------------------------------
-    @torch.inference_mode()
-    def generate(self, input_ids, max_new_tokens: int):
-        """engine.py:573-634: the graph path; with `spec` (ENGINE_SPEC=1) and a
-        batch that fits, the speculative path (engine.py:591-593)."""
-        input_ids = _rows(input_ids)
-        max_new_tokens = int(max_new_tokens)
-        b = len(input_ids)
-        ids, pos, pad, s, bias = self._pack(input_ids)
-        total = s + max_new_tokens
-        if total + 1 > self.model.rope_len:
-            self.model.ensure_rope(total + 1)
-            self.graphs.clear()
-            self.pool = torch.cuda.graph_pool_handle()
-        if max_new_tokens > MAX_STEPS or b > self.model.MAX_ROWS:
-            yield from self._generate_eager(ids, pos, pad, s, bias, max_new_tokens)
-            return
-        if self.spec and _spec_ok(b) and max_new_tokens > 1:
-            yield from self._generate_spec(ids, pos, pad, s, bias, max_new_tokens)
-            return
-
-        self._ensure_cache(b, total)
-        self._ensure_host(b)
-        g = self._get_graph(b, total)
-        first = self._first_token(ids, pos, b, s, bias)
-
-        pad_t = torch.as_tensor(pad, dtype=torch.int32)
-        g.tokens.copy_(first)
-        g.positions.copy_((s - pad_t).to(torch.int64), non_blocking=True)
-        g.start_t.copy_(pad_t, non_blocking=True)
-        g.len_t.fill_(s)
-        g.step_idx.zero_()
-
-        host = self.host_buf
-        events = self.events
-        stream = torch.cuda.current_stream()
-        launched = 0
-
-        def launch():
-            nonlocal launched
-            step = launched + 1
-            g.graph.replay()
-            host[step, :b].copy_(g.out_buf[launched], non_blocking=True)
-            events[step % len(events)].record(stream)
-            launched += 1
-
-        yield first.to(torch.int32).cpu().tolist()
-        for _ in range(min(LOOKAHEAD, max_new_tokens - 1)):
-            launch()
-        for j in range(1, max_new_tokens):
-            if launched < max_new_tokens - 1:
-                launch()
-            events[j % len(events)].synchronize()
-            yield host[j, :b].tolist()
-        self.last_stats = (launched, max_new_tokens - 1)
-        self.model.check_step_error()
-
-    def _generate_eager(self, ids, pos, pad, s, bias, max_new_tokens):
-        """engine.py:721-743 on the HIP kernels without graphs: zero caches,
-        prefill, then (n-1) x decode + argmax, in row groups of MAX_ROWS."""
+    # -- the eager path (no graph) -------------------------------------------
+    def _generate_eager(self, ids, pos, pad, s, bias, n):
+        """engine.py:721-743 on the HIP kernels without graphs: fresh caches
+        for this request, prefill, then n - 1 decode steps of all rows (tiles
+        of Qwen3.MAX_ROWS rows) and their argmax."""
         cfg = self.model.cfg
         b = ids.shape[0]
-        total = s + max_new_tokens
-        shape = (b, cfg.num_kv_heads, total, cfg.head_dim)
-        k = [torch.zeros(shape, dtype=self.model.dtype, device=self.device) for _ in range(cfg.num_layers)]
-        v = [torch.zeros(shape, dtype=self.model.dtype, device=self.device) for _ in range(cfg.num_layers)]
-        hidden = self.model.prefill(ids, pos, k, v, bias)
-        tok = self.model.argmax_token(hidden)
+        store = _KVStore(cfg.num_layers, cfg.num_kv_heads, cfg.head_dim, self.device)
+        store.allocate(b, s + n)
+        k, v = store.layer_views()
+        tok = self.model.argmax_token(self.model.prefill(ids, pos, k, v, bias))
         yield tok.tolist()
         positions = torch.as_tensor([s - p for p in pad], dtype=torch.int64, device=self.device)
         start_t = torch.as_tensor(pad, dtype=torch.int32, device=self.device)
-        groups = [(r0, min(b, r0 + self.model.MAX_ROWS)) for r0 in range(0, b, self.model.MAX_ROWS)]
-        state = []
-        for r0, r1 in groups:
-            state.append((torch.zeros(r1 - r0, dtype=torch.int64, device=self.device),
+        tiles = []
+        for r0, r1 in _tiles(b, Qwen3.MAX_ROWS):
+            kt, vt = store.layer_views(r0, r1)
+            tiles.append((r0, r1, kt, vt, torch.zeros(r1 - r0, dtype=torch.int64, device=self.device),
                           torch.full((1,), s, dtype=torch.int64, device=self.device),
-                          K.make_workspace(r1 - r0, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, total,
+                          K.make_workspace(r1 - r0, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, s + n,
                                            self.device)))
-        for _ in range(max_new_tokens - 1):
-            outs = []
-            for (r0, r1), (slot_t, len_t, ws) in zip(groups, state):
-                hidden = self.model.decode(tok[r0:r1].contiguous(), positions[r0:r1].contiguous(),
-                                           [t[r0:r1] for t in k], [t[r0:r1] for t in v], slot_t, len_t,
-                                           start_t[r0:r1].contiguous(), ws)
-                outs.append(self.model.argmax_token(hidden))
-            tok = torch.cat(outs)
-            positions = positions + 1
+        for _ in range(n - 1):
+            parts = []
+            for r0, r1, kt, vt, slot_t, len_t, ws in tiles:
+                hidden = self.model.decode(tok[r0:r1].contiguous(), positions[r0:r1].contiguous(), kt, vt, slot_t,
+                                           len_t, start_t[r0:r1].contiguous(), ws)
+                parts.append(self.model.argmax_token(hidden))
+                K.check_error_word(K.ws_error(ws), "an eager decode step")
+            tok = torch.cat(parts)
+            positions += 1
             yield tok.tolist()
 
 
+class _QuietGC:
+    """engine.py:793-808's GC policy as a context: the cyclic collector is
+    off while a request streams, and after the first request the heap that
+    survived it (weights, graphs, caches) is frozen out of later collections."""
+
+    def __init__(self):
+        self.frozen = False
+        self._was_on = False
+
+    def __enter__(self):
+        self._was_on = gc.isenabled()
+        gc.disable()
+        return self
+
+    def __exit__(self, *exc):
+        if not self.frozen:
+            gc.collect()
+            gc.freeze()
+            self.frozen = True
+        if self._was_on:
+            gc.enable()
+        return False
+
+
 class Engine:
-    """engine.py:770-830: the entry point. `fallback`, if given, is a
-    zero-argument factory of another engine used when the HIP tier fails."""
+    """engine.py:770-830: the entry point. The HIP tier serves requests; if
+    it fails (at load, or in the middle of a request) and `fallback` (a
+    zero-argument factory of another engine) was given, that engine takes
+    over; without one the failure propagates. Attributes not found here are
+    read from the serving engine (.model, .graphs, .last_stats, ...)."""
 
     def __init__(self, model_path: str | None = None, *, model: Qwen3 | None = None, fallback=None) -> None:
         self.model_path = model_path
-        self.tier = "hip"
-        self._frozen = False
         self._fallback = fallback
+        self._gc = _QuietGC()
         try:
-            self._impl = _FastEngine(model_path, model=model)
+            self._impl, self.tier = _FastEngine(model_path, model=model), "hip"
         except Exception:
             if fallback is None:
                 raise
             self._impl = None
-            self._use_fallback()
+            self._switch()
 
-    def _use_fallback(self):
+    def _switch(self) -> None:
+        """Release the failed tier's device memory, then start the fallback."""
         self._impl = None
         gc.collect()
         if torch.cuda.is_available():
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
-        self._impl = self._fallback()
-        self.tier = "fallback"
+        self._impl, self.tier = self._fallback(), "fallback"
 
     def generate(self, input_ids, max_new_tokens: int):
-        """engine.py:793-808: the cyclic GC is off for the duration of a
-        request, and the long-lived heap is frozen after the first."""
-        was_enabled = gc.isenabled()
-        gc.disable()
-        try:
-            yield from self._generate(input_ids, max_new_tokens)
-        finally:
-            if not self._frozen:
-                self._frozen = True
-                gc.collect()
-                gc.freeze()
-            if was_enabled:
-                gc.enable()
-
-    def _generate(self, input_ids, max_new_tokens: int):
-        """engine.py:810-824: greedy decoding is deterministic, so after a
-        switch the fallback replays the request and skips what was yielded."""
-        done = 0
-        if self.tier == "hip":
+        with self._gc:
+            emitted = 0
             try:
                 for step in self._impl.generate(input_ids, max_new_tokens):
-                    done += 1
+                    emitted += 1
                     yield step
                 return
             except Exception:
-                if self._fallback is None:
+                if self._fallback is None or self.tier == "fallback":
                     raise
-                self._use_fallback()
-        for i, step in enumerate(self._impl.generate(input_ids, max_new_tokens)):
-            if i >= done:
-                yield step
+            # greedy decoding is deterministic: the fallback's stream of the
+            # same request continues where the failed one stopped
+            self._switch()
+            yield from itertools.islice(self._impl.generate(input_ids, max_new_tokens), emitted, None)
 
     def __getattr__(self, name):
         impl = self.__dict__.get("_impl")

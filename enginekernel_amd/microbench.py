@@ -218,12 +218,7 @@ def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
         p1.record(stream)
         p1.synchronize()
         prefill_s = p0.elapsed_time(p1) / 1e3
-        pad_t = torch.as_tensor(pad, dtype=torch.int32)
-        graph.tokens.copy_(first)
-        graph.positions.copy_((s - pad_t).to(torch.int64))
-        graph.start_t.copy_(pad_t)
-        graph.len_t.fill_(s)
-        graph.step_idx.zero_()
+        graph.begin(first, [s - p for p in pad], pad, s)
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -233,8 +228,9 @@ def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
         e1.record(stream)
         e1.synchronize()
         step_s = e0.elapsed_time(e1) / 1e3 / steps
-        model.check_step_error()
-        if graph.step_idx.item() != steps:
+        from enginekernel_amd import ek_kernels as K
+        K.check_error_word(graph.err, "the timed batch-8 steps")
+        if int(graph.step_idx.min()) != steps:
             raise RuntimeError("graph step counter out of step with the replays")
     w_bytes = C.weight_bytes_per_token(cfg)
     kv_row = 2 * cfg["num_hidden_layers"] * cfg["num_key_value_heads"] * cfg["head_dim"] * 2

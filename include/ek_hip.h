@@ -28,6 +28,14 @@ const char* ek_version(void);
 const char* ek_last_error(void);
 /* Compute units and gfx architecture name of the current device. */
 int ek_device_info(int* n_cu, char* arch, int arch_len);
+/* set_wait_limit: the number of polls after which a bounded device-side wait
+ * (the decode step's hand-overs, the split attention's combine) gives up and
+ * sets its error word; polls <= 0 restores each kernel's default (about a
+ * second). Read when a launch is issued, so a captured graph keeps the bound
+ * it was captured with. Returns the previous setting. No counterpart in the
+ * reference (its kernels have no device-side waits); it lets tests and
+ * callers with a latency budget bound how long a failed step takes. */
+int64_t ek_set_wait_limit(int64_t polls);
 
 /* rms_norm: y[m,:] = w (x) bf16(x * rsqrt(mean(x^2) + eps)).
  * Replaces engine/ek_kernels.py:1031-1042 (rms_norm, kernel :89-103). */
@@ -132,8 +140,9 @@ int ek_embed_norm_gemv(const int64_t* tokens, const void* embed, int64_t lde, in
  * split combine (kernel :988-1019), deterministic. ticket holds two words
  * per (b, kv head) (an arrival count and an epoch), zeroed once with the
  * workspace and kept by the kernel; launches sharing a workspace must not
- * overlap. Probabilities are rounded to bf16 before the PV product, as in
- * engine/ek_model.py:475-488.
+ * overlap. err (may be NULL) is set to 1 if the combine's bounded wait for a
+ * split's words gives up (the output row is then invalid). Probabilities are
+ * rounded to bf16 before the PV product, as in engine/ek_model.py:475-488.
  * cos/sin rows: positions[b] when positions != NULL, else row b. */
 int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const void* qn, const void* kn,
                    const void* cos, const void* sin, int64_t ld_cs, const int64_t* positions, int64_t rope_len,
@@ -141,7 +150,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
                    const int64_t* seq_len, const int32_t* start, float* scores, int64_t score_ss, float* lsum,
                    float* mmax, int64_t sp, int64_t gp, void* out, int64_t ldo_b, int64_t ldo_h, int64_t b,
                    int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t splits, int64_t chunk, float sm_scale,
-                   float eps, void* part, int64_t part_words, uint32_t* ticket, void* stream);
+                   float eps, void* part, int64_t part_words, uint32_t* ticket, int* err, void* stream);
 
 /* attn_prefill: the prompt's causal GQA attention, engine/ek_model.py:315-323
  * (torch SDPA with the prompt mask of engine/engine.py:541-570): for each
@@ -214,7 +223,8 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
  * (unused), the bytes of the launch-state block and the grid (one workgroup
  * per CU). It handles batch 1, head_dim 32/64/128, n_q / n_kv in {1, 2, 4, 8},
  * hidden (<= 4096), intermediate and n_q * head_dim multiples of 512, and
- * n_q / n_kv * s_cap * 4 <= 32 KiB.
+ * n_q / n_kv * s_cap * 4 <= 32 KiB, on a device where one workgroup of the
+ * kernel fits on every CU at once (its waits need the whole grid resident).
  * Plans engine/engine.py:273-282 (_make_ws) for the step below. */
 int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
                         int64_t m, int64_t s_cap, int64_t n_layers, int64_t* sizes);
@@ -225,7 +235,8 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
  * first-index argmax and the step bookkeeping (tokens[b] = token,
  * positions[b] += 1, slot_t[b] = *len_t, *len_t += 1, out_buf[*step_idx * m +
  * b] = token if *step_idx < max_steps, *step_idx += 1, out_tok[b] = token if
- * out_tok). One workgroup per CU; workgroups hand activations to each other
+ * out_tok; logits[0..vocab) = the step's bf16 logits if logits is not
+ * NULL). One workgroup per CU; workgroups hand activations to each other
  * through the arena as {data, epoch} words that the consumer polls, with no
  * grid barrier.
  * layer_ptrs: device int64 [n_layers][10] = addresses of qkv [(n_q + 2 n_kv) D,
@@ -235,8 +246,12 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
  * hand-over arena (decode_step_plan sizes[0] bytes) and barrier: the
  * launch-state block (sizes[2] bytes), both zero before the first launch and
  * kept between launches (they hold the launch epoch); err: set to 1 (and the
- * launch abandoned) if a hand-over wait exceeds its bound -- then zero err,
- * the arena and the barrier block before the next launch.
+ * launch abandoned) if a hand-over wait exceeds its bound. An abandoned
+ * launch, and every launch that starts while err is set, still advances
+ * *step_idx and writes -1 as its token to out_buf and out_tok, leaving
+ * tokens, positions, slot_t and len_t unchanged, so the failure shows in the
+ * step's own output row; zero err, the arena and the barrier block before
+ * decoding again.
  * Launches that overlap on one device race on the arena and the barrier.
  * Replaces engine/ek_model.py:360-416 (decode) + :490-493 (argmax_token) and
  * the bookkeeping of engine/engine.py:288-292, i.e. the whole captured step
@@ -247,7 +262,7 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
                    const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb, int64_t csh, int64_t css,
                    int64_t s_cap, int64_t* tokens, int64_t* positions, int64_t* len_t, int64_t* slot_t,
                    const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
-                   void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream);
+                   void* logits, void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream);
 
 #ifdef __cplusplus
 }

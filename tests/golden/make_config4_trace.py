@@ -1,0 +1,96 @@
+"""Write the CPU oracle's config-4 greedy trace (tests/golden/config4_trace.npz).
+
+    python tests/golden/make_config4_trace.py [--steps 512] [--out PATH]
+
+Config 4 of the benchmark: the random-init Qwen3-4B-architecture model
+(checkpoint.random_weights(QWEN3_4B, seed=0)), batch 1, a prompt of 128 ids
+drawn with torch.Generator().manual_seed(1) (the prompt bench.py decodes),
+greedy decode of 512 tokens through the oracle (the reference's torch
+fallback path restated: engine.py:721-743 over ek_model.py:280-416,
+475-493). The fixture holds, per emitted token, the id and the eight largest
+bf16 logits with their ids (ties in first-index order), so a GPU test can
+teacher-force the same ids and compare its logits at those ids, and judge a
+differing argmax by the recorded top-2 gap.
+
+It also records the oracle's own summation-order drift per step: the same
+oracle re-run in lockstep, teacher-forced with the same ids, with every
+projection accumulated in a different order (fp32 operands, one fp32
+matmul, then bf16), and the largest |logit difference| over the whole
+vocabulary between the two runs. Any fp32 summation order is as faithful to
+the reference as another, so this drift is the noise floor a kernel's logits
+are judged against at full depth. It runs on the build container's CPU
+(about 1.5 s per step pair at 8 cores); nothing on the GPU box runs it.
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from enginekernel_amd import checkpoint as C  # noqa: E402
+from oracle import ek_oracle as O  # noqa: E402
+
+TOPK = 8
+
+
+def top_entries(logits_row: torch.Tensor, k: int = TOPK):
+    """The k largest logits of one row, ids ascending within equal values."""
+    vals, idx = torch.sort(logits_row.float(), descending=True, stable=True)
+    return idx[:k].to(torch.int32).numpy(), vals[:k].numpy()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--out", default=os.path.join(os.path.dirname(os.path.abspath(__file__)), "config4_trace.npz"))
+    args = ap.parse_args()
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    cfg = dict(C.QWEN3_4B)
+    t0 = time.perf_counter()
+    tensors = C.random_weights(cfg, seed=0)
+    print(f"weights in {time.perf_counter() - t0:.1f}s", flush=True)
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, cfg["vocab_size"], (args.prompt,), generator=g).tolist()
+    model = O.OracleQwen3(O.OracleConfig(cfg), tensors)
+    plain = model._proj
+
+    def reordered(x, layer, key):
+        return torch.matmul(x.float(), layer[key].float().t()).to(torch.bfloat16)
+
+    ids = np.zeros(args.steps, dtype=np.int32)
+    top_ids = np.zeros((args.steps, TOPK), dtype=np.int32)
+    top_logits = np.zeros((args.steps, TOPK), dtype=np.float32)
+    drift = np.zeros(args.steps, dtype=np.float32)
+    forced = []   # ids fed to the reordered run (the main run's own tokens)
+    main = O.generate_eager(model, [prompt], args.steps, record_logits=True)
+    alt = O.generate_eager(model, [prompt], args.steps, record_logits=True, force=forced)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        model._proj = plain
+        tok, logits = next(main)
+        model._proj = reordered
+        _, alt_logits = next(alt)
+        ids[i] = tok[0]
+        forced.append([int(tok[0])])
+        top_ids[i], top_logits[i] = top_entries(logits[0])
+        drift[i] = float((alt_logits[0].float() - logits[0].float()).abs().max())
+        assert top_ids[i, 0] == ids[i]
+        if i % 32 == 0:
+            print(f"step {i}: token {ids[i]} drift {drift[i]:.4f} ({time.perf_counter() - t0:.0f}s)", flush=True)
+    model._proj = plain
+    np.savez(args.out, prompt=np.asarray(prompt, dtype=np.int32), ids=ids, top_ids=top_ids,
+             top_logits=top_logits, drift=drift, seed=np.asarray([0, 1], dtype=np.int32))
+    print(f"wrote {args.out}: {args.steps} steps in {time.perf_counter() - t0:.0f}s")
+
+
+if __name__ == "__main__":
+    main()

@@ -15,12 +15,24 @@ from enginekernel_amd import ek_kernels as K
 def test_library_exports_every_declared_symbol():
     lib = _hip.load()
     declared = _hip.declared_symbols()
-    assert len(declared) == 22
+    assert len(declared) == 23
     for name in declared:
         assert hasattr(lib, name), name
     # the ctypes signature table covers every kernel entry point
-    assert set(_hip.SIGNATURES) == set(declared) - {"ek_version", "ek_last_error", "ek_device_info"}
+    assert set(_hip.SIGNATURES) == set(declared) - {"ek_version", "ek_last_error", "ek_device_info",
+                                                     "ek_set_wait_limit"}
     assert lib.ek_version().startswith(b"enginekernel_amd")
+
+
+def test_wait_limit_setting_round_trips():
+    """ek_set_wait_limit returns the previous bound; <= 0 restores the defaults."""
+    prev = _hip.set_wait_limit(123)
+    try:
+        assert _hip.set_wait_limit(7) == 123
+        assert _hip.set_wait_limit(0) == 7
+        assert _hip.set_wait_limit(-5) == 0
+    finally:
+        _hip.set_wait_limit(prev)
 
 
 def test_signature_arity_matches_header():
@@ -93,9 +105,11 @@ def test_plan_splits_invariants(b, bucket):
     assert (splits - 1) * chunk < bucket                 # no split starts past the bucket
     ws = K.make_workspace(b, 32, 8, 128, bucket, "cpu")
     assert ws[0].shape == (b, 8, K._next_pow2(splits), K.group_pad(32, 8), 128)
-    assert ws[7].shape == (b, 32, bucket) and len(ws) == 9
-    # the ticket block, and room for every split's partial as 64-bit words
+    assert ws[7].shape == (b, 32, bucket) and len(ws) == 10
+    # the ticket block, the error word, and room for every split's partial as 64-bit words
     assert ws[8].shape == (b, 8, 2) and ws[8].dtype == torch.int32 and int(ws[8].abs().sum()) == 0
+    assert K.ws_error(ws) is ws[9] and ws[9].shape == (1,) and int(ws[9]) == 0
+    assert K.ws_error(ws[:7]) is None
     assert ws[0].numel() // 2 >= b * 8 * splits * (32 // 8) * 128
 
 

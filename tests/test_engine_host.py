@@ -81,6 +81,29 @@ def test_midstream_failure_without_fallback_propagates(ckpt, monkeypatch):
 
 def test_rows_accepts_tensors_lists_and_arrays():
     import numpy as np
-    assert E._rows(torch.tensor([[1, 2], [3, 4]])) == [[1, 2], [3, 4]]
-    assert E._rows(np.array([[1, 2]])) == [[1, 2]]
-    assert E._rows(((5, 6),)) == [[5, 6]]
+    assert E._as_rows(torch.tensor([[1, 2], [3, 4]])) == [[1, 2], [3, 4]]
+    assert E._as_rows(np.array([[1, 2]])) == [[1, 2]]
+    assert E._as_rows(((5, 6),)) == [[5, 6]]
+    assert E._as_rows([np.array([7, 8, 9]), torch.tensor([1])]) == [[7, 8, 9], [1]]
+
+
+def test_tiles_split_rows_evenly():
+    assert E._tiles(1, 8) == [(0, 1)]
+    assert E._tiles(8, 8) == [(0, 8)]
+    assert E._tiles(16, 8) == [(0, 8), (8, 16)]
+    assert E._tiles(12, 8) == [(0, 6), (6, 12)]
+    assert E._tiles(17, 8) == [(0, 5), (5, 11), (11, 17)]
+
+
+@pytest.mark.parametrize("prompts", [[[1, 2, 3], [4, 5, 6]], PROMPTS, [[7], [1, 2, 3, 4, 5]], [[9, 9]]])
+def test_pack_matches_the_oracle_layout(prompts):
+    """engine.py:541-570's layout: left padding with id 0 at position 0, real
+    positions 0..len-1, and for ragged batches the additive bf16 mask; the
+    engine's numpy construction equals the oracle's loop, bit for bit."""
+    holder = type("Holder", (), {"device": torch.device("cpu")})()
+    ids, pos, pad, s, mask = E._FastEngine._pack(holder, prompts)
+    r_ids, r_pos, r_pad, r_s, r_mask = O.pack(prompts)
+    assert torch.equal(ids, r_ids) and torch.equal(pos, r_pos) and pad == r_pad and s == r_s
+    assert (mask is None) == (r_mask is None)
+    if mask is not None:
+        assert mask.dtype == r_mask.dtype and torch.equal(mask, r_mask)

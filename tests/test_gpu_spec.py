@@ -181,6 +181,26 @@ def test_speculative_generate_equals_plain(dev, tiny_ckpt, prompt_kind):
     assert again == plain
 
 
+def test_speculative_capture_failure_falls_back_to_plain(dev, tiny_ckpt, monkeypatch):
+    """engine.py:640-649: when the speculative graph cannot be built for a
+    shape, the request runs on the plain captured step instead of failing."""
+    from enginekernel_amd import engine as E
+    eng = Engine(tiny_ckpt)
+    prompt = [random.Random(3).randrange(1024) for _ in range(30)]
+    eng._impl.spec = False
+    plain = list(eng.generate([prompt], 24))
+
+    def refuse(self, b, bucket):
+        raise RuntimeError("speculative graph capture refused")
+
+    monkeypatch.setattr(E._FastEngine, "_capture_spec", refuse)
+    eng._impl.spec = True
+    got = list(eng.generate([prompt], 24))
+    assert got == plain
+    assert not any(key[0] == "spec" for key in eng._impl.graphs)
+    assert eng._impl.last_stats == (23, 23)          # plain steps: one replay per token
+
+
 @pytest.mark.parametrize("prompt_kind", ["repeating", "random"])
 def test_speculative_engine_4b_shapes_near_ties(dev, prompt_kind):
     """Free-running speculative greedy at the 4B shapes vs the oracle loop fed
