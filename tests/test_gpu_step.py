@@ -48,16 +48,18 @@ def _state(dev, s, b=1, start=None):
                 step_idx=torch.zeros(1, dtype=torch.int64, device=dev))
 
 
-def _argmax_ok(t_gpu: int, t_ref: int, ref_ids, ref_logits) -> bool:
+def _argmax_ok(t_gpu: int, t_ref: int, ref_ids, ref_logits, slack: float | None = None) -> bool:
     """The GPU's token is the oracle's, or the oracle's logit for it is
-    within 2 bf16 ulps of the oracle's top logit (a near-tie that a
-    summation order can flip)."""
+    within `slack` of the oracle's top logit (default 2 bf16 ulps): a
+    near-tie that a summation order can flip."""
     if t_gpu == t_ref:
         return True
     hit = np.nonzero(ref_ids == t_gpu)[0]
     if hit.size == 0:
         return False
-    return float(ref_logits[0] - ref_logits[hit[0]]) <= 2 * _ulp(float(ref_logits[0]))
+    if slack is None:
+        slack = 2 * _ulp(float(ref_logits[0]))
+    return float(ref_logits[0] - ref_logits[hit[0]]) <= slack
 
 
 @pytest.fixture(scope="module")
@@ -72,8 +74,12 @@ def test_config4_trace_teacher_forced(dev, model4):
     oracle's ids. The bound on the logits is the oracle's own summation-order
     drift D (the fixture's largest |difference| between two oracle runs whose
     projections only accumulate in a different fp32 order, over the whole
-    vocabulary): every step within 1.5 D + 2 ulps at the oracle's top-8 ids.
-    The argmax equals the oracle's except at recorded near-ties."""
+    vocabulary): every step within 1.5 D + 2 ulps at the oracle's top-32
+    ids, and the mean within 1.5x the mean drift. The argmax equals the
+    oracle's, or is a token whose oracle logit is within D of the oracle's
+    top logit (a gap two equally valid summation orders can reverse); such
+    flips may not be more frequent than twice the reordered oracle's own
+    (plus 2)."""
     fx = np.load(GOLDEN)
     ids, top_ids, top_logits = fx["ids"], fx["top_ids"], fx["top_logits"]
     drift = fx["drift"] if "drift" in fx.files else None
@@ -102,7 +108,7 @@ def test_config4_trace_teacher_forced(dev, model4):
         assert int(st["step_idx"]) == n - 1 and int(st["len_t"]) == s + n - 1
         got_tok = [int(first[0])] + st["out_buf"][: n - 1, 0].cpu().tolist()
         at_top = torch.gather(logits.float(), 1, torch.as_tensor(top_ids, dtype=torch.int64, device=dev)).cpu().numpy()
-    err = np.abs(at_top - top_logits).max(axis=1)           # per step, at the oracle's top 8
+    err = np.abs(at_top - top_logits).max(axis=1)           # per step, at the oracle's top ids
     ulp2 = np.array([2 * _ulp(float(x)) for x in top_logits[:, 0]])
     floor = float(drift.max()) if drift is not None else 0.16
     print(f"config 4 trace: max |dlogit| {err.max():.4f} (mean {err.mean():.4f}), oracle drift "
@@ -110,10 +116,15 @@ def test_config4_trace_teacher_forced(dev, model4):
     assert (err <= 1.5 * floor + ulp2).all(), np.argmax(err - 1.5 * floor - ulp2)
     if drift is not None:
         assert err[1:].mean() <= 1.5 * drift[1:].mean() + ulp2.mean()
-    bad = [i for i in range(n) if not _argmax_ok(got_tok[i], int(ids[i]), top_ids[i], top_logits[i])]
+    bad = [i for i in range(n) if not _argmax_ok(got_tok[i], int(ids[i]), top_ids[i], top_logits[i], floor)]
     assert not bad, [(i, got_tok[i], int(ids[i]), top_logits[i][:2].tolist()) for i in bad[:5]]
-    agree = sum(int(got_tok[i] == ids[i]) for i in range(n))
-    print(f"config 4 trace: {agree}/{n} greedy ids equal; the rest at oracle near-ties")
+    flips = [i for i in range(n) if got_tok[i] != ids[i]]
+    alt_flips = int((fx["alt_ids"] != ids).sum()) if "alt_ids" in fx.files else None
+    gaps = [float(top_logits[i][0] - top_logits[i][np.nonzero(top_ids[i] == got_tok[i])[0][0]]) for i in flips]
+    print(f"config 4 trace: {n - len(flips)}/{n} greedy ids equal; flips at steps {flips} (oracle gaps {gaps}); "
+          f"the reordered oracle flips at {alt_flips} steps")
+    if alt_flips is not None:
+        assert len(flips) <= 2 * alt_flips + 2
 
 
 def test_config4_free_running_first_divergence(dev, model4):
