@@ -58,6 +58,10 @@ SIGNATURES = {
                        _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                        _P, _P, _P, _P, _P, _P, _P, _I64, _P,
                        _P, _P, _I64, _P, _P, _P],
+    "ek_decode_step_noalloc": [_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _F, _F,
+                               _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                               _P, _P, _P, _P, _P, _P, _P, _I64, _P,
+                               _P, _P, _P],
 }
 
 

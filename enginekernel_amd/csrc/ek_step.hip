@@ -18,6 +18,18 @@ template <> int step_occupancy<64>(int, size_t);
 template <> int step_occupancy<128>(int, size_t);
 }  // namespace eks
 
+// The no-allocation entry point's state: the launch-state block (Bar,
+// padded to 256 bytes) followed by the hand-over arena, at most
+// kStaticArenaBytes. Each device holds its own copy of this array, zero at
+// load and kept until the process ends; its address on a device comes from
+// hipGetSymbolAddress (the array's name is not a device address in host
+// code). Nothing in it needs clearing between calls: every launch bumps the
+// per-workgroup epochs in the Bar, so words a previous call left in the
+// arena never match a later launch's epoch.
+constexpr size_t kStaticBarBytes = (sizeof(eks::Bar) + 255) / 256 * 256;
+constexpr size_t kStaticArenaBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticBarBytes + kStaticArenaBytes];
+
 namespace {
 
 constexpr int64_t kSpin = int64_t(1) << 20;           // default polls of one hand-over wait before giving up (~1 s)
@@ -114,31 +126,41 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
-                        int64_t m, int64_t s_cap, int64_t n_layers, int64_t* sizes) {
-  EK_GUARD();
-  Plan p;
-  hipError_t e = make_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
-  if (e != hipSuccess) return e;
-  if (sizes) {
-    sizes[0] = p.arena_bytes;
-    sizes[1] = 0;
-    sizes[2] = (int64_t)sizeof(eks::Bar);
-    sizes[3] = p.nwg;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, resolved once per device (with
+// that device current) and kept.
+hipError_t static_scratch(unsigned char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return ek_fail(e, "decode_step_noalloc: no current device");
+  if (dev < 0 || dev >= kMaxDevices) return ek_fail(hipErrorInvalidValue, "decode_step_noalloc: device index too large");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return ek_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                "decode_step_noalloc: the static scratch has no device address");
+    g_scratch_ptr[dev] = static_cast<unsigned char*>(ptr);
   }
+  *out = g_scratch_ptr[dev];
   return hipSuccess;
 }
 
-int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, int64_t inter, int64_t n_q,
-                   int64_t n_kv, int64_t head_dim, int64_t vocab, int64_t m, float eps, float sm_scale,
-                   const void* embed, int64_t lde, const void* lm_head, const void* final_norm, const void* cos,
-                   const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb, int64_t csh, int64_t css,
-                   int64_t s_cap, int64_t* tokens, int64_t* positions, int64_t* len_t, int64_t* slot_t,
-                   const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
-                   void* logits, void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream) {
-  EK_GUARD();
+// The launch behind both decode-step entry points; arena/barrier: the
+// hand-over arena and launch-state block (the caller's, or the static scratch).
+hipError_t decode_step_impl(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden,
+                            int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab, int64_t m,
+                            float eps, float sm_scale, const void* embed, int64_t lde, const void* lm_head,
+                            const void* final_norm, const void* cos, const void* sin, int64_t ld_cs, int64_t rope_len,
+                            int64_t csb, int64_t csh, int64_t css, int64_t s_cap, int64_t* tokens,
+                            int64_t* positions, int64_t* len_t, int64_t* slot_t, const int32_t* start_t,
+                            int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok, void* logits,
+                            void* arena, int64_t arena_bytes, void* barrier, int* err, hipStream_t st) {
   Plan p;
   hipError_t e = make_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
   if (e != hipSuccess) return e;
@@ -164,12 +186,69 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
   a.bar = (eks::Bar*)barrier; a.err = err; a.spin = ek_wait_limit(kSpin);
   a.kpad_max = p.kpad_max; a.part_max = p.part_max; a.o_rows = p.o_rows;
   const int g = (int)(n_q / n_kv);
-  hipStream_t st = (hipStream_t)stream;
   switch (head_dim) {
     case 32: return eks::launch_step<32>(a, g, p.nwg, st);
     case 64: return eks::launch_step<64>(a, g, p.nwg, st);
     default: return eks::launch_step<128>(a, g, p.nwg, st);
   }
+}
+
+}  // namespace
+
+extern "C" {
+
+int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
+                        int64_t m, int64_t s_cap, int64_t n_layers, int64_t* sizes) {
+  EK_GUARD();
+  Plan p;
+  hipError_t e = make_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
+  if (e != hipSuccess) return e;
+  if (sizes) {
+    sizes[0] = p.arena_bytes;
+    sizes[1] = 0;
+    sizes[2] = (int64_t)sizeof(eks::Bar);
+    sizes[3] = p.nwg;
+  }
+  return hipSuccess;
+}
+
+
+int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, int64_t inter, int64_t n_q,
+                   int64_t n_kv, int64_t head_dim, int64_t vocab, int64_t m, float eps, float sm_scale,
+                   const void* embed, int64_t lde, const void* lm_head, const void* final_norm, const void* cos,
+                   const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb, int64_t csh, int64_t css,
+                   int64_t s_cap, int64_t* tokens, int64_t* positions, int64_t* len_t, int64_t* slot_t,
+                   const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
+                   void* logits, void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream) {
+  EK_GUARD();
+  return decode_step_impl(layer_ptrs, n_layers, hidden, inter, n_q, n_kv, head_dim, vocab, m, eps,
+                          sm_scale, embed, lde, lm_head, final_norm, cos, sin, ld_cs, rope_len, csb, csh, css, s_cap,
+                          tokens, positions, len_t, slot_t, start_t, out_buf, step_idx, max_steps, out_tok, logits,
+                          arena, arena_bytes, barrier, err, (hipStream_t)stream);
+}
+
+int ek_decode_step_noalloc(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, int64_t inter, int64_t n_q,
+                           int64_t n_kv, int64_t head_dim, int64_t vocab, int64_t m, float eps, float sm_scale,
+                           const void* embed, int64_t lde, const void* lm_head, const void* final_norm,
+                           const void* cos, const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb,
+                           int64_t csh, int64_t css, int64_t s_cap, int64_t* tokens, int64_t* positions,
+                           int64_t* len_t, int64_t* slot_t, const int32_t* start_t, int32_t* out_buf,
+                           int64_t* step_idx, int64_t max_steps, int64_t* out_tok, void* logits, int* err,
+                           void* stream) {
+  EK_GUARD();
+  Plan p;
+  hipError_t e = make_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
+  if (e != hipSuccess) return e;
+  if ((size_t)p.arena_bytes > kStaticArenaBytes)
+    return ek_fail(hipErrorInvalidValue, "decode_step_noalloc: this shape's hand-over arena exceeds the static 16 MiB "
+                                         "(use decode_step with an arena)");
+  unsigned char* base = nullptr;
+  e = static_scratch(&base);
+  if (e != hipSuccess) return e;
+  return decode_step_impl(layer_ptrs, n_layers, hidden, inter, n_q, n_kv, head_dim, vocab, m, eps, sm_scale, embed,
+                          lde, lm_head, final_norm, cos, sin, ld_cs, rope_len, csb, csh, css, s_cap, tokens,
+                          positions, len_t, slot_t, start_t, out_buf, step_idx, max_steps, out_tok, logits,
+                          base + kStaticBarBytes, (int64_t)kStaticArenaBytes, base, err, (hipStream_t)stream);
 }
 
 }  // extern "C"

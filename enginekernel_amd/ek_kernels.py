@@ -444,24 +444,44 @@ def decode_step(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_ca
     logits. err: the error word to use (default: the scratch's own); a step
     that gives up, and every step launched while the word is set, writes
     token -1 and advances only step_idx."""
+    if err is None:
+        err = scratch.err
+    args = _step_args(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap, tokens, positions, len_t,
+                      slot_t, start_t, out_buf, step_idx, out_tok, logits, err)
+    call("ek_decode_step", *args, ptr(scratch.arena), scratch.arena_bytes, ptr(scratch.barrier), ptr(err), stream())
+    return tokens
+
+
+def decode_step_noalloc(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap, tokens, positions,
+                        len_t, slot_t, start_t, out_buf, step_idx, err, out_tok=None, logits=None):
+    """decode_step on the library's static per-device hand-over state instead
+    of a StepScratch: nothing is allocated, by the caller or the library.
+    Shapes whose arena exceeds the static 16 MiB are rejected; calls that
+    overlap on one device race (they share that device's state). err: the
+    caller's error word, as for decode_step."""
+    args = _step_args(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap, tokens, positions, len_t,
+                      slot_t, start_t, out_buf, step_idx, out_tok, logits, err)
+    call("ek_decode_step_noalloc", *args, ptr(err), stream())
+    return tokens
+
+
+def _step_args(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap, tokens, positions, len_t, slot_t,
+               start_t, out_buf, step_idx, out_tok, logits, err):
+    """The checked leading arguments shared by the two decode-step entry points."""
     _gpu(tokens, embed, lm_head, k_cache0)
     m = tokens.shape[0]
     _need(out_buf.dtype == torch.int32 and out_buf.shape[1] == m and out_buf.is_contiguous(), "out_buf")
     if logits is not None:
         _need(logits.dtype == _BF16 and logits.is_contiguous() and logits.numel() == cfg.vocab_size, "logits")
-    if err is None:
-        err = scratch.err
     _need(err.dtype == torch.int32 and err.numel() >= 1 and err.device == tokens.device, "err")
     _need(table.dtype == torch.int64 and table.shape == (cfg.num_layers, 10) and table.is_contiguous(), "table")
     _need(embed.stride(-1) == 1 and lm_head.stride(-1) == 1 and cos.stride(0) == sin.stride(0), "weights")
-    call("ek_decode_step", ptr(table), cfg.num_layers, cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
-         cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, m, float(cfg.rms_eps), float(cfg.head_dim ** -0.5),
-         ptr(embed), embed.stride(0), ptr(lm_head), ptr(final_norm), ptr(cos), ptr(sin), cos.stride(0),
-         cos.shape[0], k_cache0.stride(0), k_cache0.stride(1), k_cache0.stride(2), s_cap,
-         ptr(tokens), ptr(positions), ptr(len_t), ptr(slot_t), ptr(start_t), ptr(out_buf), ptr(step_idx),
-         out_buf.shape[0], ptr(out_tok), ptr(logits), ptr(scratch.arena), scratch.arena_bytes,
-         ptr(scratch.barrier), ptr(err), stream())
-    return tokens
+    return (ptr(table), cfg.num_layers, cfg.hidden_size, cfg.intermediate_size, cfg.num_heads,
+            cfg.num_kv_heads, cfg.head_dim, cfg.vocab_size, m, float(cfg.rms_eps), float(cfg.head_dim ** -0.5),
+            ptr(embed), embed.stride(0), ptr(lm_head), ptr(final_norm), ptr(cos), ptr(sin), cos.stride(0),
+            cos.shape[0], k_cache0.stride(0), k_cache0.stride(1), k_cache0.stride(2), s_cap,
+            ptr(tokens), ptr(positions), ptr(len_t), ptr(slot_t), ptr(start_t), ptr(out_buf), ptr(step_idx),
+            out_buf.shape[0], ptr(out_tok), ptr(logits))
 
 
 # ----------------------------------------------------------------------------

@@ -264,6 +264,29 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
                    const int32_t* start_t, int32_t* out_buf, int64_t* step_idx, int64_t max_steps, int64_t* out_tok,
                    void* logits, void* arena, int64_t arena_bytes, void* barrier, int* err, void* stream);
 
+/* decode_step_noalloc: decode_step without the caller's arena and barrier
+ * block -- the launch uses a static per-device array of this library (the
+ * 256-byte launch-state block plus a hand-over arena of at most 16 MiB,
+ * zero at load and held by each device until the process ends), so a call
+ * allocates nothing and needs no workspace from the caller. Shapes whose
+ * arena (decode_step_plan sizes[0]) exceeds 16 MiB are rejected with
+ * hipErrorInvalidValue. Every call on one device shares that device's array:
+ * calls that overlap on a device (other streams, other threads) race and must
+ * not be issued. The array never needs clearing (each launch moves its
+ * epoch on); after an abandoned launch zero only *err. Same arguments,
+ * results and error behaviour as decode_step otherwise.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). */
+int ek_decode_step_noalloc(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, int64_t inter, int64_t n_q,
+                           int64_t n_kv, int64_t head_dim, int64_t vocab, int64_t m, float eps, float sm_scale,
+                           const void* embed, int64_t lde, const void* lm_head, const void* final_norm,
+                           const void* cos, const void* sin, int64_t ld_cs, int64_t rope_len, int64_t csb,
+                           int64_t csh, int64_t css, int64_t s_cap, int64_t* tokens, int64_t* positions,
+                           int64_t* len_t, int64_t* slot_t, const int32_t* start_t, int32_t* out_buf,
+                           int64_t* step_idx, int64_t max_steps, int64_t* out_tok, void* logits, int* err,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

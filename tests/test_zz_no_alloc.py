@@ -1,0 +1,113 @@
+"""ek_decode_step_noalloc (the one-launch decode step on the library's static
+per-device hand-over state) against ek_decode_step (the same step on a
+caller-allocated arena and barrier block), both called through the C ABI.
+
+Two calls in a row, the second with a smaller input (fewer layers, a
+shorter context and cache, so a smaller hand-over arena inside the same
+static array): each runs three consecutive steps on identical copies of the
+state and caches, and everything the step writes must be bit-identical --
+the step's logits, tokens, out_buf rows, positions, slot and length, the
+step counter and the new cache rows. The kernels are the same; only where
+the hand-over words live differs.
+"""
+
+import pytest
+import torch
+
+from enginekernel_amd import _hip
+from enginekernel_amd import checkpoint as C
+from enginekernel_amd import ek_kernels as K
+from enginekernel_amd.ek_model import Qwen3
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    _hip.load()
+    return torch.device("cuda:0")
+
+
+def _inputs(cfg, dev, ctx, s_cap, seed):
+    g = torch.Generator().manual_seed(seed)
+    shape = (1, cfg["num_key_value_heads"], s_cap, cfg["head_dim"])
+    k = [(torch.randn(shape, generator=g) * 0.5).to(BF).to(dev) for _ in range(cfg["num_hidden_layers"])]
+    v = [(torch.randn(shape, generator=g) * 0.5).to(BF).to(dev) for _ in range(cfg["num_hidden_layers"])]
+    st = dict(tokens=torch.randint(0, cfg["vocab_size"], (1,), generator=g).to(dev),
+              positions=torch.full((1,), ctx, dtype=torch.int64, device=dev),
+              len_t=torch.full((1,), ctx, dtype=torch.int64, device=dev),
+              slot_t=torch.zeros(1, dtype=torch.int64, device=dev),
+              start_t=torch.zeros(1, dtype=torch.int32, device=dev),
+              out_buf=torch.full((8, 1), -7, dtype=torch.int32, device=dev),
+              step_idx=torch.zeros(1, dtype=torch.int64, device=dev),
+              err=torch.zeros(1, dtype=torch.int32, device=dev))
+    return k, v, st
+
+
+def _run(model, k, v, st, s_cap, steps, noalloc):
+    cfg = model.cfg
+    table = model._layer_table(k, v)
+    out_tok = torch.zeros(1, dtype=torch.int64, device=k[0].device)
+    logits = torch.empty(steps, cfg.vocab_size, dtype=BF, device=k[0].device)
+    scratch = None
+    if not noalloc:
+        plan = K.decode_step_plan(cfg.hidden_size, cfg.intermediate_size, cfg.num_heads, cfg.num_kv_heads,
+                                  cfg.head_dim, cfg.vocab_size, 1, s_cap, cfg.num_layers)
+        assert plan is not None
+        scratch = K.StepScratch(plan, k[0].device)
+    for i in range(steps):
+        common = (table, cfg, model.embed, model.lm_head, model.final_norm, model.cos, model.sin, k[0], s_cap,
+                  st["tokens"], st["positions"], st["len_t"], st["slot_t"], st["start_t"], st["out_buf"],
+                  st["step_idx"])
+        if noalloc:
+            K.decode_step_noalloc(*common, st["err"], out_tok=out_tok, logits=logits[i])
+        else:
+            K.decode_step(*common, scratch, out_tok=out_tok, logits=logits[i], err=st["err"])
+    torch.cuda.synchronize()
+    return logits, out_tok
+
+
+@pytest.mark.parametrize("call", [0, 1])
+def test_noalloc_step_equals_the_arena_step(dev, call):
+    # call 0: three layers, context 300 in a 512-key cache; call 1 (after it):
+    # two layers, context 40 in a 64-key cache
+    layers, ctx, s_cap, seed = [(3, 300, 512, 5), (2, 40, 64, 6)][call]
+    cfg = dict(C.QWEN3_4B, num_hidden_layers=layers)
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=seed), config=cfg)
+    assert model.persistent_plan(1, s_cap) is not None
+    print(f"no-alloc step: call {call}, {layers} layers, context {ctx}, cache {s_cap}", flush=True)
+    k_a, v_a, st_a = _inputs(cfg, dev, ctx, s_cap, seed)
+    k_b, v_b = [t.clone() for t in k_a], [t.clone() for t in v_a]
+    st_b = {n: t.clone() for n, t in st_a.items()}
+    with torch.inference_mode():
+        lg_a, tok_a = _run(model, k_a, v_a, st_a, s_cap, 3, noalloc=False)
+        lg_b, tok_b = _run(model, k_b, v_b, st_b, s_cap, 3, noalloc=True)
+    assert int(st_a["err"]) == 0 and int(st_b["err"]) == 0
+    assert torch.equal(lg_a, lg_b)
+    assert torch.equal(tok_a, tok_b)
+    for n in st_a:
+        assert torch.equal(st_a[n], st_b[n]), n
+    assert int(st_b["step_idx"]) == 3 and int(st_b["len_t"]) == ctx + 3
+    assert (st_b["out_buf"][:3] >= 0).all()
+    for a, b in zip(k_a + v_a, k_b + v_b):
+        assert torch.equal(a, b)
+
+
+def test_noalloc_rejects_an_arena_beyond_the_static_limit(dev):
+    """A shape whose hand-over arena exceeds the static 16 MiB is refused
+    with an error before anything is launched (256 layers of the 4B shape
+    need about 25 MiB)."""
+    cfg = dict(C.QWEN3_4B)
+    plan = K.decode_step_plan(2560, 9728, 32, 8, 128, cfg["vocab_size"], 1, 64, 256)
+    assert plan is not None and plan[0] > 16 << 20
+    lib = _hip.load()
+    z = torch.zeros(64, dtype=torch.int64, device=dev)
+    p = z.data_ptr()
+    rc = lib.ek_decode_step_noalloc(p, 256, 2560, 9728, 32, 8, 128, cfg["vocab_size"], 1, 1e-6, 0.088,
+                                    p, 2560, p, p, p, p, 128, 64, 0, 0, 128, 64,
+                                    p, p, p, p, p, p, p, 8, p, 0, p, 0)
+    assert rc != 0
+    assert b"16 MiB" in lib.ek_last_error()
