@@ -22,6 +22,7 @@ runs the engine on the model in DIR and checks its output that way
 from __future__ import annotations
 
 import argparse
+import json
 import os
 import sys
 from typing import Callable, Sequence
@@ -30,31 +31,42 @@ import torch
 
 LIMIT = 2.0
 
-TEXT = (
-    "The history of computing hardware spans the development of machines able to "
-    "perform arithmetic automatically. Early devices were mechanical; later ones "
-    "used vacuum tubes, then transistors, then integrated circuits. Each step "
-    "reduced cost and increased speed, which changed what problems were worth "
-    "solving. Today the limiting factor for large language model inference is "
-    "usually memory bandwidth rather than arithmetic throughput, because every "
-    "generated token requires reading the entire set of model weights. "
+# Prompt text for `--mode text`: any natural prose serves, since the rule
+# compares the engine with the replay model on the same prompt.
+CORPUS = (
+    "A river delta forms where a slow current drops the silt it has carried for "
+    "hundreds of kilometres. Each flood lays down a thin new layer, and over "
+    "centuries the channels wander, split and rejoin across the plain. Farmers "
+    "learned to read the colour of the water to judge when the next flood would "
+    "come, and towns were built on the few ridges that stayed dry. Modern "
+    "engineers measure the same process with sonar, satellite images and "
+    "sediment cores, yet the basic pattern they record is the one the farmers "
+    "knew: the land is always being rebuilt by the water that crosses it. "
 )
 
 
-def make_prompts(model_path: str | None, batch: int, in_len: int, mode: str) -> list[list[int]]:
-    """check_exact.py:28-41: seeded random ids, or slices of a tokenized text."""
+def make_prompts(model_path: str | None, batch: int, in_len: int, mode: str,
+                 vocab: int | None = None) -> list[list[int]]:
+    """`batch` prompts of `in_len` token ids (the two prompt modes of
+    check_exact.py:28-41). random: ids drawn uniformly from the checkpoint's
+    vocabulary (config.json's vocab_size, or `vocab`), seed 20240; text: the
+    tokenized corpus repeated as needed, row i starting i * in_len / batch
+    tokens further along it, so that the rows overlap by less than a prompt."""
     if mode == "random":
-        g = torch.Generator().manual_seed(0)
-        return torch.randint(0, 151000, (batch, in_len), generator=g).tolist()
+        if vocab is None:
+            with open(os.path.join(model_path, "config.json")) as f:
+                vocab = int(json.load(f)["vocab_size"])
+        g = torch.Generator().manual_seed(20240)
+        return [torch.randint(0, vocab, (in_len,), generator=g).tolist() for _ in range(batch)]
+    if mode != "text":
+        raise ValueError(f"unknown prompt mode {mode!r}")
     from transformers import AutoTokenizer
 
-    tok = AutoTokenizer.from_pretrained(model_path)
-    ids = tok(TEXT * 200, return_tensors=None)["input_ids"]
-    out = []
-    for i in range(batch):
-        s = (i * 37) % max(1, len(ids) - in_len - 1)
-        out.append(ids[s:s + in_len])
-    return out
+    piece = AutoTokenizer.from_pretrained(model_path)(CORPUS, return_tensors=None)["input_ids"]
+    step = max(1, in_len // max(1, batch))
+    need = in_len + step * batch
+    stream = piece * (need // max(1, len(piece)) + 1)
+    return [stream[i * step:i * step + in_len] for i in range(batch)]
 
 
 @torch.inference_mode()
@@ -107,13 +119,27 @@ def hf_logits_fn(model_path: str, device: str = "cuda"):
     return fn
 
 
+# command-line options: (flag, type, default, help); --model is required
+_OPTIONS = (
+    ("--model", str, None, "local HF checkpoint directory (config.json, safetensors, tokenizer for text mode)"),
+    ("--batch", int, 1, "prompts decoded together"),
+    ("--in-len", int, 512, "prompt length in tokens"),
+    ("--out-len", int, 32, "tokens generated per prompt"),
+    ("--mode", str, "text", "prompt source: random ids or the tokenized corpus"),
+)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="the 2-logit teacher-forced acceptance rule")
-    ap.add_argument("--model", required=True)
-    ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--in-len", type=int, default=512)
-    ap.add_argument("--out-len", type=int, default=32)
-    ap.add_argument("--mode", choices=["random", "text"], default="text")
+    for flag, typ, default, text in _OPTIONS:
+        kw = {"type": typ, "help": text}
+        if default is None:
+            kw["required"] = True
+        else:
+            kw["default"] = default
+        if flag == "--mode":
+            kw["choices"] = ["random", "text"]
+        ap.add_argument(flag, **kw)
     a = ap.parse_args(argv)
     prompts = make_prompts(a.model, a.batch, a.in_len, a.mode)
 

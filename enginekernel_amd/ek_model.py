@@ -61,23 +61,37 @@ class Qwen3Config:
         self.kv_size = self.num_kv_heads * self.head_dim
 
 
-def shard_map(path: str) -> dict:
-    """ek_model.py:45-60: tensor name -> safetensors file."""
-    index = os.path.join(path, "model.safetensors.index.json")
-    if os.path.exists(index):
-        with open(index) as f:
-            return json.load(f)["weight_map"]
-    files = sorted(glob.glob(os.path.join(path, "*.safetensors")))
-    if not files:
-        raise FileNotFoundError(f"no safetensors under {path}")
-    from safetensors import safe_open
+def _safetensors_names(fn: str) -> list:
+    """Tensor names in one .safetensors file, read from its header alone: an
+    8-byte little-endian length, then that many bytes of JSON whose keys are
+    the tensor names (plus an optional "__metadata__")."""
+    with open(fn, "rb") as f:
+        raw = f.read(8)
+        if len(raw) != 8:
+            raise ValueError(f"{fn}: truncated safetensors header")
+        n = int.from_bytes(raw, "little")
+        head = json.loads(f.read(n))
+    return [k for k in head if k != "__metadata__"]
 
-    out = {}
-    for fn in files:
-        with safe_open(fn, framework="pt", device="cpu") as f:
-            for k in f.keys():
-                out[k] = os.path.basename(fn)
-    return out
+
+def shard_map(path: str) -> dict:
+    """Tensor name -> shard file name of a local HF checkpoint (the lookup of
+    ek_model.py:45-60): a sharded checkpoint's index names the file of every
+    tensor; without one, each *.safetensors file's header lists its tensors.
+    A name found in two files is an error rather than a silent override."""
+    index = os.path.join(path, "model.safetensors.index.json")
+    if os.path.isfile(index):
+        with open(index) as f:
+            return dict(json.load(f)["weight_map"])
+    table: dict = {}
+    for fn in sorted(glob.glob(os.path.join(path, "*.safetensors"))):
+        base = os.path.basename(fn)
+        for name in _safetensors_names(fn):
+            if table.setdefault(name, base) != base:
+                raise ValueError(f"tensor {name} is in both {table[name]} and {base}")
+    if not table:
+        raise FileNotFoundError(f"no safetensors under {path}")
+    return table
 
 
 def load_tensors(path: str, dtype=torch.bfloat16) -> dict:

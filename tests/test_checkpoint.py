@@ -65,3 +65,20 @@ def test_rope_tables_equal_the_oracle():
         a = rope_tables(d, th, 2048)
         b = O.build_rope(d, th, 2048)
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_shard_map_reads_headers_of_unindexed_shards(tmp_path):
+    from safetensors.torch import save_file
+
+    save_file({"a": torch.zeros(2), "b": torch.ones(3)}, str(tmp_path / "x-1.safetensors"), metadata={"k": "v"})
+    save_file({"c": torch.zeros(1)}, str(tmp_path / "x-2.safetensors"))
+    assert shard_map(str(tmp_path)) == {"a": "x-1.safetensors", "b": "x-1.safetensors", "c": "x-2.safetensors"}
+    save_file({"c": torch.zeros(1)}, str(tmp_path / "x-3.safetensors"))
+    try:
+        shard_map(str(tmp_path))
+    except ValueError as e:
+        assert "x-2" in str(e) and "x-3" in str(e)
+    else:
+        raise AssertionError("a tensor in two shards must be refused")
+    json.dump({"weight_map": {"c": "x-3.safetensors"}}, open(tmp_path / "model.safetensors.index.json", "w"))
+    assert shard_map(str(tmp_path)) == {"c": "x-3.safetensors"}
