@@ -51,6 +51,19 @@ __device__ __forceinline__ float dot8_acc(const uint4& w, const uint4& x, float 
   return acc;
 }
 
+// The same sum on gfx950's bf16 dot instruction (v_dot2c_f32_bf16: two bf16
+// products added to an fp32 accumulator per instruction): 4 instructions per
+// chunk instead of 8 FMAs and 16 unpacking shifts/masks. The bf16 products
+// are exact in fp32; only the fp32 summation order differs from dot8_acc.
+typedef __bf16 ek_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot8_acc_d2(const uint4& w, const uint4& x, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ek_bf16x2, w.x), __builtin_bit_cast(ek_bf16x2, x.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ek_bf16x2, w.y), __builtin_bit_cast(ek_bf16x2, x.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ek_bf16x2, w.z), __builtin_bit_cast(ek_bf16x2, x.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ek_bf16x2, w.w), __builtin_bit_cast(ek_bf16x2, x.w), acc, false);
+  return acc;
+}
+
 // butterfly sum over all 64 lanes of a wave (every lane gets the total)
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -110,3 +123,9 @@ __device__ __forceinline__ uint4 ld16_nt(const bf16_t* p) {
   const u32x4_t v = __builtin_nontemporal_load((global_u32x4_t*)(p));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// 4-byte load from global memory as a global (not flat) load: a flat load
+// also counts against the LDS wait counter, so every later LDS access (and
+// every barrier) would wait for it.
+typedef const __attribute__((address_space(1))) uint32_t global_u32_t;
+__device__ __forceinline__ uint32_t ld4(const void* p) { return *(global_u32_t*)(p); }

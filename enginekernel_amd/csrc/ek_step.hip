@@ -33,7 +33,7 @@ static __device__ __align__(256) unsigned char scratch[kStaticBarBytes + kStatic
 namespace {
 
 constexpr int64_t kSpin = int64_t(1) << 20;           // default polls of one hand-over wait before giving up (~1 s)
-constexpr size_t kLdsLimit = 160 * 1024 - 1024;       // dynamic LDS per workgroup (static arrays aside)
+constexpr size_t kLdsLimit = eks::kStepDynLds;        // dynamic LDS per workgroup (the static arrays take the rest)
 constexpr int64_t kFusedScoreLds = 32 * 1024;         // score row bytes per attention unit
 
 int step_grid() {
@@ -89,6 +89,8 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   const int64_t g = n_q / n_kv;
   if (g != 1 && g != 2 && g != 4 && g != 8)
     return ek_fail(hipErrorInvalidValue, "decode_step: query heads per kv head must be 1, 2, 4 or 8");
+  if (n_layers > eks::MAX_LAYERS)
+    return ek_fail(hipErrorInvalidValue, "decode_step: at most 64 layers (the layer table is held in LDS)");
   if (n_layers < 1 || hidden < eks::CH || inter < eks::CH || vocab < 1 || hidden % eks::CH || inter % eks::CH ||
       (n_q * head_dim) % eks::CH)
     return ek_fail(hipErrorInvalidValue, "decode_step: hidden, intermediate and n_q * head_dim must be multiples of 512");

@@ -53,7 +53,10 @@ namespace eks {
 constexpr int SNT = eka::FNT;          // 512 threads
 constexpr int SNW = SNT / EK_WAVE;     // 8 waves
 constexpr int NB = 8;                  // weight chunks in flight per wave
-constexpr int PF = 6;                  // chunks per wave prefetched ahead of a hand-over wait (6: 0.8 % faster than 4 or 8)
+#ifndef EK_STEP_PF
+#define EK_STEP_PF 6
+#endif
+constexpr int PF = EK_STEP_PF;         // chunks per wave prefetched ahead of a hand-over wait (6: 0.8 % faster than 4 or 8)
 constexpr int OB = 12;                 // o_proj chunks per wave held in registers through attention
 constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
 constexpr int LW_FIELDS = 10;          // per-layer pointer table row
@@ -62,6 +65,8 @@ constexpr int APT = 3;                 // attention: 32-key PV tiles per wave he
 constexpr int LLW = 10;                // hand-over words in flight per thread
 constexpr int NGW = 4;                 // norm gain words per thread (hidden <= 2 * NGW * SNT)
 constexpr int MAX_WG = 1024;
+constexpr int MAX_LAYERS = 64;          // layer table rows held in LDS
+constexpr size_t kStepDynLds = 160 * 1024 - 8 * 1024;   // dynamic LDS limit (the static arrays take the rest)
 // Copies of each all-to-all hand-over region (attention out, o out, act,
 // down out): producers store each word to HC regions and workgroup w polls
 // region w % HC. Measured at the Qwen3-4B shape (config 4, 300 steps):
@@ -197,6 +202,17 @@ __device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* d
   return true;
 }
 
+// True when every thread of the workgroup passed ok. A failing thread sets
+// the LDS flag before the barrier; the flag is zeroed at kernel entry and a
+// workgroup that sees it set leaves the step, so it never needs clearing.
+// (__syncthreads_and reads the dispatch packet from memory and takes three
+// barriers.)
+__device__ __forceinline__ bool wg_all(bool ok, int* s_fail) {
+  if (!ok) *s_fail = 1;
+  __syncthreads();
+  return *s_fail == 0;   // the barrier's fences order this read after every thread's write
+}
+
 struct LinSrc {   // words [0, n) of one region
   const llw_t* p;
   __device__ const llw_t* operator()(int i) const { return p + i; }
@@ -205,6 +221,19 @@ struct LinSrc {   // words [0, n) of one region
 // ---------------------------------------------------------------------------
 // projections
 // ---------------------------------------------------------------------------
+// The chunk dot product of the projections: on the bf16 dot instruction
+// (the phases after a hand-over are bound by these instructions, not by
+// memory, when their weights are already in registers).
+#ifndef EK_STEP_DOT2
+#define EK_STEP_DOT2 1
+#endif
+__device__ __forceinline__ float step_dot8(const uint4& w, const uint4& x, float acc) {
+#if EK_STEP_DOT2
+  return dot8_acc_d2(w, x, acc);
+#else
+  return dot8_acc(w, x, acc);
+#endif
+}
 struct Gp {
   const bf16_t* w;   // [rows, K] row-major
   int K, C;          // reduction length, 1 KiB chunks per row
@@ -226,17 +255,19 @@ __device__ __forceinline__ Gp make_gp(const bf16_t* w, int k, int units, int pai
 __device__ __forceinline__ void unit_range(const Gp& g, int& u0, int& u1) {
   const int w = (int)blockIdx.x - g.wg0;
   if (w < 0 || w >= g.nwg) { u0 = u1 = 0; return; }
-  const int64_t n = g.units / g.gran;
-  u0 = g.gran * (int)(n * w / g.nwg);
-  u1 = g.gran * (int)(n * (w + 1) / g.nwg);
+  // 32-bit arithmetic (the plan bounds units / gran * workgroups below 2^31):
+  // a 64-bit division is a long emulated sequence
+  const uint32_t n = (uint32_t)(g.units / g.gran);
+  u0 = g.gran * (int)(n * (uint32_t)w / (uint32_t)g.nwg);
+  u1 = g.gran * (int)(n * (uint32_t)(w + 1) / (uint32_t)g.nwg);
 }
 
 struct WaveItems { int i0, n; };
 
 __device__ __forceinline__ WaveItems wave_items(const Gp& g, int nu, int wave) {
   const int n_items = nu * (g.pair ? 2 : 1) * g.C;
-  const int i0 = (int)((int64_t)n_items * wave / SNW);
-  const int i1 = (int)((int64_t)n_items * (wave + 1) / SNW);
+  const int i0 = (int)((uint32_t)n_items * (uint32_t)wave / (uint32_t)SNW);
+  const int i1 = (int)((uint32_t)n_items * (uint32_t)(wave + 1) / (uint32_t)SNW);
   WaveItems w;
   w.i0 = i0; w.n = i1 - i0;
   return w;
@@ -307,11 +338,23 @@ __device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, co
   const int n = sp.n;
   const int loff = lane * 8;
   int r = sp.i0 / P.C, ch = sp.i0 - (sp.i0 / P.C) * P.C;
+  // the activation chunk of every held item, read from LDS up front (item k
+  // of the wave uses chunk (ch + k) mod C of x): one LDS wait for all of
+  // them instead of one per item
+  uint4 xr[OB];
+  {
+    int c = ch;
+#pragma unroll
+    for (int u = 0; u < OB; ++u) {
+      xr[u] = *reinterpret_cast<const uint4*>(xs + c * CH + loff);
+      if (++c == P.C) c = 0;
+    }
+  }
   float acc = 0.f;
 #pragma unroll
   for (int u = 0; u < OB; ++u) {
     if (u < n) {
-      acc = dot8_acc(ob[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+      acc = step_dot8(ob[u], xr[u], acc);
       if (ch == P.C - 1 || u == n - 1) {
         const float sum = wave_sum_dpp(acc);
         if (lane == 0) part[r * SNW + wave] = sum;
@@ -321,7 +364,7 @@ __device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, co
     }
   }
   for (int k = OB; k < n; ++k) {
-    acc = dot8_acc(ld16_nt(span_item(sp, sp.i0 + k) + loff), *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+    acc = step_dot8(ld16_nt(span_item(sp, sp.i0 + k) + loff), *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
     if (ch == P.C - 1 || k == n - 1) {
       const float sum = wave_sum_dpp(acc);
       if (lane == 0) part[r * SNW + wave] = sum;
@@ -335,14 +378,18 @@ __device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, co
 // after its ring prefetch) into the L2 (one 4-byte load per 64-byte sector),
 // so that the phase later reads them from L2 instead of HBM. The loaded words are
 // folded into `sink`, which the caller consumes where it waits anyway.
-constexpr int L2T = 8;
+#ifndef EK_STEP_L2T
+#define EK_STEP_L2T 8
+#endif
+constexpr int L2T = EK_STEP_L2T;
 __device__ __forceinline__ void l2_touch(const Gp& pn, uint32_t& sink) {
   const Span sn = make_span(pn, wave_id());
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < L2T / 4; ++j) {
     const int i = PF + 4 * j + (lane >> 4);
-    if (i < sn.n) sink ^= *reinterpret_cast<const uint32_t*>(span_item(sn, sn.i0 + i) + (lane & 15) * 32);
+    // clamped, not conditional: a load under a lane condition is a branch that waits for it
+    sink ^= ld4(span_item(sn, sn.i0 + (i < sn.n ? i : 0)) + (lane & 15) * 32);
   }
 }
 
@@ -363,12 +410,18 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
   for (int u = 0; u < NB; ++u)
     if (u >= ring.nready) ring.r[u] = ld16_nt(span_item(sp, sp.i0 + (u < n ? u : 0)) + loff);
   int r = sp.i0 / P.C, ch = sp.i0 - (sp.i0 / P.C) * P.C;   // consume position (row-local, chunk)
+  // the activation chunk of the current item; the next item's chunk is read
+  // from LDS before the current item's products, so the LDS round trip
+  // overlaps them instead of stalling every item
+  uint4 xc = *reinterpret_cast<const uint4*>(xs + ch * CH + loff);
   float acc = 0.f;
   int k0 = 0;
   for (; k0 + NB <= n; k0 += NB) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-      acc = dot8_acc(ring.r[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+      const int chn = ch + 1 == P.C ? 0 : ch + 1;
+      const uint4 xn = *reinterpret_cast<const uint4*>(xs + chn * CH + loff);
+      acc = step_dot8(ring.r[u], xc, acc);
       const int kn = k0 + u + NB;
       ring.r[u] = ld16_nt(span_item(sp, sp.i0 + (kn < n ? kn : n - 1)) + loff);
       if (ch == P.C - 1) {
@@ -377,12 +430,16 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
         acc = 0.f;
       }
       if (++ch == P.C) { ch = 0; ++r; }
+      xc = xn;
     }
   }
 #pragma unroll
   for (int u = 0; u < NB; ++u) {
     if (k0 + u < n) {
-      acc = dot8_acc(ring.r[u], *reinterpret_cast<const uint4*>(xs + ch * CH + loff), acc);
+      const int chn = ch + 1 == P.C ? 0 : ch + 1;
+      const uint4 xn = *reinterpret_cast<const uint4*>(xs + chn * CH + loff);
+      acc = step_dot8(ring.r[u], xc, acc);
+      xc = xn;
       if (ch == P.C - 1 || k0 + u == n - 1) {
         const float sum = wave_sum_dpp(acc);
         if (lane == 0) part[r * SNW + wave] = sum;
@@ -492,12 +549,16 @@ __device__ __forceinline__ void zero_pad(bf16_t* xs, int k, int kpad) {
 }
 
 // the norm gain's words of this thread (i = tid + j * SNT), loaded ahead of a wait
+// (every load issued, at a clamped index, then masked: a load under a lane
+// condition becomes a branch that waits for it)
 __device__ __forceinline__ void load_gain(const bf16_t* nw, int k, uint32_t* gw) {
   const uint32_t* g32 = reinterpret_cast<const uint32_t*>(nw);
+  const int nwd = k / 2;
 #pragma unroll
   for (int j = 0; j < NGW; ++j) {
     const int i = threadIdx.x + j * SNT;
-    gw[j] = i < k / 2 ? g32[i] : 0u;
+    const uint32_t v = ld4(g32 + (i < nwd ? i : 0));
+    gw[j] = i < nwd ? v : 0u;
   }
 }
 
@@ -558,7 +619,7 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
 // ---------------------------------------------------------------------------
 template <int D, int G>
 __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
-                                                int64_t hi, uint32_t ep, unsigned char* smem, int layer
+                                                int64_t hi, uint32_t ep, unsigned char* smem, int* s_fail, int layer
 #ifdef EK_STEP_TRACE
                                                 , int64_t* ts_lds
 #endif
@@ -618,7 +679,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
       rope_lds[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
     }
     const bool ok = ll_read<2>(src, (G + 2) * hw, ep, reinterpret_cast<uint32_t*>(qrow), a.err, a.spin);
-    return __syncthreads_and(ok) != 0;
+    return wg_all(ok, s_fail);
   };
   return eka::attn_unit<D, G, ATU, APT>(u, smem + eka::align16((size_t)(G + 6) * D * 2), wait_heads);
 }
@@ -640,7 +701,8 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 __host__ __device__ inline size_t step_rr_bytes(int h) { return eka::align16((size_t)h * 4); }
 
 template <int D, int G>
-__device__ __forceinline__ void attention_loop(const StepArgs& a, uint32_t ep, int64_t hi, unsigned char* smem
+__device__ __forceinline__ void attention_loop(const StepArgs& a, const int64_t* lwt, uint32_t ep, int64_t hi,
+                                               unsigned char* smem, int* s_fail
 #ifdef EK_STEP_TRACE
                                                , int64_t* ts_lds
 #endif
@@ -648,10 +710,10 @@ __device__ __forceinline__ void attention_loop(const StepArgs& a, uint32_t ep, i
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = arena_layer_words(a.h, a.inter, qkvw, qw);
   for (int l = 0; l < a.nl; ++l) {
-    const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
+    const int64_t* lw = lwt + l * LW_FIELDS;
     const llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
     llw_t* att_ll = a.arena + (int64_t)l * lwords + qkvw / 2;
-    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, ep, smem, l
+    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, ep, smem, s_fail, l
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif
@@ -672,8 +734,8 @@ __device__ __forceinline__ Gp on_gemv_wgs(Gp g, int n_attn) {
 // then the final add + norm, lm_head and this workgroup's argmax words.
 // False when a hand-over wait gave up (the error word is then set).
 template <int D, int G>
-__device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, unsigned char* smem, float* s_red,
-                                                int* s_redi
+__device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t* lwt, uint32_t ep,
+                                                unsigned char* smem, float* s_red, int* s_redi, int* s_fail
 #ifdef EK_STEP_TRACE
                                                 , int64_t* ts_lds
 #endif
@@ -698,12 +760,12 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
   // norm gains, loaded a phase ahead of their use: gw1 = input norm of the
   // coming layer (the final norm after the last), gw2 = post-attention norm
   uint32_t gw1[NGW], gw2[NGW];
-  load_gain(reinterpret_cast<const bf16_t*>(a.lw[LW_LN1]), h, gw1);
+  load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
 
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
     EK_TS(0);
-    const int64_t* lw = a.lw + (int64_t)l * LW_FIELDS;
+    const int64_t* lw = lwt + l * LW_FIELDS;
     llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
     llw_t* att_ll = qkv_ll + qkvw / 2;           // HC copies of each region from here on
     llw_t* o_ll = att_ll + HC * (qw / 2);
@@ -736,7 +798,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
 #else
       const bool ok = ll_read(LinSrc{dn_prev + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
 #endif
-      if (!__syncthreads_and(ok)) return false;
+      if (!wg_all(ok, s_fail)) return false;
       add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
     }
     __syncthreads();
@@ -762,7 +824,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     {
       const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
       if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
-      if (!__syncthreads_and(ok)) return false;
+      if (!wg_all(ok, s_fail)) return false;
     }
     zero_pad(xs, qw, kpad_of(qw));
     EK_TS(6);
@@ -786,12 +848,12 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
 #else
       const bool ok = ll_read(LinSrc{o_ll + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
 #endif
-      if (!__syncthreads_and(ok)) return false;
+      if (!wg_all(ok, s_fail)) return false;
       EK_TS(17);
     }
     add_norm(rr, xs32, gw2, h, kpad_of(h), a.eps, xs, s_red);
     // the next input norm's gain loads with the gate/up stream
-    load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm,
+    load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm,
               h, gw1);
     __syncthreads();
     EK_TS(9);
@@ -815,7 +877,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
 #else
       const bool ok = ll_read(LinSrc{act_ll + cp * (inter / 2)}, inter / 2, ep, xs32, a.err, a.spin);
 #endif
-      if (!__syncthreads_and(ok)) return false;
+      if (!wg_all(ok, s_fail)) return false;
     }
     zero_pad(xs, inter, kpad_of(inter));
     __syncthreads();
@@ -826,7 +888,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
     epilogue_ll(gd, part, dn_ll, ep, HC, h / 2);
     EK_TS(14);
     if (l + 1 < a.nl)
-      prefetch_phase<PF>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(a.lw[(int64_t)(l + 1) * LW_FIELDS + LW_QKV]),
+      prefetch_phase<PF>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]),
                                          h, qkvw, 0, 2), n_attn), ring);
     else
       prefetch_phase<PF>(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
@@ -841,7 +903,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
   zero_part(part, part_n);
   {
     const bool ok = ll_read(LinSrc{dn_prev + my_copy() * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
-    if (!__syncthreads_and(ok)) return false;
+    if (!wg_all(ok, s_fail)) return false;
   }
   add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
   __syncthreads();
@@ -865,7 +927,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, uint32_t ep, 
 // the failure at this step's own row and every later row stays aligned.
 template <int D>
 __device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool ok, int64_t len_old,
-                                            unsigned char* smem, float* s_red, int* s_redi) {
+                                            unsigned char* smem, float* s_red, int* s_redi, int* s_fail) {
   const int tid = threadIdx.x;
   const int h = a.h;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
@@ -874,7 +936,7 @@ __device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool
   const llw_t* am_ll = a.arena + (int64_t)a.nl * arena_layer_words(h, a.inter, qkvw, qw);
   uint32_t* amw = reinterpret_cast<uint32_t*>(smem + step_rr_bytes(h) + eka::align16((size_t)a.kpad_max * 2));
   __syncthreads();
-  if (ok) ok = __syncthreads_and(ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, ep, amw, a.err, a.spin)) != 0;
+  if (ok) ok = wg_all(ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, ep, amw, a.err, a.spin), s_fail);
   float ov = 0.f;
   int oi = 0x7fffffff;
   if (ok) {
@@ -909,9 +971,13 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   __shared__ int s_redi[SNW];
   __shared__ unsigned s_ep;
   __shared__ int s_abort;
+  __shared__ int s_fail;
+  __shared__ int64_t s_lw[MAX_LAYERS * LW_FIELDS];   // the layer table, read from LDS in every phase
 
   const int tid = threadIdx.x;
+  for (int i = tid; i < a.nl * LW_FIELDS; i += SNT) s_lw[i] = a.lw[i];
   if (tid == 0) {
+    s_fail = 0;
     const unsigned e = __hip_atomic_load(&a.bar->ep[blockIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     __hip_atomic_store(&a.bar->ep[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_ep = e;
@@ -932,7 +998,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     if (aborted) return;
     int64_t hi = len_old + 1;
     hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
-    attention_loop<D, G>(a, ep, hi, smem
+    attention_loop<D, G>(a, s_lw, ep, hi, smem, &s_fail
 #ifdef EK_STEP_TRACE
                          , ts_lds
 #endif
@@ -941,13 +1007,13 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   }
   bool ok = !aborted;
   if (ok)
-    ok = projection_pass<D, G>(a, ep, smem, s_red, s_redi
+    ok = projection_pass<D, G>(a, s_lw, ep, smem, s_red, s_redi, &s_fail
 #ifdef EK_STEP_TRACE
                                , ts_lds
 #endif
                                );
   if ((int)blockIdx.x != n_attn) return;
-  finish_step<D>(a, ep, ok, len_old, smem, s_red, s_redi);
+  finish_step<D>(a, ep, ok, len_old, smem, s_red, s_redi, &s_fail);
 #ifdef EK_STEP_TRACE
   EK_TS(4);
   EK_TS_FLUSH_SYNC(a.nl);

@@ -16,8 +16,11 @@ static hipError_t launch_one(const StepArgs& a, int nwg, hipStream_t st) {
   static bool attr_done = false;   // allow more than 64 KiB of dynamic LDS (gfx950 has 160 KiB per CU)
   if (!attr_done) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<D, G>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
-    if (e != hipSuccess) return e;
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStepDynLds);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();   // do not leave the error for the next launch's check
+      return e;
+    }
     attr_done = true;
   }
   hipLaunchKernelGGL((step_kernel<D, G>), dim3(nwg), dim3(SNT), lds, st, a);
@@ -26,13 +29,18 @@ static hipError_t launch_one(const StepArgs& a, int nwg, hipStream_t st) {
 
 template <int D, int G>
 static int occupancy_one(size_t lds) {
+  // a failed query leaves no error behind for the next launch's check
   if (hipFuncSetAttribute(reinterpret_cast<const void*>(&step_kernel<D, G>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024) != hipSuccess)
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStepDynLds) != hipSuccess) {
+    (void)hipGetLastError();
     return 0;
+  }
   int n = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&step_kernel<D, G>), SNT, lds) !=
-      hipSuccess)
+      hipSuccess) {
+    (void)hipGetLastError();
     return 0;
+  }
   return n;
 }
 
