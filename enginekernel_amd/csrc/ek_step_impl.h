@@ -86,7 +86,7 @@ enum { LW_QKV = 0, LW_O, LW_GU, LW_DOWN, LW_LN1, LW_LN2, LW_QN, LW_KN, LW_KC, LW
 // launch state, zeroed once by the host
 struct Bar {
   unsigned ep[MAX_WG];   // per-workgroup launch epoch
-  int64_t* trace;        // -DEK_STEP_TRACE builds: per-phase timestamps [wg][layer][24]
+  int64_t* trace;        // -DEK_STEP_TRACE builds: per-phase timestamps [wg][layer][32]
   int64_t pad[7];
 };
 
@@ -135,11 +135,11 @@ __host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int voc
 
 // -DEK_STEP_TRACE builds stamp phase events into LDS (a global store would
 // delay the memory waits that follow it) and copy one layer's stamps to
-// bar->trace[wg][layer][24] at the layer's end.
+// bar->trace[wg][layer][32] at the layer's end.
 #ifdef EK_STEP_TRACE
 #define EK_TS(ev) do { if (threadIdx.x == 0) ts_lds[ev] = wall_clock64(); } while (0)
-#define EK_TS_FLUSH(layer) do { if (a.bar->trace && threadIdx.x < 24) \
-    a.bar->trace[((int64_t)blockIdx.x * 40 + (layer)) * 24 + threadIdx.x] = ts_lds[threadIdx.x]; } while (0)
+#define EK_TS_FLUSH(layer) do { if (a.bar->trace && threadIdx.x < 32) \
+    a.bar->trace[((int64_t)blockIdx.x * 40 + (layer)) * 32 + threadIdx.x] = ts_lds[threadIdx.x]; } while (0)
 #define EK_TS_FLUSH_SYNC(layer) do { __syncthreads(); EK_TS_FLUSH(layer); } while (0)
 #else
 #define EK_TS_FLUSH_SYNC(layer) do { } while (0)
@@ -801,6 +801,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       if (!wg_all(ok, s_fail)) return false;
       add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
     }
+    EK_TS(26);
     __syncthreads();
     EK_TS(1);
     gemv_phase(gq, ring, xs, part);
@@ -829,7 +830,9 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     zero_pad(xs, qw, kpad_of(qw));
     EK_TS(6);
     __syncthreads();
+    EK_TS(29);
     gemv_held_phase(go, ob, xs, part);
+    EK_TS(30);
     __syncthreads();
     EK_TS(7);
     epilogue_ll(go, part, o_ll, ep, HC, h / 2);
@@ -852,9 +855,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       EK_TS(17);
     }
     add_norm(rr, xs32, gw2, h, kpad_of(h), a.eps, xs, s_red);
+    EK_TS(24);
     // the next input norm's gain loads with the gate/up stream
     load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm,
               h, gw1);
+    EK_TS(25);
     __syncthreads();
     EK_TS(9);
     gemv_phase(gg, ring, xs, part);
@@ -863,6 +868,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     epilogue_swiglu_ll(gg, part, act_ll, ep, HC, inter / 2);
     EK_TS(11);
     prefetch_phase<PF>(gd, ring);
+    EK_TS(27);
 
     // ---- down projection
     __syncthreads();
@@ -986,7 +992,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     s_abort = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #ifdef EK_STEP_TRACE
-  __shared__ int64_t s_ts[24];
+  __shared__ int64_t s_ts[32];
   int64_t* ts_lds = s_ts;
 #endif
   __syncthreads();

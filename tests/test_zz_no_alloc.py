@@ -98,16 +98,18 @@ def test_noalloc_step_equals_the_arena_step(dev, call):
 
 def test_noalloc_rejects_an_arena_beyond_the_static_limit(dev):
     """A shape whose hand-over arena exceeds the static 16 MiB is refused
-    with an error before anything is launched (256 layers of the 4B shape
-    need about 25 MiB)."""
+    with an error before anything is launched (64 layers of hidden 4096,
+    64 query heads and intermediate 40960 need about 17 MiB); the step's
+    plan itself stops at 64 layers (its layer table is held in LDS)."""
     cfg = dict(C.QWEN3_4B)
-    plan = K.decode_step_plan(2560, 9728, 32, 8, 128, cfg["vocab_size"], 1, 64, 256)
+    assert K.decode_step_plan(2560, 9728, 32, 8, 128, cfg["vocab_size"], 1, 64, 65) is None
+    plan = K.decode_step_plan(4096, 40960, 64, 8, 128, cfg["vocab_size"], 1, 64, 64)
     assert plan is not None and plan[0] > 16 << 20
     lib = _hip.load()
     z = torch.zeros(64, dtype=torch.int64, device=dev)
     p = z.data_ptr()
-    rc = lib.ek_decode_step_noalloc(p, 256, 2560, 9728, 32, 8, 128, cfg["vocab_size"], 1, 1e-6, 0.088,
-                                    p, 2560, p, p, p, p, 128, 64, 0, 0, 128, 64,
+    rc = lib.ek_decode_step_noalloc(p, 64, 4096, 40960, 64, 8, 128, cfg["vocab_size"], 1, 1e-6, 0.088,
+                                    p, 4096, p, p, p, p, 128, 64, 0, 0, 128, 64,
                                     p, p, p, p, p, p, p, 8, p, 0, p, 0)
     assert rc != 0
     assert b"16 MiB" in lib.ek_last_error()
