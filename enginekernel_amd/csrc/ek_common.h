@@ -88,6 +88,26 @@ __device__ __forceinline__ float dpp_plus(float v) {
   const int moved = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false);
   return v + __int_as_float(moved);
 }
+// The same sum for N independent values, step by step across all of them
+// (each DPP step's result is needed two instructions later: interleaving the
+// N chains fills the waits that one chain alone spends in s_nop). The
+// totals are exact in lane 63; returns nothing, leaves them there.
+template <int N>
+__device__ __forceinline__ void wave_sums_dpp_lane63(float* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_plus<0xB1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_plus<0x4E>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_plus<0x124>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_plus<0x128>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_plus<0x142, 0xa>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = dpp_plus<0x143, 0xc>(v[i]);
+}
+
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = dpp_plus<0xB1>(v);        // quad_perm [1,0,3,2]
   v = dpp_plus<0x4E>(v);        // quad_perm [2,3,0,1]

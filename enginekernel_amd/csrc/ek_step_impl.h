@@ -322,18 +322,54 @@ __device__ __forceinline__ void prefetch_phase(const Gp& pn, Ring& ring) {
   ring.nready = CNT;
 }
 
-// The o projection's chunks: a wave's first OB items (all of them at the
-// Qwen3-4B shape), loaded into registers while attention runs and consumed
-// once its output arrives; items past OB (larger shapes) load one by one.
+// The o projection's chunks, loaded into registers while attention runs and
+// consumed once its output arrives. When a row is exactly SNW chunks long
+// and the workgroup's rows fit the OB registers (the Qwen3-4B shape: 4096 /
+// 512 = 8 chunks, at most 12 rows), wave w holds chunk w of every row
+// ("by column"): its products then need one activation chunk from LDS
+// instead of one per item, and its rows' sums run as one interleaved DPP
+// reduction. Otherwise a wave holds its first OB items (row-major order)
+// and items past OB (larger shapes) load one by one.
+__device__ __forceinline__ bool held_by_column(const Gp& P, int& u0, int& nr) {
+  int u1;
+  unit_range(P, u0, u1);
+  nr = u1 - u0;
+  return !P.pair && P.C == SNW && nr <= OB;
+}
+
 __device__ __forceinline__ void hold_phase(const Gp& P, uint4* ob) {
-  const Span sn = make_span(P, wave_id());
   const int loff = (threadIdx.x & 63) * 8;
+  int u0, nr;
+  if (held_by_column(P, u0, nr)) {
+    const bf16_t* col = P.w + (int64_t)u0 * P.K + wave_id() * CH + loff;
+#pragma unroll
+    for (int u = 0; u < OB; ++u) ob[u] = ld16_nt(col + (int64_t)(u < nr ? u : 0) * P.K);
+    return;
+  }
+  const Span sn = make_span(P, wave_id());
 #pragma unroll
   for (int u = 0; u < OB; ++u) ob[u] = ld16_nt(span_item(sn, sn.i0 + (u < sn.n ? u : 0)) + loff);
 }
 
 __device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, const bf16_t* xs, float* part) {
   const int lane = threadIdx.x & 63, wave = wave_id();
+  {
+    int u0, nr;
+    if (held_by_column(P, u0, nr)) {
+      // row u's partial over chunk `wave` -> part[u * SNW + wave]
+      const uint4 xw = *reinterpret_cast<const uint4*>(xs + wave * CH + lane * 8);
+      float acc[OB];
+#pragma unroll
+      for (int u = 0; u < OB; ++u) acc[u] = step_dot8(ob[u], xw, 0.f);
+      wave_sums_dpp_lane63<OB>(acc);
+      if (lane == 63) {
+#pragma unroll
+        for (int u = 0; u < OB; ++u)
+          if (u < nr) part[u * SNW + wave] = acc[u];
+      }
+      return;
+    }
+  }
   const Span sp = make_span(P, wave);
   const int n = sp.n;
   const int loff = lane * 8;
@@ -382,6 +418,7 @@ __device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, co
 #define EK_STEP_L2T 8
 #endif
 constexpr int L2T = EK_STEP_L2T;
+
 __device__ __forceinline__ void l2_touch(const Gp& pn, uint32_t& sink) {
   const Span sn = make_span(pn, wave_id());
   const int lane = threadIdx.x & 63;
