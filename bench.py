@@ -48,9 +48,9 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 #   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
 GATE_UP_TRAFFIC_B1 = 100_153_865
 #   the persistent step kernel (step_kernel<128, 4>) at batch 1, context 137..146:
-#   3,973,974 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.009x its
+#   3,975,233 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.010x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_142_155_000
+STEP_TRAFFIC_B1 = 8_144_734_072
 
 
 def log(msg: str) -> None:
@@ -216,6 +216,29 @@ def cpu_baseline(tensors, cfg, kv, first_tok, positions, s, gpu_tokens, budget_s
     }
 
 
+def cpu_config1():
+    """BASELINE config 1 end to end on the CPU oracle: the tiny random-init
+    Qwen3 (seed 0), three left-padded prompts of 5 / 9 / 16 ids (seed 1),
+    32 greedy tokens (prefill + 31 decode steps), timed whole."""
+    import torch
+    from enginekernel_amd import checkpoint as C
+    from oracle import ek_oracle as O
+
+    cfg = dict(C.QWEN3_TINY)
+    tensors = C.random_weights(cfg, seed=0)
+    g = torch.Generator().manual_seed(1)
+    prompts = [torch.randint(0, cfg["vocab_size"], (n,), generator=g).tolist() for n in (5, 9, 16)]
+    om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
+    with torch.inference_mode():
+        list(O.generate_eager(om, prompts, 4))          # warm-up
+        t0 = time.perf_counter()
+        out = list(O.generate_eager(om, prompts, 32))
+        dt = time.perf_counter() - t0
+    return {"config1_ms": round(dt * 1e3, 2), "config1_tokens_per_s": round(3 * len(out) / dt, 1),
+            "config1_sample": "BASELINE config 1 whole: tiny Qwen3, 3 left-padded prompts (5/9/16), 32 greedy "
+                              "tokens each (prefill + 31 decode steps), torch CPU oracle"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,13 +342,14 @@ def main():
             kv = ([t[0:1, :, :n_kv].cpu().clone() for t in eng.k_cache],
                   [t[0:1, :, :n_kv].cpu().clone() for t in eng.v_cache])
             # the caches the oracle extends need room for the sampled steps
-            room = 64
+            room = 65   # 64 timed steps after one warm-up step
             kv = ([torch.cat([t, torch.zeros(1, t.shape[1], room, t.shape[3], dtype=t.dtype)], 2) for t in kv[0]],
                   [torch.cat([t, torch.zeros(1, t.shape[1], room, t.shape[3], dtype=t.dtype)], 2) for t in kv[1]])
             log("timing the CPU oracle baseline")
             # GPU step 1 decoded token `first` at context s+1 and emitted tokens[0]
             cpu = cpu_baseline(tensors, cfg, kv, first.cpu(), torch.tensor([s], dtype=torch.int64), s,
                                tokens[:room], budget_s=args.cpu_budget)
+            cpu.update(cpu_config1())
 
     achieved = dom_bytes / dom_s
     line = {
