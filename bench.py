@@ -300,6 +300,7 @@ def main():
     with torch.inference_mode():
         ids, pos, pad, s, bias = eng._pack(prompt)
         eng._ensure_cache(b, total)
+        model.ensure_rope(total + 1)
         t0 = time.perf_counter()
         graph = eng._get_graph(b, total)
         log(f"graph captured in {time.perf_counter() - t0:.1f}s (bucket {graph.bucket})")
@@ -329,7 +330,11 @@ def main():
             # one kernel per replay: its launch time is the replay time
             ctx_avg = s + W + 1 + (K_steps - 1) / 2
             dom_s, dom_bytes, dom_n = step_s, step_bytes(cfg, ctx_avg), K_steps
-            dom_name, dom_traffic = "eks::step_kernel<128,4> (the whole decode step, one launch)", STEP_TRAFFIC_B1
+            split = model.persistent_plan(b, graph.bucket)[1]
+            dom_name = (f"eks::step_kernel<128,4,{'true' if split else 'false'}> (the whole decode step, one launch"
+                        + (f"; every workgroup attends 1/{split} of a kv head's keys)" if split else ")"))
+            # the PMC figure is for the default workload only
+            dom_traffic = STEP_TRAFFIC_B1 if (not split and args.prompt == 128 and not args.layers) else None
         else:
             dom_s, dom_bytes, dom_n = time_dominant_kernel(model, b)
             dom_name = "gemv_kernel<PRO_PARTS,EPI_SWIGLU> (add+RMSNorm+gate_up+SwiGLU)"

@@ -110,9 +110,17 @@ def random_weights(cfg: dict, seed: int = 0, std: float = 0.02,
     else:
         prev = torch.get_num_threads()
         torch.set_num_threads(1)     # one chunk per pool thread
+        # inference mode is per thread: the pool's threads take the caller's,
+        # or they could not write tensors the caller made under it
+        inference = torch.is_inference_mode_enabled()
+
+        def fill(j):
+            with torch.inference_mode(inference):
+                _fill(j[0], seed, j[1], j[2], std)
+
         try:
             with _cf.ThreadPoolExecutor(threads) as ex:
-                list(ex.map(lambda j: _fill(j[0], seed, j[1], j[2], std), jobs))
+                list(ex.map(fill, jobs))
         finally:
             torch.set_num_threads(prev)
     if cfg.get("tie_word_embeddings", False):

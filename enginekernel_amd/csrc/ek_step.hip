@@ -13,9 +13,9 @@ namespace eks {
 template <> hipError_t launch_step<32>(const StepArgs&, int, int, hipStream_t);
 template <> hipError_t launch_step<64>(const StepArgs&, int, int, hipStream_t);
 template <> hipError_t launch_step<128>(const StepArgs&, int, int, hipStream_t);
-template <> int step_occupancy<32>(int, size_t);
-template <> int step_occupancy<64>(int, size_t);
-template <> int step_occupancy<128>(int, size_t);
+template <> int step_occupancy<32>(int, bool, size_t);
+template <> int step_occupancy<64>(int, bool, size_t);
+template <> int step_occupancy<128>(int, bool, size_t);
 }  // namespace eks
 
 // The no-allocation entry point's state: the launch-state block (Bar,
@@ -48,9 +48,25 @@ int step_grid() {
 
 struct Plan {
   int nwg, kpad_max, part_max, o_rows;
+  int lsplit, lchunk;   // long contexts: key splits per kv head and keys per split (0: the attention-unit kernel)
+  int64_t lx;           // long contexts: hand-over words of the splits' exchange
   int64_t arena_bytes;
   size_t lds;
 };
+
+template <int D>
+size_t long_lds_d(int g, int64_t chunk) {
+  switch (g) {
+    case 1: return eks::LongLds<D, 1>::bytes(chunk);
+    case 2: return eks::LongLds<D, 2>::bytes(chunk);
+    case 4: return eks::LongLds<D, 4>::bytes(chunk);
+    default: return eks::LongLds<D, 8>::bytes(chunk);
+  }
+}
+
+size_t long_lds(int d, int g, int64_t chunk) {
+  return d == 32 ? long_lds_d<32>(g, chunk) : d == 64 ? long_lds_d<64>(g, chunk) : long_lds_d<128>(g, chunk);
+}
 
 size_t attn_lds(int d, int g, int64_t s_cap) {
   size_t attn = eka::align16((size_t)(g + 6) * d * 2) + eka::align16((size_t)g * (s_cap | 1) * 4);   // AttnLds
@@ -62,18 +78,18 @@ size_t attn_lds(int d, int g, int64_t s_cap) {
 
 // Workgroups of step_kernel<d, g> with `lds` bytes of dynamic LDS that one CU
 // holds at once (the occupancy query, cached per instantiation and size).
-int resident_per_cu(int d, int g, size_t lds) {
+int resident_per_cu(int d, int g, bool lng, size_t lds) {
   static std::mutex mu;
-  static std::map<std::tuple<int, int, size_t>, int> cache;
-  const auto key = std::make_tuple(d, g, lds);
+  static std::map<std::tuple<int, int, bool, size_t>, int> cache;
+  const auto key = std::make_tuple(d, g, lng, lds);
   std::lock_guard<std::mutex> lock(mu);
   auto it = cache.find(key);
   if (it != cache.end()) return it->second;
   int n = 0;
   switch (d) {
-    case 32: n = eks::step_occupancy<32>(g, lds); break;
-    case 64: n = eks::step_occupancy<64>(g, lds); break;
-    default: n = eks::step_occupancy<128>(g, lds); break;
+    case 32: n = eks::step_occupancy<32>(g, lng, lds); break;
+    case 64: n = eks::step_occupancy<64>(g, lng, lds); break;
+    default: n = eks::step_occupancy<128>(g, lng, lds); break;
   }
   cache[key] = n;
   return n;
@@ -98,11 +114,29 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
     return ek_fail(hipErrorInvalidValue, "decode_step: hidden must be at most 4096");
   if (hidden > (1 << 20) || inter > (1 << 20) || vocab > (1 << 30) || n_q * head_dim > (1 << 20))
     return ek_fail(hipErrorInvalidValue, "decode_step: sizes too large");
-  if (s_cap < 1 || g * s_cap * 4 > kFusedScoreLds)
-    return ek_fail(hipErrorInvalidValue, "decode_step: the attention row does not fit in LDS (use the per-kernel step)");
+  if (s_cap < 1) return ek_fail(hipErrorInvalidValue, "decode_step: empty cache");
   p.nwg = step_grid();
   if (p.nwg < 1 || p.nwg > eks::MAX_WG) return ek_fail(hipErrorInvalidValue, "decode_step: unsupported device");
-  const int n_attn = (int)(n_kv * (head_dim / eka::FDC));
+  // Rows whose scores fit one attention unit's LDS run on attention-only
+  // workgroups beside the projections; longer ones on every workgroup, the
+  // keys of each kv head split S ways (S a power of two, at most 64 and at
+  // most head_dim / 2, so that each split owns an even number of head dims
+  // of the combined output)
+  p.lsplit = p.lchunk = 0;
+  p.lx = 0;
+  if (g * s_cap * 4 > kFusedScoreLds) {
+    int sp = 1;
+    while (2 * sp <= 64 && 2 * sp <= head_dim / 2 && 2 * sp * n_kv <= p.nwg) sp *= 2;
+    if (sp < 2) return ek_fail(hipErrorInvalidValue, "decode_step: too few workgroups for the long-context split");
+    const int64_t chunk = (s_cap + sp - 1) / sp;
+    if (chunk > (1 << 16))
+      return ek_fail(hipErrorInvalidValue, "decode_step: the context's score rows exceed the LDS of the long-context split");
+    p.lsplit = sp;
+    p.lchunk = (int)chunk;
+    p.lx = eks::long_words((int)n_kv, sp, (int)g, (int)head_dim);
+  }
+  const bool lng = p.lsplit > 0;
+  const int n_attn = lng ? 0 : (int)(n_kv * (head_dim / eka::FDC));
   if (4 * n_attn > p.nwg) return ek_fail(hipErrorInvalidValue, "decode_step: too many attention units for the grid");
   const int qw = (int)(n_q * head_dim), qkvw = (int)((n_q + 2 * n_kv) * head_dim);
   int kmax = (int)hidden;
@@ -114,14 +148,17 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   p.part_max = eks::part_rows_max((int)hidden, (int)inter, qkvw, (int)vocab, n_gemv, p.o_rows);
   const size_t gemv = eks::step_rr_bytes((int)hidden) + eka::align16((size_t)p.kpad_max * 2) +
                       eka::align16((size_t)p.part_max * eks::SNW * 4);
-  const size_t attn = attn_lds((int)head_dim, (int)g, s_cap);
+  const size_t attn = lng ? eks::step_rr_bytes((int)hidden) + long_lds((int)head_dim, (int)g, p.lchunk)
+                          : attn_lds((int)head_dim, (int)g, s_cap);
   p.lds = gemv > attn ? gemv : attn;
-  if (p.lds > kLdsLimit) return ek_fail(hipErrorInvalidValue, "decode_step: LDS plan exceeds the workgroup limit");
-  p.arena_bytes = 8 * eks::arena_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg);
+  if (p.lds > kLdsLimit)
+    return ek_fail(hipErrorInvalidValue, lng ? "decode_step: the context's score rows exceed the LDS of the long-context split"
+                                             : "decode_step: LDS plan exceeds the workgroup limit");
+  p.arena_bytes = 8 * eks::arena_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg, p.lx);
   // every workgroup must be resident at once (the hand-over waits of one
   // need the others running): at least one workgroup of this instantiation,
   // with this LDS, per CU -- registers, scratch and LDS all counted
-  if (resident_per_cu((int)head_dim, (int)g, p.lds) < 1)
+  if (resident_per_cu((int)head_dim, (int)g, lng, p.lds) < 1)
     return ek_fail(hipErrorInvalidValue, "decode_step: one workgroup per CU does not fit (registers or LDS)");
   return hipSuccess;
 }
@@ -187,6 +224,7 @@ hipError_t decode_step_impl(const int64_t* layer_ptrs, int64_t n_layers, int64_t
   a.arena = (eks::llw_t*)arena;
   a.bar = (eks::Bar*)barrier; a.err = err; a.spin = ek_wait_limit(kSpin);
   a.kpad_max = p.kpad_max; a.part_max = p.part_max; a.o_rows = p.o_rows;
+  a.lsplit = p.lsplit; a.lchunk = p.lchunk; a.lx = p.lx;
   const int g = (int)(n_q / n_kv);
   switch (head_dim) {
     case 32: return eks::launch_step<32>(a, g, p.nwg, st);
@@ -207,7 +245,7 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
   if (e != hipSuccess) return e;
   if (sizes) {
     sizes[0] = p.arena_bytes;
-    sizes[1] = 0;
+    sizes[1] = p.lsplit;
     sizes[2] = (int64_t)sizeof(eks::Bar);
     sizes[3] = p.nwg;
   }

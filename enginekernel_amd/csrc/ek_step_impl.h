@@ -104,6 +104,12 @@ struct StepArgs {
   llw_t* arena;
   Bar* bar; int* err; int64_t spin;
   int kpad_max, part_max, o_rows;      // LDS plan (host-computed, see make_plan in ek_step.hip)
+  // long contexts (kernels with LONG set): every workgroup runs attention unit
+  // (kv head w % nkv, key split w / nkv) of lsplit splits of at most lchunk keys;
+  // lx hand-over words after the argmax words hold the splits' statistics and
+  // partial outputs (one region for every layer: its words carry the layer in their tag)
+  int lsplit, lchunk;
+  int64_t lx;
 };
 
 __host__ __device__ constexpr int cdiv_i(int a, int b) { return (a + b - 1) / b; }
@@ -117,9 +123,15 @@ __host__ __device__ inline int64_t arena_layer_words(int h, int inter, int qkvw,
 
 // this workgroup's copy of an all-to-all region
 __device__ __forceinline__ int my_copy() { return (int)blockIdx.x % HC; }
-// the whole arena: every layer, then two argmax words per workgroup
-__host__ __device__ inline int64_t arena_words(int nl, int h, int inter, int qkvw, int qw, int nwg) {
-  return nl * arena_layer_words(h, inter, qkvw, qw) + 2 * (int64_t)nwg;
+// long-context mode's exchange words: (max, sum) per query head of every
+// split, then every split's partial output
+__host__ __device__ inline int64_t long_words(int nkv, int splits, int g, int d) {
+  return (int64_t)nkv * splits * (2 * g + g * d);
+}
+// the whole arena: every layer, two argmax words per workgroup, then the
+// long-context exchange (lx words, 0 for the attention-unit kernel)
+__host__ __device__ inline int64_t arena_words(int nl, int h, int inter, int qkvw, int qw, int nwg, int64_t lx = 0) {
+  return nl * arena_layer_words(h, inter, qkvw, qw) + 2 * (int64_t)nwg + lx;
 }
 
 // rows of one workgroup's largest phase share (units in pairs, or single
@@ -722,7 +734,324 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 }
 
 // ---------------------------------------------------------------------------
-// the step
+// long contexts: the attention phase on every workgroup
+// ---------------------------------------------------------------------------
+// Beyond the score row one attention workgroup holds in LDS, every workgroup
+// takes part in attention: unit (kv head h, split s) = workgroup h + nkv * s
+// attends the keys [k0, k1) = [lo + s c, lo + (s + 1) c) of its row's range
+// [lo, hi), c = ceil((hi - lo) / S):
+//   scores   QK-norm + RoPE of the G query heads (and of the new key, which
+//            stands in for the cache row at the new slot), S^T = K_tile . Q^T
+//            per 16-key tile on the matrix cores, scaled, into an LDS row per
+//            head; the split's max m_s and sum l_s = sum exp(s - m_s) per head
+//   stats    every split's (m_s, l_s) of the head travel as tagged words
+//            (tag: the launch epoch and the layer, since every layer reuses
+//            the region: a layer's words are overwritten only by a workgroup
+//            past that layer's o projection wait, which needs every unit's
+//            combine, hence every read of them, done), so
+//            that every unit forms the same M = max m_s and
+//            L = sum_s l_s exp(m_s - M) (in split order)
+//   PV       p = bf16(exp(s - M) / L), the reference fallback's rounding point
+//            (engine/ek_model.py:475-488), and the split's partial output
+//            sum p v over its keys for all head dims, in fp32
+//   combine  unit s owns head dims [s D/S, (s+1) D/S) of the G query heads:
+//            it adds the S splits' partials of those dims in split order and
+//            stores them as the bf16 attention words the o projection awaits.
+// The split holding the new slot stores the new key and value rows last.
+template <int D, int G>
+struct LongLds {
+  static constexpr size_t HEADS = eka::align16((size_t)(G + 2) * D * 2);   // raw q heads, new k, new v (bf16)
+  static constexpr size_t ROPE = eka::align16((size_t)4 * D * 2);          // q gain, k gain, cos, sin
+  static constexpr size_t QS = eka::align16((size_t)G * D * 4);            // normed, rotated q (fp32)
+  static constexpr size_t KNF = eka::align16((size_t)D * 4);               // the new key (fp32)
+  static constexpr size_t KNB = eka::align16((size_t)D * 2);               // the new key (bf16)
+  static constexpr size_t ST = eka::align16((size_t)SNW * 8 * 4);          // per-wave max / sum
+  static constexpr size_t RED = eka::align16((size_t)SNW * G * D * 4);     // per-wave partial outputs
+  static constexpr size_t SPL = eka::align16((size_t)64 * 2 * G * 4);      // every split's (m, l): up to 64 splits
+  static constexpr size_t CMB = eka::align16((size_t)G * D * 4);           // the combine's words
+  static __host__ __device__ constexpr int64_t stride(int64_t chunk) { return chunk | 1; }
+  static __host__ __device__ constexpr size_t bytes(int64_t chunk) {
+    return HEADS + ROPE + QS + KNF + KNB + 2 * ST + RED + SPL + CMB + eka::align16((size_t)G * stride(chunk) * 4);
+  }
+};
+
+template <int D, int G>
+__device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
+                                               llw_t* lx, int64_t hi, uint32_t ep, uint32_t ltag, unsigned char* lds,
+                                               int* s_fail) {
+  using L = LongLds<D, G>;
+  constexpr int KS = D / 32;       // 32-dim k-steps of a score tile
+  constexpr int UT = 2;            // 16-key score tiles per wave per group
+  constexpr int DCH = D / 8;       // 16-byte chunks per key row
+  constexpr int NKG = SNT / DCH;   // key groups of the PV product
+  const int S = a.lsplit;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int r16 = lane & 15, q4 = lane >> 4;
+  const int h = (int)blockIdx.x % a.nkv, s = (int)blockIdx.x / a.nkv;
+  if (s >= S) return true;
+  const int hw = D / 2, dpu = D / S;   // dims this unit combines
+
+  bf16_t* heads = reinterpret_cast<bf16_t*>(lds);
+  bf16_t* rope = reinterpret_cast<bf16_t*>(lds + L::HEADS);
+  float (*qs)[D] = reinterpret_cast<float (*)[D]>(lds + L::HEADS + L::ROPE);
+  float* knf = reinterpret_cast<float*>(lds + L::HEADS + L::ROPE + L::QS);
+  bf16_t* knew_bf = reinterpret_cast<bf16_t*>(lds + L::HEADS + L::ROPE + L::QS + L::KNF);
+  unsigned char* p0 = lds + L::HEADS + L::ROPE + L::QS + L::KNF + L::KNB;
+  float (*stm)[8] = reinterpret_cast<float (*)[8]>(p0);
+  float (*stl)[8] = reinterpret_cast<float (*)[8]>(p0 + L::ST);
+  float* red = reinterpret_cast<float*>(p0 + 2 * L::ST);                  // [SNW][G][D]
+  float* spl = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED);         // [S][2G]
+  float* cmb = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::SPL);   // [S][G][dpu]
+  float* sc = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::SPL + L::CMB);   // [G][stride]
+  const int64_t cstride = L::stride(a.lchunk);
+
+  int64_t lo = a.start_t[0];
+  lo = lo < 0 ? 0 : lo;
+  const int64_t nrel = hi > lo ? hi - lo : 0;
+  const int64_t chunk = (nrel + S - 1) / S;   // <= a.lchunk (the plan's bound on the bucket)
+  const int64_t k0 = lo + (int64_t)s * chunk;
+  int64_t k1 = k0 + chunk;
+  k1 = k1 < hi ? k1 : hi;
+  const int64_t nk = k1 > k0 ? k1 - k0 : 0;
+  const int64_t slot = hi - 1;
+  const bool own = nk > 0 && slot >= k0 && slot < k1;
+  // loads past the split's keys (the last tiles' tails, an empty split) read
+  // row `last` instead: k0 itself may lie past the cache's last row
+  const int64_t last = slot > 0 ? slot : 0;
+  const bf16_t* kc = reinterpret_cast<const bf16_t*>(lw[LW_KC]) + h * a.csh;
+  const bf16_t* vc = reinterpret_cast<const bf16_t*>(lw[LW_VC]) + h * a.csh;
+
+  // the first key tiles load before the heads are awaited (they do not
+  // depend on them); lane holds key r16 of a tile, dims 32 i + 8 q4 .. +7
+  const int64_t ntile = (nk + 15) >> 4;
+  uint4 kt[UT][KS];
+  auto load_group = [&](int64_t t0) {
+#pragma unroll
+    for (int u = 0; u < UT; ++u) {
+      const int64_t rel = ((t0 + u * SNW) << 4) + r16;
+      const bool ok = rel < nk && k0 + rel != slot;
+      const int64_t key = rel < nk ? k0 + rel : last;
+#pragma unroll
+      for (int i = 0; i < KS; ++i) {
+        const uint4 v = ld16_nt(kc + key * a.css + 32 * i + 8 * q4);
+        kt[u][i] = ok ? v : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  load_group(wave);
+
+  // the unit's q heads, new key and new value, and the gains / cos / sin rows
+  {
+    const bf16_t* qn = reinterpret_cast<const bf16_t*>(lw[LW_QN]);
+    const bf16_t* kn = reinterpret_cast<const bf16_t*>(lw[LW_KN]);
+    int64_t crow = a.positions[0];
+    crow = crow < 0 ? 0 : (crow >= a.rope_len ? a.rope_len - 1 : crow);
+    const bf16_t* cr = a.cos + crow * a.ld_cs;
+    const bf16_t* sr = a.sin + crow * a.ld_cs;
+    for (int i = tid; i < 4 * D; i += SNT) {
+      const int t = i / D, d = i - t * D;
+      rope[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
+    }
+    struct Src {
+      const llw_t* p; int hw, g, qbase, kbase, vbase;
+      __device__ const llw_t* operator()(int i) const {
+        return p + (i < g * hw ? qbase + i : (i < (g + 1) * hw ? kbase + i - g * hw : vbase + i - (g + 1) * hw));
+      }
+    } src{qkv, hw, G, h * G * hw, (a.nq + h) * hw, (a.nq + a.nkv + h) * hw};
+    const bool ok = ll_read<2>(src, (G + 2) * hw, ep, reinterpret_cast<uint32_t*>(heads), a.err, a.spin);
+    if (!wg_all(ok, s_fail)) return false;
+  }
+  // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
+  for (int u = wave; u <= G; u += SNW) {
+    if (u < G) eka::head_norm_rope<D>(heads + u * D, rope, rope + 2 * D, rope + 3 * D, a.eps, qs[u], nullptr);
+    else eka::head_norm_rope<D>(heads + G * D, rope + D, rope + 2 * D, rope + 3 * D, a.eps, knf, knew_bf);
+  }
+  __syncthreads();
+
+  // ---- scores. B operand = Q^T: q[g = r16][32 i + 8 q4 .. +7], zero for g >= G
+  uint4 qb[KS];
+  {
+    const uint32_t qmask = r16 < G ? 0xffffffffu : 0u;
+    const int g = r16 < G ? r16 : 0;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int dd = 32 * i + 8 * q4 + 2 * e;
+        w[e] = (f2bf(qs[g][dd]) | (f2bf(qs[g][dd + 1]) << 16)) & qmask;
+      }
+      qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  float mrun = -INFINITY;
+  for (int64_t t0 = wave; t0 < ntile; t0 += (int64_t)SNW * UT) {
+    if (t0 != wave) load_group(t0);
+#pragma unroll
+    for (int u = 0; u < UT; ++u) {
+      const int64_t tb = (t0 + u * SNW) << 4;
+      if (tb >= nk) break;
+      if (own && k0 + tb + r16 == slot) {   // the new key, from LDS
+#pragma unroll
+        for (int i = 0; i < KS; ++i) kt[u][i] = *reinterpret_cast<const uint4*>(&knew_bf[32 * i + 8 * q4]);
+      }
+      eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < KS; ++i) c = eka::mfma16x16x32(kt[u][i], qb[i], c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t rel = tb + 4 * q4 + e;
+        const float sv = c[e] * a.sm_scale;
+        const bool ok = r16 < G && rel < nk;
+        if (ok) sc[r16 * cstride + rel] = sv;
+        mrun = ok ? fmaxf(mrun, sv) : mrun;
+      }
+    }
+  }
+  mrun = fmaxf(mrun, __shfl_xor(mrun, 16, EK_WAVE));
+  mrun = fmaxf(mrun, __shfl_xor(mrun, 32, EK_WAVE));
+  if (q4 == 0 && r16 < G) stm[wave][r16] = mrun;
+  __syncthreads();
+
+  // ---- the split's (max, sum of exp) per head: thread -> head tid % G
+  llw_t* st_ll = lx;                                          // [nkv][S][2G]
+  llw_t* pt_ll = lx + (int64_t)a.nkv * S * 2 * G;             // [nkv][S][G][D]
+  {
+    const int g = tid % G;
+    float ms = stm[0][g];
+#pragma unroll
+    for (int w = 1; w < SNW; ++w) ms = fmaxf(ms, stm[w][g]);
+    float ls = 0.f;
+    for (int64_t n = tid / G; n < nk; n += SNT / G) ls += expf(sc[g * cstride + n] - ms);
+#pragma unroll
+    for (int o = G; o < EK_WAVE; o <<= 1) ls += __shfl_xor(ls, o, EK_WAVE);
+    if (lane < G) stl[wave][lane] = ls;
+    __syncthreads();
+    if (tid < G) {
+      float lt = 0.f;
+#pragma unroll
+      for (int w = 0; w < SNW; ++w) lt += stl[w][tid];
+      llw_t* my = st_ll + ((int64_t)h * S + s) * 2 * G;
+      ll_put(my + 2 * tid, __float_as_uint(ms), ltag);
+      ll_put(my + 2 * tid + 1, __float_as_uint(lt), ltag);
+    }
+  }
+  // every split's statistics of this head -> M, L, then p = bf16(exp(s - M) / L)
+  {
+    const bool ok = ll_read(LinSrc{st_ll + (int64_t)h * S * 2 * G}, S * 2 * G, ltag, reinterpret_cast<uint32_t*>(spl),
+                            a.err, a.spin);
+    if (!wg_all(ok, s_fail)) return false;
+    const int g = tid % G;
+    float M = -INFINITY;
+    for (int j = 0; j < S; ++j) M = fmaxf(M, spl[j * 2 * G + 2 * g]);
+    float Ls = 0.f;
+    for (int j = 0; j < S; ++j) {
+      const float mj = spl[j * 2 * G + 2 * g];
+      Ls += mj == -INFINITY ? 0.f : spl[j * 2 * G + 2 * g + 1] * expf(mj - M);
+    }
+    for (int64_t n = tid / G; n < nk; n += SNT / G) sc[g * cstride + n] = rbf(expf(sc[g * cstride + n] - M) / Ls);
+  }
+  __syncthreads();
+
+  // ---- PV: thread -> head dims 8 dc .. +7 of keys kg, kg + NKG, ... (16-byte
+  // value loads, lane-contiguous across a key row), 8 loads in flight
+  {
+    const int dc = tid % DCH, kg = tid / DCH;
+    float acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    const int64_t nper = nk > kg ? (nk - kg + NKG - 1) / NKG : 0;
+    const uint4 vnew = *reinterpret_cast<const uint4*>(heads + (G + 1) * D + 8 * dc);
+    auto vaddr = [&](int64_t j) {
+      const int64_t key = j < nper ? k0 + kg + NKG * j : last;
+      return vc + key * a.css + 8 * dc;
+    };
+    constexpr int VR = 4;
+    uint4 vr[VR];
+#pragma unroll
+    for (int u = 0; u < VR; ++u) vr[u] = ld16_nt(vaddr(u));
+    auto use = [&](const uint4& vv, int64_t j) {
+      const int64_t n = kg + NKG * j;
+      const uint4 v = (own && k0 + n == slot) ? vnew : vv;
+      float vf[8];
+      unpack8(v, vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pg = sc[g * cstride + n];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg, vf[e], acc[g][e]);
+      }
+    };
+    int64_t j0 = 0;
+    for (; j0 + VR <= nper; j0 += VR) {
+#pragma unroll
+      for (int u = 0; u < VR; ++u) {
+        const uint4 v = vr[u];
+        vr[u] = ld16_nt(vaddr(j0 + u + VR));
+        use(v, j0 + u);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < VR; ++u)
+      if (j0 + u < nper) use(vr[u], j0 + u);
+    // key groups with the same dims: lanes dc, dc + DCH, ... of the wave, then the waves
+#pragma unroll
+    for (int o = DCH; o < EK_WAVE; o <<= 1)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, EK_WAVE);
+    if (lane < DCH) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[(wave * G + g) * D + 8 * dc + e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+  // the split's partial output -> tagged words
+  for (int i = tid; i < G * D; i += SNT) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < SNW; ++w) t += red[w * G * D + i];
+    ll_put(pt_ll + ((int64_t)h * S + s) * G * D + i, __float_as_uint(t), ltag);
+  }
+  // ---- combine this unit's dims [s dpu, (s+1) dpu) of every query head
+  {
+    struct Src {   // word i = (split j, head g, dim dd) of this unit's dims
+      const llw_t* p; int ng, hd, dpu, d0;
+      __device__ const llw_t* operator()(int i) const {
+        const int j = i / (ng * dpu), r = i - j * (ng * dpu), g = r / dpu, dd = r - g * dpu;
+        return p + ((int64_t)j * ng + g) * hd + d0 + dd;
+      }
+    } src{pt_ll + (int64_t)h * S * G * D, G, D, dpu, s * dpu};
+    const bool ok = ll_read(src, S * G * dpu, ltag, reinterpret_cast<uint32_t*>(cmb), a.err, a.spin);
+    if (!wg_all(ok, s_fail)) return false;
+    for (int i = tid; i < G * dpu / 2; i += SNT) {
+      const int g = (2 * i) / dpu, dd = 2 * i - g * dpu;
+      float t0 = 0.f, t1 = 0.f;
+      for (int j = 0; j < S; ++j) {
+        t0 += cmb[(j * G + g) * dpu + dd];
+        t1 += cmb[(j * G + g) * dpu + dd + 1];
+      }
+      for (int c = 0; c < HC; ++c)
+        ll_put(att + (int64_t)c * (a.nq * D / 2) + ((int64_t)(h * G + g) * D + s * dpu + dd) / 2, pack2(t0, t1), ep);
+    }
+  }
+  // the new key and value rows (normed and rotated key, raw value)
+  if (own && wave == SNW - 1) {
+    bf16_t* kdst = const_cast<bf16_t*>(kc) + slot * a.css;
+    bf16_t* vdst = const_cast<bf16_t*>(vc) + slot * a.css;
+    for (int d = lane; d < D; d += EK_WAVE) {
+      kdst[d] = knew_bf[d];
+      vdst[d] = heads[(G + 1) * D + d];
+    }
+  }
+  return true;
+}
+
 // ---------------------------------------------------------------------------
 // the step
 // ---------------------------------------------------------------------------
@@ -770,8 +1099,8 @@ __device__ __forceinline__ Gp on_gemv_wgs(Gp g, int n_attn) {
 // The projection workgroups' part of the step: every layer's projections,
 // then the final add + norm, lm_head and this workgroup's argmax words.
 // False when a hand-over wait gave up (the error word is then set).
-template <int D, int G>
-__device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t* lwt, uint32_t ep,
+template <int D, int G, bool LONG>
+__device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t* lwt, uint32_t ep, int64_t hi,
                                                 unsigned char* smem, float* s_red, int* s_redi, int* s_fail
 #ifdef EK_STEP_TRACE
                                                 , int64_t* ts_lds
@@ -781,7 +1110,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   const int h = a.h, inter = a.inter;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = arena_layer_words(h, inter, qkvw, qw);
-  const int n_attn = a.nkv * (D / eka::FDC);
+  const int n_attn = LONG ? 0 : a.nkv * (D / eka::FDC);
 
   float* rr = reinterpret_cast<float*>(smem);
   unsigned char* ph = smem + step_rr_bytes(h);
@@ -848,32 +1177,60 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     EK_TS(3);
     __syncthreads();
 
-    // ---- while attention runs: this workgroup's o_proj rows into registers
-    //      (all of them at the Qwen3-4B shape) and its first gate/up rows into L2
-    uint4 ob[OB];
-    hold_phase(go, ob);
-    prefetch_phase<PF>(gg, ring);
-    uint32_t sink = 0;
-    l2_touch(gg, sink);
-    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
-    EK_TS(4);
-    // ---- o projection
-    zero_part(part, part_n);
-    {
-      const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
-      if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
-      if (!wg_all(ok, s_fail)) return false;
+    if constexpr (LONG) {
+      // ---- attention on every workgroup (its LDS overlays the activation
+      //      row and the partials), then the o projection from the ring
+      llw_t* lx_ll = a.arena + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
+      if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, lx_ll, hi, ep, ep * (uint32_t)MAX_LAYERS + (uint32_t)l, ph,
+                                s_fail))
+        return false;
+      EK_TS(4);
+      prefetch_phase<PF>(go, ring);
+      load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
+      __syncthreads();
+      zero_part(part, part_n);
+      {
+        const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
+        if (!wg_all(ok, s_fail)) return false;
+      }
+      zero_pad(xs, qw, kpad_of(qw));
+      EK_TS(6);
+      __syncthreads();
+      gemv_phase(go, ring, xs, part);
+      __syncthreads();
+      EK_TS(7);
+      epilogue_ll(go, part, o_ll, ep, HC, h / 2);
+      prefetch_phase<PF>(gg, ring);
+      EK_TS(8);
+    } else {
+      (void)hi;
+      // ---- while attention runs: this workgroup's o_proj rows into registers
+      //      (all of them at the Qwen3-4B shape) and its first gate/up rows into L2
+      uint4 ob[OB];
+      hold_phase(go, ob);
+      prefetch_phase<PF>(gg, ring);
+      uint32_t sink = 0;
+      l2_touch(gg, sink);
+      load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
+      EK_TS(4);
+      // ---- o projection
+      zero_part(part, part_n);
+      {
+        const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
+        if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
+        if (!wg_all(ok, s_fail)) return false;
+      }
+      zero_pad(xs, qw, kpad_of(qw));
+      EK_TS(6);
+      __syncthreads();
+      EK_TS(29);
+      gemv_held_phase(go, ob, xs, part);
+      EK_TS(30);
+      __syncthreads();
+      EK_TS(7);
+      epilogue_ll(go, part, o_ll, ep, HC, h / 2);
+      EK_TS(8);
     }
-    zero_pad(xs, qw, kpad_of(qw));
-    EK_TS(6);
-    __syncthreads();
-    EK_TS(29);
-    gemv_held_phase(go, ob, xs, part);
-    EK_TS(30);
-    __syncthreads();
-    EK_TS(7);
-    epilogue_ll(go, part, o_ll, ep, HC, h / 2);
-    EK_TS(8);
 
     // ---- r = r + o; norm; gate/up; SwiGLU
     __syncthreads();
@@ -969,12 +1326,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
 // leaves tokens, positions, slot and length as they were, so the host reads
 // the failure at this step's own row and every later row stays aligned.
 template <int D>
-__device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool ok, int64_t len_old,
+__device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool ok, int64_t len_old, int n_attn,
                                             unsigned char* smem, float* s_red, int* s_redi, int* s_fail) {
   const int tid = threadIdx.x;
   const int h = a.h;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
-  const int n_attn = a.nkv * (D / eka::FDC);
   const int n_gemv = (int)gridDim.x - n_attn;
   const llw_t* am_ll = a.arena + (int64_t)a.nl * arena_layer_words(h, a.inter, qkvw, qw);
   uint32_t* amw = reinterpret_cast<uint32_t*>(smem + step_rr_bytes(h) + eka::align16((size_t)a.kpad_max * 2));
@@ -1007,7 +1363,7 @@ __device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool
   }
 }
 
-template <int D, int G>
+template <int D, int G, bool LONG>
 __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float s_red[SNW];
@@ -1036,11 +1392,12 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   const uint32_t ep = s_ep;
   const bool aborted = s_abort != 0;
   const int64_t len_old = *a.len_t;
-  const int n_attn = a.nkv * (D / eka::FDC);   // attention units = workgroups [0, n_attn)
+  int64_t hi = len_old + 1;
+  hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
+  // attention-only workgroups [0, n_attn) (none for long contexts)
+  const int n_attn = LONG ? 0 : a.nkv * (D / eka::FDC);
   if ((int)blockIdx.x < n_attn) {
     if (aborted) return;
-    int64_t hi = len_old + 1;
-    hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
     attention_loop<D, G>(a, s_lw, ep, hi, smem, &s_fail
 #ifdef EK_STEP_TRACE
                          , ts_lds
@@ -1050,33 +1407,37 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   }
   bool ok = !aborted;
   if (ok)
-    ok = projection_pass<D, G>(a, s_lw, ep, smem, s_red, s_redi, &s_fail
+    ok = projection_pass<D, G, LONG>(a, s_lw, ep, hi, smem, s_red, s_redi, &s_fail
 #ifdef EK_STEP_TRACE
                                , ts_lds
 #endif
                                );
   if ((int)blockIdx.x != n_attn) return;
-  finish_step<D>(a, ep, ok, len_old, smem, s_red, s_redi, &s_fail);
+  finish_step<D>(a, ep, ok, len_old, n_attn, smem, s_red, s_redi, &s_fail);
 #ifdef EK_STEP_TRACE
   EK_TS(4);
   EK_TS_FLUSH_SYNC(a.nl);
 #endif
 }
 
-// LDS bytes of step_kernel<D, G> (o_rows: the most o_proj rows of one workgroup, qw = n_q * D)
-template <int D, int G>
-inline size_t step_lds_bytes(int h, int kpad_max, int part_max, int64_t s_cap, int o_rows, int qw) {
-  (void)o_rows; (void)qw;
+// LDS bytes of step_kernel<D, G, LONG>: the projection layout, and either
+// an attention unit's (held apart from the residual row only by the
+// attention-only workgroups) or, for long contexts, the split attention's
+// after the residual row (lchunk: keys per split)
+template <int D, int G, bool LONG>
+inline size_t step_lds_bytes(int h, int kpad_max, int part_max, int64_t s_cap, int lchunk) {
   const size_t gemv = step_rr_bytes(h) + eka::align16((size_t)kpad_max * 2) + eka::align16((size_t)part_max * SNW * 4);
-  const size_t attn = eka::align16((size_t)(G + 6) * D * 2) + eka::AttnLds<D, G>::bytes(s_cap);
+  const size_t attn = LONG ? step_rr_bytes(h) + LongLds<D, G>::bytes(lchunk)
+                           : eka::align16((size_t)(G + 6) * D * 2) + eka::AttnLds<D, G>::bytes(s_cap);
   return gemv > attn ? gemv : attn;
 }
 
-// launch of one head-dim instantiation for any G (ek_step_inst.hip)
+// launch of one head-dim instantiation for any G (ek_step_inst.hip); the
+// long-context kernel when a.lsplit > 0
 template <int D>
 hipError_t launch_step(const StepArgs& a, int g, int nwg, hipStream_t st);
-// workgroups of step_kernel<D, g> with `lds` dynamic LDS bytes resident per CU
+// workgroups of step_kernel<D, g, lng> with `lds` dynamic LDS bytes resident per CU
 template <int D>
-int step_occupancy(int g, size_t lds);
+int step_occupancy(int g, bool lng, size_t lds);
 
 }  // namespace eks

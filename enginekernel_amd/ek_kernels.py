@@ -386,8 +386,12 @@ def lm_head_argmax(hidden, lm_head, scratch: ArgmaxScratch, out_tok=None, logits
 # ----------------------------------------------------------------------------
 def decode_step_plan(hidden: int, inter: int, n_q: int, n_kv: int, head_dim: int, vocab: int, m: int,
                      s_cap: int, n_layers: int):
-    """(arena bytes, argmax entries, barrier bytes, grid) when the persistent
-    decode-step kernel handles this shape, else None (see decode_step)."""
+    """(arena bytes, long-context key split, barrier bytes, grid) when the
+    persistent decode-step kernel handles this shape, else None (see
+    decode_step). The split is 0 when each kv head's scores fit one attention
+    unit's LDS (attention then runs on workgroups of its own beside the
+    projections); otherwise every workgroup attends 1 / split of a kv head's
+    keys and the splits combine through the arena."""
     import ctypes
     lib = _hip.load()
     sizes = (ctypes.c_int64 * 4)()
@@ -401,7 +405,7 @@ class StepScratch:
     """Device state of the persistent decode step: the hand-over arena, the
     launch-state block and the error word, sized by decode_step_plan and
     zeroed once (the kernel keeps a launch epoch in them). One per (model,
-    batch); launches sharing it must not overlap."""
+    batch, arena size); launches sharing it must not overlap."""
 
     def __init__(self, sizes, device):
         arena_bytes, _, bar_bytes, grid = sizes

@@ -154,7 +154,10 @@ class _StepBuffers:
         self.att = torch.empty(b, cfg.q_size, dtype=bf, device=device)   # verify attention rows
         self.argmax = K.ArgmaxScratch(b, cfg.vocab_size, device)
         self.next_tok = torch.empty(b, dtype=torch.int64, device=device)
-        self.step = None   # K.StepScratch of the persistent step, made on first use
+        self.step = None   # K.StepScratch of the persistent step's last launch, made on first use
+        # every StepScratch made for this batch, by arena size (the long-context
+        # plan's arena is larger); one a captured graph uses is never freed
+        self.steps = {}
 
 
 class Qwen3(torch.nn.Module):
@@ -390,8 +393,8 @@ class Qwen3(torch.nn.Module):
     def check_step_error(self) -> None:
         """Raise if a persistent step abandoned a hand-over wait."""
         for bufs in self._bufs.values():
-            if bufs.step is not None:
-                bufs.step.check()
+            for scratch in bufs.steps.values():
+                scratch.check()
 
     def step(self, tokens, positions, k_cache, v_cache, slot_t, len_t, start_t, ws, out_buf, step_idx,
              logits=None):
@@ -410,8 +413,12 @@ class Qwen3(torch.nn.Module):
         plan = self.persistent_plan(b, s_cap) if self.persistent else None
         if plan is not None:
             bufs = self.buffers(b)
-            if bufs.step is None:
-                bufs.step = K.StepScratch(plan, self.device)
+            scratch = bufs.steps.get(plan[0])
+            if scratch is None:
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError("decode_step: run one step of this bucket before capturing it")
+                scratch = bufs.steps[plan[0]] = K.StepScratch(plan, self.device)
+            bufs.step = scratch
             K.decode_step(self._layer_table(k_cache, v_cache), self.cfg, self.embed, self.lm_head, self.final_norm,
                           self.cos, self.sin, k_cache[0], s_cap, tokens, positions, len_t, slot_t, start_t,
                           out_buf, step_idx, bufs.step, out_tok=bufs.next_tok, logits=logits,

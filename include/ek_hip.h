@@ -219,12 +219,17 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
                       int64_t* st_step, int64_t max_steps, int64_t rpw, int64_t blocks, void* stream);
 
 /* decode_step_plan: whether the persistent decode-step kernel handles this
- * shape (returns 0) and, in sizes[4], the bytes of the hand-over arena, 0
- * (unused), the bytes of the launch-state block and the grid (one workgroup
- * per CU). It handles batch 1, head_dim 32/64/128, n_q / n_kv in {1, 2, 4, 8},
- * hidden (<= 4096), intermediate and n_q * head_dim multiples of 512, and
- * n_q / n_kv * s_cap * 4 <= 32 KiB, on a device where one workgroup of the
- * kernel fits on every CU at once (its waits need the whole grid resident).
+ * shape (returns 0) and, in sizes[4], the bytes of the hand-over arena, the
+ * long-context key split (0 when n_q / n_kv * s_cap * 4 <= 32 KiB: attention
+ * then runs on n_kv * head_dim / 32 workgroups of its own beside the
+ * projections; otherwise every workgroup attends 1 / split of one kv head's
+ * keys), the bytes of the launch-state block and the grid (one workgroup per
+ * CU). It handles batch 1, up to 64 layers, head_dim 32/64/128, n_q / n_kv in
+ * {1, 2, 4, 8}, hidden (<= 4096), intermediate and n_q * head_dim multiples
+ * of 512, and s_cap up to what one split's score rows fit in LDS (about
+ * 100 K keys at n_q / n_kv = 4 on 256 CUs), on a device where one workgroup
+ * of the kernel fits on every CU at once (its waits need the whole grid
+ * resident).
  * Plans engine/engine.py:273-282 (_make_ws) for the step below. */
 int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
                         int64_t m, int64_t s_cap, int64_t n_layers, int64_t* sizes);

@@ -68,9 +68,9 @@ def test_decode_step_plan_rejects_unsupported_shapes_without_a_gpu():
     # 32 query heads per kv head: not a supported group
     rc = lib.ek_decode_step_plan(2560, 9728, 32, 1, 128, 151936, 1, 768, 36, sizes)
     assert rc == 1 and b"query heads" in lib.ek_last_error()
-    # a score row of 4 x 8192 fp32 does not fit the unit's 32 KiB
-    rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 8192, 36, sizes)
-    assert rc == 1 and b"LDS" in lib.ek_last_error()
+    # 65 layers: the layer table held in LDS has 64 rows
+    rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 768, 65, sizes)
+    assert rc == 1 and b"64 layers" in lib.ek_last_error()
     zeros = [None if t is ctypes.c_void_p else 0.0 if t is ctypes.c_float else 0
              for t in _hip.SIGNATURES["ek_decode_step"]]
     assert lib.ek_decode_step(*zeros) == 1

@@ -10,11 +10,16 @@ the benchmarked kernel) pinned against the oracle.
 * Long contexts at two layers: contexts 701..2047, where the attention
   workgroups run their tiles past the keys they hold in registers; every
   step's full logits against the oracle run live.
+* Buckets of 4096 and 16384 keys at two layers, where every workgroup
+  attends a split of one kv head's keys: random cache rows on both sides,
+  every step's full logits against the oracle run live, with left padding,
+  empty splits and the bucket's last slot.
 * Failure reporting: a step whose device-side waits give up emits -1 and
   sets the error word; the engine raises before yielding that step's tokens,
   and Engine(fallback=...) continues the request on the fallback exactly.
 """
 
+import ctypes
 import os
 
 import numpy as np
@@ -196,6 +201,93 @@ def test_persistent_step_long_contexts(dev, prompt_len, steps):
                 a, r = got_c[0, :, s:n].cpu().float(), ref_c[0, :, s:n].float()
                 assert (a - r).abs().max().item() <= 2e-2 * r.abs().max().item()
     print(f"contexts {s + 1}..{s + steps}: worst logit error {worst:.4f} of scale")
+
+
+@pytest.fixture(scope="module")
+def split_model(dev):
+    cfg = dict(MID_4B)
+    tensors = C.random_weights(cfg, seed=0)
+    return cfg, O.OracleQwen3(O.OracleConfig(cfg), tensors), Qwen3(None, dev, tensors=tensors, config=cfg)
+
+
+@pytest.mark.parametrize("bucket,s,start,steps", [
+    (4096, 4000, 0, 4),       # contexts 4001..4004
+    (4096, 2600, 300, 3),     # left padding: keys [300, s) attended
+    (4096, 3, 0, 3),          # most of the 32 splits of a kv head empty
+    (16384, 9000, 0, 2),
+    (16384, 16380, 0, 3),     # up to the bucket's last slot
+])
+def test_persistent_step_split_contexts(dev, split_model, bucket, s, start, steps):
+    """Buckets past 2048 keys: the persistent step splits each kv head's keys
+    over every workgroup (the plan reports the split) and combines the
+    splits through the arena, at every Qwen3-4B shape with two layers. Both
+    sides start from the same random cache rows [0, s) (rows before `start`
+    are padding, masked on both sides) and are fed the oracle's ids; every
+    step's full logits are within 2e-2 of their scale, the argmax is the
+    oracle's up to a near-tie, and the new cache rows match."""
+    cfg, om, model = split_model
+    plan = model.persistent_plan(1, bucket)
+    assert plan is not None and plan[1] >= 2, plan
+    g = torch.Generator().manual_seed(bucket + s)
+    ost = O.EagerState(om, 1, s, [start], bucket)
+    for t in ost.k + ost.v:
+        t[0, :, :s] = torch.randn(t[0, :, :s].shape, generator=g).to(BF)
+    tok = torch.randint(0, cfg["vocab_size"], (1,), generator=g)
+    with torch.inference_mode():
+        kd = [t.to(dev) for t in ost.k]
+        vd = [t.to(dev) for t in ost.v]
+        st = _state(dev, s, start=[start])
+        st["positions"].fill_(s - start)
+        ws = K.make_workspace(1, 32, 8, 128, bucket, dev)
+        tokens = tok.to(dev)
+        logits = torch.empty(1, cfg["vocab_size"], dtype=BF, device=dev)
+        worst = 0.0
+        for i in range(steps):
+            l_ref = O.lm_logits(om.decode(tok, ost.positions, ost.k, ost.v, ost.slot_t, ost.len_t, ost.start_t),
+                                om.lm_head).float()[0]
+            tokens.copy_(tok)
+            model.step(tokens, st["positions"], kd, vd, st["slot_t"], st["len_t"], st["start_t"], ws,
+                       st["out_buf"], st["step_idx"], logits=logits)
+            lg = logits.float().cpu()[0]
+            rel = (lg - l_ref).abs().max().item() / l_ref.abs().max().item()
+            worst = max(worst, rel)
+            assert rel <= 2e-2, (i, rel)
+            t_ref = int(torch.argmax(l_ref))
+            t_gpu = int(st["out_buf"][i, 0])
+            assert t_gpu == int(torch.argmax(lg))
+            if t_gpu != t_ref:
+                assert float(l_ref[t_ref] - l_ref[t_gpu]) <= 2 * _ulp(float(l_ref[t_ref])), (i, t_gpu, t_ref)
+            tok = torch.tensor([t_ref])
+            ost.positions = ost.positions + 1
+        K.check_error_word(K.ws_error(ws), "split-context steps")
+        assert model.buffers(1).step.arena_bytes == plan[0]
+        n = int(ost.len_t)
+        assert n == s + steps and int(st["len_t"]) == n and int(st["positions"][0]) == n - start
+        for layer in range(2):
+            for got_c, ref_c in ((kd[layer], ost.k[layer]), (vd[layer], ost.v[layer])):
+                assert torch.equal(got_c[0, :, :s].cpu(), ref_c[0, :, :s])
+                a, r = got_c[0, :, s:n].cpu().float(), ref_c[0, :, s:n].float()
+                assert (a - r).abs().max().item() <= 2e-2 * r.abs().max().item()
+                assert not got_c[0, :, n:].cpu().any()
+    print(f"bucket {bucket}, contexts {s + 1}..{s + steps}: worst logit error {worst:.4f} of scale")
+
+
+def test_persistent_plan_split_bounds(dev):
+    """The split plan at the Qwen3-4B shape: none up to 2048 keys (attention
+    units beside the projections), 32 splits of a kv head beyond, and a
+    clear rejection once one split's score rows exceed the LDS."""
+    lib = _hip.load()
+    sizes = (ctypes.c_int64 * 4)()
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 2048, 36, sizes) == 0
+    short_arena = sizes[0]
+    assert sizes[1] == 0
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 2049, 36, sizes) == 0
+    assert sizes[1] == 32 and sizes[3] == 256
+    # the split exchange: (max, sum) per query head and a partial output per split
+    assert sizes[0] == short_arena + 8 * 8 * 32 * (2 * 4 + 4 * 128)
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 131072, 36, sizes) == 0
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1 << 18, 36, sizes) == 1
+    assert b"LDS" in lib.ek_last_error()
 
 
 class _OracleEngine:
