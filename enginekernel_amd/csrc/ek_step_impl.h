@@ -86,7 +86,7 @@ enum { LW_QKV = 0, LW_O, LW_GU, LW_DOWN, LW_LN1, LW_LN2, LW_QN, LW_KN, LW_KC, LW
 // launch state, zeroed once by the host
 struct Bar {
   unsigned ep[MAX_WG];   // per-workgroup launch epoch
-  int64_t* trace;        // -DEK_STEP_TRACE builds: per-phase timestamps [wg][layer][32]
+  int64_t* trace;        // -DEK_STEP_TRACE builds: per-phase timestamps [wg][layer][48]
   int64_t pad[7];
 };
 
@@ -147,11 +147,11 @@ __host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int voc
 
 // -DEK_STEP_TRACE builds stamp phase events into LDS (a global store would
 // delay the memory waits that follow it) and copy one layer's stamps to
-// bar->trace[wg][layer][32] at the layer's end.
+// bar->trace[wg][layer][48] at the layer's end.
 #ifdef EK_STEP_TRACE
 #define EK_TS(ev) do { if (threadIdx.x == 0) ts_lds[ev] = wall_clock64(); } while (0)
-#define EK_TS_FLUSH(layer) do { if (a.bar->trace && threadIdx.x < 32) \
-    a.bar->trace[((int64_t)blockIdx.x * 40 + (layer)) * 32 + threadIdx.x] = ts_lds[threadIdx.x]; } while (0)
+#define EK_TS_FLUSH(layer) do { if (a.bar->trace && threadIdx.x < 48) \
+    a.bar->trace[((int64_t)blockIdx.x * 40 + (layer)) * 48 + threadIdx.x] = ts_lds[threadIdx.x]; } while (0)
 #define EK_TS_FLUSH_SYNC(layer) do { __syncthreads(); EK_TS_FLUSH(layer); } while (0)
 #else
 #define EK_TS_FLUSH_SYNC(layer) do { } while (0)
@@ -229,6 +229,23 @@ struct LinSrc {   // words [0, n) of one region
   const llw_t* p;
   __device__ const llw_t* operator()(int i) const { return p + i; }
 };
+
+// One thread's wait for one word (the data half into `out`); false (the
+// error word set) when the wait runs out or another wait gave up.
+__device__ __forceinline__ bool ll_wait1(const llw_t* p, uint32_t tag, uint32_t& out, int* err, int64_t spin) {
+  llw_t v = ll_get(p);
+  int64_t it = 0;
+  while (!ll_ok(v, tag)) {
+    if (++it > spin) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    v = ll_get(p);
+  }
+  out = (uint32_t)v;
+  return true;
+}
 
 // ---------------------------------------------------------------------------
 // projections
@@ -758,6 +775,16 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 //            it adds the S splits' partials of those dims in split order and
 //            stores them as the bf16 attention words the o projection awaits.
 // The split holding the new slot stores the new key and value rows last.
+// long contexts: 16-key score tiles per wave and value rows per thread in flight
+#ifndef EK_STEP_LUT
+#define EK_STEP_LUT 2
+#endif
+#ifndef EK_STEP_LVR
+#define EK_STEP_LVR 8
+#endif
+constexpr int LUT = EK_STEP_LUT;
+constexpr int LVR = EK_STEP_LVR;
+
 template <int D, int G>
 struct LongLds {
   static constexpr size_t HEADS = eka::align16((size_t)(G + 2) * D * 2);   // raw q heads, new k, new v (bf16)
@@ -767,23 +794,27 @@ struct LongLds {
   static constexpr size_t KNB = eka::align16((size_t)D * 2);               // the new key (bf16)
   static constexpr size_t ST = eka::align16((size_t)SNW * 8 * 4);          // per-wave max / sum
   static constexpr size_t RED = eka::align16((size_t)SNW * G * D * 4);     // per-wave partial outputs
-  static constexpr size_t SPL = eka::align16((size_t)64 * 2 * G * 4);      // every split's (m, l): up to 64 splits
-  static constexpr size_t CMB = eka::align16((size_t)G * D * 4);           // the combine's words
+  static constexpr size_t CMB = eka::align16((size_t)G * D * 4);           // the combined outputs
   static __host__ __device__ constexpr int64_t stride(int64_t chunk) { return chunk | 1; }
   static __host__ __device__ constexpr size_t bytes(int64_t chunk) {
-    return HEADS + ROPE + QS + KNF + KNB + 2 * ST + RED + SPL + CMB + eka::align16((size_t)G * stride(chunk) * 4);
+    return HEADS + ROPE + QS + KNF + KNB + 2 * ST + RED + CMB + eka::align16((size_t)G * stride(chunk) * 4);
   }
 };
 
 template <int D, int G>
 __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
                                                llw_t* lx, int64_t hi, uint32_t ep, uint32_t ltag, unsigned char* lds,
-                                               int* s_fail) {
+                                               int* s_fail
+#ifdef EK_STEP_TRACE
+                                               , int64_t* ts_lds
+#endif
+                                               ) {
   using L = LongLds<D, G>;
   constexpr int KS = D / 32;       // 32-dim k-steps of a score tile
-  constexpr int UT = 2;            // 16-key score tiles per wave per group
+  constexpr int UT = LUT;          // 16-key score tiles per wave in flight
   constexpr int DCH = D / 8;       // 16-byte chunks per key row
   constexpr int NKG = SNT / DCH;   // key groups of the PV product
+  constexpr int VR = LVR;          // value rows per thread in flight
   const int S = a.lsplit;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int r16 = lane & 15, q4 = lane >> 4;
@@ -800,9 +831,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   float (*stm)[8] = reinterpret_cast<float (*)[8]>(p0);
   float (*stl)[8] = reinterpret_cast<float (*)[8]>(p0 + L::ST);
   float* red = reinterpret_cast<float*>(p0 + 2 * L::ST);                  // [SNW][G][D]
-  float* spl = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED);         // [S][2G]
-  float* cmb = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::SPL);   // [S][G][dpu]
-  float* sc = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::SPL + L::CMB);   // [G][stride]
+  float* cmb = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED);         // [G dpu]
+  float* sc = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::CMB);   // [G][stride]
   const int64_t cstride = L::stride(a.lchunk);
 
   int64_t lo = a.start_t[0];
@@ -816,29 +846,32 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   const int64_t slot = hi - 1;
   const bool own = nk > 0 && slot >= k0 && slot < k1;
   // loads past the split's keys (the last tiles' tails, an empty split) read
-  // row `last` instead: k0 itself may lie past the cache's last row
+  // row `last` instead: k0 itself may lie past the cache's last row. Their
+  // products are never used, nor is the cache row at the new slot (the new
+  // key and value stand in for it), so no load is masked: a select on a
+  // loaded value would wait for the load where it stands.
   const int64_t last = slot > 0 ? slot : 0;
   const bf16_t* kc = reinterpret_cast<const bf16_t*>(lw[LW_KC]) + h * a.csh;
   const bf16_t* vc = reinterpret_cast<const bf16_t*>(lw[LW_VC]) + h * a.csh;
 
-  // the first key tiles load before the heads are awaited (they do not
-  // depend on them); lane holds key r16 of a tile, dims 32 i + 8 q4 .. +7
-  const int64_t ntile = (nk + 15) >> 4;
+  // key tiles, a ring of UT per wave: slot u holds tile wave + (u + UT j) SNW
+  // of the split; lane holds key r16 of a tile, dims 32 i + 8 q4 .. +7
+  // (32-bit key indices: the plan bounds a split's keys by 65536)
+  const int nk32 = (int)nk;
+  const int ntile = (nk32 + 15) >> 4;
   uint4 kt[UT][KS];
-  auto load_group = [&](int64_t t0) {
+  const bf16_t* kbase = kc + k0 * a.css + 8 * q4;
+  const bf16_t* klast = kc + last * a.css + 8 * q4;
+  const int kcs = (int)a.css;
+  auto load_tile = [&](int u, int t) {
+    const int rel = (t << 4) + r16;
+    const bf16_t* src = rel < nk32 ? kbase + rel * kcs : klast;
 #pragma unroll
-    for (int u = 0; u < UT; ++u) {
-      const int64_t rel = ((t0 + u * SNW) << 4) + r16;
-      const bool ok = rel < nk && k0 + rel != slot;
-      const int64_t key = rel < nk ? k0 + rel : last;
-#pragma unroll
-      for (int i = 0; i < KS; ++i) {
-        const uint4 v = ld16_nt(kc + key * a.css + 32 * i + 8 * q4);
-        kt[u][i] = ok ? v : make_uint4(0, 0, 0, 0);
-      }
-    }
+    for (int i = 0; i < KS; ++i) kt[u][i] = ld16_nt(src + 32 * i);
   };
-  load_group(wave);
+  // the first tiles load before the heads are awaited (they do not depend on them)
+#pragma unroll
+  for (int u = 0; u < UT; ++u) load_tile(u, wave + u * SNW);
 
   // the unit's q heads, new key and new value, and the gains / cos / sin rows
   {
@@ -861,6 +894,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     const bool ok = ll_read<2>(src, (G + 2) * hw, ep, reinterpret_cast<uint32_t*>(heads), a.err, a.spin);
     if (!wg_all(ok, s_fail)) return false;
   }
+  EK_TS(28);
   // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
   for (int u = wave; u <= G; u += SNW) {
     if (u < G) eka::head_norm_rope<D>(heads + u * D, rope, rope + 2 * D, rope + 3 * D, a.eps, qs[u], nullptr);
@@ -884,34 +918,60 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
       qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
+  // The wave's tiles run in rounds of UT with no early exit (an exit inside
+  // the unrolled ring would roll it into a loop over one register set, one
+  // tile in flight): tiles past the split's end compute on re-read rows and
+  // their scores are dropped.
   float mrun = -INFINITY;
-  for (int64_t t0 = wave; t0 < ntile; t0 += (int64_t)SNW * UT) {
-    if (t0 != wave) load_group(t0);
+  const int ntw = wave < ntile ? (int)((ntile - 1 - wave) / SNW) + 1 : 0;   // this wave's tiles
+  const int srel = own ? (int)(slot - k0) : -1;                              // the new slot's key
+  for (int k = 0; k < ntw; k += UT) {
 #pragma unroll
     for (int u = 0; u < UT; ++u) {
-      const int64_t tb = (t0 + u * SNW) << 4;
-      if (tb >= nk) break;
-      if (own && k0 + tb + r16 == slot) {   // the new key, from LDS
+      const int t = wave + (k + u) * SNW;
+      const int tb = t << 4;
+      if (tb + r16 == srel) {   // the new key, from LDS
 #pragma unroll
         for (int i = 0; i < KS; ++i) kt[u][i] = *reinterpret_cast<const uint4*>(&knew_bf[32 * i + 8 * q4]);
       }
       eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int i = 0; i < KS; ++i) c = eka::mfma16x16x32(kt[u][i], qb[i], c);
+      load_tile(u, t + SNW * UT);   // refill the slot
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t rel = tb + 4 * q4 + e;
+        const int rel = tb + 4 * q4 + e;
         const float sv = c[e] * a.sm_scale;
-        const bool ok = r16 < G && rel < nk;
+        const bool ok = r16 < G && rel < nk32;
         if (ok) sc[r16 * cstride + rel] = sv;
         mrun = ok ? fmaxf(mrun, sv) : mrun;
       }
     }
   }
+  // the first value rows of the PV product load while the statistics travel:
+  // thread -> head dims 8 dc .. +7 of keys kg, kg + NKG, ... (16-byte loads,
+  // lane-contiguous across a key row), a ring of VR rows per thread
+  const int dc = tid % DCH, kg = tid / DCH;
+  const int nper = nk32 > kg ? (nk32 - kg + NKG - 1) / NKG : 0;
+  const bf16_t* vbase = vc + (k0 + kg) * a.css + 8 * dc;
+  const bf16_t* vlast = vc + last * a.css + 8 * dc;
+  const int vstep = NKG * (int)a.css;
+  auto vaddr = [&](int j) { return j < nper ? vbase + j * vstep : vlast; };
+  // the key row j of this thread that is the new slot (-1: none)
+  int jslot = -1;
+  if (own) {
+    const int r = srel - kg;
+    jslot = (r >= 0 && r % NKG == 0) ? r / NKG : -1;
+  }
+  uint4 vr[VR];
+#pragma unroll
+  for (int u = 0; u < VR; ++u) vr[u] = ld16_nt(vaddr(u));
+
   mrun = fmaxf(mrun, __shfl_xor(mrun, 16, EK_WAVE));
   mrun = fmaxf(mrun, __shfl_xor(mrun, 32, EK_WAVE));
   if (q4 == 0 && r16 < G) stm[wave][r16] = mrun;
   __syncthreads();
+  EK_TS(31);
 
   // ---- the split's (max, sum of exp) per head: thread -> head tid % G
   llw_t* st_ll = lx;                                          // [nkv][S][2G]
@@ -922,7 +982,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
 #pragma unroll
     for (int w = 1; w < SNW; ++w) ms = fmaxf(ms, stm[w][g]);
     float ls = 0.f;
-    for (int64_t n = tid / G; n < nk; n += SNT / G) ls += expf(sc[g * cstride + n] - ms);
+    for (int n = tid / G; n < nk32; n += SNT / G) ls += expf(sc[g * cstride + n] - ms);
 #pragma unroll
     for (int o = G; o < EK_WAVE; o <<= 1) ls += __shfl_xor(ls, o, EK_WAVE);
     if (lane < G) stl[wave][lane] = ls;
@@ -936,45 +996,46 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
       ll_put(my + 2 * tid + 1, __float_as_uint(lt), ltag);
     }
   }
-  // every split's statistics of this head -> M, L, then p = bf16(exp(s - M) / L)
+  // every split's statistics of this head -> M = max m_j and
+  // L = sum l_j exp(m_j - M): wave g for head g, lane j polls split j's two
+  // words itself, then two wave reductions in a fixed order; then
+  // p = bf16(exp(s - M) / L) in place
   {
-    const bool ok = ll_read(LinSrc{st_ll + (int64_t)h * S * 2 * G}, S * 2 * G, ltag, reinterpret_cast<uint32_t*>(spl),
-                            a.err, a.spin);
-    if (!wg_all(ok, s_fail)) return false;
-    const int g = tid % G;
-    float M = -INFINITY;
-    for (int j = 0; j < S; ++j) M = fmaxf(M, spl[j * 2 * G + 2 * g]);
-    float Ls = 0.f;
-    for (int j = 0; j < S; ++j) {
-      const float mj = spl[j * 2 * G + 2 * g];
-      Ls += mj == -INFINITY ? 0.f : spl[j * 2 * G + 2 * g + 1] * expf(mj - M);
+    bool ok = true;
+    if (wave < G) {
+      uint32_t mw = __float_as_uint(-INFINITY), lw32 = 0u;
+      if (lane < S) {
+        const llw_t* w = st_ll + ((int64_t)h * S + lane) * 2 * G + 2 * wave;
+        ok = ll_wait1(w, ltag, mw, a.err, a.spin) && ll_wait1(w + 1, ltag, lw32, a.err, a.spin);
+      }
+      const float mj = __uint_as_float(mw), lj = __uint_as_float(lw32);
+      const float M = wave_max(mj);
+      const float Ls = wave_sum_dpp(mj == -INFINITY ? 0.f : lj * expf(mj - M));
+      if (lane == 0) {
+        stm[0][wave] = M;
+        stl[0][wave] = Ls;
+      }
     }
-    for (int64_t n = tid / G; n < nk; n += SNT / G) sc[g * cstride + n] = rbf(expf(sc[g * cstride + n] - M) / Ls);
+    if (!wg_all(ok, s_fail)) return false;
+    EK_TS(29);
+    const int g = tid % G;
+    const float M = stm[0][g], Ls = stl[0][g];
+    for (int n = tid / G; n < nk32; n += SNT / G) sc[g * cstride + n] = rbf(expf(sc[g * cstride + n] - M) / Ls);
   }
   __syncthreads();
+  EK_TS(32);
 
-  // ---- PV: thread -> head dims 8 dc .. +7 of keys kg, kg + NKG, ... (16-byte
-  // value loads, lane-contiguous across a key row), 8 loads in flight
+  // ---- PV: the split's partial output sum p v over its keys, every head dim, fp32
   {
-    const int dc = tid % DCH, kg = tid / DCH;
     float acc[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-    const int64_t nper = nk > kg ? (nk - kg + NKG - 1) / NKG : 0;
     const uint4 vnew = *reinterpret_cast<const uint4*>(heads + (G + 1) * D + 8 * dc);
-    auto vaddr = [&](int64_t j) {
-      const int64_t key = j < nper ? k0 + kg + NKG * j : last;
-      return vc + key * a.css + 8 * dc;
-    };
-    constexpr int VR = 4;
-    uint4 vr[VR];
-#pragma unroll
-    for (int u = 0; u < VR; ++u) vr[u] = ld16_nt(vaddr(u));
-    auto use = [&](const uint4& vv, int64_t j) {
-      const int64_t n = kg + NKG * j;
-      const uint4 v = (own && k0 + n == slot) ? vnew : vv;
+    auto use = [&](const uint4& vv, int j) {
+      const int n = kg + NKG * j;
+      const uint4 v = j == jslot ? vnew : vv;
       float vf[8];
       unpack8(v, vf);
 #pragma unroll
@@ -984,18 +1045,24 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
         for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg, vf[e], acc[g][e]);
       }
     };
-    int64_t j0 = 0;
+    // the ring: each slot is consumed, then refilled (refilling first would
+    // copy every slot at the loop's head, which waits for all of them); the
+    // scheduling barrier keeps each refill where it stands (the scheduler
+    // otherwise sinks all of them to the loop's end, and every round then
+    // waits for the whole ring)
+    int j0 = 0;
     for (; j0 + VR <= nper; j0 += VR) {
 #pragma unroll
       for (int u = 0; u < VR; ++u) {
-        const uint4 v = vr[u];
+        use(vr[u], j0 + u);
         vr[u] = ld16_nt(vaddr(j0 + u + VR));
-        use(v, j0 + u);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
     for (int u = 0; u < VR; ++u)
       if (j0 + u < nper) use(vr[u], j0 + u);
+    EK_TS(33);
     // key groups with the same dims: lanes dc, dc + DCH, ... of the wave, then the waves
 #pragma unroll
     for (int o = DCH; o < EK_WAVE; o <<= 1)
@@ -1010,7 +1077,9 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
         for (int e = 0; e < 8; ++e) red[(wave * G + g) * D + 8 * dc + e] = acc[g][e];
     }
   }
+  EK_TS(34);
   __syncthreads();
+  EK_TS(35);
   // the split's partial output -> tagged words
   for (int i = tid; i < G * D; i += SNT) {
     float t = 0.f;
@@ -1018,26 +1087,29 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     for (int w = 0; w < SNW; ++w) t += red[w * G * D + i];
     ll_put(pt_ll + ((int64_t)h * S + s) * G * D + i, __float_as_uint(t), ltag);
   }
-  // ---- combine this unit's dims [s dpu, (s+1) dpu) of every query head
+  EK_TS(30);
+  // ---- combine this unit's dims [s dpu, (s+1) dpu) of every query head:
+  // thread t -> output o = t / S (head o / dpu, dim o % dpu), split j = t % S
+  // polls that one word; the S lanes of an output (S <= 64, a power of two,
+  // so they sit in one wave) add theirs by a butterfly, in a fixed order
   {
-    struct Src {   // word i = (split j, head g, dim dd) of this unit's dims
-      const llw_t* p; int ng, hd, dpu, d0;
-      __device__ const llw_t* operator()(int i) const {
-        const int j = i / (ng * dpu), r = i - j * (ng * dpu), g = r / dpu, dd = r - g * dpu;
-        return p + ((int64_t)j * ng + g) * hd + d0 + dd;
-      }
-    } src{pt_ll + (int64_t)h * S * G * D, G, D, dpu, s * dpu};
-    const bool ok = ll_read(src, S * G * dpu, ltag, reinterpret_cast<uint32_t*>(cmb), a.err, a.spin);
+    bool ok = true;
+    for (int t = tid; t < G * D; t += SNT) {   // G * dpu * S = G * D
+      const int o = t / S, j = t - o * S;
+      const int g = o / dpu, dd = o - g * dpu;
+      uint32_t w = 0u;
+      ok = ok && ll_wait1(pt_ll + (((int64_t)h * S + j) * G + g) * D + s * dpu + dd, ltag, w, a.err, a.spin);
+      float v = __uint_as_float(w);
+      for (int m = 1; m < S; m <<= 1) v += __shfl_xor(v, m, EK_WAVE);
+      if (j == 0) cmb[o] = v;
+    }
     if (!wg_all(ok, s_fail)) return false;
+    EK_TS(5);
     for (int i = tid; i < G * dpu / 2; i += SNT) {
       const int g = (2 * i) / dpu, dd = 2 * i - g * dpu;
-      float t0 = 0.f, t1 = 0.f;
-      for (int j = 0; j < S; ++j) {
-        t0 += cmb[(j * G + g) * dpu + dd];
-        t1 += cmb[(j * G + g) * dpu + dd + 1];
-      }
       for (int c = 0; c < HC; ++c)
-        ll_put(att + (int64_t)c * (a.nq * D / 2) + ((int64_t)(h * G + g) * D + s * dpu + dd) / 2, pack2(t0, t1), ep);
+        ll_put(att + (int64_t)c * (a.nq * D / 2) + ((int64_t)(h * G + g) * D + s * dpu + dd) / 2,
+               pack2(cmb[2 * i], cmb[2 * i + 1]), ep);
     }
   }
   // the new key and value rows (normed and rotated key, raw value)
@@ -1182,7 +1254,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       //      row and the partials), then the o projection from the ring
       llw_t* lx_ll = a.arena + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
       if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, lx_ll, hi, ep, ep * (uint32_t)MAX_LAYERS + (uint32_t)l, ph,
-                                s_fail))
+                                s_fail
+#ifdef EK_STEP_TRACE
+                                , ts_lds
+#endif
+                                ))
         return false;
       EK_TS(4);
       prefetch_phase<PF>(go, ring);
@@ -1385,7 +1461,7 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
     s_abort = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #ifdef EK_STEP_TRACE
-  __shared__ int64_t s_ts[32];
+  __shared__ int64_t s_ts[48];
   int64_t* ts_lds = s_ts;
 #endif
   __syncthreads();
