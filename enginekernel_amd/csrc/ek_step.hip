@@ -34,7 +34,17 @@ namespace {
 
 constexpr int64_t kSpin = int64_t(1) << 20;           // default polls of one hand-over wait before giving up (~1 s)
 constexpr size_t kLdsLimit = eks::kStepDynLds;        // dynamic LDS per workgroup (the static arrays take the rest)
-constexpr int64_t kFusedScoreLds = 32 * 1024;         // score row bytes per attention unit
+// Rows of at most kUnitMaxKeys keys whose scores fit kFusedScoreLds bytes
+// run on the attention units beside the projections; longer ones on the
+// split kernel. At the Qwen3-4B shape the split kernel is the faster one
+// from a 1792-key bucket on (2.121 vs 2.235 ms per step at context 1.5 K,
+// 2.116 vs 1.974 at 1 K, 2.106 vs 1.773 at 0.5 K): the 32 attention units
+// then stream more keys than the projections take to run.
+#ifndef EK_STEP_UNIT_MAX_KEYS
+#define EK_STEP_UNIT_MAX_KEYS 1536
+#endif
+constexpr int64_t kFusedScoreLds = 32 * 1024;
+constexpr int64_t kUnitMaxKeys = EK_STEP_UNIT_MAX_KEYS;
 
 int step_grid() {
   static int n = 0;
@@ -117,14 +127,14 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   if (s_cap < 1) return ek_fail(hipErrorInvalidValue, "decode_step: empty cache");
   p.nwg = step_grid();
   if (p.nwg < 1 || p.nwg > eks::MAX_WG) return ek_fail(hipErrorInvalidValue, "decode_step: unsupported device");
-  // Rows whose scores fit one attention unit's LDS run on attention-only
-  // workgroups beside the projections; longer ones on every workgroup, the
+  // Short rows run on attention-only workgroups beside the projections
+  // (kUnitMaxKeys above); longer ones on every workgroup, the
   // keys of each kv head split S ways (S a power of two, at most 64 and at
   // most head_dim / 2, so that each split owns an even number of head dims
   // of the combined output)
   p.lsplit = p.lchunk = 0;
   p.lx = 0;
-  if (g * s_cap * 4 > kFusedScoreLds) {
+  if (s_cap > kUnitMaxKeys || g * s_cap * 4 > kFusedScoreLds) {
     int sp = 1;
     while (2 * sp <= 64 && 2 * sp <= head_dim / 2 && 2 * sp * n_kv <= p.nwg) sp *= 2;
     if (sp < 2) return ek_fail(hipErrorInvalidValue, "decode_step: too few workgroups for the long-context split");

@@ -220,10 +220,10 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
 
 /* decode_step_plan: whether the persistent decode-step kernel handles this
  * shape (returns 0) and, in sizes[4], the bytes of the hand-over arena, the
- * long-context key split (0 when n_q / n_kv * s_cap * 4 <= 32 KiB: attention
- * then runs on n_kv * head_dim / 32 workgroups of its own beside the
- * projections; otherwise every workgroup attends 1 / split of one kv head's
- * keys), the bytes of the launch-state block and the grid (one workgroup per
+ * long-context key split (0 when s_cap <= 1536 and n_q / n_kv * s_cap * 4 <=
+ * 32 KiB: attention then runs on n_kv * head_dim / 32 workgroups of its own
+ * beside the projections; otherwise every workgroup attends 1 / split of one
+ * kv head's keys), the bytes of the launch-state block and the grid (one workgroup per
  * CU). It handles batch 1, up to 64 layers, head_dim 32/64/128, n_q / n_kv in
  * {1, 2, 4, 8}, hidden (<= 4096), intermediate and n_q * head_dim multiples
  * of 512, and s_cap up to what one split's score rows fit in LDS (about

@@ -2,10 +2,12 @@
 per-device hand-over state) against ek_decode_step (the same step on a
 caller-allocated arena and barrier block), both called through the C ABI.
 
-Two calls in a row, the second with a smaller input (fewer layers, a
-shorter context and cache, so a smaller hand-over arena inside the same
-static array): each runs three consecutive steps on identical copies of the
-state and caches, and everything the step writes must be bit-identical --
+Three calls in a row, each with a smaller input than the one before (the
+first a split-attention bucket of 4096 keys, then attention-unit buckets
+with fewer layers and shorter contexts, so ever smaller hand-over arenas
+inside the same static array): each runs three consecutive steps on
+identical copies of the state and caches, and everything the step writes
+must be bit-identical --
 the step's logits, tokens, out_buf rows, positions, slot and length, the
 step counter and the new cache rows. The kernels are the same; only where
 the hand-over words live differs.
@@ -70,14 +72,16 @@ def _run(model, k, v, st, s_cap, steps, noalloc):
     return logits, out_tok
 
 
-@pytest.mark.parametrize("call", [0, 1])
+@pytest.mark.parametrize("call", [0, 1, 2])
 def test_noalloc_step_equals_the_arena_step(dev, call):
-    # call 0: three layers, context 300 in a 512-key cache; call 1 (after it):
-    # two layers, context 40 in a 64-key cache
-    layers, ctx, s_cap, seed = [(3, 300, 512, 5), (2, 40, 64, 6)][call]
+    # call 0: three layers, context 3000 in a 4096-key cache (split
+    # attention); call 1: three layers, context 300 in a 512-key cache;
+    # call 2: two layers, context 40 in a 64-key cache
+    layers, ctx, s_cap, seed, split = [(3, 3000, 4096, 5, True), (3, 300, 512, 7, False), (2, 40, 64, 6, False)][call]
     cfg = dict(C.QWEN3_4B, num_hidden_layers=layers)
     model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=seed), config=cfg)
-    assert model.persistent_plan(1, s_cap) is not None
+    plan = model.persistent_plan(1, s_cap)
+    assert plan is not None and (plan[1] > 0) == split
     print(f"no-alloc step: call {call}, {layers} layers, context {ctx}, cache {s_cap}", flush=True)
     k_a, v_a, st_a = _inputs(cfg, dev, ctx, s_cap, seed)
     k_b, v_b = [t.clone() for t in k_a], [t.clone() for t in v_a]
