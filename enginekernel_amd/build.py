@@ -25,6 +25,8 @@ LIB = os.path.join(HERE, "libek_hip.so")
 SOURCES = ["ek_abi.hip", "ek_norm.hip", "ek_gemv.hip", "ek_attn.hip", "ek_prefill.hip", "ek_spec.hip", "ek_step.hip"]
 # head dims of the persistent decode-step kernel; ek_step_inst.hip is compiled once per head dim
 STEP_HEAD_DIMS = [32, 64, 128]
+# row bounds of the batch decode-step kernel; ek_bstep_inst.hip is compiled once per bound
+BSTEP_ROWS = [2, 4, 8]
 # (prologue, epilogue) pairs of the GEMV family; ek_gemv_inst.hip is compiled
 # once per pair (must match EK_GEMV_PAIRS in csrc/ek_gemv_impl.h)
 GEMV_PAIRS = [(0, 0), (0, 1), (0, 2), (0, 3), (1, 0), (1, 2), (2, 0), (2, 2),
@@ -48,6 +50,8 @@ def _units():
                     [f"-DEK_PRO={pro}", f"-DEK_EPI={epi}"]))
     for d in STEP_HEAD_DIMS:
         out.append(("ek_step_inst.hip", f"ek_step_inst_{d}", [f"-DEK_STEP_D={d}"]))
+    for mb in BSTEP_ROWS:
+        out.append(("ek_bstep_inst.hip", f"ek_bstep_inst_{mb}", [f"-DEK_BSTEP_MB={mb}"]))
     return out
 
 

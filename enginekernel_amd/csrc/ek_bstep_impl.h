@@ -1,0 +1,674 @@
+// The persistent decode step at 2..8 batch rows: one launch per step, every
+// workgroup running every phase (engine.py:284-292 for B rows, the body the
+// reference captures: ek_model.py:360-416 decode + :490-493 argmax_token +
+// the tokens/positions/out_buf/step_idx advance).
+//
+// Per layer, on every workgroup (one per CU), for MB rows at once:
+//   wait dn words of the MB rows; r += dn; RMSNorm   (layer 0: the embedding rows)
+//   qkv rows: each weight chunk against the MB activation chunks in LDS -> qkv words
+//   split attention: unit (row b, kv head h, key split s) = workgroup
+//     b (n_kv S) + s n_kv + h, the batch-1 split kernel's unit (long_attention)
+//   wait att words; o rows -> o words; wait o words; r += o; RMSNorm
+//   gate/up rows + SwiGLU -> act words
+//   down rows over the act row in K slices of BSLICE chunks (MB rows of a
+//     9728-wide act row do not fit the LDS at once): wait the slice's act
+//     words, its partial products added into the same per-wave partials
+//   -> dn words
+// then the final add + norm, the lm_head rows (whole rows per wave, so each
+// wave keeps a running first-index argmax per batch row instead of per-row
+// partials) and the argmax words; workgroup 0 reduces them and advances the
+// step state of every row.
+//
+// Weights are read once per step whatever MB is: each 16-byte weight chunk
+// meets the MB activation chunks (LDS) on the bf16 dot instruction. The
+// residual rows are kept in LDS as bf16 (every add rounds to bf16, so this is
+// exact), one per batch row. Rows past the launch's m (MB is m rounded up to
+// 2, 4 or 8) compute on whatever their LDS rows hold and are never stored.
+#pragma once
+
+#include "ek_step_impl.h"
+
+namespace eks {
+
+static_assert(HC == 1, "the batch step keeps one copy of each hand-over region");
+
+#ifndef EK_BSTEP_LLW
+#define EK_BSTEP_LLW 16
+#endif
+constexpr int BLLW = EK_BSTEP_LLW;   // hand-over words in flight per thread (MB times the batch-1 words)
+// rows whose next activation chunk is read ahead of the current products
+// (at 8 rows the 8 extra chunks in registers spill, and the products of 8
+// rows cover the LDS round trip anyway)
+#ifndef EK_BSTEP_XA
+#define EK_BSTEP_XA 4
+#endif
+constexpr int BSLICE = 10;    // activation chunks per LDS slice of a row (5120 bf16)
+
+// ---------------------------------------------------------------------------
+// projections over MB activation rows
+// ---------------------------------------------------------------------------
+// A wave's items of one phase: item i -> (row i / C, chunk i % C) of the
+// workgroup's share, gate rows then up rows for a pair phase; rows are ldw
+// elements apart (ldw > K for a K slice of a wider matrix).
+struct BSpan {
+  const bf16_t* g;    // row u0 of the share
+  const bf16_t* up;   // row up_off + u0 (pair phases)
+  int nu;             // rows of the first half (every row of a plain phase)
+  int C;
+  int64_t ldw;
+  int i0, n;          // this wave's items [i0, i0 + n)
+};
+
+// by_rows: the wave's items are whole rows (rows split evenly over the waves)
+__device__ __forceinline__ BSpan make_bspan(const Gp& P, int64_t ldw, int wave, bool by_rows) {
+  int u0, u1;
+  unit_range(P, u0, u1);
+  const int nu = u1 - u0;
+  BSpan s;
+  s.g = P.w + (int64_t)u0 * ldw;
+  s.up = P.pair ? P.w + (int64_t)(P.up_off + u0) * ldw : s.g;
+  s.nu = P.pair ? nu : 0x7fffffff;
+  s.C = P.C;
+  s.ldw = ldw;
+  if (by_rows) {
+    const int r0 = (int)((uint32_t)nu * (uint32_t)wave / (uint32_t)SNW);
+    const int r1 = (int)((uint32_t)nu * (uint32_t)(wave + 1) / (uint32_t)SNW);
+    s.i0 = r0 * P.C;
+    s.n = (r1 - r0) * P.C;
+  } else {
+    const WaveItems w = wave_items(P, nu, wave);
+    s.i0 = w.i0;
+    s.n = w.n;
+  }
+  return s;
+}
+
+__device__ __forceinline__ const bf16_t* bspan_at(const BSpan& s, int r, int c) {
+  return (r < s.nu ? s.g + (int64_t)r * s.ldw : s.up + (int64_t)(r - s.nu) * s.ldw) + c * CH;
+}
+
+template <int CNT>
+__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring) {
+  const BSpan s = make_bspan(P, ldw, wave_id(), by_rows);
+  const int loff = (opaque_tid() & 63) * 8;
+  int r = s.i0 / s.C, c = s.i0 - (s.i0 / s.C) * s.C;
+#pragma unroll
+  for (int u = 0; u < CNT; ++u) {
+    ring.r[u] = ld16_nt(bspan_at(s, r, c) + loff);
+    if (u + 1 < s.n && ++c == s.C) { c = 0; ++r; }
+  }
+  ring.nready = CNT;
+}
+
+// The wave's row sums over MB activation rows, handed per finished row (or
+// row part, where a wave's items start or end inside a row) to
+// sink(row, acc), in lane 63: PartWriter stores (or, for the K slices of one
+// matrix, adds) them as per-wave partials, ArgmaxSink (lm_head, whole rows
+// per wave) keeps a running argmax. The ring works as in gemv_phase.
+template <int MB, typename SINK>
+__device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+                                             int xstride, SINK& sink) {
+  const int lane = opaque_tid() & 63, wave = wave_id();
+  const BSpan sp = make_bspan(P, ldw, wave, by_rows);
+  const int n = sp.n, C = sp.C;
+  const int loff = lane * 8;
+  // refill cursor: the item NB places ahead of the one consumed (the last
+  // item again past the end)
+  int rf = sp.i0 / C, cf = sp.i0 - (sp.i0 / C) * C;
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    if (u >= ring.nready) ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
+    if (u + 1 < n && ++cf == C) { cf = 0; ++rf; }
+  }
+  int kf = NB < n ? NB : n - 1;   // item index of the cursor
+  int r = sp.i0 / C, ch = sp.i0 - (sp.i0 / C) * C;
+  uint4 xc[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) xc[m] = *reinterpret_cast<const uint4*>(xs + m * xstride + ch * CH + loff);
+  float acc[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+  auto flush = [&](int row) {
+    wave_sums_dpp_lane63<MB>(acc);
+    if (lane == 63) sink(row, acc);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+  };
+  // the next item's activation chunks are read ahead of this item's products
+  // (up to EK_BSTEP_XA rows; beyond, after them)
+  constexpr int XA = MB <= EK_BSTEP_XA ? MB : 0;
+  auto step = [&](const uint4& w) {
+    const int chn = ch + 1 == C ? 0 : ch + 1;
+    uint4 xn[XA > 0 ? XA : 1];
+#pragma unroll
+    for (int m = 0; m < XA; ++m) xn[m] = *reinterpret_cast<const uint4*>(xs + m * xstride + chn * CH + loff);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[m] = step_dot8(w, xc[m], acc[m]);
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+      xc[m] = m < XA ? xn[m < XA ? m : 0] : *reinterpret_cast<const uint4*>(xs + m * xstride + chn * CH + loff);
+  };
+  int k0 = 0;
+  for (; k0 + NB <= n; k0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      step(ring.r[u]);
+      ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
+      if (kf + 1 < n) {
+        ++kf;
+        if (++cf == C) { cf = 0; ++rf; }
+      }
+      if (ch == C - 1) flush(r);
+      if (++ch == C) { ch = 0; ++r; }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    if (k0 + u < n) {
+      step(ring.r[u]);
+      if (ch == C - 1 || k0 + u == n - 1) flush(r);
+      if (++ch == C) { ch = 0; ++r; }
+    }
+  }
+  if (k0 == n && n > 0 && ch != 0) flush(r);   // the wave's items ended inside a row at a block edge
+  ring.nready = 0;
+}
+
+template <int MB, bool ACC>
+struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= acc[m]
+  float* part;
+  int wave;
+  __device__ void operator()(int row, const float* acc) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      float* p = part + (row * SNW + wave) * MB + m;
+      *p = ACC ? *p + acc[m] : acc[m];
+    }
+  }
+};
+
+template <int MB>
+__device__ __forceinline__ float row_sum_b(const float* part, int r, int m) {
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < SNW; ++w) s += part[(r * SNW + w) * MB + m];
+  return s;
+}
+
+// row m's out word (u0 + 2i) / 2 at out + m * rw + u0 / 2 + i, rows m < nrows
+template <int MB>
+__device__ __forceinline__ void epilogue_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw, int nrows,
+                                              uint32_t ep) {
+  int u0, u1;
+  unit_range(P, u0, u1);
+  const int np = (u1 - u0) / 2;
+  for (int i = threadIdx.x; i < np * nrows; i += SNT) {
+    const int m = i / np, p = i - m * np;
+    const uint32_t w = pack2(row_sum_b<MB>(part, 2 * p, m), row_sum_b<MB>(part, 2 * p + 1, m));
+    ll_put(out + m * rw + u0 / 2 + p, w, ep);
+  }
+}
+
+template <int MB>
+__device__ __forceinline__ float swiglu_one_b(const float* part, int nu, int ul, int m) {
+  const float gt = rbf(row_sum_b<MB>(part, ul, m));
+  const float up = rbf(row_sum_b<MB>(part, nu + ul, m));
+  const float s = rbf(gt / (1.0f + expf(-gt)));
+  return s * up;
+}
+
+template <int MB>
+__device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw,
+                                                     int nrows, uint32_t ep) {
+  int u0, u1;
+  unit_range(P, u0, u1);
+  const int nu = u1 - u0, np = nu / 2;
+  for (int i = threadIdx.x; i < np * nrows; i += SNT) {
+    const int m = i / np, p = i - m * np;
+    const uint32_t w = pack2(swiglu_one_b<MB>(part, nu, 2 * p, m), swiglu_one_b<MB>(part, nu, 2 * p + 1, m));
+    ll_put(out + m * rw + u0 / 2 + p, w, ep);
+  }
+}
+
+// rr (bf16 pairs, [MB][k / 2]) = bf16(rr + x) for rows m < nrows (x pairs
+// [m][k / 2] in xw, or no add when xw is null); xs row m (xstride apart) =
+// bf16(w * bf16(rr * rsqrt(mean(rr^2) + eps)))   (ek_kernels.py:1025-1059)
+template <int MB>
+__device__ __forceinline__ void add_norm_b(uint32_t* rr, const uint32_t* xw, const uint32_t* gw, int k, int nrows,
+                                           float eps, bf16_t* xs, int xstride, float* red) {
+  const int tid = opaque_tid(), lane = tid & 63, wave = wave_id();
+  const int nw = k / 2;
+  float ss[MB];
+  uint32_t rv[MB][NGW];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    ss[m] = 0.f;
+    if (m >= nrows) continue;
+#pragma unroll
+    for (int j = 0; j < NGW; ++j) {
+      const int i = tid + j * SNT;
+      const int ic = i < nw ? i : 0;
+      uint32_t r = rr[m * nw + ic];
+      if (xw) {
+        const uint32_t x = xw[m * nw + ic];
+        r = pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x));
+      }
+      rv[m][j] = r;
+      const float msk = i < nw ? 1.f : 0.f;
+      ss[m] = fmaf(lo_bf(r) * msk, lo_bf(r), ss[m]);
+      ss[m] = fmaf(hi_bf(r) * msk, hi_bf(r), ss[m]);
+    }
+  }
+  if (xw) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      if (m >= nrows) continue;
+#pragma unroll
+      for (int j = 0; j < NGW; ++j) {
+        const int i = tid + j * SNT;
+        if (i < nw) rr[m * nw + i] = rv[m][j];
+      }
+    }
+  }
+  wave_sums_dpp_lane63<MB>(ss);
+  if (lane == 63) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) red[wave * MB + m] = ss[m];
+  }
+  __syncthreads();
+  uint32_t* xs32 = reinterpret_cast<uint32_t*>(xs);
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    if (m >= nrows) continue;
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < SNW; ++w) t += red[w * MB + m];
+    const float rstd = 1.0f / sqrtf(t / (float)k + eps);
+#pragma unroll
+    for (int j = 0; j < NGW; ++j) {
+      const int i = tid + j * SNT;
+      const float o0 = rbf(lo_bf(gw[j]) * rbf(lo_bf(rv[m][j]) * rstd));
+      const float o1 = rbf(hi_bf(gw[j]) * rbf(hi_bf(rv[m][j]) * rstd));
+      if (i < nw) xs32[m * (xstride / 2) + i] = pack2(o0, o1);
+    }
+  }
+  const int kpad = kpad_of(k);
+  for (int m = 0; m < nrows; ++m) zero_pad(xs + m * xstride, k, kpad);
+}
+
+// lm_head rows of this wave (whole rows): a running first-index argmax per
+// batch row, kept in lane 63 (where the row sums land), and the optional
+// logits
+template <int MB>
+struct ArgmaxSink {
+  float bv[MB];
+  int bi[MB];
+  bf16_t* logits;      // [nrows][vocab] or null
+  int vocab, nrows, u0;
+  __device__ void operator()(int row, const float* acc) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float v = rbf(acc[m]);
+      const int idx = u0 + row;
+      if (logits && m < nrows) logits[(int64_t)m * vocab + idx] = (bf16_t)f2bf(v);
+      if (am_better(v, idx, bv[m], bi[m])) { bv[m] = v; bi[m] = idx; }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// the batch step
+// ---------------------------------------------------------------------------
+__host__ __device__ inline size_t bstep_rr_bytes(int mb, int h) { return eka::align16((size_t)mb * h * 2); }
+// activation rows: MB rows of the widest LDS row (hidden, n_q D or a slice)
+__host__ __device__ inline int bstep_xcols(int h, int qw) {
+  int x = kpad_of(h);
+  x = x > qw ? x : qw;
+  x = x > BSLICE * CH ? x : BSLICE * CH;
+  return x;
+}
+// part rows of the largest projection share (lm_head keeps no partials)
+__host__ __device__ inline int bstep_part_rows(int h, int inter, int qkvw, int nwg) {
+  int r = 2 * cdiv_i(qkvw / 2, nwg);
+  r = r > 2 * cdiv_i(h / 2, nwg) ? r : 2 * cdiv_i(h / 2, nwg);
+  r = r > 4 * cdiv_i(inter / 2, nwg) ? r : 4 * cdiv_i(inter / 2, nwg);
+  return r;
+}
+
+// Words of nrows rows (rw words apart, sw of each) into LDS rows xw words
+// apart: i -> row i / xw, word i % xw (past sw: the row's last word again,
+// a tail the products do not read)
+struct RowsSrc {
+  const llw_t* p;
+  int rw, sw, xw;
+  __device__ const llw_t* operator()(int i) const {
+    const int m = i / xw, j = i - m * xw;
+    return p + (int64_t)m * rw + (j < sw ? j : sw - 1);
+  }
+};
+
+template <int D, int G, int MB>
+__device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt, uint32_t ep, int64_t hi,
+                                           unsigned char* smem, float* s_red, int* s_fail
+#ifdef EK_STEP_TRACE
+                                           , int64_t* ts_lds
+#endif
+                                           ) {
+  const int tid = threadIdx.x;
+  const int h = a.h, inter = a.inter, nrows = a.m;
+  const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
+  const int64_t lwords = (int64_t)MB * arena_layer_words(h, inter, qkvw, qw);
+  const int xcols = bstep_xcols(h, qw);
+
+  uint32_t* rr = reinterpret_cast<uint32_t*>(smem);
+  unsigned char* ph = smem + bstep_rr_bytes(MB, h);
+  bf16_t* xs = reinterpret_cast<bf16_t*>(ph);
+  uint32_t* xs32 = reinterpret_cast<uint32_t*>(ph);
+  float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)MB * xcols * 2));
+  const int part_n = a.part_max * SNW * MB;
+  PartWriter<MB, false> put{part, wave_id()};
+  PartWriter<MB, true> add{part, wave_id()};
+
+  // attention unit of this workgroup
+  const int S = a.lsplit;
+  const int ub = (int)blockIdx.x / (a.nkv * S), ur = (int)blockIdx.x - ub * (a.nkv * S);
+  const int uh = ur % a.nkv, us = ur / a.nkv;
+  const bool attends = ub < nrows;
+
+  Ring ring;
+  ring.nready = 0;
+#pragma unroll
+  for (int u = 0; u < NB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
+  uint32_t gw1[NGW], gw2[NGW];
+  load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
+
+  llw_t* lx_base = a.arena + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB;
+  const int64_t lx_row = long_words(a.nkv, S, G, D);
+  const int nsl = cdiv_i(inter, BSLICE * CH);   // K slices of the down projection
+
+  const llw_t* dn_prev = nullptr;
+  for (int l = 0; l < a.nl; ++l) {
+    const int64_t* lw = lwt + l * LW_FIELDS;
+    llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
+    llw_t* att_ll = qkv_ll + (int64_t)MB * qkvw / 2;
+    llw_t* o_ll = att_ll + (int64_t)MB * qw / 2;
+    llw_t* act_ll = o_ll + (int64_t)MB * h / 2;
+    llw_t* dn_ll = act_ll + (int64_t)MB * inter / 2;
+    const Gp gq = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 2);
+    const Gp go = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 2);
+    const Gp gg = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 2);
+    const bf16_t* wdown = reinterpret_cast<const bf16_t*>(lw[LW_DOWN]);
+    auto down_slice = [&](int sl) {
+      const int c0 = sl * BSLICE, c1 = (sl + 1) * BSLICE < inter / CH ? (sl + 1) * BSLICE : inter / CH;
+      return make_gp(wdown + c0 * CH, (c1 - c0) * CH, h, 0, 2);
+    };
+
+    // ---- r = (layer 0) embed[token] | r + down(l-1); norm; qkv
+    EK_TS(0);
+    zero_part(part, part_n);
+    if (l == 0) {
+      for (int m = 0; m < nrows; ++m) {
+        int64_t t = a.tokens[m];
+        t = t < 0 ? 0 : (t >= a.vocab ? a.vocab - 1 : t);
+        const uint32_t* e32 = reinterpret_cast<const uint32_t*>(a.embed + t * a.lde);
+        for (int i = tid; i < h / 2; i += SNT) rr[m * (h / 2) + i] = e32[i];
+      }
+      __syncthreads();
+      add_norm_b<MB>(rr, nullptr, gw1, h, nrows, a.eps, xs, xcols, s_red);
+    } else {
+      const bool ok = ll_read<BLLW>(LinSrc{dn_prev}, nrows * (h / 2), ep, xs32, a.err, a.spin);
+      if (!wg_all(ok, s_fail)) return false;
+      add_norm_b<MB>(rr, xs32, gw1, h, nrows, a.eps, xs, xcols, s_red);
+    }
+    __syncthreads();
+    EK_TS(1);
+    gemv_phase_b<MB>(gq, h, false, ring, xs, xcols, put);
+    __syncthreads();
+    EK_TS(2);
+    epilogue_ll_b<MB>(gq, part, qkv_ll, qkvw / 2, nrows, ep);
+    __syncthreads();
+    EK_TS(3);
+
+    // ---- split attention (its LDS overlays the activation rows and partials)
+    if (attends) {
+      const uint32_t ltag = ep * (uint32_t)MAX_LAYERS + (uint32_t)l;
+      if (!long_attention<D, G>(a, lw, qkv_ll + (int64_t)ub * (qkvw / 2), att_ll + (int64_t)ub * (qw / 2), 0,
+                                lx_base + ub * lx_row, ub, uh, us, hi, ep, ltag, ph, s_fail
+#ifdef EK_STEP_TRACE
+                                , ts_lds
+#endif
+                                ))
+        return false;
+    }
+    EK_TS(4);
+    prefetch_phase_b<PF>(go, qw, false, ring);
+    load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
+    __syncthreads();
+
+    // ---- o projection
+    zero_part(part, part_n);
+    {
+      // row m's words land xcols / 2 words apart (the tail of each LDS row
+      // re-reads the row's last word and is not used)
+      const bool ok = ll_read<BLLW>(RowsSrc{att_ll, qw / 2, qw / 2, xcols / 2}, (nrows - 1) * (xcols / 2) + qw / 2, ep,
+                                    xs32, a.err, a.spin);
+      if (!wg_all(ok, s_fail)) return false;
+    }
+    EK_TS(6);
+    __syncthreads();
+    gemv_phase_b<MB>(go, qw, false, ring, xs, xcols, put);
+    __syncthreads();
+    EK_TS(7);
+    epilogue_ll_b<MB>(go, part, o_ll, h / 2, nrows, ep);
+    EK_TS(8);
+    prefetch_phase_b<PF>(gg, h, false, ring);
+
+    // ---- r = r + o; norm; gate/up; SwiGLU
+    __syncthreads();
+    zero_part(part, part_n);
+    {
+      const bool ok = ll_read<BLLW>(LinSrc{o_ll}, nrows * (h / 2), ep, xs32, a.err, a.spin);
+      if (!wg_all(ok, s_fail)) return false;
+    }
+    EK_TS(16);
+    add_norm_b<MB>(rr, xs32, gw2, h, nrows, a.eps, xs, xcols, s_red);
+    load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm, h, gw1);
+    __syncthreads();
+    EK_TS(9);
+    gemv_phase_b<MB>(gg, h, false, ring, xs, xcols, put);
+    __syncthreads();
+    EK_TS(10);
+    epilogue_swiglu_ll_b<MB>(gg, part, act_ll, inter / 2, nrows, ep);
+    EK_TS(11);
+    prefetch_phase_b<PF>(down_slice(0), inter, false, ring);
+
+    // ---- down projection, one K slice of the act rows at a time
+    __syncthreads();
+    zero_part(part, part_n);
+    for (int sl = 0; sl < nsl; ++sl) {
+      const Gp gd = down_slice(sl);
+      const int c0 = sl * BSLICE;
+      const int sw = gd.K / 2;   // words of a row's slice
+      if (sl > 0) __syncthreads();   // the previous slice's products have read their LDS rows
+      {
+        const bool ok = ll_read<BLLW>(RowsSrc{act_ll + c0 * (CH / 2), inter / 2, sw, xcols / 2},
+                                      (nrows - 1) * (xcols / 2) + sw, ep, xs32, a.err, a.spin);
+        if (!wg_all(ok, s_fail)) return false;
+      }
+      if (sl == 0) EK_TS(20);
+      else EK_TS(21);
+      __syncthreads();
+      gemv_phase_b<MB>(gd, inter, false, ring, xs, xcols, add);
+      if (sl == 0) EK_TS(12);
+      else EK_TS(13);
+      // the next slice's first chunks, or the next phase's (every iteration
+      // leaves the ring in the same state, so the products above see a
+      // prefetched ring at compile time)
+      if (sl + 1 < nsl)
+        prefetch_phase_b<PF>(down_slice(sl + 1), inter, false, ring);
+      else if (l + 1 < a.nl)
+        prefetch_phase_b<PF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
+                                     0, 2), h, false, ring);
+      else
+        prefetch_phase_b<PF>(make_gp(a.lm_head, h, a.vocab, 0, 1), h, true, ring);
+    }
+    __syncthreads();
+    epilogue_ll_b<MB>(down_slice(0), part, dn_ll, h / 2, nrows, ep);
+    EK_TS(14);
+    dn_prev = dn_ll;
+    __syncthreads();
+    EK_TS_FLUSH(l);
+  }
+
+  // ---- final add + norm, lm_head, per-workgroup argmax per row
+  {
+    const bool ok = ll_read<BLLW>(LinSrc{dn_prev}, nrows * (h / 2), ep, xs32, a.err, a.spin);
+    if (!wg_all(ok, s_fail)) return false;
+  }
+  add_norm_b<MB>(rr, xs32, gw1, h, nrows, a.eps, xs, xcols, s_red);
+  __syncthreads();
+  const Gp gl = make_gp(a.lm_head, h, a.vocab, 0, 1);
+  int u0, u1;
+  unit_range(gl, u0, u1);
+  ArgmaxSink<MB> am;
+#pragma unroll
+  for (int m = 0; m < MB; ++m) { am.bv[m] = -INFINITY; am.bi[m] = 0x7fffffff; }
+  am.logits = a.logits;
+  am.vocab = a.vocab;
+  am.nrows = nrows;
+  am.u0 = u0;
+  gemv_phase_b<MB>(gl, h, true, ring, xs, xcols, am);
+  // the waves' bests (lane 63) -> the workgroup's, per row -> two words per row
+  float* sv = reinterpret_cast<float*>(ph);            // [SNW][MB] (the activation rows are no longer read)
+  int* si = reinterpret_cast<int*>(ph) + SNW * MB;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 63) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) { sv[wave_id() * MB + m] = am.bv[m]; si[wave_id() * MB + m] = am.bi[m]; }
+  }
+  __syncthreads();
+  llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
+  if (tid < nrows) {
+    float ov = sv[tid];
+    int oi = si[tid];
+    for (int w = 1; w < SNW; ++w)
+      if (am_better(sv[w * MB + tid], si[w * MB + tid], ov, oi)) { ov = sv[w * MB + tid]; oi = si[w * MB + tid]; }
+    ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid), __float_as_uint(ov), ep);
+    ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid) + 1, (uint32_t)oi, ep);
+  }
+  return true;
+}
+
+// Workgroup 0's end of the step: per row, the first-index argmax over every
+// workgroup's words, then the step's bookkeeping for every row (as the
+// batch-1 finish_step; a step that gave up writes -1 for every row).
+template <int MB>
+__device__ __forceinline__ void finish_step_b(const StepArgs& a, uint32_t ep, bool ok, int64_t len_old, int qw,
+                                              int qkvw, unsigned char* smem, float* s_red, int* s_redi, int* s_fail) {
+  const int tid = threadIdx.x, nrows = a.m;
+  const int64_t lwords = (int64_t)MB * arena_layer_words(a.h, a.inter, qkvw, qw);
+  const llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
+  const int nwg = (int)gridDim.x;
+  uint32_t* amw = reinterpret_cast<uint32_t*>(smem + bstep_rr_bytes(MB, a.h));
+  int* toks = reinterpret_cast<int*>(amw + 2 * nwg * MB);
+  __syncthreads();
+  if (ok) {
+    struct Src {   // workgroup w's two words of row m at 2 (w MB + m)
+      const llw_t* p; int nrows;
+      __device__ const llw_t* operator()(int i) const {
+        const int w = i / (2 * nrows), j = i - w * (2 * nrows);
+        return p + 2 * (int64_t)w * MB + j;
+      }
+    };
+    ok = wg_all(ll_read<BLLW>(Src{am_ll, nrows}, 2 * nwg * nrows, ep, amw, a.err, a.spin), s_fail);
+  }
+  if (ok) {
+    for (int m = 0; m < nrows; ++m) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int w = tid; w < nwg; w += SNT) {
+        const float v = __uint_as_float(amw[2 * (w * nrows + m)]);
+        const int i = (int)amw[2 * (w * nrows + m) + 1];
+        if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+      }
+      float ov;
+      int oi;
+      wg_argmax(bv, bi, s_red, s_redi, ov, oi);
+      if (tid == 0) toks[m] = oi == 0x7fffffff ? 0 : oi;
+      __syncthreads();
+    }
+  }
+  if (tid == 0) {
+    const int64_t step = *a.step_idx;
+    for (int m = 0; m < nrows; ++m) {
+      const int64_t tok = !ok ? -1 : toks[m];
+      if (a.out_tok) a.out_tok[m] = tok;
+      if (step >= 0 && step < a.max_steps) a.out_buf[step * nrows + m] = (int32_t)tok;
+      if (ok) {
+        a.tokens[m] = tok;
+        a.positions[m] += 1;
+        a.slot_t[m] = len_old;
+      }
+    }
+    if (ok) *a.len_t = len_old + 1;
+    *a.step_idx = step + 1;
+  }
+}
+
+template <int D, int G, int MB>
+__global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float s_red[SNW * MB];
+  __shared__ int s_redi[SNW];
+  __shared__ unsigned s_ep;
+  __shared__ int s_abort;
+  __shared__ int s_fail;
+  __shared__ int64_t s_lw[MAX_LAYERS * LW_FIELDS];
+#ifdef EK_STEP_TRACE
+  __shared__ int64_t s_ts[48];
+  int64_t* ts_lds = s_ts;
+#endif
+
+  const int tid = threadIdx.x;
+  for (int i = tid; i < a.nl * LW_FIELDS; i += SNT) s_lw[i] = a.lw[i];
+  if (tid == 0) {
+    s_fail = 0;
+    const unsigned e = __hip_atomic_load(&a.bar->ep[blockIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    __hip_atomic_store(&a.bar->ep[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_ep = e;
+    s_abort = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  const uint32_t ep = s_ep;
+  const int64_t len_old = *a.len_t;
+  int64_t hi = len_old + 1;
+  hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
+  bool ok = s_abort == 0;
+  if (ok) ok = batch_pass<D, G, MB>(a, s_lw, ep, hi, smem, s_red, &s_fail
+#ifdef EK_STEP_TRACE
+                                     , ts_lds
+#endif
+                                     );
+  if (blockIdx.x != 0) return;
+  finish_step_b<MB>(a, ep, ok, len_old, a.nq * D, (a.nq + 2 * a.nkv) * D, smem, s_red, s_redi, &s_fail);
+}
+
+// LDS bytes of batch_step_kernel<D, G, MB>
+template <int D, int G, int MB>
+inline size_t bstep_lds_bytes(int h, int qw, int part_rows, int lchunk, int nwg) {
+  const size_t rr = bstep_rr_bytes(MB, h);
+  const size_t gemv = eka::align16((size_t)MB * bstep_xcols(h, qw) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4);
+  const size_t attn = LongLds<D, G>::bytes(lchunk);
+  const size_t fin = (size_t)2 * nwg * MB * 4 + (size_t)MB * 4;
+  size_t x = gemv > attn ? gemv : attn;
+  x = x > fin ? x : fin;
+  return rr + x;
+}
+
+// launch / occupancy of one batch instantiation (ek_bstep_inst.hip, one per MB)
+template <int MB>
+hipError_t launch_bstep(const StepArgs& a, int g, int nwg, hipStream_t st);
+template <int MB>
+int bstep_occupancy(int g, size_t lds);
+
+}  // namespace eks

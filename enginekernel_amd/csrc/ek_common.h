@@ -124,6 +124,16 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// The thread index, opaque to the optimizer: per-lane offsets derived from
+// it are then computed where they are used instead of hoisted out of a
+// caller's loop (where they would stay live, in registers, across
+// everything else the loop does).
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  __asm__ volatile("" : "+v"(t));
+  return t;
+}
+
 // index of this thread's wave in the workgroup, as a wave-uniform (scalar) value
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 

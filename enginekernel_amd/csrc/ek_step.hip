@@ -1,7 +1,7 @@
 // C ABI of the persistent decode-step kernel (ek_step_impl.h): the plan query
 // and the launch.
 
-#include "ek_step_impl.h"
+#include "ek_bstep_impl.h"
 #include "ek_abi_internal.h"
 #include "ek_hip.h"
 
@@ -16,6 +16,12 @@ template <> hipError_t launch_step<128>(const StepArgs&, int, int, hipStream_t);
 template <> int step_occupancy<32>(int, bool, size_t);
 template <> int step_occupancy<64>(int, bool, size_t);
 template <> int step_occupancy<128>(int, bool, size_t);
+template <> hipError_t launch_bstep<2>(const StepArgs&, int, int, hipStream_t);
+template <> hipError_t launch_bstep<4>(const StepArgs&, int, int, hipStream_t);
+template <> hipError_t launch_bstep<8>(const StepArgs&, int, int, hipStream_t);
+template <> int bstep_occupancy<2>(int, size_t);
+template <> int bstep_occupancy<4>(int, size_t);
+template <> int bstep_occupancy<8>(int, size_t);
 }  // namespace eks
 
 // The no-allocation entry point's state: the launch-state block (Bar,
@@ -57,6 +63,7 @@ int step_grid() {
 }
 
 struct Plan {
+  int mb;               // batch rows of the kernel (1, or m rounded up to 2, 4, 8: the batch kernel)
   int nwg, kpad_max, part_max, o_rows;
   int lsplit, lchunk;   // long contexts: key splits per kv head and keys per split (0: the attention-unit kernel)
   int64_t lx;           // long contexts: hand-over words of the splits' exchange
@@ -105,10 +112,77 @@ int resident_per_cu(int d, int g, bool lng, size_t lds) {
   return n;
 }
 
+int resident_batch(int mb, int g, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, int, size_t>, int> cache;
+  const auto key = std::make_tuple(mb, g, lds);
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  const int n = mb == 2 ? eks::bstep_occupancy<2>(g, lds) : mb == 4 ? eks::bstep_occupancy<4>(g, lds)
+                                                                     : eks::bstep_occupancy<8>(g, lds);
+  cache[key] = n;
+  return n;
+}
+
+hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
+                     int64_t m, int64_t s_cap, int64_t n_layers, Plan& p);
+
+// The batch kernel's plan (2..8 rows, ek_bstep_impl.h): every workgroup runs
+// the projections of all rows and one attention unit (row, kv head, key
+// split); the shape checks common to both kernels are done by the caller.
+hipError_t make_batch_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
+                           int64_t m, int64_t s_cap, int64_t n_layers, Plan& p) {
+  if (head_dim != 128) return ek_fail(hipErrorInvalidValue, "decode_step: batches of 2-8 rows need head_dim 128");
+  const int g = (int)(n_q / n_kv);
+  p.mb = m <= 2 ? 2 : m <= 4 ? 4 : 8;
+  const int mb = p.mb;
+  int sp = 1;
+  while (2 * sp <= 64 && 2 * sp <= head_dim / 2 && (int64_t)2 * sp * n_kv * mb <= p.nwg) sp *= 2;
+  if ((int64_t)sp * n_kv * mb > p.nwg) return ek_fail(hipErrorInvalidValue, "decode_step: too many attention units");
+  const int64_t chunk = (s_cap + sp - 1) / sp;
+  if (chunk > (1 << 16))
+    return ek_fail(hipErrorInvalidValue, "decode_step: the context's score rows exceed the LDS of one split");
+  p.lsplit = sp;
+  p.lchunk = (int)chunk;
+  p.lx = (int64_t)mb * eks::long_words((int)n_kv, sp, g, 128);
+  const int qw = (int)(n_q * head_dim), qkvw = (int)((n_q + 2 * n_kv) * head_dim);
+  p.kpad_max = eks::bstep_xcols((int)hidden, qw);
+  p.part_max = eks::bstep_part_rows((int)hidden, (int)inter, qkvw, p.nwg);
+  p.o_rows = 0;
+  size_t lds = 0;
+  switch (mb) {
+    case 2: lds = g == 1 ? eks::bstep_lds_bytes<128, 1, 2>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                : g == 2 ? eks::bstep_lds_bytes<128, 2, 2>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                : g == 4 ? eks::bstep_lds_bytes<128, 4, 2>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                         : eks::bstep_lds_bytes<128, 8, 2>((int)hidden, qw, p.part_max, p.lchunk, p.nwg);
+            break;
+    case 4: lds = g == 1 ? eks::bstep_lds_bytes<128, 1, 4>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                : g == 2 ? eks::bstep_lds_bytes<128, 2, 4>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                : g == 4 ? eks::bstep_lds_bytes<128, 4, 4>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                         : eks::bstep_lds_bytes<128, 8, 4>((int)hidden, qw, p.part_max, p.lchunk, p.nwg);
+            break;
+    default: lds = g == 1 ? eks::bstep_lds_bytes<128, 1, 8>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                 : g == 2 ? eks::bstep_lds_bytes<128, 2, 8>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                 : g == 4 ? eks::bstep_lds_bytes<128, 4, 8>((int)hidden, qw, p.part_max, p.lchunk, p.nwg)
+                          : eks::bstep_lds_bytes<128, 8, 8>((int)hidden, qw, p.part_max, p.lchunk, p.nwg);
+  }
+  p.lds = lds;
+  if (p.lds > kLdsLimit)
+    return ek_fail(hipErrorInvalidValue, "decode_step: this batch's rows or context exceed the workgroup's LDS");
+  p.arena_bytes = 8 * ((int64_t)mb * n_layers * eks::arena_layer_words((int)hidden, (int)inter, qkvw, qw) +
+                       2 * (int64_t)p.nwg * mb + p.lx);
+  if (resident_batch(mb, g, p.lds) < 1)
+    return ek_fail(hipErrorInvalidValue, "decode_step: one workgroup per CU does not fit (registers or LDS)");
+  (void)vocab;
+  return hipSuccess;
+}
+
 // Returns an error (with a message) when the shape is outside what the kernel handles.
 hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
                      int64_t m, int64_t s_cap, int64_t n_layers, Plan& p) {
-  if (m != 1) return ek_fail(hipErrorInvalidValue, "decode_step: batch must be 1 (use the per-kernel step)");
+  if (m < 1 || m > 8) return ek_fail(hipErrorInvalidValue, "decode_step: batch must be 1 to 8 rows");
+  p.mb = 1;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128)
     return ek_fail(hipErrorInvalidValue, "decode_step: head_dim must be 32, 64 or 128");
   if (n_kv < 1 || n_q < n_kv || n_q % n_kv) return ek_fail(hipErrorInvalidValue, "decode_step: bad head counts");
@@ -127,6 +201,7 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   if (s_cap < 1) return ek_fail(hipErrorInvalidValue, "decode_step: empty cache");
   p.nwg = step_grid();
   if (p.nwg < 1 || p.nwg > eks::MAX_WG) return ek_fail(hipErrorInvalidValue, "decode_step: unsupported device");
+  if (m > 1) return make_batch_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
   // Short rows run on attention-only workgroups beside the projections
   // (kUnitMaxKeys above); longer ones on every workgroup, the
   // keys of each kv head split S ways (S a power of two, at most 64 and at
@@ -235,7 +310,15 @@ hipError_t decode_step_impl(const int64_t* layer_ptrs, int64_t n_layers, int64_t
   a.bar = (eks::Bar*)barrier; a.err = err; a.spin = ek_wait_limit(kSpin);
   a.kpad_max = p.kpad_max; a.part_max = p.part_max; a.o_rows = p.o_rows;
   a.lsplit = p.lsplit; a.lchunk = p.lchunk; a.lx = p.lx;
+  a.m = (int)m;
   const int g = (int)(n_q / n_kv);
+  if (p.mb > 1) {
+    switch (p.mb) {
+      case 2: return eks::launch_bstep<2>(a, g, p.nwg, st);
+      case 4: return eks::launch_bstep<4>(a, g, p.nwg, st);
+      default: return eks::launch_bstep<8>(a, g, p.nwg, st);
+    }
+  }
   switch (head_dim) {
     case 32: return eks::launch_step<32>(a, g, p.nwg, st);
     case 64: return eks::launch_step<64>(a, g, p.nwg, st);

@@ -110,6 +110,7 @@ struct StepArgs {
   // partial outputs (one region for every layer: its words carry the layer in their tag)
   int lsplit, lchunk;
   int64_t lx;
+  int m;                               // batch rows (the batch kernel, ek_bstep_impl.h; 0 for batch 1)
 };
 
 __host__ __device__ constexpr int cdiv_i(int a, int b) { return (a + b - 1) / b; }
@@ -802,9 +803,11 @@ struct LongLds {
 };
 
 template <int D, int G>
+// Unit (kv head h, split s) of batch row b; qkv, att and lx point at row b's
+// words (att's copies att_cstride words apart).
 __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
-                                               llw_t* lx, int64_t hi, uint32_t ep, uint32_t ltag, unsigned char* lds,
-                                               int* s_fail
+                                               int64_t att_cstride, llw_t* lx, int b, int h, int s, int64_t hi,
+                                               uint32_t ep, uint32_t ltag, unsigned char* lds, int* s_fail
 #ifdef EK_STEP_TRACE
                                                , int64_t* ts_lds
 #endif
@@ -816,9 +819,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   constexpr int NKG = SNT / DCH;   // key groups of the PV product
   constexpr int VR = LVR;          // value rows per thread in flight
   const int S = a.lsplit;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int tid = opaque_tid(), lane = tid & 63, wave = wave_id();
   const int r16 = lane & 15, q4 = lane >> 4;
-  const int h = (int)blockIdx.x % a.nkv, s = (int)blockIdx.x / a.nkv;
   if (s >= S) return true;
   const int hw = D / 2, dpu = D / S;   // dims this unit combines
 
@@ -835,7 +837,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   float* sc = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::CMB);   // [G][stride]
   const int64_t cstride = L::stride(a.lchunk);
 
-  int64_t lo = a.start_t[0];
+  int64_t lo = a.start_t[b];
   lo = lo < 0 ? 0 : lo;
   const int64_t nrel = hi > lo ? hi - lo : 0;
   const int64_t chunk = (nrel + S - 1) / S;   // <= a.lchunk (the plan's bound on the bucket)
@@ -851,8 +853,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   // key and value stand in for it), so no load is masked: a select on a
   // loaded value would wait for the load where it stands.
   const int64_t last = slot > 0 ? slot : 0;
-  const bf16_t* kc = reinterpret_cast<const bf16_t*>(lw[LW_KC]) + h * a.csh;
-  const bf16_t* vc = reinterpret_cast<const bf16_t*>(lw[LW_VC]) + h * a.csh;
+  const bf16_t* kc = reinterpret_cast<const bf16_t*>(lw[LW_KC]) + b * a.csb + h * a.csh;
+  const bf16_t* vc = reinterpret_cast<const bf16_t*>(lw[LW_VC]) + b * a.csb + h * a.csh;
 
   // key tiles, a ring of UT per wave: slot u holds tile wave + (u + UT j) SNW
   // of the split; lane holds key r16 of a tile, dims 32 i + 8 q4 .. +7
@@ -877,7 +879,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   {
     const bf16_t* qn = reinterpret_cast<const bf16_t*>(lw[LW_QN]);
     const bf16_t* kn = reinterpret_cast<const bf16_t*>(lw[LW_KN]);
-    int64_t crow = a.positions[0];
+    int64_t crow = a.positions[b];
     crow = crow < 0 ? 0 : (crow >= a.rope_len ? a.rope_len - 1 : crow);
     const bf16_t* cr = a.cos + crow * a.ld_cs;
     const bf16_t* sr = a.sin + crow * a.ld_cs;
@@ -1108,7 +1110,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     for (int i = tid; i < G * dpu / 2; i += SNT) {
       const int g = (2 * i) / dpu, dd = 2 * i - g * dpu;
       for (int c = 0; c < HC; ++c)
-        ll_put(att + (int64_t)c * (a.nq * D / 2) + ((int64_t)(h * G + g) * D + s * dpu + dd) / 2,
+        ll_put(att + (int64_t)c * att_cstride + ((int64_t)(h * G + g) * D + s * dpu + dd) / 2,
                pack2(cmb[2 * i], cmb[2 * i + 1]), ep);
     }
   }
@@ -1253,7 +1255,8 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       // ---- attention on every workgroup (its LDS overlays the activation
       //      row and the partials), then the o projection from the ring
       llw_t* lx_ll = a.arena + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
-      if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, lx_ll, hi, ep, ep * (uint32_t)MAX_LAYERS + (uint32_t)l, ph,
+      if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, (int64_t)qw / 2, lx_ll, 0, (int)blockIdx.x % a.nkv,
+                                (int)blockIdx.x / a.nkv, hi, ep, ep * (uint32_t)MAX_LAYERS + (uint32_t)l, ph,
                                 s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds

@@ -443,9 +443,9 @@ def decode_step(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_ca
     body) as ONE persistent launch: every layer, the final norm, lm_head, the
     first-index argmax and the step bookkeeping (tokens <- next, positions +=
     1, slot_t <- len, len += 1, out_buf[step_idx] <- next, step_idx += 1).
-    Batch 1; `table` from layer_table; k_cache0 gives the cache strides.
-    logits: optional bf16 tensor of vocab elements that receives the step's
-    logits. err: the error word to use (default: the scratch's own); a step
+    Batch 1..8 rows (2..8: the batch form of the kernel); `table` from
+    layer_table; k_cache0 gives the cache strides. logits: optional bf16
+    tensor of rows x vocab elements that receives the step's logits. err: the error word to use (default: the scratch's own); a step
     that gives up, and every step launched while the word is set, writes
     token -1 and advances only step_idx."""
     if err is None:
@@ -475,8 +475,10 @@ def _step_args(table, cfg, embed, lm_head, final_norm, cos, sin, k_cache0, s_cap
     _gpu(tokens, embed, lm_head, k_cache0)
     m = tokens.shape[0]
     _need(out_buf.dtype == torch.int32 and out_buf.shape[1] == m and out_buf.is_contiguous(), "out_buf")
+    _need(positions.numel() >= m and slot_t.numel() >= m and start_t.numel() >= m and k_cache0.shape[0] >= m,
+          "row state / cache rows")
     if logits is not None:
-        _need(logits.dtype == _BF16 and logits.is_contiguous() and logits.numel() == cfg.vocab_size, "logits")
+        _need(logits.dtype == _BF16 and logits.is_contiguous() and logits.numel() == m * cfg.vocab_size, "logits")
     _need(err.dtype == torch.int32 and err.numel() >= 1 and err.device == tokens.device, "err")
     _need(table.dtype == torch.int64 and table.shape == (cfg.num_layers, 10) and table.is_contiguous(), "table")
     _need(embed.stride(-1) == 1 and lm_head.stride(-1) == 1 and cos.stride(0) == sin.stride(0), "weights")

@@ -186,9 +186,14 @@ class Qwen3(torch.nn.Module):
         self._bufs: dict = {}
         self._plans: dict = {}
         self._tables: dict = {}
-        # the whole batch-1 step as one persistent launch where its plan allows
-        # (ENGINE_PERSISTENT=0 selects the per-kernel graph step everywhere)
+        # the whole step as one persistent launch where its plan allows
+        # (ENGINE_PERSISTENT=0 selects the per-kernel graph step everywhere),
+        # up to persistent_rows rows: at the Qwen3-4B shape and config 5's
+        # prompts the one-launch step is faster at 2, 4 and 6 rows (2.57 /
+        # 3.28 / 4.00 ms against 3.09 / 3.57 / 4.30) and slower at 8 (4.53
+        # against 3.99), where every workgroup reads 8 rows of hand-over words
         self.persistent = os.environ.get("ENGINE_PERSISTENT", "1") != "0"
+        self.persistent_rows = int(os.environ.get("ENGINE_PERSISTENT_ROWS", "6"))
         # the prefill's hipBLASLt projections: no reduced-precision bf16 reductions
         torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
 
@@ -410,7 +415,7 @@ class Qwen3(torch.nn.Module):
         s_cap = k_cache[0].shape[2]
         if ws is not None and len(ws) >= 8:
             s_cap = min(s_cap, ws[7].shape[2])
-        plan = self.persistent_plan(b, s_cap) if self.persistent else None
+        plan = self.persistent_plan(b, s_cap) if self.persistent and b <= self.persistent_rows else None
         if plan is not None:
             bufs = self.buffers(b)
             scratch = bufs.steps.get(plan[0])

@@ -62,8 +62,8 @@ def test_argument_errors_return_invalid_value_without_a_gpu():
 def test_decode_step_plan_rejects_unsupported_shapes_without_a_gpu():
     lib = _hip.load()
     sizes = (ctypes.c_int64 * 4)()
-    # 4B shape at batch 2: the persistent step takes batch 1 only
-    rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 2, 768, 36, sizes)
+    # 4B shape at batch 9: the persistent step takes 1 to 8 rows
+    rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 9, 768, 36, sizes)
     assert rc == 1 and b"batch" in lib.ek_last_error()
     # 32 query heads per kv head: not a supported group
     rc = lib.ek_decode_step_plan(2560, 9728, 32, 1, 128, 151936, 1, 768, 36, sizes)

@@ -1,0 +1,201 @@
+"""The one-launch decode step at 2..8 batch rows (ek_decode_step's batch
+kernel, csrc/ek_bstep_impl.h) pinned against the oracle.
+
+Every Qwen3-4B shape with two layers, the oracle's prefill cache of ragged
+left-padded prompts on both sides, the oracle's tokens fed back (teacher
+forcing): per step and row the step's own logits (its optional [rows, vocab]
+logits output) are within 2e-2 of the oracle's scale, the emitted token is
+the oracle's argmax or within 2 bf16 ulps of its top logit (a near-tie that
+a summation order can flip), and after the steps the prefill slots are
+untouched, the new cache rows match, and every row's position, the shared
+length and the step counter advanced. Cases: 2, 3, 5 (a row bound of 8 with
+3 rows unused) and 8 rows; config 5 at its stated size (eight prompts of
+U[64, 2048] tokens, cache 8192, the engine's bucket); and a batch whose
+bucket needs many keys per split.
+"""
+
+import pytest
+import torch
+
+from enginekernel_amd import checkpoint as C
+from enginekernel_amd import ek_kernels as K
+from enginekernel_amd.ek_model import Qwen3
+from oracle import ek_oracle as O
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+MID_4B = dict(C.QWEN3_4B, num_hidden_layers=2)
+
+
+@pytest.fixture(scope="module")
+def mid(dev):
+    cfg = dict(MID_4B)
+    tensors = C.random_weights(cfg, seed=0)
+    return cfg, O.OracleQwen3(O.OracleConfig(cfg), tensors), Qwen3(None, dev, tensors=tensors, config=cfg)
+
+
+def _prompts(lengths, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randint(0, 151936, (n,), generator=g).tolist() for n in lengths]
+
+
+def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
+    """random_cache: both sides start from the same random cache rows [0, s)
+    (rows before a row's first key are padding, masked on both sides) and a
+    random token, instead of the oracle's prefill (too slow on the CPU for
+    long prompts)."""
+    cfg, om, model = mid
+    model.persistent_rows = 8     # the batch kernel at every row count (the default stops at 6)
+    b = len(prompts)
+    ids, pos, pad, s, bias = O.pack(prompts)
+    total = cap or s + steps + 1
+    bucket = bucket or total
+    st = O.EagerState(om, b, s, pad, total)
+    om.ensure_rope(total + 1)
+    plan = model.persistent_plan(b, min(total, bucket))
+    assert plan is not None and plan[1] >= 1, plan     # the batch kernel: every workgroup attends a split
+    worst, agree = 0.0, 0
+    with torch.inference_mode():
+        if random_cache:
+            g = torch.Generator().manual_seed(s)
+            for t in st.k + st.v:
+                t[:, :, :s] = torch.randn(t[:, :, :s].shape, generator=g).to(BF)
+            tok = torch.randint(0, cfg["vocab_size"], (b,), generator=g)
+        else:
+            tok = O.argmax_token(om.prefill(ids, pos, st.k, st.v, bias), om.lm_head)
+        kd = [t.to(dev) for t in st.k]
+        vd = [t.to(dev) for t in st.v]
+        tokens = tok.to(dev)
+        positions = st.positions.to(dev)
+        slot_t = torch.zeros(b, dtype=torch.int64, device=dev)
+        len_t = torch.full((1,), s, dtype=torch.int64, device=dev)
+        start_t = torch.as_tensor(pad, dtype=torch.int32, device=dev)
+        out_buf = torch.full((64, b), -7, dtype=torch.int32, device=dev)
+        step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        ws = K.make_workspace(b, 32, 8, 128, bucket, dev)
+        logits = torch.empty(b, cfg["vocab_size"], dtype=BF, device=dev)
+        for i in range(steps):
+            l_ref = O.lm_logits(om.decode(tok, st.positions, st.k, st.v, st.slot_t, st.len_t, st.start_t),
+                                om.lm_head).float()
+            tokens.copy_(tok)
+            model.step(tokens, positions, kd, vd, slot_t, len_t, start_t, ws, out_buf, step_idx, logits=logits)
+            lg = logits.float().cpu()
+            got = out_buf[i].cpu()
+            for r in range(b):
+                rel = (lg[r] - l_ref[r]).abs().max().item() / l_ref[r].abs().max().item()
+                worst = max(worst, rel)
+                assert rel <= 2e-2, (i, r, rel)
+                t_ref, t_gpu = int(torch.argmax(l_ref[r])), int(got[r])
+                assert t_gpu == int(torch.argmax(lg[r])), (i, r)
+                if t_gpu == t_ref:
+                    agree += 1
+                else:
+                    gap = float(l_ref[r, t_ref] - l_ref[r, t_gpu])
+                    assert gap <= 2 * O.bf16_ulp(float(l_ref[r, t_ref])), (i, r, t_gpu, t_ref, gap)
+            tok = torch.argmax(l_ref, -1)
+            st.positions = st.positions + 1
+        K.check_error_word(K.ws_error(ws), "batch steps")
+        assert int(step_idx) == steps and int(len_t) == s + steps
+        assert torch.equal(positions.cpu(), st.positions)
+        assert torch.equal(slot_t.cpu(), torch.full((b,), s + steps - 1, dtype=torch.int64))
+        assert (out_buf[steps:] == -7).all()
+        n = int(st.len_t)
+        for layer in range(cfg["num_hidden_layers"]):
+            for got_c, ref_c in ((kd[layer], st.k[layer]), (vd[layer], st.v[layer])):
+                assert torch.equal(got_c[:, :, :s].cpu(), ref_c[:, :, :s])
+                a, r = got_c[:, :, s:n].cpu().float(), ref_c[:, :, s:n].float()
+                assert (a - r).abs().max().item() <= 2e-2 * r.abs().max().item()
+                assert not got_c[:, :, n:].cpu().any()
+    print(f"batch {b}, contexts {s + 1}..{s + steps}: worst logit error {worst:.4f} of scale, "
+          f"{agree}/{b * steps} tokens equal")
+    assert agree >= b * steps - 2
+    return model
+
+
+@pytest.mark.parametrize("lengths,seed", [((50, 130), 1), ((64, 100, 37), 2), ((90, 12, 200, 33, 140), 3),
+                                          ((16, 300, 45, 120, 77, 250, 9, 180), 4)])
+def test_batch_step_parity(dev, mid, lengths, seed):
+    _run(dev, mid, _prompts(lengths, seed), 6)
+
+
+def test_batch_step_config5_full_size(dev, mid):
+    """Config 5's batch at its stated size: eight prompts of U[64, 2048]
+    tokens (seed 2), a cache of 8192 slots and the bucket the engine builds
+    for a 256-token request."""
+    from enginekernel_amd.microbench import batch8_prompts
+    prompts = batch8_prompts(151936)
+    s = max(len(p) for p in prompts)
+    bucket = -(-(s + 256) // 256) * 256
+    _run(dev, mid, prompts, 4, cap=8192, bucket=bucket)
+
+
+def test_batch_step_long_split(dev, mid):
+    """Two rows in a 12288-key bucket (random cache rows): 16 splits per
+    (row, kv head) of up to 768 keys each."""
+    _run(dev, mid, _prompts((11000, 6000), 5), 3, bucket=12288, cap=12288, random_cache=True)
+
+
+def test_batch_rows_as_if_alone_full_depth(dev):
+    """The 36-layer Qwen3-4B shape, as a property: after one GPU prefill of
+    four of config 5's prompts (cache 8192), 3 steps of the batch kernel
+    against each row stepped alone by the batch-1 kernel (its own copy of
+    its cache row and first key), both fed the batch's tokens. The two
+    differ only in fp32 summation order, so their logits agree within the
+    oracle's reorder drift bound at this depth (1.5 x 0.16 + 2 ulps) and a
+    different argmax is a near-tie."""
+    from enginekernel_amd.engine import _FastEngine
+    from enginekernel_amd.microbench import batch8_prompts
+    cfg = dict(C.QWEN3_4B)
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+    model.persistent_rows = 8
+    eng = _FastEngine(model=model)
+    prompts = batch8_prompts(cfg["vocab_size"])[:4]
+    b, steps, V = len(prompts), 3, cfg["vocab_size"]
+    with torch.inference_mode():
+        ids, pos, pad, s, bias = eng._pack(prompts)
+        eng._ensure_cache(b, 8192)
+        kb, vb = eng.store.layer_views(0, b)
+        tok = model.argmax_token(model.prefill(ids, pos, kb, vb, bias))
+        alone = []
+        for r in range(b):
+            alone.append(dict(k=[t[r:r + 1].clone() for t in kb], v=[t[r:r + 1].clone() for t in vb],
+                              tokens=tok[r:r + 1].clone(), positions=torch.tensor([s - pad[r]], device=dev),
+                              slot=torch.zeros(1, dtype=torch.int64, device=dev),
+                              len=torch.full((1,), s, dtype=torch.int64, device=dev),
+                              start=torch.tensor([pad[r]], dtype=torch.int32, device=dev),
+                              out=torch.zeros((16, 1), dtype=torch.int32, device=dev),
+                              step=torch.zeros(1, dtype=torch.int64, device=dev),
+                              ws=K.make_workspace(1, 32, 8, 128, 8192, dev)))
+        bucket = -(-(s + 256) // 256) * 256
+        wsb = K.make_workspace(b, 32, 8, 128, bucket, dev)
+        assert model.persistent_plan(b, bucket)[1] >= 1
+        tokens = tok.clone()
+        positions = torch.as_tensor([s - p for p in pad], dtype=torch.int64, device=dev)
+        slot_t = torch.zeros(b, dtype=torch.int64, device=dev)
+        len_t = torch.full((1,), s, dtype=torch.int64, device=dev)
+        start_t = torch.as_tensor(pad, dtype=torch.int32, device=dev)
+        outb = torch.zeros((16, b), dtype=torch.int32, device=dev)
+        stepb = torch.zeros(1, dtype=torch.int64, device=dev)
+        lb = torch.empty(b, V, dtype=BF, device=dev)
+        l1 = torch.empty(1, V, dtype=BF, device=dev)
+        worst, agree = 0.0, 0
+        for i in range(steps):
+            fed = tokens.clone()
+            model.step(tokens, positions, kb, vb, slot_t, len_t, start_t, wsb, outb, stepb, logits=lb)
+            for r, st in enumerate(alone):
+                st["tokens"].copy_(fed[r:r + 1])
+                model.step(st["tokens"], st["positions"], st["k"], st["v"], st["slot"], st["len"], st["start"],
+                           st["ws"], st["out"], st["step"], logits=l1)
+                a, ref = l1.float()[0].cpu(), lb.float()[r].cpu()
+                err = (a - ref).abs().max().item()
+                ulp = O.bf16_ulp(float(ref.abs().max()))
+                worst = max(worst, err)
+                assert err <= 1.5 * 0.16 + 2 * ulp, (i, r, err)
+                tb_, t1 = int(outb[i, r]), int(st["out"][i, 0])
+                if tb_ == t1:
+                    agree += 1
+                else:
+                    assert float(ref[tb_] - ref[t1]) <= 2 * ulp, (i, r, tb_, t1)
+        K.check_error_word(K.ws_error(wsb), "batch steps")
+    print(f"batch {b} vs rows alone (36 layers): worst logit difference {worst:.4f}, {agree}/{b * steps} equal")
+    assert agree >= b * steps - 1
