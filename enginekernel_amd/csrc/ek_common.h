@@ -15,12 +15,12 @@ typedef uint16_t bf16_t;
 
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+// gfx950's conversion instruction (v_cvt_pk_bf16_f32): round to nearest
+// even, one instruction for two values (the bit arithmetic it replaces --
+// NaN test, add 0x7fff plus the lsb, shift -- took six per value)
+typedef __bf16 ek_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float ek_f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // round an fp32 value to the nearest bf16 and widen it back
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
@@ -36,7 +36,10 @@ __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[6] = lo_bf(v.w); f[7] = hi_bf(v.w);
 }
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  const ek_f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ek_bf16x2_t));
+}
 
 // sum of 8 products of two packed-bf16 chunks, added to acc in order
 __device__ __forceinline__ float dot8_acc(const uint4& w, const uint4& x, float acc) {
