@@ -232,68 +232,59 @@ __device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* p
 
 // rr (bf16 pairs, [MB][k / 2]) = bf16(rr + x) for rows m < nrows (x pairs
 // [m][k / 2] in xw, or no add when xw is null); xs row m (xstride apart) =
-// bf16(w * bf16(rr * rsqrt(mean(rr^2) + eps)))   (ek_kernels.py:1025-1059)
+// bf16(w * bf16(rr * rsqrt(mean(rr^2) + eps)))   (ek_kernels.py:1025-1059).
+// Row m belongs to the WPR = 8 / MB waves m WPR .. m WPR + WPR - 1, which take
+// its words in turn (64 at a time). One barrier: it separates the residual
+// update and the row sums of squares (pass 1, which reads the staged words
+// in xw) from the output (pass 2, which may overwrite them: xs and xw share
+// the LDS), and carries the waves' partial sums (red, fixed order). The gain
+// words come from the registers gw (thread t: words t + j SNT) via the LDS
+// row gl.
 template <int MB>
-__device__ __forceinline__ void add_norm_b(uint32_t* rr, const uint32_t* xw, const uint32_t* gw, int k, int nrows,
-                                           float eps, bf16_t* xs, int xstride, float* red) {
+__device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, const uint32_t* gw, uint32_t* gl,
+                                              int k, int nrows, float eps, bf16_t* xs, int xstride, float* red) {
+  static_assert(MB <= SNW && SNW % MB == 0, "whole waves per row");
+  constexpr int WPR = SNW / MB;
   const int tid = opaque_tid(), lane = tid & 63, wave = wave_id();
+  const int m = wave / WPR, part = wave - m * WPR;
   const int nw = k / 2;
-  float ss[MB];
-  uint32_t rv[MB][NGW];
 #pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    ss[m] = 0.f;
-    if (m >= nrows) continue;
-#pragma unroll
-    for (int j = 0; j < NGW; ++j) {
-      const int i = tid + j * SNT;
-      const int ic = i < nw ? i : 0;
-      uint32_t r = rr[m * nw + ic];
+  for (int j = 0; j < NGW; ++j) {
+    const int i = tid + j * SNT;
+    if (i < nw) gl[i] = gw[j];
+  }
+  const int i0 = part * EK_WAVE + lane;
+  if (m < nrows) {
+    uint32_t* rrow = rr + m * nw;
+    float ss = 0.f;
+    for (int i = i0; i < nw; i += WPR * EK_WAVE) {
+      uint32_t r = rrow[i];
       if (xw) {
-        const uint32_t x = xw[m * nw + ic];
+        const uint32_t x = xw[m * nw + i];
         r = pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x));
+        rrow[i] = r;
       }
-      rv[m][j] = r;
-      const float msk = i < nw ? 1.f : 0.f;
-      ss[m] = fmaf(lo_bf(r) * msk, lo_bf(r), ss[m]);
-      ss[m] = fmaf(hi_bf(r) * msk, hi_bf(r), ss[m]);
+      ss = fmaf(lo_bf(r), lo_bf(r), ss);
+      ss = fmaf(hi_bf(r), hi_bf(r), ss);
     }
-  }
-  if (xw) {
-#pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      if (m >= nrows) continue;
-#pragma unroll
-      for (int j = 0; j < NGW; ++j) {
-        const int i = tid + j * SNT;
-        if (i < nw) rr[m * nw + i] = rv[m][j];
-      }
-    }
-  }
-  wave_sums_dpp_lane63<MB>(ss);
-  if (lane == 63) {
-#pragma unroll
-    for (int m = 0; m < MB; ++m) red[wave * MB + m] = ss[m];
+    ss = wave_sum_dpp(ss);
+    if (lane == 0) red[wave] = ss;
   }
   __syncthreads();
-  uint32_t* xs32 = reinterpret_cast<uint32_t*>(xs);
-#pragma unroll
-  for (int m = 0; m < MB; ++m) {
-    if (m >= nrows) continue;
+  if (m < nrows) {
     float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < SNW; ++w) t += red[w * MB + m];
+    for (int q = 0; q < WPR; ++q) t += red[m * WPR + q];
     const float rstd = 1.0f / sqrtf(t / (float)k + eps);
-#pragma unroll
-    for (int j = 0; j < NGW; ++j) {
-      const int i = tid + j * SNT;
-      const float o0 = rbf(lo_bf(gw[j]) * rbf(lo_bf(rv[m][j]) * rstd));
-      const float o1 = rbf(hi_bf(gw[j]) * rbf(hi_bf(rv[m][j]) * rstd));
-      if (i < nw) xs32[m * (xstride / 2) + i] = pack2(o0, o1);
+    const uint32_t* rrow = rr + m * nw;
+    uint32_t* xrow = reinterpret_cast<uint32_t*>(xs + m * xstride);
+    for (int i = i0; i < nw; i += WPR * EK_WAVE) {
+      const uint32_t r = rrow[i], g = gl[i];
+      xrow[i] = pack2(rbf(lo_bf(g) * rbf(lo_bf(r) * rstd)), rbf(hi_bf(g) * rbf(hi_bf(r) * rstd)));
     }
+    const int kpad = kpad_of(k);
+    for (int i = k + part * EK_WAVE + lane; i < kpad; i += WPR * EK_WAVE) xs[m * xstride + i] = 0;
   }
-  const int kpad = kpad_of(k);
-  for (int m = 0; m < nrows; ++m) zero_pad(xs + m * xstride, k, kpad);
 }
 
 // lm_head rows of this wave (whole rows): a running first-index argmax per
@@ -366,6 +357,8 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   uint32_t* xs32 = reinterpret_cast<uint32_t*>(ph);
   float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)MB * xcols * 2));
   const int part_n = a.part_max * SNW * MB;
+  uint32_t* gain_lds = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(part) +
+                                                   eka::align16((size_t)a.part_max * SNW * MB * 4));   // the norm's gain row
   PartWriter<MB, false> put{part, wave_id()};
   PartWriter<MB, true> add{part, wave_id()};
 
@@ -414,11 +407,13 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         for (int i = tid; i < h / 2; i += SNT) rr[m * (h / 2) + i] = e32[i];
       }
       __syncthreads();
-      add_norm_b<MB>(rr, nullptr, gw1, h, nrows, a.eps, xs, xcols, s_red);
+      add_norm_rows<MB>(rr, nullptr, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
     } else {
       const bool ok = ll_read<BLLW>(LinSrc{dn_prev}, nrows * (h / 2), ep, xs32, a.err, a.spin);
       if (!wg_all(ok, s_fail)) return false;
-      add_norm_b<MB>(rr, xs32, gw1, h, nrows, a.eps, xs, xcols, s_red);
+      EK_TS(22);
+      add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
+      EK_TS(23);
     }
     __syncthreads();
     EK_TS(1);
@@ -471,8 +466,10 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(16);
-    add_norm_b<MB>(rr, xs32, gw2, h, nrows, a.eps, xs, xcols, s_red);
+    add_norm_rows<MB>(rr, xs32, gw2, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
+    EK_TS(17);
     load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm, h, gw1);
+    EK_TS(18);
     __syncthreads();
     EK_TS(9);
     gemv_phase_b<MB>(gg, h, false, ring, xs, xcols, put);
@@ -525,7 +522,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     const bool ok = ll_read<BLLW>(LinSrc{dn_prev}, nrows * (h / 2), ep, xs32, a.err, a.spin);
     if (!wg_all(ok, s_fail)) return false;
   }
-  add_norm_b<MB>(rr, xs32, gw1, h, nrows, a.eps, xs, xcols, s_red);
+  add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
   __syncthreads();
   const Gp gl = make_gp(a.lm_head, h, a.vocab, 0, 1);
   int u0, u1;
@@ -657,7 +654,8 @@ __global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
 template <int D, int G, int MB>
 inline size_t bstep_lds_bytes(int h, int qw, int part_rows, int lchunk, int nwg) {
   const size_t rr = bstep_rr_bytes(MB, h);
-  const size_t gemv = eka::align16((size_t)MB * bstep_xcols(h, qw) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4);
+  const size_t gemv = eka::align16((size_t)MB * bstep_xcols(h, qw) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4) +
+                      eka::align16((size_t)h / 2 * 4);
   const size_t attn = LongLds<D, G>::bytes(lchunk);
   const size_t fin = (size_t)2 * nwg * MB * 4 + (size_t)MB * 4;
   size_t x = gemv > attn ? gemv : attn;
