@@ -326,15 +326,21 @@ __host__ __device__ inline int bstep_part_rows(int h, int inter, int qkvw, int n
   return r;
 }
 
-// Words of nrows rows (rw words apart, sw of each) into LDS rows xw words
-// apart: i -> row i / xw, word i % xw (past sw: the row's last word again,
-// a tail the products do not read)
+// Words of nrows rows (rw words apart, the first sw of each) into LDS rows
+// xw words apart: word i -> row i / sw, word i % sw
 struct RowsSrc {
   const llw_t* p;
-  int rw, sw, xw;
+  int rw, sw;
   __device__ const llw_t* operator()(int i) const {
-    const int m = i / xw, j = i - m * xw;
-    return p + (int64_t)m * rw + (j < sw ? j : sw - 1);
+    const int m = i / sw;
+    return p + (int64_t)m * rw + (i - m * sw);
+  }
+};
+struct RowsDst {
+  int sw, xw;
+  __device__ int operator()(int i) const {
+    const int m = i / sw;
+    return m * xw + (i - m * sw);
   }
 };
 
@@ -443,10 +449,9 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     // ---- o projection
     zero_part(part, part_n);
     {
-      // row m's words land xcols / 2 words apart (the tail of each LDS row
-      // re-reads the row's last word and is not used)
-      const bool ok = ll_read<BLLW>(RowsSrc{att_ll, qw / 2, qw / 2, xcols / 2}, (nrows - 1) * (xcols / 2) + qw / 2, ep,
-                                    xs32, a.err, a.spin);
+      // row m's words land xcols / 2 words apart
+      const bool ok = ll_read<BLLW>(RowsSrc{att_ll, qw / 2, qw / 2}, nrows * (qw / 2), ep, xs32, a.err, a.spin,
+                                    nullptr, RowsDst{qw / 2, xcols / 2});
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(6);
@@ -488,8 +493,8 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       const int sw = gd.K / 2;   // words of a row's slice
       if (sl > 0) __syncthreads();   // the previous slice's products have read their LDS rows
       {
-        const bool ok = ll_read<BLLW>(RowsSrc{act_ll + c0 * (CH / 2), inter / 2, sw, xcols / 2},
-                                      (nrows - 1) * (xcols / 2) + sw, ep, xs32, a.err, a.spin);
+        const bool ok = ll_read<BLLW>(RowsSrc{act_ll + c0 * (CH / 2), inter / 2, sw}, nrows * sw, ep, xs32, a.err,
+                                      a.spin, nullptr, RowsDst{sw, xcols / 2});
         if (!wg_all(ok, s_fail)) return false;
       }
       if (sl == 0) EK_TS(20);

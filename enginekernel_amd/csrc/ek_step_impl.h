@@ -177,9 +177,13 @@ __device__ __forceinline__ bool ll_ok(llw_t v, uint32_t ep) { return (uint32_t)(
 // halves in dst[i] (LDS). Thread t handles i = t + k * SNT; up to LLW words
 // per thread are in flight at once, and only the words not yet valid are
 // loaded again. False (the error word set) when a wait runs out.
-template <int W = LLW, typename SRC>
+struct LinDst {   // word i -> LDS word i
+  __device__ int operator()(int i) const { return i; }
+};
+
+template <int W = LLW, typename SRC, typename DST = LinDst>
 __device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* dst, int* err, int64_t spin,
-                                        int64_t* rounds = nullptr) {
+                                        int64_t* rounds = nullptr, DST dix = DST()) {
   const int tid = threadIdx.x;
   for (int base = 0; base < n; base += W * SNT) {
     llw_t v[W];
@@ -209,7 +213,7 @@ __device__ __forceinline__ bool ll_read(SRC src, int n, uint32_t ep, uint32_t* d
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       const int i = base + tid + k * SNT;
-      if (i < n) dst[i] = (uint32_t)v[k];
+      if (i < n) dst[dix(i)] = (uint32_t)v[k];
     }
   }
   return true;
