@@ -3,8 +3,8 @@ fraction of the HBM roofline.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
     python bench.py --probe-traffic     (the launches the PMC traffic profile counts)
-    python bench.py --config 2|3|5|6    (GEMV sweep, attention sweep, batch-8 decode,
-                                         batch-1 speculative decode vs plain)
+    python bench.py --config 2|3|5|6|7  (GEMV sweep, attention sweep, batch-8 decode,
+                                         batch-1 speculative decode vs plain, 2..8-row step)
 
 Workload: a random-init bf16 model of the Qwen3-4B
 architecture (36 layers, hidden 2560, intermediate 9728, 32/8 heads, head
@@ -47,10 +47,10 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 # 256 MiB device copy (FETCH 0.50007, WRITE 1.0). Re-measure when the kernel changes.
 #   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
 GATE_UP_TRAFFIC_B1 = 100_153_865
-#   the persistent step kernel (step_kernel<128, 4>) at batch 1, context 137..146:
-#   3,975,233 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.010x its
+#   the persistent step kernel (step_kernel<128, 4, false>) at batch 1, context 137..146:
+#   3,975,140 KiB / 0.50007 fetched + 4,414 KiB written per launch, 1.010x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_144_734_072
+STEP_TRAFFIC_B1 = 8_144_553_907
 
 
 def log(msg: str) -> None:
@@ -249,10 +249,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--probe-traffic", action="store_true", help="run only the launches of the PMC traffic profile")
-    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5, 6),
-                    help="4 (default): the batch-1 decode line; 2 / 3 / 5 / 6: the GEMV sweep, the attention "
-                         "sweep, the batch-8 decode or batch-1 speculative vs plain decode, one JSON line each "
-                         "(enginekernel_amd.microbench)")
+    ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5, 6, 7),
+                    help="4 (default): the batch-1 decode line; 2 / 3 / 5 / 6 / 7: the GEMV sweep, the attention "
+                         "sweep, the batch-8 decode, batch-1 speculative vs plain decode, or the 2..8-row step in "
+                         "both forms, one JSON line each (enginekernel_amd.microbench)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for {args.gpus}).",

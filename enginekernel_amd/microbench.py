@@ -11,8 +11,12 @@ batch-1 end-to-end figure of bench.py:
             16384, 32768}, swept over the split count, again over copies
             that defeat the Infinity Cache.
   config 5  batch 8, left-padded prompts of U[64, 2048] random ids (seed 2),
-            256 greedy tokens through the per-kernel captured graph, cache
+            256 greedy tokens through the engine's captured graph (at 8
+            rows the per-kernel graph, the faster form there), cache
             capacity 8192; also the prompt's prefill time (the first token).
+  config 7  the step at 2, 4, 6 and 8 rows (the first rows of config 5's
+            batch), one graph replay per step, in both forms: the one-launch
+            batch kernel and the per-kernel graph.
 
 Every figure is HIP-event time on the launching stream divided by the
 launches inside the timed region; bytes are algorithmic (each weight, key,
@@ -310,8 +314,64 @@ def spec_decode(tokens: int = 256, log=print):
     return out
 
 
+def batch_sweep(rows=(2, 4, 6, 8), steps: int = 64, cap: int = 8192, log=print):
+    """Config 7: the decode step at 2..8 rows, one captured graph replay per
+    step, both forms: the one-launch batch kernel (every row count, whatever
+    the default row limit) and the per-kernel graph. The batch is the first
+    `b` of config 5's prompts (U[64, 2048] tokens, seed 2), cache 8192;
+    bytes per step are the weights plus the K/V rows attended."""
+    import torch
+    from enginekernel_amd import checkpoint as C
+    from enginekernel_amd import ek_kernels as K
+    from enginekernel_amd.ek_model import Qwen3
+    from enginekernel_amd.engine import _FastEngine
+
+    dev = torch.device("cuda:0")
+    cfg = dict(C.QWEN3_4B)
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+    w_bytes = C.weight_bytes_per_token(cfg)
+    kv_row = 2 * cfg["num_hidden_layers"] * cfg["num_key_value_heads"] * cfg["head_dim"] * 2
+    out = []
+    for b in rows:
+        prompts = batch8_prompts(cfg["vocab_size"])[:b]
+        rec = {"batch": b, "prompt_lens": [len(p) for p in prompts]}
+        for persistent in (True, False):
+            model.persistent = persistent
+            model.persistent_rows = 8
+            eng = _FastEngine(model=model)
+            with torch.inference_mode():
+                ids, pos, pad, s, bias = eng._pack(prompts)
+                eng._ensure_cache(b, cap)
+                graph = eng._get_graph(b, s + steps + 8)
+                first = eng._first_token(ids, pos, b, s, bias)
+                graph.begin(first, [s - p for p in pad], pad, s)
+                for _ in range(4):
+                    graph.graph.replay()
+                torch.cuda.synchronize()
+                stream = torch.cuda.current_stream()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(steps):
+                    graph.graph.replay()
+                e1.record(stream)
+                e1.synchronize()
+                step_s = e0.elapsed_time(e1) / 1e3 / steps
+                K.check_error_word(graph.err, "the timed batch steps")
+            attended = sum(s + 4 + j - p for p in pad for j in range(1, steps + 1)) / steps
+            nbytes = batch8_bytes(w_bytes, kv_row, attended)
+            key = "one_launch" if persistent else "per_kernel"
+            rec[key + "_ms"] = round(step_s * 1e3, 4)
+            rec[key + "_frac"] = round(nbytes / step_s / PEAK_HBM, 4)
+            del eng, graph
+            torch.cuda.empty_cache()
+        log(f"config 7: batch {b}: one launch {rec['one_launch_ms']} ms, per-kernel {rec['per_kernel_ms']} ms")
+        out.append(rec)
+    model.persistent, model.persistent_rows = True, 6
+    return out
+
+
 def run(config: int, log=print) -> dict:
-    """One JSON-ready record for config 2, 3, 5 or 6."""
+    """One JSON-ready record for config 2, 3, 5, 6 or 7."""
     import torch
     if not torch.cuda.is_available():
         raise RuntimeError("the microbenchmarks need a GPU")
@@ -329,7 +389,8 @@ def run(config: int, log=print) -> dict:
         return {"metric": "batch-8 decode tokens/s and % of HBM roofline (config 5)", "unit": "tokens/s",
                 "higher_is_better": True, "dtype": "bf16",
                 "data": "synthetic (random-init weights seed 0, prompts seed 2)",
-                "config": {"workload": "config 5: Qwen3-4B architecture, batch 8 ragged, per-kernel graph"},
+                "config": {"workload": "config 5: Qwen3-4B architecture, batch 8 ragged, the engine's default step "
+                                       "(per-kernel graph at 8 rows)"},
                 "results": [batch8_decode(log=log)]}
     if config == 6:
         return {"metric": "batch-1 speculative decode tokens/s vs plain (config 6)", "unit": "tokens/s",
@@ -337,4 +398,11 @@ def run(config: int, log=print) -> dict:
                 "data": "synthetic (random-init weights seed 0; random and repeating prompts, seed 1)",
                 "config": {"workload": "config 6: Qwen3-4B architecture, batch 1, n-gram draft + verify"},
                 "results": spec_decode(log=log)}
+    if config == 7:
+        return {"metric": "decode step time at 2..8 rows, one-launch vs per-kernel (config 7)", "unit": "ms",
+                "higher_is_better": False, "dtype": "bf16",
+                "data": "synthetic (random-init weights seed 0, config 5 prompts seed 2)",
+                "config": {"workload": "config 7: Qwen3-4B architecture, the first b of config 5's prompts, "
+                                       "cache 8192, one graph replay per step"},
+                "results": batch_sweep(log=log)}
     raise ValueError(f"no microbenchmark for config {config}")

@@ -224,7 +224,8 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
  * 32 KiB: attention then runs on n_kv * head_dim / 32 workgroups of its own
  * beside the projections; otherwise every workgroup attends 1 / split of one
  * kv head's keys), the bytes of the launch-state block and the grid (one workgroup per
- * CU). It handles batch 1, up to 64 layers, head_dim 32/64/128, n_q / n_kv in
+ * CU). It handles batch m = 1..8 (2..8 rows: head_dim 128, every workgroup
+ * attending a key split of one (row, kv head)), up to 64 layers, head_dim 32/64/128, n_q / n_kv in
  * {1, 2, 4, 8}, hidden (<= 4096), intermediate and n_q * head_dim multiples
  * of 512, and s_cap up to what one split's score rows fit in LDS (about
  * 100 K keys at n_q / n_kv = 4 on 256 CUs), on a device where one workgroup
@@ -240,8 +241,8 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
  * first-index argmax and the step bookkeeping (tokens[b] = token,
  * positions[b] += 1, slot_t[b] = *len_t, *len_t += 1, out_buf[*step_idx * m +
  * b] = token if *step_idx < max_steps, *step_idx += 1, out_tok[b] = token if
- * out_tok; logits[0..vocab) = the step's bf16 logits if logits is not
- * NULL). One workgroup per CU; workgroups hand activations to each other
+ * out_tok; logits[b * vocab ..) = row b's bf16 logits if logits is not
+ * NULL), for the m rows of the batch (b < m). One workgroup per CU; workgroups hand activations to each other
  * through the arena as {data, epoch} words that the consumer polls, with no
  * grid barrier.
  * layer_ptrs: device int64 [n_layers][10] = addresses of qkv [(n_q + 2 n_kv) D,
