@@ -504,9 +504,6 @@ __global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
   u.out = p.out + b * p.ldo_b + (int64_t)h * G * p.ldo_h;
   u.out_stride = p.ldo_h;
   u.ll_out = nullptr;
-  u.ll_copies = 1;
-  u.ll_copy_stride = 0;
-  u.ll_ep = 0;
 #ifdef EK_STEP_TRACE
   u.trace_lds = nullptr;
 #endif

@@ -100,11 +100,10 @@ struct AttnUnit {
   bool writer;                           // stores the new key/value at slot hi - 1
   int d0;                                // first head dim of this unit
   bf16_t* out; int64_t out_stride;       // out[g * out_stride + d0 + d]
-  // When set, the output goes instead to 8-byte words {bf16 pair, epoch} at
-  // ll_out[(g * out_stride + d0 + d) / 2] (device scope: read by other
-  // workgroups of the same launch, which poll for the epoch)
-  unsigned long long* ll_out; uint32_t ll_ep;
-  int ll_copies; int64_t ll_copy_stride;   // the words are stored to ll_copies regions, ll_copy_stride words apart
+  // When set, the output goes instead to dense 8-byte words of four bf16 at
+  // ll_out[(g * out_stride + d0 + d) / 4] (dw_put: device scope, read by
+  // other workgroups of the same launch, which poll for them)
+  unsigned long long* ll_out;
 #ifdef EK_STEP_TRACE
   int64_t* trace_lds;                    // per-stage timestamps of this unit, in LDS (trace builds)
 #endif
@@ -390,15 +389,14 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
   __syncthreads();
   EK_ATTN_MARK(19);
   if (a.ll_out) {
-    for (int i = tid; i < G * FDC / 2; i += FNT) {
-      const int g = i / (FDC / 2), d = 2 * (i % (FDC / 2));
-      float t0 = 0.f, t1 = 0.f;
+    for (int i = tid; i < G * FDC / 4; i += FNT) {
+      const int g = i / (FDC / 4), d = 4 * (i % (FDC / 4));
+      float t[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < FNW; ++w) { t0 += outp[w][g][d]; t1 += outp[w][g][d + 1]; }
-      const unsigned long long word = ((unsigned long long)a.ll_ep << 32) | pack2(t0, t1);
-      for (int c = 0; c < a.ll_copies; ++c)
-        __hip_atomic_store(a.ll_out + c * a.ll_copy_stride + (g * a.out_stride + d0 + d) / 2, word, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+      for (int w = 0; w < FNW; ++w)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] += outp[w][g][d + e];
+      dw_put(a.ll_out + (g * a.out_stride + d0 + d) / 4, pack2(t[0], t[1]), pack2(t[2], t[3]));
     }
     store_new_row();
     return true;

@@ -30,12 +30,7 @@
 
 namespace eks {
 
-static_assert(HC == 1, "the batch step keeps one copy of each hand-over region");
-
-#ifndef EK_BSTEP_LLW
-#define EK_BSTEP_LLW 16
-#endif
-constexpr int BLLW = EK_BSTEP_LLW;   // hand-over words in flight per thread (MB times the batch-1 words)
+constexpr int BLLW = 16;      // tagged (argmax) words in flight per thread
 // rows whose next activation chunk is read ahead of the current products
 // (at 8 rows the 8 extra chunks in registers spill, and the products of 8
 // rows cover the LDS round trip anyway)
@@ -43,6 +38,10 @@ constexpr int BLLW = EK_BSTEP_LLW;   // hand-over words in flight per thread (MB
 #define EK_BSTEP_XA 4
 #endif
 constexpr int BSLICE = 10;    // activation chunks per LDS slice of a row (5120 bf16)
+// dense 16-byte units in flight per thread: MB for the rows up to 4096 wide,
+// and one K slice of MB act rows in one round
+template <int MB>
+constexpr int bstep_slice_units() { return (MB * BSLICE * CH / 8 + SNT - 1) / SNT; }
 
 // ---------------------------------------------------------------------------
 // projections over MB activation rows
@@ -195,17 +194,16 @@ __device__ __forceinline__ float row_sum_b(const float* part, int r, int m) {
   return s;
 }
 
-// row m's out word (u0 + 2i) / 2 at out + m * rw + u0 / 2 + i, rows m < nrows
+// row m's dense word (u0 + 4i) / 4 at out + m * rw + u0 / 4 + i, rows m < nrows
 template <int MB>
-__device__ __forceinline__ void epilogue_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw, int nrows,
-                                              uint32_t ep) {
+__device__ __forceinline__ void epilogue_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw, int nrows) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int np = (u1 - u0) / 2;
-  for (int i = threadIdx.x; i < np * nrows; i += SNT) {
-    const int m = i / np, p = i - m * np;
-    const uint32_t w = pack2(row_sum_b<MB>(part, 2 * p, m), row_sum_b<MB>(part, 2 * p + 1, m));
-    ll_put(out + m * rw + u0 / 2 + p, w, ep);
+  const int nq = (u1 - u0) / 4;
+  for (int i = threadIdx.x; i < nq * nrows; i += SNT) {
+    const int m = i / nq, q = i - m * nq;
+    dw_put(out + m * rw + u0 / 4 + q, pack2(row_sum_b<MB>(part, 4 * q, m), row_sum_b<MB>(part, 4 * q + 1, m)),
+           pack2(row_sum_b<MB>(part, 4 * q + 2, m), row_sum_b<MB>(part, 4 * q + 3, m)));
   }
 }
 
@@ -219,14 +217,15 @@ __device__ __forceinline__ float swiglu_one_b(const float* part, int nu, int ul,
 
 template <int MB>
 __device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw,
-                                                     int nrows, uint32_t ep) {
+                                                     int nrows) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0, np = nu / 2;
-  for (int i = threadIdx.x; i < np * nrows; i += SNT) {
-    const int m = i / np, p = i - m * np;
-    const uint32_t w = pack2(swiglu_one_b<MB>(part, nu, 2 * p, m), swiglu_one_b<MB>(part, nu, 2 * p + 1, m));
-    ll_put(out + m * rw + u0 / 2 + p, w, ep);
+  const int nu = u1 - u0, nq = nu / 4;
+  for (int i = threadIdx.x; i < nq * nrows; i += SNT) {
+    const int m = i / nq, q = i - m * nq;
+    dw_put(out + m * rw + u0 / 4 + q,
+           pack2(swiglu_one_b<MB>(part, nu, 4 * q, m), swiglu_one_b<MB>(part, nu, 4 * q + 1, m)),
+           pack2(swiglu_one_b<MB>(part, nu, 4 * q + 2, m), swiglu_one_b<MB>(part, nu, 4 * q + 3, m)));
   }
 }
 
@@ -320,27 +319,26 @@ __host__ __device__ inline int bstep_xcols(int h, int qw) {
 }
 // part rows of the largest projection share (lm_head keeps no partials)
 __host__ __device__ inline int bstep_part_rows(int h, int inter, int qkvw, int nwg) {
-  int r = 2 * cdiv_i(qkvw / 2, nwg);
-  r = r > 2 * cdiv_i(h / 2, nwg) ? r : 2 * cdiv_i(h / 2, nwg);
-  r = r > 4 * cdiv_i(inter / 2, nwg) ? r : 4 * cdiv_i(inter / 2, nwg);
+  int r = 4 * cdiv_i(qkvw / 4, nwg);
+  r = r > 4 * cdiv_i(h / 4, nwg) ? r : 4 * cdiv_i(h / 4, nwg);
+  r = r > 8 * cdiv_i(inter / 4, nwg) ? r : 8 * cdiv_i(inter / 4, nwg);
   return r;
 }
 
-// Words of nrows rows (rw words apart, the first sw of each) into LDS rows
-// xw words apart: word i -> row i / sw, word i % sw
-struct RowsSrc {
-  const llw_t* p;
-  int rw, sw;
-  __device__ const llw_t* operator()(int i) const {
-    const int m = i / sw;
-    return p + (int64_t)m * rw + (i - m * sw);
+// Units (16 bytes) of nrows rows (rw dense words apart, the first su units
+// of each) into LDS rows xw u32 apart: unit j -> row j / su, unit j % su
+struct RowsUnits {
+  int rw, su;
+  __device__ int operator()(int j) const {
+    const int m = j / su;
+    return 8 * m * rw + 16 * (j - m * su);
   }
 };
-struct RowsDst {
-  int sw, xw;
-  __device__ int operator()(int i) const {
-    const int m = i / sw;
-    return m * xw + (i - m * sw);
+struct RowsLds {
+  int su, xw;
+  __device__ int operator()(int j) const {
+    const int m = j / su;
+    return m * xw + 4 * (j - m * su);
   }
 };
 
@@ -381,25 +379,26 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   uint32_t gw1[NGW], gw2[NGW];
   load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
 
-  llw_t* lx_base = a.arena + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB;
+  llw_t* half = cur_half(a, ep);
+  llw_t* lx_base = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB;
   const int64_t lx_row = long_words(a.nkv, S, G, D);
   const int nsl = cdiv_i(inter, BSLICE * CH);   // K slices of the down projection
 
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
     const int64_t* lw = lwt + l * LW_FIELDS;
-    llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
-    llw_t* att_ll = qkv_ll + (int64_t)MB * qkvw / 2;
-    llw_t* o_ll = att_ll + (int64_t)MB * qw / 2;
-    llw_t* act_ll = o_ll + (int64_t)MB * h / 2;
-    llw_t* dn_ll = act_ll + (int64_t)MB * inter / 2;
-    const Gp gq = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 2);
-    const Gp go = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 2);
-    const Gp gg = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 2);
+    llw_t* qkv_ll = half + (int64_t)l * lwords;
+    llw_t* att_ll = qkv_ll + (int64_t)MB * qkvw / 4;
+    llw_t* o_ll = att_ll + (int64_t)MB * qw / 4;
+    llw_t* act_ll = o_ll + (int64_t)MB * h / 4;
+    llw_t* dn_ll = act_ll + (int64_t)MB * inter / 4;
+    const Gp gq = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 4);
+    const Gp go = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 4);
+    const Gp gg = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 4);
     const bf16_t* wdown = reinterpret_cast<const bf16_t*>(lw[LW_DOWN]);
     auto down_slice = [&](int sl) {
       const int c0 = sl * BSLICE, c1 = (sl + 1) * BSLICE < inter / CH ? (sl + 1) * BSLICE : inter / CH;
-      return make_gp(wdown + c0 * CH, (c1 - c0) * CH, h, 0, 2);
+      return make_gp(wdown + c0 * CH, (c1 - c0) * CH, h, 0, 4);
     };
 
     // ---- r = (layer 0) embed[token] | r + down(l-1); norm; qkv
@@ -415,7 +414,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       __syncthreads();
       add_norm_rows<MB>(rr, nullptr, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
     } else {
-      const bool ok = ll_read<BLLW>(LinSrc{dn_prev}, nrows * (h / 2), ep, xs32, a.err, a.spin);
+      const bool ok = dw_read<MB>(dn_prev, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
       if (!wg_all(ok, s_fail)) return false;
       EK_TS(22);
       add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
@@ -426,15 +425,14 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     gemv_phase_b<MB>(gq, h, false, ring, xs, xcols, put);
     __syncthreads();
     EK_TS(2);
-    epilogue_ll_b<MB>(gq, part, qkv_ll, qkvw / 2, nrows, ep);
+    epilogue_ll_b<MB>(gq, part, qkv_ll, qkvw / 4, nrows);
     __syncthreads();
     EK_TS(3);
 
     // ---- split attention (its LDS overlays the activation rows and partials)
     if (attends) {
-      const uint32_t ltag = ep * (uint32_t)MAX_LAYERS + (uint32_t)l;
-      if (!long_attention<D, G>(a, lw, qkv_ll + (int64_t)ub * (qkvw / 2), att_ll + (int64_t)ub * (qw / 2), 0,
-                                lx_base + ub * lx_row, ub, uh, us, hi, ep, ltag, ph, s_fail
+      if (!long_attention<D, G>(a, lw, qkv_ll + (int64_t)ub * (qkvw / 4), att_ll + (int64_t)ub * (qw / 4),
+                                lx_base + ub * lx_row, ub, uh, us, hi, (uint32_t)l + 1u, ph, s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif
@@ -449,9 +447,9 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     // ---- o projection
     zero_part(part, part_n);
     {
-      // row m's words land xcols / 2 words apart
-      const bool ok = ll_read<BLLW>(RowsSrc{att_ll, qw / 2, qw / 2}, nrows * (qw / 2), ep, xs32, a.err, a.spin,
-                                    nullptr, RowsDst{qw / 2, xcols / 2});
+      // row m's values land xcols apart
+      const bool ok = dw_read<MB>(att_ll, RowsUnits{qw / 4, qw / 8}, nrows * (qw / 8), xs32,
+                                  RowsLds{qw / 8, xcols / 2}, a.err, a.spin);
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(6);
@@ -459,7 +457,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     gemv_phase_b<MB>(go, qw, false, ring, xs, xcols, put);
     __syncthreads();
     EK_TS(7);
-    epilogue_ll_b<MB>(go, part, o_ll, h / 2, nrows, ep);
+    epilogue_ll_b<MB>(go, part, o_ll, h / 4, nrows);
     EK_TS(8);
     prefetch_phase_b<PF>(gg, h, false, ring);
 
@@ -467,7 +465,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     __syncthreads();
     zero_part(part, part_n);
     {
-      const bool ok = ll_read<BLLW>(LinSrc{o_ll}, nrows * (h / 2), ep, xs32, a.err, a.spin);
+      const bool ok = dw_read<MB>(o_ll, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(16);
@@ -480,7 +478,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     gemv_phase_b<MB>(gg, h, false, ring, xs, xcols, put);
     __syncthreads();
     EK_TS(10);
-    epilogue_swiglu_ll_b<MB>(gg, part, act_ll, inter / 2, nrows, ep);
+    epilogue_swiglu_ll_b<MB>(gg, part, act_ll, inter / 4, nrows);
     EK_TS(11);
     prefetch_phase_b<PF>(down_slice(0), inter, false, ring);
 
@@ -490,11 +488,11 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     for (int sl = 0; sl < nsl; ++sl) {
       const Gp gd = down_slice(sl);
       const int c0 = sl * BSLICE;
-      const int sw = gd.K / 2;   // words of a row's slice
+      const int su = gd.K / 8;   // units of a row's slice
       if (sl > 0) __syncthreads();   // the previous slice's products have read their LDS rows
       {
-        const bool ok = ll_read<BLLW>(RowsSrc{act_ll + c0 * (CH / 2), inter / 2, sw}, nrows * sw, ep, xs32, a.err,
-                                      a.spin, nullptr, RowsDst{sw, xcols / 2});
+        const bool ok = dw_read<bstep_slice_units<MB>()>(act_ll + c0 * (CH / 4), RowsUnits{inter / 4, su}, nrows * su,
+                                                         xs32, RowsLds{su, xcols / 2}, a.err, a.spin);
         if (!wg_all(ok, s_fail)) return false;
       }
       if (sl == 0) EK_TS(20);
@@ -510,12 +508,12 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         prefetch_phase_b<PF>(down_slice(sl + 1), inter, false, ring);
       else if (l + 1 < a.nl)
         prefetch_phase_b<PF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
-                                     0, 2), h, false, ring);
+                                     0, 4), h, false, ring);
       else
         prefetch_phase_b<PF>(make_gp(a.lm_head, h, a.vocab, 0, 1), h, true, ring);
     }
     __syncthreads();
-    epilogue_ll_b<MB>(down_slice(0), part, dn_ll, h / 2, nrows, ep);
+    epilogue_ll_b<MB>(down_slice(0), part, dn_ll, h / 4, nrows);
     EK_TS(14);
     dn_prev = dn_ll;
     __syncthreads();
@@ -524,7 +522,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
 
   // ---- final add + norm, lm_head, per-workgroup argmax per row
   {
-    const bool ok = ll_read<BLLW>(LinSrc{dn_prev}, nrows * (h / 2), ep, xs32, a.err, a.spin);
+    const bool ok = dw_read<MB>(dn_prev, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
     if (!wg_all(ok, s_fail)) return false;
   }
   add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
@@ -549,14 +547,14 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     for (int m = 0; m < MB; ++m) { sv[wave_id() * MB + m] = am.bv[m]; si[wave_id() * MB + m] = am.bi[m]; }
   }
   __syncthreads();
-  llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
+  llw_t* am_ll = half + (int64_t)a.nl * lwords;
   if (tid < nrows) {
     float ov = sv[tid];
     int oi = si[tid];
     for (int w = 1; w < SNW; ++w)
       if (am_better(sv[w * MB + tid], si[w * MB + tid], ov, oi)) { ov = sv[w * MB + tid]; oi = si[w * MB + tid]; }
-    ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid), __float_as_uint(ov), ep);
-    ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid) + 1, (uint32_t)oi, ep);
+    ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid), __float_as_uint(ov), AM_TAG);
+    ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid) + 1, (uint32_t)oi, AM_TAG);
   }
   return true;
 }
@@ -569,7 +567,7 @@ __device__ __forceinline__ void finish_step_b(const StepArgs& a, uint32_t ep, bo
                                               int qkvw, unsigned char* smem, float* s_red, int* s_redi, int* s_fail) {
   const int tid = threadIdx.x, nrows = a.m;
   const int64_t lwords = (int64_t)MB * arena_layer_words(a.h, a.inter, qkvw, qw);
-  const llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
+  const llw_t* am_ll = cur_half(a, ep) + (int64_t)a.nl * lwords;
   const int nwg = (int)gridDim.x;
   uint32_t* amw = reinterpret_cast<uint32_t*>(smem + bstep_rr_bytes(MB, a.h));
   int* toks = reinterpret_cast<int*>(amw + 2 * nwg * MB);
@@ -582,7 +580,7 @@ __device__ __forceinline__ void finish_step_b(const StepArgs& a, uint32_t ep, bo
         return p + 2 * (int64_t)w * MB + j;
       }
     };
-    ok = wg_all(ll_read<BLLW>(Src{am_ll, nrows}, 2 * nwg * nrows, ep, amw, a.err, a.spin), s_fail);
+    ok = wg_all(ll_read<BLLW>(Src{am_ll, nrows}, 2 * nwg * nrows, AM_TAG, amw, a.err, a.spin), s_fail);
   }
   if (ok) {
     for (int m = 0; m < nrows; ++m) {
@@ -641,7 +639,8 @@ __global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
     s_abort = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  const uint32_t ep = s_ep;
+  const uint32_t ep = __builtin_amdgcn_readfirstlane(s_ep);   // wave-uniform: the halves' addresses stay scalar
+  clear_next_half(a, ep);   // also in a launch that gives up: the next one needs it
   const int64_t len_old = *a.len_t;
   int64_t hi = len_old + 1;
   hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);

@@ -162,3 +162,17 @@ __device__ __forceinline__ uint4 ld16_nt(const bf16_t* p) {
 // every barrier) would wait for it.
 typedef const __attribute__((address_space(1))) uint32_t global_u32_t;
 __device__ __forceinline__ uint32_t ld4(const void* p) { return *(global_u32_t*)(p); }
+
+// Dense hand-over words of the persistent step kernels: word i of a region
+// holds its values 4i .. 4i + 3 (value 4i + j in bits 16j .. 16j + 15, so a
+// region is its bf16 row in memory order), sign bits flipped so that no
+// stored word is zero (zero means "not written yet"), stored with one
+// device-scope store.
+constexpr unsigned long long DW_FLIP = 0x8000800080008000ull;
+constexpr uint32_t DW_FLIP32 = 0x80008000u;
+
+__device__ __forceinline__ void dw_put(unsigned long long* p, uint32_t v01, uint32_t v23) {
+  unsigned long long w = (((unsigned long long)v23 << 32) | v01) ^ DW_FLIP;
+  w = w ? w : 0x8000ull;   // four -0.0 would read as unwritten: the first travels as +0.0
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}

@@ -30,8 +30,8 @@ template <> int bstep_occupancy<8>(int, size_t);
 // load and kept until the process ends; its address on a device comes from
 // hipGetSymbolAddress (the array's name is not a device address in host
 // code). Nothing in it needs clearing between calls: every launch bumps the
-// per-workgroup epochs in the Bar, so words a previous call left in the
-// arena never match a later launch's epoch.
+// per-workgroup epochs in the Bar and zeroes the half of the arena that the
+// next launch hands over through, whatever the shapes of the two calls.
 constexpr size_t kStaticBarBytes = (sizeof(eks::Bar) + 255) / 256 * 256;
 constexpr size_t kStaticArenaBytes = size_t(16) << 20;
 static __device__ __align__(256) unsigned char scratch[kStaticBarBytes + kStaticArenaBytes];
@@ -67,6 +67,7 @@ struct Plan {
   int nwg, kpad_max, part_max, o_rows;
   int lsplit, lchunk;   // long contexts: key splits per kv head and keys per split (0: the attention-unit kernel)
   int64_t lx;           // long contexts: hand-over words of the splits' exchange
+  int64_t half;         // words of one arena half the kernel needs
   int64_t arena_bytes;
   size_t lds;
 };
@@ -138,7 +139,7 @@ hipError_t make_batch_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n
   p.mb = m <= 2 ? 2 : m <= 4 ? 4 : 8;
   const int mb = p.mb;
   int sp = 1;
-  while (2 * sp <= 64 && 2 * sp <= head_dim / 2 && (int64_t)2 * sp * n_kv * mb <= p.nwg) sp *= 2;
+  while (2 * sp <= 32 && 2 * sp <= head_dim / 4 && (int64_t)2 * sp * n_kv * mb <= p.nwg) sp *= 2;
   if ((int64_t)sp * n_kv * mb > p.nwg) return ek_fail(hipErrorInvalidValue, "decode_step: too many attention units");
   const int64_t chunk = (s_cap + sp - 1) / sp;
   if (chunk > (1 << 16))
@@ -170,8 +171,8 @@ hipError_t make_batch_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n
   p.lds = lds;
   if (p.lds > kLdsLimit)
     return ek_fail(hipErrorInvalidValue, "decode_step: this batch's rows or context exceed the workgroup's LDS");
-  p.arena_bytes = 8 * ((int64_t)mb * n_layers * eks::arena_layer_words((int)hidden, (int)inter, qkvw, qw) +
-                       2 * (int64_t)p.nwg * mb + p.lx);
+  p.half = eks::arena_half_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg, mb, p.lx);
+  p.arena_bytes = 16 * p.half;
   if (resident_batch(mb, g, p.lds) < 1)
     return ek_fail(hipErrorInvalidValue, "decode_step: one workgroup per CU does not fit (registers or LDS)");
   (void)vocab;
@@ -204,14 +205,14 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   if (m > 1) return make_batch_plan(hidden, inter, n_q, n_kv, head_dim, vocab, m, s_cap, n_layers, p);
   // Short rows run on attention-only workgroups beside the projections
   // (kUnitMaxKeys above); longer ones on every workgroup, the
-  // keys of each kv head split S ways (S a power of two, at most 64 and at
-  // most head_dim / 2, so that each split owns an even number of head dims
-  // of the combined output)
+  // keys of each kv head split S ways (S a power of two, at most 32 and at
+  // most head_dim / 4, so that each split owns whole 4-value words of the
+  // combined output)
   p.lsplit = p.lchunk = 0;
   p.lx = 0;
   if (s_cap > kUnitMaxKeys || g * s_cap * 4 > kFusedScoreLds) {
     int sp = 1;
-    while (2 * sp <= 64 && 2 * sp <= head_dim / 2 && 2 * sp * n_kv <= p.nwg) sp *= 2;
+    while (2 * sp <= 32 && 2 * sp <= head_dim / 4 && 2 * sp * n_kv <= p.nwg) sp *= 2;
     if (sp < 2) return ek_fail(hipErrorInvalidValue, "decode_step: too few workgroups for the long-context split");
     const int64_t chunk = (s_cap + sp - 1) / sp;
     if (chunk > (1 << 16))
@@ -229,7 +230,7 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   kmax = kmax > (int)inter ? kmax : (int)inter;
   p.kpad_max = eks::kpad_of(kmax);
   const int n_gemv = p.nwg - n_attn;   // projection workgroups
-  p.o_rows = 2 * eks::cdiv_i((int)hidden / 2, n_gemv);
+  p.o_rows = 4 * eks::cdiv_i((int)hidden / 4, n_gemv);
   p.part_max = eks::part_rows_max((int)hidden, (int)inter, qkvw, (int)vocab, n_gemv, p.o_rows);
   const size_t gemv = eks::step_rr_bytes((int)hidden) + eka::align16((size_t)p.kpad_max * 2) +
                       eka::align16((size_t)p.part_max * eks::SNW * 4);
@@ -239,7 +240,8 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   if (p.lds > kLdsLimit)
     return ek_fail(hipErrorInvalidValue, lng ? "decode_step: the context's score rows exceed the LDS of the long-context split"
                                              : "decode_step: LDS plan exceeds the workgroup limit");
-  p.arena_bytes = 8 * eks::arena_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg, p.lx);
+  p.half = eks::arena_half_words((int)n_layers, (int)hidden, (int)inter, qkvw, qw, p.nwg, 1, p.lx);
+  p.arena_bytes = 16 * p.half;
   // every workgroup must be resident at once (the hand-over waits of one
   // need the others running): at least one workgroup of this instantiation,
   // with this LDS, per CU -- registers, scratch and LDS all counted
@@ -291,8 +293,8 @@ hipError_t decode_step_impl(const int64_t* layer_ptrs, int64_t n_layers, int64_t
   if (!layer_ptrs || !embed || !lm_head || !final_norm || !cos || !sin || !tokens || !positions || !len_t ||
       !slot_t || !start_t || !out_buf || !step_idx || !arena || !barrier || !err)
     return ek_fail(hipErrorInvalidValue, "decode_step: null pointer argument");
-  if (arena_bytes < p.arena_bytes)
-    return ek_fail(hipErrorInvalidValue, "decode_step: arena smaller than the plan");
+  const int64_t half = eks::arena_half_of(arena_bytes);
+  if (half < p.half) return ek_fail(hipErrorInvalidValue, "decode_step: arena smaller than the plan");
   if (rope_len < 1 || ld_cs < head_dim || lde < hidden || css % 8 || csh % 8 || csb % 8 ||
       (reinterpret_cast<uintptr_t>(arena) & 15) || (reinterpret_cast<uintptr_t>(embed) & 15))
     return ek_fail(hipErrorInvalidValue, "decode_step: bad strides or alignment");
@@ -307,6 +309,7 @@ hipError_t decode_step_impl(const int64_t* layer_ptrs, int64_t n_layers, int64_t
   a.out_buf = out_buf; a.step_idx = step_idx; a.max_steps = max_steps; a.out_tok = out_tok;
   a.logits = (bf16_t*)logits;
   a.arena = (eks::llw_t*)arena;
+  a.half = half;
   a.bar = (eks::Bar*)barrier; a.err = err; a.spin = ek_wait_limit(kSpin);
   a.kpad_max = p.kpad_max; a.part_max = p.part_max; a.o_rows = p.o_rows;
   a.lsplit = p.lsplit; a.lchunk = p.lchunk; a.lx = p.lx;

@@ -5,17 +5,23 @@
 // add + RMSNorm + gate/up projection + SwiGLU, down projection; then the
 // final add + norm, lm_head and argmax, and the step's bookkeeping.
 //
-// No grid barriers. Every value one workgroup hands to another travels in an
-// 8-byte word {two bf16, epoch} stored with one device-scope store; the
-// consumer polls the words themselves until each carries this launch's epoch.
-// A hand-over therefore costs one store-to-load trip (about a microsecond
+// No grid barriers. Every activation one workgroup hands to another travels
+// in dense 8-byte words of four bf16 values, each stored with one
+// device-scope store with its sign bits flipped, so that no stored word is
+// zero; the consumer polls the words themselves until they are nonzero. A
+// hand-over therefore costs one store-to-load trip (about a microsecond
 // under full HBM load) instead of a store drain, a barrier round trip and a
-// separate load. Every workgroup keeps its own copy of the residual row in
-// LDS and applies the same bf16 adds to it, so the residual never travels.
-// The eight XCD L2 caches are not coherent with each other: the words are
-// stored and loaded with device scope (past the L2), and each location is
-// written once per launch (one arena region per layer), so an old epoch can
-// never be mistaken for a new one. Each workgroup advances its own epoch
+// separate load, and it reads 8 values per 16-byte load. The arena holds
+// two halves: a launch with epoch e hands over through half e & 1 and, at
+// entry, zeroes the whole of half (e + 1) & 1 for the next launch (the
+// launches of one stream run one after another: nothing reads that half
+// meanwhile, and the kernel boundary makes the zeros visible before the next
+// launch starts). Every location of a half is written at most once per
+// launch (one region per layer), so a nonzero word is always this launch's.
+// Every workgroup keeps its own copy of the residual row in LDS and applies
+// the same bf16 adds to it, so the residual never travels. The eight XCD L2
+// caches are not coherent with each other: the words are stored and loaded
+// with device scope (past the L2). Each workgroup advances its own epoch
 // counter at entry, so all workgroups of a launch agree on it without
 // talking. Every wait is bounded: a workgroup that polls past the limit sets
 // the error word and leaves, and every other workgroup leaves at its next
@@ -62,21 +68,13 @@ constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
 constexpr int LW_FIELDS = 10;          // per-layer pointer table row
 constexpr int ATU = 6;                 // attention: 16-key score tiles per wave held in registers
 constexpr int APT = 3;                 // attention: 32-key PV tiles per wave held in registers
-constexpr int LLW = 10;                // hand-over words in flight per thread
+constexpr int LLW = 10;                // tagged words in flight per thread
+constexpr int HW = 1;                  // dense 16-byte units in flight per thread: rows up to 4096 wide
+constexpr int AW = 3;                  // the same for the act row (up to 12288 wide)
 constexpr int NGW = 4;                 // norm gain words per thread (hidden <= 2 * NGW * SNT)
 constexpr int MAX_WG = 1024;
 constexpr int MAX_LAYERS = 64;          // layer table rows held in LDS
 constexpr size_t kStepDynLds = 160 * 1024 - 8 * 1024;   // dynamic LDS limit (the static arrays take the rest)
-// Copies of each all-to-all hand-over region (attention out, o out, act,
-// down out): producers store each word to HC regions and workgroup w polls
-// region w % HC. Measured at the Qwen3-4B shape (config 4, 300 steps):
-// 1.901 ms per step with one region, 1.920 with 2 or 4, 1.954 with 8 -- the
-// 224 pollers of one region do not contend measurably, while every extra
-// copy costs its stores. One region is the default.
-#ifndef EK_HANDOVER_COPIES
-#define EK_HANDOVER_COPIES 1
-#endif
-constexpr int HC = EK_HANDOVER_COPIES;
 
 typedef unsigned long long llw_t;
 
@@ -101,13 +99,14 @@ struct StepArgs {
   int64_t* tokens; int64_t* positions; int64_t* len_t; int64_t* slot_t; const int32_t* start_t;
   int32_t* out_buf; int64_t* step_idx; int64_t max_steps; int64_t* out_tok;
   bf16_t* logits;                      // optional [vocab] bf16 logits of the step (null on the hot path)
-  llw_t* arena;
+  llw_t* arena;                        // two halves of `half` words (the launch uses half ep & 1)
+  int64_t half;
   Bar* bar; int* err; int64_t spin;
   int kpad_max, part_max, o_rows;      // LDS plan (host-computed, see make_plan in ek_step.hip)
   // long contexts (kernels with LONG set): every workgroup runs attention unit
   // (kv head w % nkv, key split w / nkv) of lsplit splits of at most lchunk keys;
-  // lx hand-over words after the argmax words hold the splits' statistics and
-  // partial outputs (one region for every layer: its words carry the layer in their tag)
+  // lx words after the argmax words hold the splits' statistics and partial
+  // outputs (one region for every layer: its words carry the layer in their tag)
   int lsplit, lchunk;
   int64_t lx;
   int m;                               // batch rows (the batch kernel, ek_bstep_impl.h; 0 for batch 1)
@@ -116,31 +115,36 @@ struct StepArgs {
 __host__ __device__ constexpr int cdiv_i(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ constexpr int kpad_of(int k) { return cdiv_i(k, CH) * CH; }
 
-// words per layer of the hand-over arena: qkv, then HC copies each of
-// attention out, o out, act and down out
+// dense words (4 values each) per layer and batch row of a half: qkv,
+// attention out, o out, act, down out (every count a multiple of 8 values,
+// so each region starts on 16 bytes)
 __host__ __device__ inline int64_t arena_layer_words(int h, int inter, int qkvw, int qw) {
-  return (int64_t)(qkvw + HC * (qw + h + inter + h)) / 2;
+  return (int64_t)(qkvw + qw + h + inter + h) / 4;
 }
 
-// this workgroup's copy of an all-to-all region
-__device__ __forceinline__ int my_copy() { return (int)blockIdx.x % HC; }
 // long-context mode's exchange words: (max, sum) per query head of every
 // split, then every split's partial output
 __host__ __device__ inline int64_t long_words(int nkv, int splits, int g, int d) {
   return (int64_t)nkv * splits * (2 * g + g * d);
 }
-// the whole arena: every layer, two argmax words per workgroup, then the
-// long-context exchange (lx words, 0 for the attention-unit kernel)
-__host__ __device__ inline int64_t arena_words(int nl, int h, int inter, int qkvw, int qw, int nwg, int64_t lx = 0) {
-  return nl * arena_layer_words(h, inter, qkvw, qw) + 2 * (int64_t)nwg + lx;
+// words of one half: every layer (mb batch rows each), two tagged argmax
+// words per workgroup and row, then the long-context exchange (lx words, 0
+// for the attention-unit kernel), rounded up to 256 bytes
+__host__ __device__ inline int64_t arena_half_words(int nl, int h, int inter, int qkvw, int qw, int nwg, int mb,
+                                                    int64_t lx) {
+  const int64_t w = nl * mb * arena_layer_words(h, inter, qkvw, qw) + 2 * (int64_t)nwg * mb + lx;
+  return (w + 31) / 32 * 32;
 }
+// the half a launch uses, from an arena of `bytes` (the caller's whole
+// buffer: every launch on one buffer splits it the same way, whatever its plan)
+__host__ __device__ inline int64_t arena_half_of(int64_t bytes) { return bytes / 2 / 256 * 32; }
 
-// rows of one workgroup's largest phase share (units in pairs, or single
+// rows of one workgroup's largest phase share (units in quads, or single
 // rows for lm_head), times two for the gate/up phase
 __host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int vocab, int nwg, int o_rows) {
-  int r = 2 * cdiv_i(qkvw / 2, nwg);
-  r = r > 2 * cdiv_i(h / 2, nwg) ? r : 2 * cdiv_i(h / 2, nwg);
-  r = r > 4 * cdiv_i(inter / 2, nwg) ? r : 4 * cdiv_i(inter / 2, nwg);
+  int r = 4 * cdiv_i(qkvw / 4, nwg);
+  r = r > 4 * cdiv_i(h / 4, nwg) ? r : 4 * cdiv_i(h / 4, nwg);
+  r = r > 8 * cdiv_i(inter / 4, nwg) ? r : 8 * cdiv_i(inter / 4, nwg);
   r = r > cdiv_i(vocab, nwg) ? r : cdiv_i(vocab, nwg);
   r = r > o_rows ? r : o_rows;
   return r;
@@ -163,17 +167,24 @@ __host__ __device__ inline int part_rows_max(int h, int inter, int qkvw, int voc
 // ---------------------------------------------------------------------------
 // hand-over words
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void ll_put(llw_t* p, uint32_t data, uint32_t ep) {
-  __hip_atomic_store(p, ((llw_t)ep << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Tagged words {32-bit data, 32-bit tag}, for the few values that are not
+// bf16 activations: the argmax words (written once per launch, tag AM_TAG)
+// and the long-context exchange (one region reused by every layer, tag
+// layer + 1). They live in the launch's half too, so a zeroed word never
+// matches a tag.
+constexpr uint32_t AM_TAG = 1;
+
+__device__ __forceinline__ void ll_put(llw_t* p, uint32_t data, uint32_t tag) {
+  __hip_atomic_store(p, ((llw_t)tag << 32) | data, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ llw_t ll_get(const llw_t* p) {
   return __hip_atomic_load(const_cast<llw_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ bool ll_ok(llw_t v, uint32_t ep) { return (uint32_t)(v >> 32) == ep; }
+__device__ __forceinline__ bool ll_ok(llw_t v, uint32_t tag) { return (uint32_t)(v >> 32) == tag; }
 
-// Wait until the n words src(i), i < n, carry epoch ep and store their data
+// Wait until the n words src(i), i < n, carry tag `ep` and store their data
 // halves in dst[i] (LDS). Thread t handles i = t + k * SNT; up to LLW words
 // per thread are in flight at once, and only the words not yet valid are
 // loaded again. False (the error word set) when a wait runs out.
@@ -250,6 +261,88 @@ __device__ __forceinline__ bool ll_wait1(const llw_t* p, uint32_t tag, uint32_t&
   }
   out = (uint32_t)v;
   return true;
+}
+
+// Two words (16 bytes) at byte offset `off` of a region, loaded with device
+// scope: the cache-policy bits of the agent-scope atomic load (sc1) on a
+// buffer load, since a 16-byte load has no atomic form. Each 8-byte half is
+// what one producer store wrote, and is checked on its own.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dw_rsrc(const llw_t* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<llw_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t dw_get2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
+__device__ __forceinline__ bool dw_ok2(const u32x4_t& v) { return (v.x | v.y) != 0u && (v.z | v.w) != 0u; }
+
+// Wait until the n units j < n (16 bytes at byte offset src(j) of the region
+// at base, 8 values) are written, and store their values in LDS at
+// dst + dix(j) (a u32 index, a multiple of 4). Thread t handles j = t + k SNT;
+// up to W units per thread are in flight at once, and only the units not
+// yet whole are loaded again. False (the error word set) when a wait runs out.
+struct LinUnits {   // unit j of one region -> byte 16 j; LDS u32 4 j
+  __device__ int operator()(int j) const { return 16 * j; }
+};
+struct LinLds {
+  __device__ int operator()(int j) const { return 4 * j; }
+};
+
+template <int W, typename SRC, typename DST>
+__device__ __forceinline__ bool dw_read(const llw_t* base, SRC src, int n, uint32_t* dst, DST dix, int* err,
+                                        int64_t spin, int64_t* rounds = nullptr) {
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t r = dw_rsrc(base);
+  for (int b0 = 0; b0 < n; b0 += W * SNT) {
+    u32x4_t v[W];
+    // every load issued, at a clamped unit past n (a load under a lane
+    // condition becomes a branch that waits for it), then masked
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int j = b0 + tid + k * SNT;
+      v[k] = dw_get2(r, src(j < n ? j : 0));
+    }
+    int64_t it = 0;
+    while (true) {
+      bool done = true;
+#pragma unroll
+      for (int k = 0; k < W; ++k) done = done && (b0 + tid + k * SNT >= n || dw_ok2(v[k]));
+      if (done) break;
+      if (rounds) ++*rounds;
+      if (++it > spin) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
+      }
+      if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+#pragma unroll
+      for (int k = 0; k < W; ++k) {
+        const int j = b0 + tid + k * SNT;
+        if (j < n && !dw_ok2(v[k])) v[k] = dw_get2(r, src(j));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int j = b0 + tid + k * SNT;
+      if (j < n)
+        *reinterpret_cast<uint4*>(dst + dix(j)) =
+            make_uint4(v[k].x ^ DW_FLIP32, v[k].y ^ DW_FLIP32, v[k].z ^ DW_FLIP32, v[k].w ^ DW_FLIP32);
+    }
+  }
+  return true;
+}
+
+// Zero this workgroup's share of the half the next launch uses (16-byte
+// global stores spread over the grid; a.half is a multiple of 32 words).
+typedef __attribute__((address_space(1))) u32x4_t global_w_u32x4_t;
+__device__ __forceinline__ void clear_next_half(const StepArgs& a, uint32_t ep) {
+  global_w_u32x4_t* h = (global_w_u32x4_t*)(a.arena + (int64_t)((ep + 1u) & 1u) * a.half);
+  const int64_t n = a.half / 2;
+  const u32x4_t z = {0u, 0u, 0u, 0u};
+  for (int64_t i = (int64_t)blockIdx.x * SNT + threadIdx.x; i < n; i += (int64_t)gridDim.x * SNT) h[i] = z;
+}
+
+// the half this launch hands over through
+__device__ __forceinline__ llw_t* cur_half(const StepArgs& a, uint32_t ep) {
+  return a.arena + (int64_t)(ep & 1u) * a.half;
 }
 
 // ---------------------------------------------------------------------------
@@ -534,17 +627,15 @@ __device__ __forceinline__ float row_sum(const float* part, int r) {
   return s;
 }
 
-// out word (u0 + 2i) / 2 = {bf16(row u0 + 2i), bf16(row u0 + 2i + 1)} for this
-// workgroup's rows, stored to `copies` regions `stride` words apart
-__device__ __forceinline__ void epilogue_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep, int copies = 1,
-                                            int64_t stride = 0) {
+// out word (u0 + 4i) / 4 = bf16 rows u0 + 4i .. u0 + 4i + 3 of this
+// workgroup's rows (units in quads)
+__device__ __forceinline__ void epilogue_ll(const Gp& P, const float* part, llw_t* out) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int np = (u1 - u0) / 2;
-  for (int i = threadIdx.x; i < np; i += SNT) {
-    const uint32_t w = pack2(row_sum(part, 2 * i), row_sum(part, 2 * i + 1));
-    for (int c = 0; c < copies; ++c) ll_put(out + c * stride + u0 / 2 + i, w, ep);
-  }
+  const int nq = (u1 - u0) / 4;
+  for (int i = threadIdx.x; i < nq; i += SNT)
+    dw_put(out + u0 / 4 + i, pack2(row_sum(part, 4 * i), row_sum(part, 4 * i + 1)),
+           pack2(row_sum(part, 4 * i + 2), row_sum(part, 4 * i + 3)));
 }
 
 // act = bf16(bf16(silu(bf16 g)) * bf16 u)   (ek_kernels.py:1247-1261, :1062-1076)
@@ -555,15 +646,13 @@ __device__ __forceinline__ float swiglu_one(const float* part, int nu, int ul) {
   return s * up;
 }
 
-__device__ __forceinline__ void epilogue_swiglu_ll(const Gp& P, const float* part, llw_t* out, uint32_t ep,
-                                                   int copies, int64_t stride) {
+__device__ __forceinline__ void epilogue_swiglu_ll(const Gp& P, const float* part, llw_t* out) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0, np = nu / 2;
-  for (int i = threadIdx.x; i < np; i += SNT) {
-    const uint32_t w = pack2(swiglu_one(part, nu, 2 * i), swiglu_one(part, nu, 2 * i + 1));
-    for (int c = 0; c < copies; ++c) ll_put(out + c * stride + u0 / 2 + i, w, ep);
-  }
+  const int nu = u1 - u0, nq = nu / 4;
+  for (int i = threadIdx.x; i < nq; i += SNT)
+    dw_put(out + u0 / 4 + i, pack2(swiglu_one(part, nu, 4 * i), swiglu_one(part, nu, 4 * i + 1)),
+           pack2(swiglu_one(part, nu, 4 * i + 2), swiglu_one(part, nu, 4 * i + 3)));
 }
 
 // (a better, b) under "larger value, then lower index"; index 0x7fffffff = none
@@ -588,7 +677,7 @@ __device__ __forceinline__ void wg_argmax(float bv, int bi, float* sv, int* si, 
 }
 
 __device__ __forceinline__ void epilogue_argmax_ll(const Gp& P, const float* part, float* sv, int* si, llw_t* am,
-                                                   uint32_t ep, bf16_t* logits) {
+                                                   bf16_t* logits) {
   int u0, u1;
   unit_range(P, u0, u1);
   const int nu = u1 - u0;
@@ -603,8 +692,8 @@ __device__ __forceinline__ void epilogue_argmax_ll(const Gp& P, const float* par
   int oi;
   wg_argmax(bv, bi, sv, si, ov, oi);
   if (threadIdx.x == 0) {
-    ll_put(am + 2 * blockIdx.x, __float_as_uint(ov), ep);
-    ll_put(am + 2 * blockIdx.x + 1, (uint32_t)oi, ep);
+    ll_put(am + 2 * blockIdx.x, __float_as_uint(ov), AM_TAG);
+    ll_put(am + 2 * blockIdx.x + 1, (uint32_t)oi, AM_TAG);
   }
 }
 
@@ -685,28 +774,34 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
   zero_pad(xs, k, kpad);
 }
 
+// The qkv units (8 values) an attention unit of kv head h reads, in its LDS
+// order: its G query heads, the new key, the new value (byte offsets in the
+// qkv region of one batch row)
+template <int D, int G>
+struct HeadUnits {
+  int h, nq, nkv;
+  __device__ int operator()(int j) const {
+    const int t = j / (D / 8), r = j - t * (D / 8);
+    const int head = t < G ? h * G + t : (t == G ? nq + h : nq + nkv + h);
+    return head * D * 2 + r * 16;
+  }
+};
+
 // ---------------------------------------------------------------------------
 // attention phase: workgroup w < n_kv * D / 32 runs unit w
 // ---------------------------------------------------------------------------
 template <int D, int G>
 __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
-                                                int64_t hi, uint32_t ep, unsigned char* smem, int* s_fail, int layer
+                                                int64_t hi, unsigned char* smem, int* s_fail, int layer
 #ifdef EK_STEP_TRACE
                                                 , int64_t* ts_lds
 #endif
                                                 ) {
   (void)layer;
   const int h = (int)blockIdx.x % a.nkv, c = (int)blockIdx.x / a.nkv;
-  // this unit's q heads, new key and new value -> LDS (bf16 pairs)
+  // this unit's q heads, new key and new value -> LDS (bf16 rows)
   bf16_t* qrow = reinterpret_cast<bf16_t*>(smem);
-  const int hw = D / 2;   // words per head
-  const int qbase = h * G * hw, kbase = (a.nq + h) * hw, vbase = (a.nq + a.nkv + h) * hw;
-  struct Src {
-    const llw_t* p; int hw, g, qbase, kbase, vbase;
-    __device__ const llw_t* operator()(int i) const {
-      return p + (i < g * hw ? qbase + i : (i < (g + 1) * hw ? kbase + i - g * hw : vbase + i - (g + 1) * hw));
-    }
-  } src{qkv, hw, G, qbase, kbase, vbase};
+  const HeadUnits<D, G> src{h, a.nq, a.nkv};
   // the q/k norm gains and this position's cos/sin rows, copied to LDS while
   // the unit waits, so that the RoPE work after the wait reads only LDS
   bf16_t* rope_lds = qrow + (G + 2) * D;   // [q gain | k gain | cos | sin] x D
@@ -736,10 +831,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
   u.d0 = c * eka::FDC;
   u.out = nullptr;
   u.out_stride = D;
-  u.ll_out = att + (int64_t)h * G * hw;
-  u.ll_ep = ep;
-  u.ll_copies = HC;
-  u.ll_copy_stride = (int64_t)a.nq * D / 2;
+  u.ll_out = att + (int64_t)h * G * (D / 4);
 #ifdef EK_STEP_TRACE
   u.trace_lds = ts_lds;
 #endif
@@ -749,7 +841,8 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
       const int t = i / D, d = i - t * D;
       rope_lds[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
     }
-    const bool ok = ll_read<2>(src, (G + 2) * hw, ep, reinterpret_cast<uint32_t*>(qrow), a.err, a.spin);
+    const bool ok = dw_read<1>(qkv, src, (G + 2) * (D / 8), reinterpret_cast<uint32_t*>(qrow), LinLds{}, a.err,
+                               a.spin);
     return wg_all(ok, s_fail);
   };
   return eka::attn_unit<D, G, ATU, APT>(u, smem + eka::align16((size_t)(G + 6) * D * 2), wait_heads);
@@ -767,7 +860,7 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 //            per 16-key tile on the matrix cores, scaled, into an LDS row per
 //            head; the split's max m_s and sum l_s = sum exp(s - m_s) per head
 //   stats    every split's (m_s, l_s) of the head travel as tagged words
-//            (tag: the launch epoch and the layer, since every layer reuses
+//            (tag: the layer + 1, since every layer of the launch reuses
 //            the region: a layer's words are overwritten only by a workgroup
 //            past that layer's o projection wait, which needs every unit's
 //            combine, hence every read of them, done), so
@@ -776,9 +869,10 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 //   PV       p = bf16(exp(s - M) / L), the reference fallback's rounding point
 //            (engine/ek_model.py:475-488), and the split's partial output
 //            sum p v over its keys for all head dims, in fp32
-//   combine  unit s owns head dims [s D/S, (s+1) D/S) of the G query heads:
-//            it adds the S splits' partials of those dims in split order and
-//            stores them as the bf16 attention words the o projection awaits.
+//   combine  unit s owns head dims [s D/S, (s+1) D/S) of the G query heads
+//            (S <= D / 4: whole dense words): it adds the S splits' partials
+//            of those dims in split order and stores them as the bf16
+//            attention words the o projection awaits.
 // The split holding the new slot stores the new key and value rows last.
 // long contexts: 16-key score tiles per wave and value rows per thread in flight
 #ifndef EK_STEP_LUT
@@ -808,10 +902,10 @@ struct LongLds {
 
 template <int D, int G>
 // Unit (kv head h, split s) of batch row b; qkv, att and lx point at row b's
-// words (att's copies att_cstride words apart).
+// words; ltag tags this layer's exchange words.
 __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
-                                               int64_t att_cstride, llw_t* lx, int b, int h, int s, int64_t hi,
-                                               uint32_t ep, uint32_t ltag, unsigned char* lds, int* s_fail
+                                               llw_t* lx, int b, int h, int s, int64_t hi, uint32_t ltag,
+                                               unsigned char* lds, int* s_fail
 #ifdef EK_STEP_TRACE
                                                , int64_t* ts_lds
 #endif
@@ -826,7 +920,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   const int tid = opaque_tid(), lane = tid & 63, wave = wave_id();
   const int r16 = lane & 15, q4 = lane >> 4;
   if (s >= S) return true;
-  const int hw = D / 2, dpu = D / S;   // dims this unit combines
+  const int dpu = D / S;   // dims this unit combines
 
   bf16_t* heads = reinterpret_cast<bf16_t*>(lds);
   bf16_t* rope = reinterpret_cast<bf16_t*>(lds + L::HEADS);
@@ -891,13 +985,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
       const int t = i / D, d = i - t * D;
       rope[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
     }
-    struct Src {
-      const llw_t* p; int hw, g, qbase, kbase, vbase;
-      __device__ const llw_t* operator()(int i) const {
-        return p + (i < g * hw ? qbase + i : (i < (g + 1) * hw ? kbase + i - g * hw : vbase + i - (g + 1) * hw));
-      }
-    } src{qkv, hw, G, h * G * hw, (a.nq + h) * hw, (a.nq + a.nkv + h) * hw};
-    const bool ok = ll_read<2>(src, (G + 2) * hw, ep, reinterpret_cast<uint32_t*>(heads), a.err, a.spin);
+    const bool ok = dw_read<1>(qkv, HeadUnits<D, G>{h, a.nq, a.nkv}, (G + 2) * (D / 8),
+                               reinterpret_cast<uint32_t*>(heads), LinLds{}, a.err, a.spin);
     if (!wg_all(ok, s_fail)) return false;
   }
   EK_TS(28);
@@ -1111,11 +1200,10 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     }
     if (!wg_all(ok, s_fail)) return false;
     EK_TS(5);
-    for (int i = tid; i < G * dpu / 2; i += SNT) {
-      const int g = (2 * i) / dpu, dd = 2 * i - g * dpu;
-      for (int c = 0; c < HC; ++c)
-        ll_put(att + (int64_t)c * att_cstride + ((int64_t)(h * G + g) * D + s * dpu + dd) / 2,
-               pack2(cmb[2 * i], cmb[2 * i + 1]), ep);
+    for (int i = tid; i < G * dpu / 4; i += SNT) {
+      const int g = (4 * i) / dpu, dd = 4 * i - g * dpu;
+      dw_put(att + ((int64_t)(h * G + g) * D + s * dpu + dd) / 4, pack2(cmb[4 * i], cmb[4 * i + 1]),
+             pack2(cmb[4 * i + 2], cmb[4 * i + 3]));
     }
   }
   // the new key and value rows (normed and rotated key, raw value)
@@ -1153,11 +1241,12 @@ __device__ __forceinline__ void attention_loop(const StepArgs& a, const int64_t*
                                                ) {
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = arena_layer_words(a.h, a.inter, qkvw, qw);
+  llw_t* half = cur_half(a, ep);
   for (int l = 0; l < a.nl; ++l) {
     const int64_t* lw = lwt + l * LW_FIELDS;
-    const llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
-    llw_t* att_ll = a.arena + (int64_t)l * lwords + qkvw / 2;
-    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, ep, smem, s_fail, l
+    const llw_t* qkv_ll = half + (int64_t)l * lwords;
+    llw_t* att_ll = half + (int64_t)l * lwords + qkvw / 4;
+    if (!attention_phase<D, G>(a, lw, qkv_ll, att_ll, hi, smem, s_fail, l
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif
@@ -1206,20 +1295,20 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   uint32_t gw1[NGW], gw2[NGW];
   load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
 
+  llw_t* half = cur_half(a, ep);
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
     EK_TS(0);
     const int64_t* lw = lwt + l * LW_FIELDS;
-    llw_t* qkv_ll = a.arena + (int64_t)l * lwords;
-    llw_t* att_ll = qkv_ll + qkvw / 2;           // HC copies of each region from here on
-    llw_t* o_ll = att_ll + HC * (qw / 2);
-    llw_t* act_ll = o_ll + HC * (h / 2);
-    llw_t* dn_ll = act_ll + HC * (inter / 2);
-    const int cp = my_copy();
-    const Gp gq = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 2), n_attn);
-    const Gp go = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 2), n_attn);
-    const Gp gg = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 2), n_attn);
-    const Gp gd = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_DOWN]), inter, h, 0, 2), n_attn);
+    llw_t* qkv_ll = half + (int64_t)l * lwords;
+    llw_t* att_ll = qkv_ll + qkvw / 4;
+    llw_t* o_ll = att_ll + qw / 4;
+    llw_t* act_ll = o_ll + h / 4;
+    llw_t* dn_ll = act_ll + inter / 4;
+    const Gp gq = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 4), n_attn);
+    const Gp go = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 4), n_attn);
+    const Gp gg = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 4), n_attn);
+    const Gp gd = on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lw[LW_DOWN]), inter, h, 0, 4), n_attn);
 
     // ---- r = (layer 0) embed[token] | r + down(l-1); norm; qkv
     zero_part(part, part_n);
@@ -1237,10 +1326,10 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       EK_TS(22);
 #ifdef EK_STEP_TRACE
       int64_t rounds = 0;
-      const bool ok = ll_read(LinSrc{dn_prev + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin, &rounds);
+      const bool ok = dw_read<HW>(dn_prev, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin, &rounds);
       if (threadIdx.x == 0) ts_lds[23] = rounds;
 #else
-      const bool ok = ll_read(LinSrc{dn_prev + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
+      const bool ok = dw_read<HW>(dn_prev, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin);
 #endif
       if (!wg_all(ok, s_fail)) return false;
       add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
@@ -1251,17 +1340,16 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     gemv_phase(gq, ring, xs, part);
     __syncthreads();
     EK_TS(2);
-    epilogue_ll(gq, part, qkv_ll, ep);
+    epilogue_ll(gq, part, qkv_ll);
     EK_TS(3);
     __syncthreads();
 
     if constexpr (LONG) {
       // ---- attention on every workgroup (its LDS overlays the activation
       //      row and the partials), then the o projection from the ring
-      llw_t* lx_ll = a.arena + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
-      if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, (int64_t)qw / 2, lx_ll, 0, (int)blockIdx.x % a.nkv,
-                                (int)blockIdx.x / a.nkv, hi, ep, ep * (uint32_t)MAX_LAYERS + (uint32_t)l, ph,
-                                s_fail
+      llw_t* lx_ll = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
+      if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, lx_ll, 0, (int)blockIdx.x % a.nkv, (int)blockIdx.x / a.nkv,
+                                hi, (uint32_t)l + 1u, ph, s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif
@@ -1273,7 +1361,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       __syncthreads();
       zero_part(part, part_n);
       {
-        const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
+        const bool ok = dw_read<HW>(att_ll, LinUnits{}, qw / 8, xs32, LinLds{}, a.err, a.spin);
         if (!wg_all(ok, s_fail)) return false;
       }
       zero_pad(xs, qw, kpad_of(qw));
@@ -1282,7 +1370,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       gemv_phase(go, ring, xs, part);
       __syncthreads();
       EK_TS(7);
-      epilogue_ll(go, part, o_ll, ep, HC, h / 2);
+      epilogue_ll(go, part, o_ll);
       prefetch_phase<PF>(gg, ring);
       EK_TS(8);
     } else {
@@ -1299,7 +1387,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       // ---- o projection
       zero_part(part, part_n);
       {
-        const bool ok = ll_read(LinSrc{att_ll + cp * (qw / 2)}, qw / 2, ep, xs32, a.err, a.spin);
+        const bool ok = dw_read<HW>(att_ll, LinUnits{}, qw / 8, xs32, LinLds{}, a.err, a.spin);
         if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
         if (!wg_all(ok, s_fail)) return false;
       }
@@ -1311,7 +1399,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       EK_TS(30);
       __syncthreads();
       EK_TS(7);
-      epilogue_ll(go, part, o_ll, ep, HC, h / 2);
+      epilogue_ll(go, part, o_ll);
       EK_TS(8);
     }
 
@@ -1322,11 +1410,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       EK_TS(15);
 #ifdef EK_STEP_TRACE
       int64_t rounds = 0;
-      const bool ok = ll_read(LinSrc{o_ll + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin, &rounds);
+      const bool ok = dw_read<HW>(o_ll, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin, &rounds);
       EK_TS(16);
       if (threadIdx.x == 0) ts_lds[18] = rounds;
 #else
-      const bool ok = ll_read(LinSrc{o_ll + cp * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
+      const bool ok = dw_read<HW>(o_ll, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin);
 #endif
       if (!wg_all(ok, s_fail)) return false;
       EK_TS(17);
@@ -1342,7 +1430,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     gemv_phase(gg, ring, xs, part);
     __syncthreads();
     EK_TS(10);
-    epilogue_swiglu_ll(gg, part, act_ll, ep, HC, inter / 2);
+    epilogue_swiglu_ll(gg, part, act_ll);
     EK_TS(11);
     prefetch_phase<PF>(gd, ring);
     EK_TS(27);
@@ -1354,11 +1442,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       EK_TS(19);
 #ifdef EK_STEP_TRACE
       int64_t rounds = 0;
-      const bool ok = ll_read(LinSrc{act_ll + cp * (inter / 2)}, inter / 2, ep, xs32, a.err, a.spin, &rounds);
+      const bool ok = dw_read<AW>(act_ll, LinUnits{}, inter / 8, xs32, LinLds{}, a.err, a.spin, &rounds);
       EK_TS(20);
       if (threadIdx.x == 0) ts_lds[21] = rounds;
 #else
-      const bool ok = ll_read(LinSrc{act_ll + cp * (inter / 2)}, inter / 2, ep, xs32, a.err, a.spin);
+      const bool ok = dw_read<AW>(act_ll, LinUnits{}, inter / 8, xs32, LinLds{}, a.err, a.spin);
 #endif
       if (!wg_all(ok, s_fail)) return false;
     }
@@ -1368,11 +1456,11 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     gemv_phase(gd, ring, xs, part);
     __syncthreads();
     EK_TS(13);
-    epilogue_ll(gd, part, dn_ll, ep, HC, h / 2);
+    epilogue_ll(gd, part, dn_ll);
     EK_TS(14);
     if (l + 1 < a.nl)
       prefetch_phase<PF>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]),
-                                         h, qkvw, 0, 2), n_attn), ring);
+                                         h, qkvw, 0, 4), n_attn), ring);
     else
       prefetch_phase<PF>(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
     dn_prev = dn_ll;
@@ -1382,10 +1470,10 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
 
   // ---- final add + norm, lm_head, per-workgroup argmax
   EK_TS(0);
-  llw_t* am_ll = a.arena + (int64_t)a.nl * lwords;
+  llw_t* am_ll = half + (int64_t)a.nl * lwords;
   zero_part(part, part_n);
   {
-    const bool ok = ll_read(LinSrc{dn_prev + my_copy() * (h / 2)}, h / 2, ep, xs32, a.err, a.spin);
+    const bool ok = dw_read<HW>(dn_prev, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin);
     if (!wg_all(ok, s_fail)) return false;
   }
   add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
@@ -1395,7 +1483,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   gemv_phase(gl, ring, xs, part);
   __syncthreads();
   EK_TS(2);
-  epilogue_argmax_ll(gl, part, s_red, s_redi, am_ll, ep, a.logits);
+  epilogue_argmax_ll(gl, part, s_red, s_redi, am_ll, a.logits);
   EK_TS(3);
   EK_TS_FLUSH_SYNC(a.nl);
   return true;
@@ -1415,10 +1503,10 @@ __device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool
   const int h = a.h;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int n_gemv = (int)gridDim.x - n_attn;
-  const llw_t* am_ll = a.arena + (int64_t)a.nl * arena_layer_words(h, a.inter, qkvw, qw);
+  const llw_t* am_ll = cur_half(a, ep) + (int64_t)a.nl * arena_layer_words(h, a.inter, qkvw, qw);
   uint32_t* amw = reinterpret_cast<uint32_t*>(smem + step_rr_bytes(h) + eka::align16((size_t)a.kpad_max * 2));
   __syncthreads();
-  if (ok) ok = wg_all(ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, ep, amw, a.err, a.spin), s_fail);
+  if (ok) ok = wg_all(ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, AM_TAG, amw, a.err, a.spin), s_fail);
   float ov = 0.f;
   int oi = 0x7fffffff;
   if (ok) {
@@ -1472,8 +1560,9 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
   int64_t* ts_lds = s_ts;
 #endif
   __syncthreads();
-  const uint32_t ep = s_ep;
+  const uint32_t ep = __builtin_amdgcn_readfirstlane(s_ep);   // wave-uniform: the halves' addresses stay scalar
   const bool aborted = s_abort != 0;
+  clear_next_half(a, ep);   // also in a launch that gives up: the next one needs it
   const int64_t len_old = *a.len_t;
   int64_t hi = len_old + 1;
   hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);

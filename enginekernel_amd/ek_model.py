@@ -188,12 +188,12 @@ class Qwen3(torch.nn.Module):
         self._tables: dict = {}
         # the whole step as one persistent launch where its plan allows
         # (ENGINE_PERSISTENT=0 selects the per-kernel graph step everywhere),
-        # up to persistent_rows rows: at the Qwen3-4B shape and config 5's
-        # prompts the one-launch step is faster at 2, 4 and 6 rows (2.57 /
-        # 3.28 / 4.00 ms against 3.09 / 3.57 / 4.30) and slower at 8 (4.53
-        # against 3.99), where every workgroup reads 8 rows of hand-over words
+        # up to persistent_rows rows (ENGINE_PERSISTENT_ROWS): at the
+        # Qwen3-4B shape and config 5's prompts the one-launch step is the
+        # faster one at every batch it takes (2, 4 and 8 rows: 2.19 / 2.62 /
+        # 3.45 ms against 3.03 / 3.49 / 3.95 for the per-kernel graph)
         self.persistent = os.environ.get("ENGINE_PERSISTENT", "1") != "0"
-        self.persistent_rows = int(os.environ.get("ENGINE_PERSISTENT_ROWS", "6"))
+        self.persistent_rows = int(os.environ.get("ENGINE_PERSISTENT_ROWS", "8"))
         # the prefill's hipBLASLt projections: no reduced-precision bf16 reductions
         torch.backends.cuda.matmul.allow_bf16_reduced_precision_reduction = False
 

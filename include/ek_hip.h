@@ -243,15 +243,18 @@ int ek_decode_step_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv
  * b] = token if *step_idx < max_steps, *step_idx += 1, out_tok[b] = token if
  * out_tok; logits[b * vocab ..) = row b's bf16 logits if logits is not
  * NULL), for the m rows of the batch (b < m). One workgroup per CU; workgroups hand activations to each other
- * through the arena as {data, epoch} words that the consumer polls, with no
- * grid barrier.
+ * through the arena as dense words of four bf16 that the consumer polls
+ * until they are nonzero, with no grid barrier: the arena is two halves,
+ * each launch hands over through one and zeroes the other for the next.
  * layer_ptrs: device int64 [n_layers][10] = addresses of qkv [(n_q + 2 n_kv) D,
  * hidden], o [hidden, n_q D], gate/up [2 inter, hidden], down [hidden, inter],
  * ln1, ln2 [hidden], q_norm, k_norm [D], k_cache, v_cache [B, n_kv, S, D] of
  * each layer (bf16, all caches with strides csb/csh/css). arena: the
- * hand-over arena (decode_step_plan sizes[0] bytes) and barrier: the
- * launch-state block (sizes[2] bytes), both zero before the first launch and
- * kept between launches (they hold the launch epoch); err: set to 1 (and the
+ * hand-over arena (at least decode_step_plan sizes[0] bytes; every launch on
+ * one arena must pass the same arena_bytes, which fixes where its halves
+ * lie) and barrier: the launch-state block (sizes[2] bytes), both zero before
+ * the first launch and kept between launches (they hold the launch epoch and
+ * the next launch's cleared half); err: set to 1 (and the
  * launch abandoned) if a hand-over wait exceeds its bound. An abandoned
  * launch, and every launch that starts while err is set, still advances
  * *step_idx and writes -1 as its token to out_buf and out_tok, leaving
@@ -279,7 +282,8 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
  * hipErrorInvalidValue. Every call on one device shares that device's array:
  * calls that overlap on a device (other streams, other threads) race and must
  * not be issued. The array never needs clearing (each launch moves its
- * epoch on); after an abandoned launch zero only *err. Same arguments,
+ * epoch on and clears the half the next launch uses); after an abandoned
+ * launch zero only *err. Same arguments,
  * results and error behaviour as decode_step otherwise.
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses

@@ -45,7 +45,7 @@ def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
     random token, instead of the oracle's prefill (too slow on the CPU for
     long prompts)."""
     cfg, om, model = mid
-    model.persistent_rows = 8     # the batch kernel at every row count (the default stops at 6)
+    model.persistent_rows = 8     # the batch kernel at every row count (the default, set here explicitly)
     b = len(prompts)
     ids, pos, pad, s, bias = O.pack(prompts)
     total = cap or s + steps + 1

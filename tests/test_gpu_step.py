@@ -285,8 +285,9 @@ def test_persistent_plan_split_bounds(dev):
     assert sizes[1] == 0
     assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1537, 36, sizes) == 0
     assert sizes[1] == 32 and sizes[3] == 256
-    # the split exchange: (max, sum) per query head and a partial output per split
-    assert sizes[0] == short_arena + 8 * 8 * 32 * (2 * 4 + 4 * 128)
+    # the split exchange: (max, sum) per query head and a partial output per
+    # split, 8-byte words, in each of the arena's two halves
+    assert sizes[0] == short_arena + 2 * 8 * 8 * 32 * (2 * 4 + 4 * 128)
     assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 131072, 36, sizes) == 0
     assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1 << 18, 36, sizes) == 1
     assert b"LDS" in lib.ek_last_error()
