@@ -233,12 +233,19 @@ __device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* p
 // [m][k / 2] in xw, or no add when xw is null); xs row m (xstride apart) =
 // bf16(w * bf16(rr * rsqrt(mean(rr^2) + eps)))   (ek_kernels.py:1025-1059).
 // Row m belongs to the WPR = 8 / MB waves m WPR .. m WPR + WPR - 1, which take
-// its words in turn (64 at a time). One barrier: it separates the residual
-// update and the row sums of squares (pass 1, which reads the staged words
-// in xw) from the output (pass 2, which may overwrite them: xs and xw share
-// the LDS), and carries the waves' partial sums (red, fixed order). The gain
-// words come from the registers gw (thread t: words t + j SNT) via the LDS
-// row gl.
+// its 16-byte pieces (8 values) in turn, 64 at a time (k is a multiple of
+// 512, so every round is whole for a wave). One barrier: it separates the
+// residual update and the row sums of squares (pass 1, which reads the
+// staged words in xw) from the output (pass 2, which may overwrite them: xs
+// and xw share the LDS), and carries the waves' partial sums (red, fixed
+// order). The gain words come from the registers gw (thread t: words
+// t + j SNT) via the LDS row gl.
+__device__ __forceinline__ uint32_t add2_bf(uint32_t r, uint32_t x) { return pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x)); }
+__device__ __forceinline__ float sq2(uint32_t r, float ss) { return fmaf(hi_bf(r), hi_bf(r), fmaf(lo_bf(r), lo_bf(r), ss)); }
+__device__ __forceinline__ uint32_t norm2(uint32_t r, uint32_t g, float rstd) {
+  return pack2(rbf(lo_bf(g) * rbf(lo_bf(r) * rstd)), rbf(hi_bf(g) * rbf(hi_bf(r) * rstd)));
+}
+
 template <int MB>
 __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, const uint32_t* gw, uint32_t* gl,
                                               int k, int nrows, float eps, bf16_t* xs, int xstride, float* red) {
@@ -246,7 +253,7 @@ __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, 
   constexpr int WPR = SNW / MB;
   const int tid = opaque_tid(), lane = tid & 63, wave = wave_id();
   const int m = wave / WPR, part = wave - m * WPR;
-  const int nw = k / 2;
+  const int nw = k / 2, n4 = k / 8;   // words, 16-byte pieces of a row
 #pragma unroll
   for (int j = 0; j < NGW; ++j) {
     const int i = tid + j * SNT;
@@ -254,17 +261,18 @@ __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, 
   }
   const int i0 = part * EK_WAVE + lane;
   if (m < nrows) {
-    uint32_t* rrow = rr + m * nw;
+    uint4* rrow = reinterpret_cast<uint4*>(rr + m * nw);
+    const uint4* xrow = reinterpret_cast<const uint4*>(xw + m * nw);
     float ss = 0.f;
-    for (int i = i0; i < nw; i += WPR * EK_WAVE) {
-      uint32_t r = rrow[i];
+#pragma unroll 4
+    for (int i = i0; i < n4; i += WPR * EK_WAVE) {
+      uint4 r = rrow[i];
       if (xw) {
-        const uint32_t x = xw[m * nw + i];
-        r = pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x));
+        const uint4 x = xrow[i];
+        r = make_uint4(add2_bf(r.x, x.x), add2_bf(r.y, x.y), add2_bf(r.z, x.z), add2_bf(r.w, x.w));
         rrow[i] = r;
       }
-      ss = fmaf(lo_bf(r), lo_bf(r), ss);
-      ss = fmaf(hi_bf(r), hi_bf(r), ss);
+      ss = sq2(r.w, sq2(r.z, sq2(r.y, sq2(r.x, ss))));
     }
     ss = wave_sum_dpp(ss);
     if (lane == 0) red[wave] = ss;
@@ -275,14 +283,14 @@ __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, 
 #pragma unroll
     for (int q = 0; q < WPR; ++q) t += red[m * WPR + q];
     const float rstd = 1.0f / sqrtf(t / (float)k + eps);
-    const uint32_t* rrow = rr + m * nw;
-    uint32_t* xrow = reinterpret_cast<uint32_t*>(xs + m * xstride);
-    for (int i = i0; i < nw; i += WPR * EK_WAVE) {
-      const uint32_t r = rrow[i], g = gl[i];
-      xrow[i] = pack2(rbf(lo_bf(g) * rbf(lo_bf(r) * rstd)), rbf(hi_bf(g) * rbf(hi_bf(r) * rstd)));
+    const uint4* rrow = reinterpret_cast<const uint4*>(rr + m * nw);
+    const uint4* grow = reinterpret_cast<const uint4*>(gl);
+    uint4* xrow = reinterpret_cast<uint4*>(xs + m * xstride);
+#pragma unroll 4
+    for (int i = i0; i < n4; i += WPR * EK_WAVE) {
+      const uint4 r = rrow[i], g = grow[i];
+      xrow[i] = make_uint4(norm2(r.x, g.x, rstd), norm2(r.y, g.y, rstd), norm2(r.z, g.z, rstd), norm2(r.w, g.w, rstd));
     }
-    const int kpad = kpad_of(k);
-    for (int i = k + part * EK_WAVE + lane; i < kpad; i += WPR * EK_WAVE) xs[m * xstride + i] = 0;
   }
 }
 
@@ -342,9 +350,50 @@ struct RowsLds {
   }
 };
 
+// Key splits of the batch rows' attention (slots nwg / nkv per kv head, the
+// rows taking consecutive slots): every
+// row first takes the fewest splits that keep its keys per split within the
+// plan's score row (a.lchunk; the plan guarantees that these fit the slots),
+// then, while slots remain, the row with the most keys per split (the lowest
+// row on ties) doubles its splits, up to min(32, D / 4). Every workgroup
+// computes the same from the step's row ranges (one thread, 32-bit shifts:
+// the key counts are below 2^31), then its own unit: unit[] = {row (nrows:
+// none), split, the row's splits, the row's first slot} of slot w / nkv.
+template <int D>
+__device__ __forceinline__ void split_rows(const StepArgs& a, int64_t hi, int nrows, int* unit) {
+  constexpr int SMAX = D / 4 < 32 ? D / 4 : 32;
+  const int slots = (int)gridDim.x / a.nkv;
+  uint32_t nk[8];
+  int lg[8];
+  int used = 0;
+  for (int b = 0; b < nrows; ++b) {
+    int64_t lo = a.start_t[b];
+    lo = lo < 0 ? 0 : lo;
+    nk[b] = (uint32_t)(hi > lo ? hi - lo : 0);
+    lg[b] = 0;
+    while (((nk[b] + (1u << lg[b]) - 1) >> lg[b]) > (uint32_t)a.lchunk && (1 << lg[b]) < SMAX) ++lg[b];
+    used += 1 << lg[b];
+  }
+  while (true) {
+    int best = -1;
+    uint32_t bl = 1;   // a row down to one key per split gains nothing
+    for (int b = 0; b < nrows; ++b) {
+      const uint32_t l = (nk[b] + (1u << lg[b]) - 1) >> lg[b];
+      if ((2 << lg[b]) <= SMAX && used + (1 << lg[b]) <= slots && l > bl) { bl = l; best = b; }
+    }
+    if (best < 0) break;
+    used += 1 << lg[best];
+    ++lg[best];
+  }
+  const int uj = (int)blockIdx.x / a.nkv;
+  unit[0] = nrows; unit[1] = 0; unit[2] = 1; unit[3] = 0;
+  for (int b = 0, p = 0; b < nrows; p += 1 << lg[b], ++b)
+    if (uj >= p && uj < p + (1 << lg[b])) { unit[0] = b; unit[1] = uj - p; unit[2] = 1 << lg[b]; unit[3] = p; }
+}
+
 template <int D, int G, int MB>
 __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt, uint32_t ep, int64_t hi,
-                                           unsigned char* smem, float* s_red, int* s_fail
+                                           const int* s_unit, unsigned char* smem, float* s_red, int* s_fail
 #ifdef EK_STEP_TRACE
                                            , int64_t* ts_lds
 #endif
@@ -366,10 +415,11 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   PartWriter<MB, false> put{part, wave_id()};
   PartWriter<MB, true> add{part, wave_id()};
 
-  // attention unit of this workgroup
-  const int S = a.lsplit;
-  const int ub = (int)blockIdx.x / (a.nkv * S), ur = (int)blockIdx.x - ub * (a.nkv * S);
-  const int uh = ur % a.nkv, us = ur / a.nkv;
+  // attention unit of this workgroup (s_unit: row, split, splits, the row's
+  // first slot; wave-uniform)
+  const int uh = (int)blockIdx.x % a.nkv;
+  const int ub = __builtin_amdgcn_readfirstlane(s_unit[0]), us = __builtin_amdgcn_readfirstlane(s_unit[1]);
+  const int uS = __builtin_amdgcn_readfirstlane(s_unit[2]), upre = __builtin_amdgcn_readfirstlane(s_unit[3]);
   const bool attends = ub < nrows;
 
   Ring ring;
@@ -380,8 +430,8 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
 
   llw_t* half = cur_half(a, ep);
-  llw_t* lx_base = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB;
-  const int64_t lx_row = long_words(a.nkv, S, G, D);
+  // the unit's row's exchange words: its slots' units, after the rows before
+  llw_t* lx_row = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB + long_words(a.nkv, upre, G, D);
   const int nsl = cdiv_i(inter, BSLICE * CH);   // K slices of the down projection
 
   const llw_t* dn_prev = nullptr;
@@ -431,8 +481,8 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
 
     // ---- split attention (its LDS overlays the activation rows and partials)
     if (attends) {
-      if (!long_attention<D, G>(a, lw, qkv_ll + (int64_t)ub * (qkvw / 4), att_ll + (int64_t)ub * (qw / 4),
-                                lx_base + ub * lx_row, ub, uh, us, hi, (uint32_t)l + 1u, ph, s_fail
+      if (!long_attention<D, G>(a, lw, qkv_ll + (int64_t)ub * (qkvw / 4), att_ll + (int64_t)ub * (qw / 4), lx_row,
+                                ub, uh, us, uS, hi, (uint32_t)l + 1u, ph, s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif
@@ -624,12 +674,16 @@ __global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
   __shared__ int s_abort;
   __shared__ int s_fail;
   __shared__ int64_t s_lw[MAX_LAYERS * LW_FIELDS];
+  __shared__ int s_unit[4];
 #ifdef EK_STEP_TRACE
   __shared__ int64_t s_ts[48];
   int64_t* ts_lds = s_ts;
 #endif
 
   const int tid = threadIdx.x;
+  const int64_t len_old = *a.len_t;
+  int64_t hi = len_old + 1;
+  hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
   for (int i = tid; i < a.nl * LW_FIELDS; i += SNT) s_lw[i] = a.lw[i];
   if (tid == 0) {
     s_fail = 0;
@@ -637,15 +691,13 @@ __global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
     __hip_atomic_store(&a.bar->ep[blockIdx.x], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_ep = e;
     s_abort = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    split_rows<D>(a, hi, a.m, s_unit);
   }
   __syncthreads();
   const uint32_t ep = __builtin_amdgcn_readfirstlane(s_ep);   // wave-uniform: the halves' addresses stay scalar
   clear_next_half(a, ep);   // also in a launch that gives up: the next one needs it
-  const int64_t len_old = *a.len_t;
-  int64_t hi = len_old + 1;
-  hi = hi < 0 ? 0 : (hi > a.s_cap ? a.s_cap : hi);
   bool ok = s_abort == 0;
-  if (ok) ok = batch_pass<D, G, MB>(a, s_lw, ep, hi, smem, s_red, &s_fail
+  if (ok) ok = batch_pass<D, G, MB>(a, s_lw, ep, hi, s_unit, smem, s_red, &s_fail
 #ifdef EK_STEP_TRACE
                                      , ts_lds
 #endif

@@ -132,6 +132,10 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
 // The batch kernel's plan (2..8 rows, ek_bstep_impl.h): every workgroup runs
 // the projections of all rows and one attention unit (row, kv head, key
 // split); the shape checks common to both kernels are done by the caller.
+// sp is the split count that bounds a split's keys (lchunk) for any row of
+// the bucket with every row split alike; the kernel gives each row at least
+// the splits its own keys need (never more than sp) and shares the remaining
+// nwg / n_kv slots per kv head out by keys (split_rows).
 hipError_t make_batch_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, int64_t head_dim, int64_t vocab,
                            int64_t m, int64_t s_cap, int64_t n_layers, Plan& p) {
   if (head_dim != 128) return ek_fail(hipErrorInvalidValue, "decode_step: batches of 2-8 rows need head_dim 128");
@@ -146,7 +150,7 @@ hipError_t make_batch_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n
     return ek_fail(hipErrorInvalidValue, "decode_step: the context's score rows exceed the LDS of one split");
   p.lsplit = sp;
   p.lchunk = (int)chunk;
-  p.lx = (int64_t)mb * eks::long_words((int)n_kv, sp, g, 128);
+  p.lx = eks::long_words((int)n_kv, (int)(p.nwg / n_kv), g, 128);   // every slot's unit, whatever its row
   const int qw = (int)(n_q * head_dim), qkvw = (int)((n_q + 2 * n_kv) * head_dim);
   p.kpad_max = eks::bstep_xcols((int)hidden, qw);
   p.part_max = eks::bstep_part_rows((int)hidden, (int)inter, qkvw, p.nwg);

@@ -901,10 +901,11 @@ struct LongLds {
 };
 
 template <int D, int G>
-// Unit (kv head h, split s) of batch row b; qkv, att and lx point at row b's
-// words; ltag tags this layer's exchange words.
+// Unit (kv head h, split s of S) of batch row b; qkv, att and lx point at
+// row b's words (lx: its nkv S units' exchange); ltag tags this layer's
+// exchange words. The row's keys per split must be at most a.lchunk.
 __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
-                                               llw_t* lx, int b, int h, int s, int64_t hi, uint32_t ltag,
+                                               llw_t* lx, int b, int h, int s, int S, int64_t hi, uint32_t ltag,
                                                unsigned char* lds, int* s_fail
 #ifdef EK_STEP_TRACE
                                                , int64_t* ts_lds
@@ -916,7 +917,6 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   constexpr int DCH = D / 8;       // 16-byte chunks per key row
   constexpr int NKG = SNT / DCH;   // key groups of the PV product
   constexpr int VR = LVR;          // value rows per thread in flight
-  const int S = a.lsplit;
   const int tid = opaque_tid(), lane = tid & 63, wave = wave_id();
   const int r16 = lane & 15, q4 = lane >> 4;
   if (s >= S) return true;
@@ -938,7 +938,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   int64_t lo = a.start_t[b];
   lo = lo < 0 ? 0 : lo;
   const int64_t nrel = hi > lo ? hi - lo : 0;
-  const int64_t chunk = (nrel + S - 1) / S;   // <= a.lchunk (the plan's bound on the bucket)
+  const int64_t chunk = (nrel + S - 1) / S;   // <= a.lchunk (the caller's split count ensures it)
   const int64_t k0 = lo + (int64_t)s * chunk;
   int64_t k1 = k0 + chunk;
   k1 = k1 < hi ? k1 : hi;
@@ -1349,7 +1349,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       //      row and the partials), then the o projection from the ring
       llw_t* lx_ll = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
       if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, lx_ll, 0, (int)blockIdx.x % a.nkv, (int)blockIdx.x / a.nkv,
-                                hi, (uint32_t)l + 1u, ph, s_fail
+                                a.lsplit, hi, (uint32_t)l + 1u, ph, s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif
