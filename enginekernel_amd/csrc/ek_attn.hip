@@ -1,5 +1,7 @@
 // Decode attention over the static KV cache, for gfx950: a two-launch
-// split-K pair over a (split, kv head, batch row) grid for any length, and a
+// split-K pair over a (split, kv head, batch row) grid for any length, a
+// one-launch split form when the whole grid fits on the device at once
+// (attn_onepass_kernel, the split unit of the persistent decode step), and a
 // single-launch variant for rows whose scores fit in LDS (attn_fused_kernel,
 // below) when the plan asks for one split.
 //
@@ -47,7 +49,12 @@
 #include "ek_common.h"
 #include "ek_abi_internal.h"
 #include "ek_attn_impl.h"
+#include "ek_step_impl.h"
 #include "ek_hip.h"
+
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace {
 
@@ -513,10 +520,127 @@ __global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
 // Score rows up to this many bytes per workgroup take the single-launch path
 // (with the kernel's static LDS, at most 64 KiB per workgroup) when the plan
 // asks for one split.
+// ---------------------------------------------------------------------------
+// one launch: the persistent step's split unit
+// ---------------------------------------------------------------------------
+// When every workgroup of the (split, kv head, row) grid can be resident at
+// once, one launch does it all: unit (b, h, s) is eks::long_attention --
+// scores of its keys on the matrix cores into LDS, its (max, sum) per head
+// as tagged words, every split's words merged into the row's M and L (so p
+// keeps the reference's rounding point), its partial sum p v, and the
+// combine of head dims [s D / S, (s + 1) D / S) from every split's partial
+// words, stored as bf16. Split s takes the keys [lo + s c, lo + (s + 1) c)
+// of the row's range [lo, len), c = ceil((len - lo) / S). The words go to
+// `part` (per row: n_kv S (2G + G D) of them); their tag is one more than
+// the (row, kv head)'s epoch word in the ticket block, which split 0 moves on
+// once its combine has seen every split's words (so every workgroup of the
+// pair has read it), as the pair's last workgroup does.
+struct PlainIO {
+  const bf16_t* q;           // row b: rope: the raw fused qkv row; else the rotated heads, ldq_h apart
+  int64_t ldq_h;
+  int rope_on;
+  const int64_t* positions;  // cos/sin row of row b (row b when null)
+  bf16_t* out;               // row b's output heads, ldo_h apart
+  int64_t ldo_h;
+  int nq, nkv;
+  __device__ bool rope() const { return rope_on != 0; }
+  __device__ int64_t cs_row(const eks::StepArgs&, int b) const { return positions ? positions[b] : b; }
+  template <int D, int G>
+  __device__ bool read_heads(const eks::StepArgs&, int h, bf16_t* heads, int*) const {
+    if (rope_on) {
+      for (int i = threadIdx.x; i < (G + 2) * D; i += eks::SNT) {
+        const int t = i / D, d = i - t * D;
+        const int head = t < G ? h * G + t : (t == G ? nq + h : nq + nkv + h);
+        heads[i] = q[(int64_t)head * D + d];
+      }
+    } else {
+      for (int i = threadIdx.x; i < G * D; i += eks::SNT) heads[i] = q[(int64_t)(h * G + i / D) * ldq_h + i % D];
+    }
+    __syncthreads();
+    return true;
+  }
+  template <int D, int G>
+  __device__ void put4(int h, int g, int d, const float* v) const {
+    bf16_t* o = out + (int64_t)(h * G + g) * ldo_h + d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = (bf16_t)f2bf(v[e]);
+  }
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(eks::SNT) void attn_onepass_kernel(AttnParams p, int lchunk) {
+  extern __shared__ __align__(16) unsigned char lds[];
+  __shared__ int s_fail;
+  __shared__ uint32_t s_tag;
+  const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * p.nkv + h;
+  if (threadIdx.x == 0) {
+    s_fail = 0;
+    s_tag = __hip_atomic_load(p.ticket + 2 * bh + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  }
+  __syncthreads();
+  const uint32_t tag = s_tag;
+  eks::StepArgs a = {};
+  a.nq = p.nq; a.nkv = p.nkv; a.eps = p.eps; a.sm_scale = p.sm_scale;
+  a.cos = p.cos; a.sin = p.sin; a.ld_cs = p.ld_cs; a.rope_len = p.rope_len;
+  a.csb = p.csb; a.csh = p.csh; a.css = p.css; a.s_cap = p.s_cap;
+  a.start_t = p.start; a.err = p.err; a.spin = p.spin; a.lchunk = lchunk;
+  int64_t lw[eks::LW_FIELDS] = {};
+  lw[eks::LW_QN] = (int64_t)p.qn;
+  lw[eks::LW_KN] = (int64_t)p.kn;
+  lw[eks::LW_KC] = (int64_t)p.kc;
+  lw[eks::LW_VC] = (int64_t)p.vc;
+  int64_t hi = *p.seq_len;
+  hi = hi < 0 ? 0 : (hi > p.s_cap ? p.s_cap : hi);
+  const PlainIO io{p.q + b * p.ldq_b, p.ldq_h, p.rope, p.positions, p.out + b * p.ldo_b, p.ldo_h, p.nq, p.nkv};
+  eks::long_attention<D, G>(a, lw, io, p.part + b * eks::long_words(p.nkv, p.splits, G, D), b, h, s, p.splits, hi,
+                            tag, lds, &s_fail);
+  // also after a wait gave up (the error word is then set): the next launch
+  // must not take this launch's words for its own
+  if (s == 0 && threadIdx.x == 0)
+    __hip_atomic_store(p.ticket + 2 * bh + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The one-launch form's LDS (keys per split at most lchunk), and whether its
+// (splits, n_kv, b) grid is resident at once on the current device
+template <int D, int G>
+size_t onepass_lds(int lchunk) { return eks::LongLds<D, G>::bytes(lchunk); }
+
+int device_cus() {
+  static int n = -1;
+  if (n < 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 0;
+  }
+  return n;
+}
+
+template <int D, int G>
+bool onepass_fits(int64_t grid, size_t lds) {
+  static std::mutex mu;
+  static std::map<size_t, int> cache;
+  int per_cu = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(lds);
+    if (it != cache.end()) {
+      per_cu = it->second;
+    } else {
+      if (hipFuncSetAttribute((const void*)attn_onepass_kernel<D, G>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)eks::kStepDynLds) != hipSuccess ||
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attn_onepass_kernel<D, G>, eks::SNT, lds) != hipSuccess)
+        per_cu = 0;
+      cache[lds] = per_cu;
+    }
+  }
+  return grid <= (int64_t)per_cu * device_cus();
+}
+
 constexpr size_t kFusedScoreLds = 32 * 1024;
 
 template <int D, int G>
-hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
+hipError_t launch_attn(const AttnParams& p, int b, int64_t part_words, hipStream_t st) {
   if (p.splits == 1 && (size_t)G * p.s_cap * sizeof(float) <= kFusedScoreLds) {
     dim3 grid((unsigned)(b * p.nkv), (unsigned)(D / eka::FDC));
     const size_t lds = eka::AttnLds<D, G>::bytes(p.s_cap);
@@ -524,6 +648,20 @@ hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
     return hipGetLastError();
   }
   dim3 grid((unsigned)p.splits, (unsigned)p.nkv, (unsigned)b);
+  // the one-launch form: splits a power of two up to min(32, D / 4) (each
+  // split combines whole 4-dim groups; the combine's lanes sit in one wave),
+  // an error word for its bounded waits, room for its words, its score rows
+  // in LDS, and the whole grid resident at once
+  const int64_t lchunk = (p.s_cap + p.splits - 1) / p.splits;
+  const int smax = D / 4 < 32 ? D / 4 : 32;
+  if (p.err && p.splits <= smax && (p.splits & (p.splits - 1)) == 0 && lchunk <= 65536 &&
+      part_words >= (int64_t)b * eks::long_words(p.nkv, p.splits, G, D)) {
+    const size_t lds = onepass_lds<D, G>((int)lchunk);
+    if (lds <= eks::kStepDynLds && onepass_fits<D, G>((int64_t)p.splits * p.nkv * b, lds)) {
+      hipLaunchKernelGGL((attn_onepass_kernel<D, G>), grid, dim3(eks::SNT), lds, st, p, (int)lchunk);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((attn_qk_kernel<D, G>), grid, dim3(NT), 0, st, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -532,12 +670,12 @@ hipError_t launch_attn(const AttnParams& p, int b, hipStream_t st) {
 }
 
 template <int D>
-hipError_t launch_attn_g(const AttnParams& p, int g, int b, hipStream_t st) {
+hipError_t launch_attn_g(const AttnParams& p, int g, int b, int64_t part_words, hipStream_t st) {
   switch (g) {
-    case 1: return launch_attn<D, 1>(p, b, st);
-    case 2: return launch_attn<D, 2>(p, b, st);
-    case 4: return launch_attn<D, 4>(p, b, st);
-    case 8: return launch_attn<D, 8>(p, b, st);
+    case 1: return launch_attn<D, 1>(p, b, part_words, st);
+    case 2: return launch_attn<D, 2>(p, b, part_words, st);
+    case 4: return launch_attn<D, 4>(p, b, part_words, st);
+    case 8: return launch_attn<D, 8>(p, b, part_words, st);
     default: return ek_fail(hipErrorInvalidValue, "attn: query heads per kv head must be 1, 2, 4 or 8");
   }
 }
@@ -587,9 +725,9 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
   p.err = err; p.spin = ek_wait_limit(int64_t(1) << 22);
   hipStream_t st = (hipStream_t)stream;
   switch (head_dim) {
-    case 32: return launch_attn_g<32>(p, (int)g, (int)b, st);
-    case 64: return launch_attn_g<64>(p, (int)g, (int)b, st);
-    case 128: return launch_attn_g<128>(p, (int)g, (int)b, st);
+    case 32: return launch_attn_g<32>(p, (int)g, (int)b, part_words, st);
+    case 64: return launch_attn_g<64>(p, (int)g, (int)b, part_words, st);
+    case 128: return launch_attn_g<128>(p, (int)g, (int)b, part_words, st);
     default: return ek_fail(hipErrorInvalidValue, "attn: head_dim must be 32, 64 or 128");
   }
 }

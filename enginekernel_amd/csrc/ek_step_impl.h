@@ -900,11 +900,36 @@ struct LongLds {
   }
 };
 
-template <int D, int G>
-// Unit (kv head h, split s of S) of batch row b; qkv, att and lx point at
-// row b's words (lx: its nkv S units' exchange); ltag tags this layer's
-// exchange words. The row's keys per split must be at most a.lchunk.
-__device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const llw_t* qkv, llw_t* att,
+// Where a split unit's q heads come from and its output goes. The step's
+// (StepIO): the qkv hand-over words of batch row b (q heads raw, QK-normed
+// and rotated by the unit, which also writes the new key and value) and the
+// dense attention words. An IO type provides rope() (false: the q heads are
+// already rotated, no new row), cs_row(a, b) (the cos/sin row),
+// read_heads(a, h, heads, s_fail) (the G q heads, then with rope the new key
+// and value, as bf16 rows into LDS; false when a wait gave up) and
+// put4(h, g, d, v) (the combined output of head h G + g, dims d .. d + 3).
+struct StepIO {
+  const llw_t* qkv;
+  llw_t* att;
+  __device__ bool rope() const { return true; }
+  __device__ int64_t cs_row(const StepArgs& a, int b) const { return a.positions[b]; }
+  template <int D, int G>
+  __device__ bool read_heads(const StepArgs& a, int h, bf16_t* heads, int* s_fail) const {
+    const bool ok = dw_read<1>(qkv, HeadUnits<D, G>{h, a.nq, a.nkv}, (G + 2) * (D / 8),
+                               reinterpret_cast<uint32_t*>(heads), LinLds{}, a.err, a.spin);
+    return wg_all(ok, s_fail);
+  }
+  template <int D, int G>
+  __device__ void put4(int h, int g, int d, const float* v) const {
+    dw_put(att + ((int64_t)(h * G + g) * D + d) / 4, pack2(v[0], v[1]), pack2(v[2], v[3]));
+  }
+};
+
+template <int D, int G, typename IO>
+// Unit (kv head h, split s of S) of batch row b; io holds row b's inputs and
+// output, lx its nkv S units' exchange words; ltag tags these words. The
+// row's keys per split must be at most a.lchunk.
+__device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t* lw, const IO& io,
                                                llw_t* lx, int b, int h, int s, int S, int64_t hi, uint32_t ltag,
                                                unsigned char* lds, int* s_fail
 #ifdef EK_STEP_TRACE
@@ -944,7 +969,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   k1 = k1 < hi ? k1 : hi;
   const int64_t nk = k1 > k0 ? k1 - k0 : 0;
   const int64_t slot = hi - 1;
-  const bool own = nk > 0 && slot >= k0 && slot < k1;
+  const bool own = io.rope() && nk > 0 && slot >= k0 && slot < k1;
   // loads past the split's keys (the last tiles' tails, an empty split) read
   // row `last` instead: k0 itself may lie past the cache's last row. Their
   // products are never used, nor is the cache row at the new slot (the new
@@ -975,25 +1000,29 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
 
   // the unit's q heads, new key and new value, and the gains / cos / sin rows
   {
-    const bf16_t* qn = reinterpret_cast<const bf16_t*>(lw[LW_QN]);
-    const bf16_t* kn = reinterpret_cast<const bf16_t*>(lw[LW_KN]);
-    int64_t crow = a.positions[b];
-    crow = crow < 0 ? 0 : (crow >= a.rope_len ? a.rope_len - 1 : crow);
-    const bf16_t* cr = a.cos + crow * a.ld_cs;
-    const bf16_t* sr = a.sin + crow * a.ld_cs;
-    for (int i = tid; i < 4 * D; i += SNT) {
-      const int t = i / D, d = i - t * D;
-      rope[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
+    if (io.rope()) {
+      const bf16_t* qn = reinterpret_cast<const bf16_t*>(lw[LW_QN]);
+      const bf16_t* kn = reinterpret_cast<const bf16_t*>(lw[LW_KN]);
+      int64_t crow = io.cs_row(a, b);
+      crow = crow < 0 ? 0 : (crow >= a.rope_len ? a.rope_len - 1 : crow);
+      const bf16_t* cr = a.cos + crow * a.ld_cs;
+      const bf16_t* sr = a.sin + crow * a.ld_cs;
+      for (int i = tid; i < 4 * D; i += SNT) {
+        const int t = i / D, d = i - t * D;
+        rope[i] = (t == 0 ? qn : t == 1 ? kn : t == 2 ? cr : sr)[d];
+      }
     }
-    const bool ok = dw_read<1>(qkv, HeadUnits<D, G>{h, a.nq, a.nkv}, (G + 2) * (D / 8),
-                               reinterpret_cast<uint32_t*>(heads), LinLds{}, a.err, a.spin);
-    if (!wg_all(ok, s_fail)) return false;
+    if (!io.template read_heads<D, G>(a, h, heads, s_fail)) return false;
   }
   EK_TS(28);
-  // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
-  for (int u = wave; u <= G; u += SNW) {
-    if (u < G) eka::head_norm_rope<D>(heads + u * D, rope, rope + 2 * D, rope + 3 * D, a.eps, qs[u], nullptr);
-    else eka::head_norm_rope<D>(heads + G * D, rope + D, rope + 2 * D, rope + 3 * D, a.eps, knf, knew_bf);
+  if (io.rope()) {
+    // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
+    for (int u = wave; u <= G; u += SNW) {
+      if (u < G) eka::head_norm_rope<D>(heads + u * D, rope, rope + 2 * D, rope + 3 * D, a.eps, qs[u], nullptr);
+      else eka::head_norm_rope<D>(heads + G * D, rope + D, rope + 2 * D, rope + 3 * D, a.eps, knf, knew_bf);
+    }
+  } else {
+    for (int i = tid; i < G * D; i += SNT) qs[i / D][i % D] = bf2f(heads[i]);
   }
   __syncthreads();
 
@@ -1202,8 +1231,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     EK_TS(5);
     for (int i = tid; i < G * dpu / 4; i += SNT) {
       const int g = (4 * i) / dpu, dd = 4 * i - g * dpu;
-      dw_put(att + ((int64_t)(h * G + g) * D + s * dpu + dd) / 4, pack2(cmb[4 * i], cmb[4 * i + 1]),
-             pack2(cmb[4 * i + 2], cmb[4 * i + 3]));
+      io.template put4<D, G>(h, g, s * dpu + dd, cmb + 4 * i);
     }
   }
   // the new key and value rows (normed and rotated key, raw value)
@@ -1348,8 +1376,8 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       // ---- attention on every workgroup (its LDS overlays the activation
       //      row and the partials), then the o projection from the ring
       llw_t* lx_ll = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x;
-      if (!long_attention<D, G>(a, lw, qkv_ll, att_ll, lx_ll, 0, (int)blockIdx.x % a.nkv, (int)blockIdx.x / a.nkv,
-                                a.lsplit, hi, (uint32_t)l + 1u, ph, s_fail
+      if (!long_attention<D, G>(a, lw, StepIO{qkv_ll, att_ll}, lx_ll, 0, (int)blockIdx.x % a.nkv,
+                                (int)blockIdx.x / a.nkv, a.lsplit, hi, (uint32_t)l + 1u, ph, s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds
 #endif

@@ -552,10 +552,12 @@ def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, devi
     scratch [B, n_q, bucket] fp32, the split combine's ticket block
     (int32 [B, n_kv, 2], zeroed; the kernels keep an arrival count and an
     epoch in it) and an error word (int32 [1]: set by a device-side wait
-    that gave up, cleared by the caller; ws_error returns it). `acc`
-    ([B, n_kv, SP, GP, D] fp32, as in the reference) holds the splits'
-    partial outputs as 64-bit {value, tag} words, which fit because
-    GP >= 2 * (n_q / n_kv)."""
+    that gave up, cleared by the caller; ws_error returns it), then the
+    splits' exchange words (int64 [B, n_kv, SP, G (D + 2)]: partial outputs
+    and per-split statistics as 64-bit {value, tag} words, enough for the
+    one-launch split form; the reference's `acc` ([B, n_kv, SP, GP, D] fp32)
+    is kept for its callers and holds the pair's partials when a 7-tuple
+    workspace comes in)."""
     s, c, bn = plan_splits(b, n_kv, bucket)
     if splits is not None:
         s = splits
@@ -569,7 +571,9 @@ def make_workspace(b: int, n_q: int, n_kv: int, head_dim: int, bucket: int, devi
     scores = torch.empty((b, n_q, bucket), dtype=torch.float32, device=device)
     ticket = torch.zeros((b, n_kv, 2), dtype=torch.int32, device=device)
     err = torch.zeros(1, dtype=torch.int32, device=device)
-    return (acc, lsum, mmax, out, s, c, bn, scores, ticket, err)
+    g = n_q // n_kv
+    words = torch.zeros((b, n_kv, sp, g * (head_dim + 2)), dtype=torch.int64, device=device)
+    return (acc, lsum, mmax, out, s, c, bn, scores, ticket, err, words)
 
 
 def ws_error(ws):
@@ -617,6 +621,8 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
     _need(scores.shape[0] >= b and scores.shape[1] == n_q and scores.is_contiguous(), "score scratch")
     _need(ticket.dtype == torch.int32 and ticket.is_contiguous() and ticket.numel() >= 2 * b * n_kv, "ticket block")
     _need(acc.dtype == torch.float32 and acc.is_contiguous(), "acc (the splits' partial words)")
+    part, part_words = (workspace[10], workspace[10].numel()) if len(workspace) >= 11 else (acc, acc.numel() // 2)
+    _need(part.is_contiguous(), "exchange words")
     # the workspace bounds the attended length, as the reference's chunk plan does
     s_cap = min(s_cap, scores.shape[2])
     ld_cs = cos.stride(0) if cos is not None else 0
@@ -625,7 +631,7 @@ def _attn(q, ldq_b, ldq_h, rope, qn, kn, cos, sin, positions, k_cache, v_cache, 
          ptr(positions), rope_len, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
          k_cache.stride(2), s_cap, ptr(seq_len_t), ptr(start_t), ptr(scores), scores.stride(1),
          ptr(lsum), ptr(mmax), lsum.shape[2], lsum.shape[3], ptr(out), out.stride(0),
-         out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), ptr(acc), acc.numel() // 2,
+         out.stride(1), b, n_q, n_kv, d, splits, chunk, float(sm_scale), float(eps), ptr(part), part_words,
          ptr(ticket), ptr(ws_error(workspace)), stream())
     return out
 

@@ -105,12 +105,15 @@ def test_plan_splits_invariants(b, bucket):
     assert (splits - 1) * chunk < bucket                 # no split starts past the bucket
     ws = K.make_workspace(b, 32, 8, 128, bucket, "cpu")
     assert ws[0].shape == (b, 8, K._next_pow2(splits), K.group_pad(32, 8), 128)
-    assert ws[7].shape == (b, 32, bucket) and len(ws) == 10
+    assert ws[7].shape == (b, 32, bucket) and len(ws) == 11
     # the ticket block, the error word, and room for every split's partial as 64-bit words
     assert ws[8].shape == (b, 8, 2) and ws[8].dtype == torch.int32 and int(ws[8].abs().sum()) == 0
     assert K.ws_error(ws) is ws[9] and ws[9].shape == (1,) and int(ws[9]) == 0
     assert K.ws_error(ws[:7]) is None
     assert ws[0].numel() // 2 >= b * 8 * splits * (32 // 8) * 128
+    # the exchange words of the one-launch split form: (max, sum) and a
+    # partial output per split and query head
+    assert ws[10].dtype == torch.int64 and ws[10].numel() >= b * 8 * splits * (32 // 8) * (128 + 2)
 
 
 def test_group_pad_and_helpers():

@@ -446,6 +446,60 @@ def test_rope_attn_decode(dev, b, d, nq, nkv, slen, pad, smax):
     assert torch.equal(kcd[:, :, keep].cpu(), kc[:, :, keep]) and torch.equal(vcd[:, :, keep].cpu(), vc[:, :, keep])
 
 
+@pytest.mark.parametrize("rope,b,d,nq,nkv,slen,pads,cap,splits", [
+    (0, 1, 128, 32, 8, 4001, (0,), 8192, 16), (0, 3, 128, 32, 8, 3001, (0, 17, 900), 4096, 8),
+    (1, 2, 128, 32, 8, 2000, (11, 0), 4096, 8), (1, 2, 64, 16, 2, 1500, (3, 700), 2048, 16)])
+def test_attn_one_launch_and_pair(dev, rope, b, d, nq, nkv, slen, pads, cap, splits):
+    """The two split forms of attn_decode on the same inputs, both against the
+    oracle: the one-launch form (the default workspace: its exchange words
+    fit, and the grid is resident at once) and the two-launch pair (a
+    reference-style 10-tuple workspace without them). Which form ran shows in
+    the buffers each writes: the one-launch form's tagged words, the pair's
+    partial words in acc. With rope, both also write the same new K/V row."""
+    g = _gen(slen + 7 * b + d)
+    start = torch.tensor(pads, dtype=torch.int32)
+    kc = torch.randn(b, nkv, cap, d, generator=g).to(BF)
+    vc = torch.randn(b, nkv, cap, d, generator=g).to(BF)
+    vmax = vc.abs().max().item()
+    if rope:
+        qkv = torch.randn(b, (nq + 2 * nkv) * d, generator=g).to(BF)
+        qn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF)
+        kn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF)
+        cos_t, sin_t = O.build_rope(d, 1e6, 4096)
+        pos = torch.randint(0, 4000, (b,), generator=g)
+        q_ref, kc_ref, vc_ref = qkv.clone(), kc.clone(), vc.clone()
+        O.qk_norm_rope_kv(q_ref, qn, kn, cos_t[pos], sin_t[pos], kc_ref, vc_ref,
+                          torch.full((b,), slen - 1, dtype=torch.int64), nq, nkv, 1e-6, 1)
+        want = O.decode_attn(q_ref[:, :nq * d].view(b, nq, d), kc_ref, vc_ref, slen, start, d ** -0.5)
+    else:
+        q = torch.randn(b, nq, d, generator=g).to(BF)
+        want = O.decode_attn(q, kc, vc, slen, start, d ** -0.5)
+    ws = K.make_workspace(b, nq, nkv, d, cap, dev, splits=splits, chunk=cap // splits)
+    results = []
+    for form, w in (("one launch", ws), ("pair", ws[:10])):
+        kcd, vcd = kc.to(dev), vc.to(dev)
+        if rope:
+            got = K.rope_attn_decode(qkv.to(dev), qn.to(dev), kn.to(dev), cos_t.to(dev), sin_t.to(dev), kcd, vcd,
+                                     torch.tensor([slen], device=dev), start.to(dev), w, d ** -0.5, nq, 1e-6,
+                                     positions=pos.to(dev)).clone()
+            assert_close_ulps(kcd[:, :, slen - 1], kc_ref[:, :, slen - 1], name=f"{form}: new k")
+            assert torch.equal(vcd[:, :, slen - 1].cpu(), vc_ref[:, :, slen - 1])
+        else:
+            got = K.flash_decode(q.to(dev), kcd, vcd, torch.tensor([slen], device=dev), start.to(dev), w,
+                                 d ** -0.5).clone()
+        K.check_error_word(K.ws_error(ws), form)
+        assert_close_ulps(got, want, min_equal=0.99, name=f"{form} vs oracle", abs_tol=2.0 ** -13 * vmax)
+        results.append(got)
+        if form == "one launch":
+            assert ws[10].ne(0).any() and not ws[0].ne(0).any(), "the one-launch form did not run"
+        else:
+            assert ws[0].ne(0).any(), "the pair did not run"
+    vm = results[0].float().abs().max().item()
+    assert (results[0].float() - results[1].float()).abs().max().item() <= 2.0 ** -6 * vm
+    # every launch moved each (row, kv head)'s epoch on, whichever form ran
+    assert ws[8].cpu()[..., 1].eq(2).all() and ws[8].cpu()[..., 0].eq(0).all()
+
+
 # ----------------------------------------------------------------------------
 # prefill attention (ek_model.py:315-323, SDPA with the _pack mask)
 # ----------------------------------------------------------------------------
