@@ -48,9 +48,9 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 #   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
 GATE_UP_TRAFFIC_B1 = 100_153_865
 #   the persistent step kernel (step_kernel<128, 4, false>) at batch 1, context 137..146:
-#   3,962,889 KiB / 0.500066 fetched + 4,418 KiB written per launch, 1.0066x its
+#   3,961,738 KiB / 0.500065 fetched + 4,418 KiB written per launch, 1.0063x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_119_444_470
+STEP_TRAFFIC_B1 = 8_117_116_020
 
 
 def log(msg: str) -> None:

@@ -31,6 +31,10 @@
 namespace eks {
 
 constexpr int BLLW = 16;      // tagged (argmax) words in flight per thread
+#ifndef EK_BSTEP_PF
+#define EK_BSTEP_PF 6
+#endif
+constexpr int BPF = EK_BSTEP_PF;   // chunks per wave prefetched ahead of a hand-over wait
 // rows whose next activation chunk is read ahead of the current products
 // (at 8 rows the 8 extra chunks in registers spill, and the products of 8
 // rows cover the LDS round trip anyway)
@@ -490,7 +494,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         return false;
     }
     EK_TS(4);
-    prefetch_phase_b<PF>(go, qw, false, ring);
+    prefetch_phase_b<BPF>(go, qw, false, ring);
     load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
     __syncthreads();
 
@@ -509,7 +513,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     EK_TS(7);
     epilogue_ll_b<MB>(go, part, o_ll, h / 4, nrows);
     EK_TS(8);
-    prefetch_phase_b<PF>(gg, h, false, ring);
+    prefetch_phase_b<BPF>(gg, h, false, ring);
 
     // ---- r = r + o; norm; gate/up; SwiGLU
     __syncthreads();
@@ -530,7 +534,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     EK_TS(10);
     epilogue_swiglu_ll_b<MB>(gg, part, act_ll, inter / 4, nrows);
     EK_TS(11);
-    prefetch_phase_b<PF>(down_slice(0), inter, false, ring);
+    prefetch_phase_b<BPF>(down_slice(0), inter, false, ring);
 
     // ---- down projection, one K slice of the act rows at a time
     __syncthreads();
@@ -555,12 +559,12 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       // leaves the ring in the same state, so the products above see a
       // prefetched ring at compile time)
       if (sl + 1 < nsl)
-        prefetch_phase_b<PF>(down_slice(sl + 1), inter, false, ring);
+        prefetch_phase_b<BPF>(down_slice(sl + 1), inter, false, ring);
       else if (l + 1 < a.nl)
-        prefetch_phase_b<PF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
+        prefetch_phase_b<BPF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
                                      0, 4), h, false, ring);
       else
-        prefetch_phase_b<PF>(make_gp(a.lm_head, h, a.vocab, 0, 1), h, true, ring);
+        prefetch_phase_b<BPF>(make_gp(a.lm_head, h, a.vocab, 0, 1), h, true, ring);
     }
     __syncthreads();
     epilogue_ll_b<MB>(down_slice(0), part, dn_ll, h / 4, nrows);

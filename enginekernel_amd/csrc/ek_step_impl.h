@@ -60,9 +60,12 @@ constexpr int SNT = eka::FNT;          // 512 threads
 constexpr int SNW = SNT / EK_WAVE;     // 8 waves
 constexpr int NB = 8;                  // weight chunks in flight per wave
 #ifndef EK_STEP_PF
-#define EK_STEP_PF 6
+#define EK_STEP_PF 4
 #endif
-constexpr int PF = EK_STEP_PF;         // chunks per wave prefetched ahead of a hand-over wait (6: 0.8 % faster than 4 or 8)
+// chunks per wave prefetched ahead of a hand-over wait: 4 (0.6 % faster than
+// 3, 6 or 8 with the dense hand-over words; with {bf16 pair, tag} words, whose
+// polls queued behind twice the loads, 6 was the best)
+constexpr int PF = EK_STEP_PF;
 constexpr int OB = 12;                 // o_proj chunks per wave held in registers through attention
 constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
 constexpr int LW_FIELDS = 10;          // per-layer pointer table row
