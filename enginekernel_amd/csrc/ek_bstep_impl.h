@@ -536,18 +536,30 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     EK_TS(11);
     prefetch_phase_b<BPF>(down_slice(0), inter, false, ring);
 
-    // ---- down projection, one K slice of the act rows at a time
+    // ---- down projection, one K slice of the act rows at a time; up to 4
+    //      rows, each slice's words are loaded (once) before the previous
+    //      slice's products, so that their round trip overlaps them (at 8
+    //      rows their registers would spill)
     __syncthreads();
     zero_part(part, part_n);
+    constexpr int SW = bstep_slice_units<MB>();
+    constexpr bool EARLY = MB <= 4;
+    u32x4_t nx[SW];
     for (int sl = 0; sl < nsl; ++sl) {
       const Gp gd = down_slice(sl);
       const int c0 = sl * BSLICE;
       const int su = gd.K / 8;   // units of a row's slice
+      const RowsUnits src{inter / 4, su};
       if (sl > 0) __syncthreads();   // the previous slice's products have read their LDS rows
       {
-        const bool ok = dw_read<bstep_slice_units<MB>()>(act_ll + c0 * (CH / 4), RowsUnits{inter / 4, su}, nrows * su,
-                                                         xs32, RowsLds{su, xcols / 2}, a.err, a.spin);
+        if (sl == 0 || !EARLY) dw_issue<SW>(act_ll + c0 * (CH / 4), src, nrows * su, nx);
+        const bool ok = dw_finish<SW>(act_ll + c0 * (CH / 4), src, nrows * su, nx, xs32, RowsLds{su, xcols / 2},
+                                      a.err, a.spin);
         if (!wg_all(ok, s_fail)) return false;
+      }
+      if (EARLY && sl + 1 < nsl) {
+        const int sun = down_slice(sl + 1).K / 8;
+        dw_issue<SW>(act_ll + (c0 + BSLICE) * (CH / 4), RowsUnits{inter / 4, sun}, nrows * sun, nx);
       }
       if (sl == 0) EK_TS(20);
       else EK_TS(21);

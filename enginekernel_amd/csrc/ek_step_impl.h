@@ -333,6 +333,51 @@ __device__ __forceinline__ bool dw_read(const llw_t* base, SRC src, int n, uint3
   return true;
 }
 
+// dw_read of at most W SNT units in two halves, for a wait whose loads go
+// out early (ahead of other work): dw_issue loads every unit once into v;
+// dw_finish polls the units not yet whole and stores all of them in LDS.
+template <int W, typename SRC>
+__device__ __forceinline__ void dw_issue(const llw_t* base, SRC src, int n, u32x4_t* v) {
+  const __amdgpu_buffer_rsrc_t r = dw_rsrc(base);
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int j = (int)threadIdx.x + k * SNT;
+    v[k] = dw_get2(r, src(j < n ? j : 0));
+  }
+}
+
+template <int W, typename SRC, typename DST>
+__device__ __forceinline__ bool dw_finish(const llw_t* base, SRC src, int n, u32x4_t* v, uint32_t* dst, DST dix,
+                                          int* err, int64_t spin) {
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t r = dw_rsrc(base);
+  int64_t it = 0;
+  while (true) {
+    bool done = true;
+#pragma unroll
+    for (int k = 0; k < W; ++k) done = done && (tid + k * SNT >= n || dw_ok2(v[k]));
+    if (done) break;
+    if (++it > spin) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int j = tid + k * SNT;
+      if (j < n && !dw_ok2(v[k])) v[k] = dw_get2(r, src(j));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int j = tid + k * SNT;
+    if (j < n)
+      *reinterpret_cast<uint4*>(dst + dix(j)) =
+          make_uint4(v[k].x ^ DW_FLIP32, v[k].y ^ DW_FLIP32, v[k].z ^ DW_FLIP32, v[k].w ^ DW_FLIP32);
+  }
+  return true;
+}
+
 // Zero this workgroup's share of the half the next launch uses (16-byte
 // global stores spread over the grid; a.half is a multiple of 32 words).
 typedef __attribute__((address_space(1))) u32x4_t global_w_u32x4_t;
