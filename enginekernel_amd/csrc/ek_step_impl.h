@@ -290,48 +290,13 @@ struct LinLds {
   __device__ int operator()(int j) const { return 4 * j; }
 };
 
-template <int W, typename SRC, typename DST>
-__device__ __forceinline__ bool dw_read(const llw_t* base, SRC src, int n, uint32_t* dst, DST dix, int* err,
-                                        int64_t spin, int64_t* rounds = nullptr) {
-  const int tid = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t r = dw_rsrc(base);
-  for (int b0 = 0; b0 < n; b0 += W * SNT) {
-    u32x4_t v[W];
-    // every load issued, at a clamped unit past n (a load under a lane
-    // condition becomes a branch that waits for it), then masked
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const int j = b0 + tid + k * SNT;
-      v[k] = dw_get2(r, src(j < n ? j : 0));
-    }
-    int64_t it = 0;
-    while (true) {
-      bool done = true;
-#pragma unroll
-      for (int k = 0; k < W; ++k) done = done && (b0 + tid + k * SNT >= n || dw_ok2(v[k]));
-      if (done) break;
-      if (rounds) ++*rounds;
-      if (++it > spin) {
-        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return false;
-      }
-      if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
-#pragma unroll
-      for (int k = 0; k < W; ++k) {
-        const int j = b0 + tid + k * SNT;
-        if (j < n && !dw_ok2(v[k])) v[k] = dw_get2(r, src(j));
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < W; ++k) {
-      const int j = b0 + tid + k * SNT;
-      if (j < n)
-        *reinterpret_cast<uint4*>(dst + dix(j)) =
-            make_uint4(v[k].x ^ DW_FLIP32, v[k].y ^ DW_FLIP32, v[k].z ^ DW_FLIP32, v[k].w ^ DW_FLIP32);
-    }
-  }
-  return true;
-}
+// units j of a map shifted by b0 (a later round of a read)
+template <typename F>
+struct OffUnits {
+  F f;
+  int b0;
+  __device__ int operator()(int j) const { return f(b0 + j); }
+};
 
 // dw_read of at most W SNT units in two halves, for a wait whose loads go
 // out early (ahead of other work): dw_issue loads every unit once into v;
@@ -348,7 +313,7 @@ __device__ __forceinline__ void dw_issue(const llw_t* base, SRC src, int n, u32x
 
 template <int W, typename SRC, typename DST>
 __device__ __forceinline__ bool dw_finish(const llw_t* base, SRC src, int n, u32x4_t* v, uint32_t* dst, DST dix,
-                                          int* err, int64_t spin) {
+                                          int* err, int64_t spin, int64_t* rounds = nullptr) {
   const int tid = threadIdx.x;
   const __amdgpu_buffer_rsrc_t r = dw_rsrc(base);
   int64_t it = 0;
@@ -357,6 +322,7 @@ __device__ __forceinline__ bool dw_finish(const llw_t* base, SRC src, int n, u32
 #pragma unroll
     for (int k = 0; k < W; ++k) done = done && (tid + k * SNT >= n || dw_ok2(v[k]));
     if (done) break;
+    if (rounds) ++*rounds;
     if (++it > spin) {
       __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
@@ -374,6 +340,19 @@ __device__ __forceinline__ bool dw_finish(const llw_t* base, SRC src, int n, u32
     if (j < n)
       *reinterpret_cast<uint4*>(dst + dix(j)) =
           make_uint4(v[k].x ^ DW_FLIP32, v[k].y ^ DW_FLIP32, v[k].z ^ DW_FLIP32, v[k].w ^ DW_FLIP32);
+  }
+  return true;
+}
+
+template <int W, typename SRC, typename DST>
+__device__ __forceinline__ bool dw_read(const llw_t* base, SRC src, int n, uint32_t* dst, DST dix, int* err,
+                                        int64_t spin, int64_t* rounds = nullptr) {
+  for (int b0 = 0; b0 < n; b0 += W * SNT) {
+    const OffUnits<SRC> s2{src, b0};
+    const OffUnits<DST> d2{dix, b0};
+    u32x4_t v[W];
+    dw_issue<W>(base, s2, n - b0, v);
+    if (!dw_finish<W>(base, s2, n - b0, v, dst, d2, err, spin, rounds)) return false;
   }
   return true;
 }
