@@ -11,7 +11,8 @@ untouched, the new cache rows match, and every row's position, the shared
 length and the step counter advanced. Cases: 2, 3, 5 (a row bound of 8 with
 3 rows unused) and 8 rows; config 5 at its stated size (eight prompts of
 U[64, 2048] tokens, cache 8192, the engine's bucket); and a batch whose
-bucket needs many keys per split.
+bucket needs many keys per split, and one with one long row among short
+ones.
 """
 
 import pytest
@@ -133,6 +134,13 @@ def test_batch_step_long_split(dev, mid):
     """Two rows in a 12288-key bucket (random cache rows): 16 splits per
     (row, kv head) of up to 768 keys each."""
     _run(dev, mid, _prompts((11000, 6000), 5), 3, bucket=12288, cap=12288, random_cache=True)
+
+
+def test_batch_step_uneven_rows(dev, mid):
+    """One long row among short ones (random cache rows): the long row takes
+    most of each kv head's key-split slots, the short rows one each, and
+    every row still matches the oracle."""
+    _run(dev, mid, _prompts((3000, 40, 41, 39), 6), 3, bucket=4096, cap=4096, random_cache=True)
 
 
 def test_batch_rows_as_if_alone_full_depth(dev):
