@@ -66,6 +66,11 @@ constexpr int NB = 8;                  // weight chunks in flight per wave
 // 3, 6 or 8 with the dense hand-over words; with {bf16 pair, tag} words, whose
 // polls queued behind twice the loads, 6 was the best)
 constexpr int PF = EK_STEP_PF;
+// the same ahead of the split-attention form's waits
+#ifndef EK_STEP_PF_LONG
+#define EK_STEP_PF_LONG 6
+#endif
+constexpr int PF_LONG = EK_STEP_PF_LONG;
 constexpr int OB = 12;                 // o_proj chunks per wave held in registers through attention
 constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
 constexpr int LW_FIELDS = 10;          // per-layer pointer table row
@@ -1333,6 +1338,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = arena_layer_words(h, inter, qkvw, qw);
   const int n_attn = LONG ? 0 : a.nkv * (D / eka::FDC);
+  constexpr int PFM = LONG ? PF_LONG : PF;
 
   float* rr = reinterpret_cast<float*>(smem);
   unsigned char* ph = smem + step_rr_bytes(h);
@@ -1411,7 +1417,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
                                 ))
         return false;
       EK_TS(4);
-      prefetch_phase<PF>(go, ring);
+      prefetch_phase<PFM>(go, ring);
       load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
       __syncthreads();
       zero_part(part, part_n);
@@ -1426,7 +1432,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       __syncthreads();
       EK_TS(7);
       epilogue_ll(go, part, o_ll);
-      prefetch_phase<PF>(gg, ring);
+      prefetch_phase<PFM>(gg, ring);
       EK_TS(8);
     } else {
       (void)hi;
@@ -1434,7 +1440,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       //      (all of them at the Qwen3-4B shape) and its first gate/up rows into L2
       uint4 ob[OB];
       hold_phase(go, ob);
-      prefetch_phase<PF>(gg, ring);
+      prefetch_phase<PFM>(gg, ring);
       uint32_t sink = 0;
       l2_touch(gg, sink);
       load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
@@ -1487,7 +1493,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     EK_TS(10);
     epilogue_swiglu_ll(gg, part, act_ll);
     EK_TS(11);
-    prefetch_phase<PF>(gd, ring);
+    prefetch_phase<PFM>(gd, ring);
     EK_TS(27);
 
     // ---- down projection
@@ -1514,10 +1520,10 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     epilogue_ll(gd, part, dn_ll);
     EK_TS(14);
     if (l + 1 < a.nl)
-      prefetch_phase<PF>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]),
+      prefetch_phase<PFM>(on_gemv_wgs(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]),
                                          h, qkvw, 0, 4), n_attn), ring);
     else
-      prefetch_phase<PF>(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
+      prefetch_phase<PFM>(on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn), ring);
     dn_prev = dn_ll;
     __syncthreads();
     EK_TS_FLUSH(l);
