@@ -220,7 +220,7 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
 
 /* decode_step_plan: whether the persistent decode-step kernel handles this
  * shape (returns 0) and, in sizes[4], the bytes of the hand-over arena, the
- * long-context key split (0 when s_cap <= 1536 and n_q / n_kv * s_cap * 4 <=
+ * long-context key split (0 when s_cap <= 1024 and n_q / n_kv * s_cap * 4 <=
  * 32 KiB: attention then runs on n_kv * head_dim / 32 workgroups of its own
  * beside the projections; otherwise every workgroup attends 1 / split of one
  * kv head's keys), the bytes of the launch-state block and the grid (one workgroup per
