@@ -529,7 +529,11 @@ def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta
     splits, 7 % faster per step than 8), and two rules are added: a split
     gets at least MIN_SPLIT_KEYS keys (the split combine costs more than the
     parallelism gains below that), and buckets up to FUSED_BUCKET take one
-    split (the single-launch kernel, which keeps the scores in LDS)."""
+    split (the single-launch kernel, which keeps the scores in LDS). The
+    split count is then rounded down to a power of two, so that the
+    one-launch split form of ek_attn_decode takes the row (its combine needs
+    one; at batch 1 and a 2304-key bucket: 8 splits in one launch rather
+    than 9 in the two-launch pair)."""
     sms = _sm_count()
     target_cta = target_cta or int(os.environ.get("ENGINE_ATTN_CTA", "0")) or sms
     base = batch * n_kv
@@ -542,6 +546,7 @@ def plan_splits(batch: int, n_kv: int, bucket: int, block_n: int = 0, target_cta
     if not block_n:
         block_n = 128 if (splits == 1 and base <= sms) else 64
     splits = max(1, min(splits, _cdiv(bucket, block_n)))
+    splits = 1 << (splits.bit_length() - 1)
     chunk = _cdiv(_cdiv(bucket, splits), block_n) * block_n
     return splits, chunk, block_n
 
