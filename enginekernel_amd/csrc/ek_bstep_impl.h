@@ -10,9 +10,10 @@
 //     b (n_kv S) + s n_kv + h, the batch-1 split kernel's unit (long_attention)
 //   wait att words; o rows -> o words; wait o words; r += o; RMSNorm
 //   gate/up rows + SwiGLU -> act words
-//   down rows over the act row in K slices of BSLICE chunks (MB rows of a
-//     9728-wide act row do not fit the LDS at once): wait the slice's act
-//     words, its partial products added into the same per-wave partials
+//   down rows over the act row in K slices of bstep_slice(MB) chunks (up to
+//     4 rows the whole of a 9728-wide act row; 8 such rows do not fit the
+//     LDS at once): wait the slice's act words, its partial products added
+//     into the same per-wave partials
 //   -> dn words
 // then the final add + norm, the lm_head rows (whole rows per wave, so each
 // wave keeps a running first-index argmax per batch row instead of per-row
@@ -41,11 +42,27 @@ constexpr int BPF = EK_BSTEP_PF;   // chunks per wave prefetched ahead of a hand
 #ifndef EK_BSTEP_XA
 #define EK_BSTEP_XA 4
 #endif
-constexpr int BSLICE = 10;    // activation chunks per LDS slice of a row (5120 bf16)
+// activation chunks per LDS slice of a row in the down projection: up to 4
+// rows 20 (10240 bf16: a 9728-wide act row in one slice, so the phase has no
+// slice boundary, where the ring drains and the next act words make a round
+// trip: 3.3-3.7 us each); 8 rows hold 10 (5120 bf16) beside their residual rows
+#ifndef EK_BSTEP_SLICE
+#define EK_BSTEP_SLICE 10
+#endif
+#ifndef EK_BSTEP_SLICE_NARROW
+#define EK_BSTEP_SLICE_NARROW 20
+#endif
+__host__ __device__ constexpr int bstep_slice(int mb) { return mb <= 4 ? EK_BSTEP_SLICE_NARROW : EK_BSTEP_SLICE; }
+// a K slice's act words are loaded ahead of the previous slice's products
+// when they take at most this many 16-byte units per thread and a kv head has
+// at most 4 q heads (beyond either, the extra registers spill)
+#ifndef EK_BSTEP_EARLY_UNITS
+#define EK_BSTEP_EARLY_UNITS 5
+#endif
 // dense 16-byte units in flight per thread: MB for the rows up to 4096 wide,
 // and one K slice of MB act rows in one round
 template <int MB>
-constexpr int bstep_slice_units() { return (MB * BSLICE * CH / 8 + SNT - 1) / SNT; }
+constexpr int bstep_slice_units() { return (MB * bstep_slice(MB) * CH / 8 + SNT - 1) / SNT; }
 
 // ---------------------------------------------------------------------------
 // projections over MB activation rows
@@ -323,10 +340,10 @@ struct ArgmaxSink {
 // ---------------------------------------------------------------------------
 __host__ __device__ inline size_t bstep_rr_bytes(int mb, int h) { return eka::align16((size_t)mb * h * 2); }
 // activation rows: MB rows of the widest LDS row (hidden, n_q D or a slice)
-__host__ __device__ inline int bstep_xcols(int h, int qw) {
+__host__ __device__ inline int bstep_xcols(int h, int qw, int mb) {
   int x = kpad_of(h);
   x = x > qw ? x : qw;
-  x = x > BSLICE * CH ? x : BSLICE * CH;
+  x = x > bstep_slice(mb) * CH ? x : bstep_slice(mb) * CH;
   return x;
 }
 // part rows of the largest projection share (lm_head keeps no partials)
@@ -406,7 +423,8 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   const int h = a.h, inter = a.inter, nrows = a.m;
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = (int64_t)MB * arena_layer_words(h, inter, qkvw, qw);
-  const int xcols = bstep_xcols(h, qw);
+  constexpr int BSLICE = bstep_slice(MB);
+  const int xcols = bstep_xcols(h, qw, MB);
 
   uint32_t* rr = reinterpret_cast<uint32_t*>(smem);
   unsigned char* ph = smem + bstep_rr_bytes(MB, h);
@@ -536,14 +554,14 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     EK_TS(11);
     prefetch_phase_b<BPF>(down_slice(0), inter, false, ring);
 
-    // ---- down projection, one K slice of the act rows at a time; up to 4
-    //      rows, each slice's words are loaded (once) before the previous
-    //      slice's products, so that their round trip overlaps them (at 8
-    //      rows their registers would spill)
+    // ---- down projection, one K slice of the act rows at a time (one slice
+    //      for a 9728-wide act row up to 4 rows); when their registers fit,
+    //      each slice's words are loaded (once) before the previous slice's
+    //      products, so that their round trip overlaps them
     __syncthreads();
     zero_part(part, part_n);
     constexpr int SW = bstep_slice_units<MB>();
-    constexpr bool EARLY = MB <= 4;
+    constexpr bool EARLY = SW <= EK_BSTEP_EARLY_UNITS && G <= 4;
     u32x4_t nx[SW];
     for (int sl = 0; sl < nsl; ++sl) {
       const Gp gd = down_slice(sl);
@@ -726,7 +744,7 @@ __global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
 template <int D, int G, int MB>
 inline size_t bstep_lds_bytes(int h, int qw, int part_rows, int lchunk, int nwg) {
   const size_t rr = bstep_rr_bytes(MB, h);
-  const size_t gemv = eka::align16((size_t)MB * bstep_xcols(h, qw) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4) +
+  const size_t gemv = eka::align16((size_t)MB * bstep_xcols(h, qw, MB) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4) +
                       eka::align16((size_t)h / 2 * 4);
   const size_t attn = LongLds<D, G>::bytes(lchunk);
   const size_t fin = (size_t)2 * nwg * MB * 4 + (size_t)MB * 4;
