@@ -10,9 +10,9 @@ a summation order can flip), and after the steps the prefill slots are
 untouched, the new cache rows match, and every row's position, the shared
 length and the step counter advanced. Cases: 2, 3, 5 (a row bound of 8 with
 3 rows unused) and 8 rows; config 5 at its stated size (eight prompts of
-U[64, 2048] tokens, cache 8192, the engine's bucket); and a batch whose
-bucket needs many keys per split, and one with one long row among short
-ones.
+U[64, 2048] tokens, cache 8192, the engine's bucket); a batch whose bucket
+needs many keys per split, one with one long row among short ones; and an
+MLP wider than one LDS slice of act rows at every row bound.
 """
 
 import pytest
@@ -209,3 +209,15 @@ def test_batch_rows_as_if_alone_full_depth(dev):
     # each disagreement above is a checked <= 2-ulp near-tie; at this depth the
     # random-init model's flat logits make a couple of them per dozen usual
     assert agree >= b * steps - 2
+
+
+def test_batch_step_wide_mlp(dev):
+    """An intermediate size of 10752 (21 chunks of 512): the down projection
+    runs over K slices at every row bound, the last slice one chunk wide --
+    up to 4 rows slices of 20 chunks (at 2 rows each slice's act words load
+    before the previous slice's products), at 8 rows slices of 10."""
+    cfg = dict(MID_4B, intermediate_size=10752)
+    tensors = C.random_weights(cfg, seed=7)
+    wide = (cfg, O.OracleQwen3(O.OracleConfig(cfg), tensors), Qwen3(None, dev, tensors=tensors, config=cfg))
+    for lengths, seed in (((70, 140), 8), ((33, 90, 150, 61), 9), ((40, 75, 12, 160, 99, 31, 128, 57), 10)):
+        _run(dev, wide, _prompts(lengths, seed), 3)
