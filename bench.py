@@ -44,13 +44,16 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 
 # HBM bytes per launch, from two rocprofv3 PMC runs of `bench.py --probe-traffic`
 # (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same counter reads for a
-# 256 MiB device copy (FETCH 0.50007, WRITE 1.0). Re-measure when the kernel changes.
+# 256 MiB device copy (FETCH 0.50006, WRITE 1.0). Each constant names the commit
+# whose kernel sources it was measured with; re-measure when those change.
 #   gate_up (per-kernel path): gemv_kernel<PRO_PARTS, EPI_SWIGLU, 1, 5, 1> at batch 1
 GATE_UP_TRAFFIC_B1 = 100_153_865
+GATE_UP_TRAFFIC_AT = "1ea3e7e"
 #   the persistent step kernel (step_kernel<128, 4, false>) at batch 1, context 137..146:
-#   3,961,738 KiB / 0.500065 fetched + 4,418 KiB written per launch, 1.0063x its
+#   3,961,667 KiB / 0.500065 fetched + 4,418 KiB written per launch, 1.0063x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_117_116_020
+STEP_TRAFFIC_B1 = 8_116_958_425
+STEP_TRAFFIC_AT = "12382b3"   # step kernel sources last changed in a4ccc11
 
 
 def log(msg: str) -> None:
@@ -165,35 +168,50 @@ def probe_traffic(b: int = 1, layers: int = 36) -> None:
                       "gate_up_bytes": gate_up_bytes(b, h, inter, sk), "sk": sk}), flush=True)
 
 
-def cpu_baseline(tensors, cfg, kv, first_tok, positions, s, gpu_tokens, budget_s=15.0):
+FIXTURE = os.path.join(ROOT, "tests", "golden", "config4_trace.npz")
+CPU_STEPS = 64   # timed CPU decode steps (after one warm-up step), whatever --steps is
+
+
+def cpu_baseline(tensors, cfg, kv, s, gpu_tokens, budget_s=60.0):
     """The oracle's decode loop (engine.py:721-743 restated) on this host's
-    cores, from the GPU prefill's KV cache, teacher-forced with the GPU's
-    tokens. Times whole decode steps (argmax included), prefill excluded."""
+    cores, from the GPU prefill's KV cache, teacher-forced with the committed
+    config-4 fixture's ids (tests/golden/config4_trace.npz: the oracle's own
+    greedy tokens for this prompt), so the sample is CPU_STEPS + 1 steps
+    whatever --steps is. Times whole decode steps (argmax included), prefill
+    excluded. Reports how many of its tokens equal the fixture's, and how many
+    equal the GPU's over the steps where the GPU's free-running tokens still
+    follow the fixture (after a GPU near-tie flip the contexts differ)."""
+    import numpy as np
     import torch
     from oracle import ek_oracle as O
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
+    ids = np.load(FIXTURE)["ids"].astype(np.int64)
+    n = CPU_STEPS + 1
     om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
     k_cpu, v_cpu = kv
     b = 1
     st = O.EagerState.__new__(O.EagerState)
     st.k, st.v = k_cpu, v_cpu
-    st.positions = positions.clone()
+    st.positions = torch.tensor([s], dtype=torch.int64)
     st.slot_t = torch.zeros(b, dtype=torch.int64)
     st.len_t = torch.full((1,), s, dtype=torch.int64)
     st.start_t = torch.zeros(b, dtype=torch.int32)
-    tok = first_tok.clone()
-    times, agree = [], 0
+    # the GPU's tokens follow the fixture up to its first differing step
+    follow = next((i for i in range(len(gpu_tokens)) if gpu_tokens[i] != ids[i + 1]), len(gpu_tokens))
+    times, agree_fx, agree_gpu = [], 0, 0
     t_start = time.perf_counter()
     with torch.inference_mode():
-        for i in range(len(gpu_tokens)):
+        for i in range(n):
             t0 = time.perf_counter()
-            hidden = om.decode(tok, st.positions, st.k, st.v, st.slot_t, st.len_t, st.start_t)
-            nxt = O.argmax_token(hidden, om.lm_head)
+            hidden = om.decode(torch.tensor([int(ids[i])], dtype=torch.int64), st.positions, st.k, st.v,
+                               st.slot_t, st.len_t, st.start_t)
+            nxt = int(O.argmax_token(hidden, om.lm_head).item())
             times.append(time.perf_counter() - t0)
-            agree += int(nxt.item() == gpu_tokens[i])
-            tok = torch.tensor([gpu_tokens[i]], dtype=torch.int64)
+            agree_fx += int(nxt == ids[i + 1])
+            if i < follow:
+                agree_gpu += int(nxt == gpu_tokens[i])
             st.positions = st.positions + 1
             if time.perf_counter() - t_start > budget_s and i >= 3:
                 break
@@ -211,8 +229,10 @@ def cpu_baseline(tensors, cfg, kv, first_tok, positions, s, gpu_tokens, budget_s
         "value": round(b / per, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
         "ms_per_token": round(per * 1e3, 2),
         "sample": (f"{len(timed)} timed decode steps (of {len(times)} run) of config 4 at context "
-                   f"{s + 1}..{s + len(times)}, batch 1, torch CPU oracle, {cpu_model}"),
-        "agree_with_gpu": f"{agree}/{len(times)}",
+                   f"{s + 1}..{s + len(times)}, batch 1, teacher-forced with the committed fixture's ids, "
+                   f"torch CPU oracle, {cpu_model}"),
+        "agree_with_fixture": f"{agree_fx}/{len(times)}",
+        "agree_with_gpu": f"{agree_gpu}/{min(follow, len(times))}",
     }
 
 
@@ -247,7 +267,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (diagnostics only)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--cpu-budget", type=float, default=60.0)
     ap.add_argument("--probe-traffic", action="store_true", help="run only the launches of the PMC traffic profile")
     ap.add_argument("--config", type=int, default=4, choices=(2, 3, 4, 5, 6, 7),
                     help="4 (default): the batch-1 decode line; 2 / 3 / 5 / 6 / 7: the GEMV sweep, the attention "
@@ -335,25 +355,26 @@ def main():
                         + (f"; every workgroup attends 1/{split} of a kv head's keys)" if split else ")"))
             # the PMC figure is for the default workload only
             dom_traffic = STEP_TRAFFIC_B1 if (not split and args.prompt == 128 and not args.layers) else None
+            traffic_at = STEP_TRAFFIC_AT if dom_traffic else None
         else:
             dom_s, dom_bytes, dom_n = time_dominant_kernel(model, b)
             dom_name = "gemv_kernel<PRO_PARTS,EPI_SWIGLU> (add+RMSNorm+gate_up+SwiGLU)"
             dom_traffic = GATE_UP_TRAFFIC_B1 if b == 1 else None
+            traffic_at = GATE_UP_TRAFFIC_AT if dom_traffic else None
             log(f"gate_up kernel: {dom_s * 1e6:.2f} us over {dom_n} launches")
 
         cpu = None
-        if not args.no_cpu:
-            n_kv = s + 1
-            kv = ([t[0:1, :, :n_kv].cpu().clone() for t in eng.k_cache],
-                  [t[0:1, :, :n_kv].cpu().clone() for t in eng.v_cache])
-            # the caches the oracle extends need room for the sampled steps
-            room = 65   # 64 timed steps after one warm-up step
+        if not args.no_cpu and args.prompt == 128 and not args.layers:
+            # the GPU prefill's KV cache of the prompt (rows [0, s)), with room
+            # for the sampled steps
+            room = CPU_STEPS + 2
+            kv = ([t[0:1, :, :s].cpu().clone() for t in eng.k_cache],
+                  [t[0:1, :, :s].cpu().clone() for t in eng.v_cache])
             kv = ([torch.cat([t, torch.zeros(1, t.shape[1], room, t.shape[3], dtype=t.dtype)], 2) for t in kv[0]],
                   [torch.cat([t, torch.zeros(1, t.shape[1], room, t.shape[3], dtype=t.dtype)], 2) for t in kv[1]])
             log("timing the CPU oracle baseline")
-            # GPU step 1 decoded token `first` at context s+1 and emitted tokens[0]
-            cpu = cpu_baseline(tensors, cfg, kv, first.cpu(), torch.tensor([s], dtype=torch.int64), s,
-                               tokens[:room], budget_s=args.cpu_budget)
+            # GPU step 1 decoded token `first` (fixture id 0) at context s+1 and emitted tokens[0]
+            cpu = cpu_baseline(tensors, cfg, kv, s, tokens, budget_s=args.cpu_budget)
             cpu.update(cpu_config1())
 
     achieved = dom_bytes / dom_s
@@ -384,7 +405,7 @@ def main():
         "roofline": {
             "bound": "hbm", "kernel": dom_name,
             "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM, 4), "traffic": dom_traffic,
+            "frac": round(achieved / PEAK_HBM, 4), "traffic": dom_traffic, "traffic_measured_at": traffic_at,
             "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_s * 1e6, 3), "launches": dom_n,
         },
         "cpu_baseline": cpu,
