@@ -36,12 +36,6 @@ constexpr int BLLW = 16;      // tagged (argmax) words in flight per thread
 #define EK_BSTEP_PF 6
 #endif
 constexpr int BPF = EK_BSTEP_PF;   // chunks per wave prefetched ahead of a hand-over wait
-// rows whose next activation chunk is read ahead of the current products
-// (at 8 rows the 8 extra chunks in registers spill, and the products of 8
-// rows cover the LDS round trip anyway)
-#ifndef EK_BSTEP_XA
-#define EK_BSTEP_XA 4
-#endif
 // activation chunks per LDS slice of a row in the down projection: up to 4
 // rows 20 (10240 bf16: a 9728-wide act row in one slice, so the phase has no
 // slice boundary, where the ring drains and the next act words make a round
@@ -65,144 +59,229 @@ template <int MB>
 constexpr int bstep_slice_units() { return (MB * bstep_slice(MB) * CH / 8 + SNT - 1) / SNT; }
 
 // ---------------------------------------------------------------------------
-// projections over MB activation rows
+// projections over MB activation rows, on the matrix cores
 // ---------------------------------------------------------------------------
-// A wave's items of one phase: item i -> (row i / C, chunk i % C) of the
-// workgroup's share, gate rows then up rows for a pair phase; rows are ldw
-// elements apart (ldw > K for a K slice of a wider matrix).
-struct BSpan {
-  const bf16_t* g;    // row u0 of the share
-  const bf16_t* up;   // row up_off + u0 (pair phases)
-  int nu;             // rows of the first half (every row of a plain phase)
-  int C;
+// v_mfma_f32_4x4x4_16b_bf16: 16 blocks of 4 lanes, lane l = 4 blk + j holds
+// A[blk][row j][4 k], B[blk][4 k][column j] and C[blk][rows 0..3][column j].
+// A tile is 4 weight rows of the workgroup's share and an item one 128-wide
+// K chunk of a tile: lanes 16 r .. 16 r + 15 load the 256 contiguous bytes
+// of row r (1 KiB per load instruction, the pattern HBM streams best; the
+// MFMA layout's interleaved rows stream markedly slower), and four
+// ds_bpermute move piece blk of row j to lane 4 blk + j. Two MFMAs per
+// column group (4 batch rows) take the piece's two 4-k halves against the
+// batch rows' 16 bytes at the same k, read from the LDS activation rows
+// (rows >= MB repeat a real row; their outputs are dropped). Block blk
+// accumulates k offsets 8 blk .. 8 blk + 7 of every chunk of the tile; at
+// the tile's end (or at the wave's last item inside it) tile_sum adds the
+// 16 blocks. A phase has as many items as 1 KiB chunks of its rows, split
+// over the waves as evenly as the rows' chunks were.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+using eka::f32x4_t;
+constexpr int MT = 4;      // weight rows per tile
+constexpr int MCH = 128;   // K per tile chunk (one 16-byte load per lane)
+
+__device__ __forceinline__ f32x4_t mfma4x4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
+  const s16x4_t a = __builtin_bit_cast(s16x4_t, make_uint2(a0, a1));
+  const s16x4_t b = __builtin_bit_cast(s16x4_t, make_uint2(b0, b1));
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// The 16 blocks' sum of one column group's accumulator: lane l gets row
+// l / 16 of column l % 4. Rows 0 / 2 and 1 / 3 meet across the wave's
+// halves (blocks b and b + 8, one permlane32 swap each), then 0 / 1 and 2 / 3
+// across 16-lane rows (blocks b and b + 4, one permlane16 swap), then the 4
+// blocks of a 16-lane row (two DPP rotations). The order is fixed.
+__device__ __forceinline__ float tile_sum(f32x4_t a) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[2]), false, false);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[1]), __float_as_uint(a[3]), false, false);
+  const float s0 = __uint_as_float(p[0]) + __uint_as_float(p[1]);   // lanes < 32: row 0, else row 2
+  const float s1 = __uint_as_float(q[0]) + __uint_as_float(q[1]);   // lanes < 32: row 1, else row 3
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(s0), __float_as_uint(s1), false, false);
+  float v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  v = dpp_plus<0x128>(v);   // row_ror:8
+  v = dpp_plus<0x124>(v);   // row_ror:4
+  return v;
+}
+
+// A wave's items of one phase: item i -> (tile i / C4, chunk i % C4) of the
+// workgroup's share, gate tiles then up tiles for a pair phase; rows are ldw
+// elements apart (ldw > K for a K slice of a wider matrix). Rows past rmax
+// (relative to their half) re-read it: a share's rows past the matrix (the
+// lm_head's last tile) and the clamped cursors past a wave's last item.
+struct TSpan {
+  const bf16_t* g;    // row u0 of the share, this lane's k offset (16-byte piece lane % 16)
+  const bf16_t* up;   // row up_off + u0 (pair phases), the same offset
+  int tg;             // tiles of the first half (every tile of a plain phase)
+  int C4;             // chunks per tile
+  int rmax;
   int64_t ldw;
   int i0, n;          // this wave's items [i0, i0 + n)
 };
 
-// by_rows: the wave's items are whole rows (rows split evenly over the waves)
-__device__ __forceinline__ BSpan make_bspan(const Gp& P, int64_t ldw, int wave, bool by_rows) {
+// by_rows: the wave's items are whole tiles (tiles split evenly over the
+// waves); rows_end: the matrix's rows (the lm_head's share may pass them)
+// (Every count is pinned to a scalar register: the compiler cannot prove
+// them wave-uniform after the kernel's earlier divergent loops, and would
+// otherwise keep the cursors in vector registers behind exec-mask branches.)
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ TSpan make_tspan(const Gp& P, int64_t ldw, int wave, bool by_rows, int rows_end) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0;
-  BSpan s;
-  s.g = P.w + (int64_t)u0 * ldw;
-  s.up = P.pair ? P.w + (int64_t)(P.up_off + u0) * ldw : s.g;
-  s.nu = P.pair ? nu : 0x7fffffff;
-  s.C = P.C;
+  u0 = uni(u0);
+  u1 = uni(u1);
+  const int nu = u1 - u0;   // a multiple of MT (the phases' unit granularity)
+  TSpan s;
+  const int lpc = opaque_tid() & 15;
+  s.g = P.w + (int64_t)u0 * ldw + lpc * 8;
+  s.up = P.pair ? P.w + (int64_t)(P.up_off + u0) * ldw + lpc * 8 : s.g;
+  s.tg = uni(P.pair ? nu / MT : 0x7fffffff);
+  s.C4 = uni(P.K / MCH);
+  const int re = (rows_end < u1 ? rows_end : u1) - u0 - 1;
+  s.rmax = uni(re > 0 ? re : 0);   // a share without rows re-reads its first row
   s.ldw = ldw;
   if (by_rows) {
-    const int r0 = (int)((uint32_t)nu * (uint32_t)wave / (uint32_t)SNW);
-    const int r1 = (int)((uint32_t)nu * (uint32_t)(wave + 1) / (uint32_t)SNW);
-    s.i0 = r0 * P.C;
-    s.n = (r1 - r0) * P.C;
+    const int nt = nu / MT;
+    const int t0 = (int)((uint32_t)nt * (uint32_t)wave / (uint32_t)SNW);
+    const int t1 = (int)((uint32_t)nt * (uint32_t)(wave + 1) / (uint32_t)SNW);
+    s.i0 = uni(t0 * s.C4);
+    s.n = uni((t1 - t0) * s.C4);
   } else {
     const WaveItems w = wave_items(P, nu, wave);
-    s.i0 = w.i0;
-    s.n = w.n;
+    s.i0 = uni(w.i0);
+    s.n = uni(w.n);
   }
   return s;
 }
 
-__device__ __forceinline__ const bf16_t* bspan_at(const BSpan& s, int r, int c) {
-  return (r < s.nu ? s.g + (int64_t)r * s.ldw : s.up + (int64_t)(r - s.nu) * s.ldw) + c * CH;
+// this lane's load address in tile t (chunk 0): row 4 t + lane / 16
+__device__ __forceinline__ const bf16_t* tile_at(const TSpan& s, int t) {
+  const bool gate = t < s.tg;
+  int r = MT * (gate ? t : t - s.tg) + ((opaque_tid() & 63) >> 4);
+  r = r < s.rmax ? r : s.rmax;
+  return (gate ? s.g : s.up) + (int64_t)r * s.ldw;
 }
 
 template <int CNT>
-__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring) {
-  const BSpan s = make_bspan(P, ldw, wave_id(), by_rows);
-  const int loff = (opaque_tid() & 63) * 8;
-  int r = s.i0 / s.C, c = s.i0 - (s.i0 / s.C) * s.C;
+__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring,
+                                                 int rows_end = 0x7fffffff) {
+  const TSpan s = make_tspan(P, ldw, wave_id(), by_rows, rows_end);
+  int t = s.i0 / s.C4, c = s.i0 - (s.i0 / s.C4) * s.C4;
+  const bf16_t* tp = tile_at(s, t);
 #pragma unroll
   for (int u = 0; u < CNT; ++u) {
-    ring.r[u] = ld16_nt(bspan_at(s, r, c) + loff);
-    if (u + 1 < s.n && ++c == s.C) { c = 0; ++r; }
+    ring.r[u] = ld16_nt(tp + c * MCH);
+    if (u + 1 < s.n && ++c == s.C4) { c = 0; ++t; tp = tile_at(s, t); }
   }
   ring.nready = CNT;
 }
 
-// The wave's row sums over MB activation rows, handed per finished row (or
-// row part, where a wave's items start or end inside a row) to
-// sink(row, acc), in lane 63: PartWriter stores (or, for the K slices of one
-// matrix, adds) them as per-wave partials, ArgmaxSink (lm_head, whole rows
-// per wave) keeps a running argmax. The ring works as in gemv_phase.
+// The wave's sums over MB activation rows, handed per finished tile (or
+// tile part, where a wave's items start or end inside a tile) to sink(t,
+// v): lane l holds v[c] = row 4 t + l / 16 (of the share), batch row 4 c +
+// l % 4. PartWriter stores (or, for the K slices of one matrix, adds) them
+// as per-wave partials, ArgmaxSink (lm_head, whole tiles per wave) keeps a
+// running argmax. The ring works as in gemv_phase: slot u holds the item
+// NB places ahead, refilled as soon as its words are moved to the MFMA
+// layout.
 template <int MB, typename SINK>
 __device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
-                                             int xstride, SINK& sink) {
-  const int lane = opaque_tid() & 63, wave = wave_id();
-  const BSpan sp = make_bspan(P, ldw, wave, by_rows);
-  const int n = sp.n, C = sp.C;
-  const int loff = lane * 8;
+                                             int xld, SINK& sink, int rows_end = 0x7fffffff) {
+  constexpr int CG = MB > 4 ? 2 : 1;   // column groups of 4 batch rows
+  const int lane = opaque_tid() & 63;
+  const int blk = lane >> 2, j4 = lane & 3;
+  const int src = (16 * j4 + blk) * 4;   // ds_bpermute source: row j4's piece blk
+  const TSpan sp = make_tspan(P, ldw, wave_id(), by_rows, rows_end);
+  const int n = sp.n, C4 = sp.C4;
   // refill cursor: the item NB places ahead of the one consumed (the last
   // item again past the end)
-  int rf = sp.i0 / C, cf = sp.i0 - (sp.i0 / C) * C;
+  int tf = sp.i0 / C4, cf = sp.i0 - (sp.i0 / C4) * C4;
+  const bf16_t* tpf = tile_at(sp, tf);
 #pragma unroll
   for (int u = 0; u < NB; ++u) {
-    if (u >= ring.nready) ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
-    if (u + 1 < n && ++cf == C) { cf = 0; ++rf; }
+    if (u >= ring.nready) ring.r[u] = ld16_nt(tpf + cf * MCH);
+    if (u + 1 < n && ++cf == C4) { cf = 0; ++tf; tpf = tile_at(sp, tf); }
   }
   int kf = NB < n ? NB : n - 1;   // item index of the cursor
-  int r = sp.i0 / C, ch = sp.i0 - (sp.i0 / C) * C;
-  uint4 xc[MB];
+  int t = sp.i0 / C4, ch = sp.i0 - (sp.i0 / C4) * C4;
+  const bf16_t* xr[CG];
 #pragma unroll
-  for (int m = 0; m < MB; ++m) xc[m] = *reinterpret_cast<const uint4*>(xs + m * xstride + ch * CH + loff);
-  float acc[MB];
+  for (int c = 0; c < CG; ++c) xr[c] = xs + ((4 * c + j4) & (MB - 1)) * xld + blk * 8;
+  f32x4_t acc[CG];
 #pragma unroll
-  for (int m = 0; m < MB; ++m) acc[m] = 0.f;
-  auto flush = [&](int row) {
-    wave_sums_dpp_lane63<MB>(acc);
-    if (lane == 63) sink(row, acc);
+  for (int c = 0; c < CG; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto flush = [&](int tile) {
+    float v[CG];
 #pragma unroll
-    for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+    for (int c = 0; c < CG; ++c) {
+      v[c] = tile_sum(acc[c]);
+      acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+    sink(tile, v);
   };
-  // the next item's activation chunks are read ahead of this item's products
-  // (up to EK_BSTEP_XA rows; beyond, after them)
-  constexpr int XA = MB <= EK_BSTEP_XA ? MB : 0;
-  auto step = [&](const uint4& w) {
-    const int chn = ch + 1 == C ? 0 : ch + 1;
-    uint4 xn[XA > 0 ? XA : 1];
+  // one item: its weights into the MFMA layout, then the slot's refill,
+  // then the products
+  auto step = [&](uint4& slot, bool refill) {
+    uint4 xv[CG];
 #pragma unroll
-    for (int m = 0; m < XA; ++m) xn[m] = *reinterpret_cast<const uint4*>(xs + m * xstride + chn * CH + loff);
+    for (int c = 0; c < CG; ++c) xv[c] = *reinterpret_cast<const uint4*>(xr[c] + ch * MCH);
+    uint4 w;
+    w.x = __builtin_amdgcn_ds_bpermute(src, (int)slot.x);
+    w.y = __builtin_amdgcn_ds_bpermute(src, (int)slot.y);
+    w.z = __builtin_amdgcn_ds_bpermute(src, (int)slot.z);
+    w.w = __builtin_amdgcn_ds_bpermute(src, (int)slot.w);
+    if (refill) {
+      slot = ld16_nt(tpf + cf * MCH);
+      if (kf + 1 < n) {
+        ++kf;
+        if (++cf == C4) { cf = 0; ++tf; tpf = tile_at(sp, tf); }
+      }
+    }
 #pragma unroll
-    for (int m = 0; m < MB; ++m) acc[m] = step_dot8(w, xc[m], acc[m]);
-#pragma unroll
-    for (int m = 0; m < MB; ++m)
-      xc[m] = m < XA ? xn[m < XA ? m : 0] : *reinterpret_cast<const uint4*>(xs + m * xstride + chn * CH + loff);
+    for (int c = 0; c < CG; ++c) {
+      acc[c] = mfma4x4(w.x, w.y, xv[c].x, xv[c].y, acc[c]);
+      acc[c] = mfma4x4(w.z, w.w, xv[c].z, xv[c].w, acc[c]);
+    }
   };
   int k0 = 0;
   for (; k0 + NB <= n; k0 += NB) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-      step(ring.r[u]);
-      ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
-      if (kf + 1 < n) {
-        ++kf;
-        if (++cf == C) { cf = 0; ++rf; }
-      }
-      if (ch == C - 1) flush(r);
-      if (++ch == C) { ch = 0; ++r; }
+      step(ring.r[u], true);
+      if (ch == C4 - 1) flush(t);
+      if (++ch == C4) { ch = 0; ++t; }
+      // keep each slot's refill where it is: the scheduler would otherwise
+      // sink the refills below later items' products and drain the ring
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
   for (int u = 0; u < NB; ++u) {
     if (k0 + u < n) {
-      step(ring.r[u]);
-      if (ch == C - 1 || k0 + u == n - 1) flush(r);
-      if (++ch == C) { ch = 0; ++r; }
+      step(ring.r[u], false);
+      if (ch == C4 - 1 || k0 + u == n - 1) flush(t);
+      if (++ch == C4) { ch = 0; ++t; }
     }
   }
-  if (k0 == n && n > 0 && ch != 0) flush(r);   // the wave's items ended inside a row at a block edge
+  if (k0 == n && n > 0 && ch != 0) flush(t);   // the wave's items ended inside a tile at a ring edge
   ring.nready = 0;
 }
 
 template <int MB, bool ACC>
-struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= acc[m]
+struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= the row's sum for batch row m
   float* part;
   int wave;
-  __device__ void operator()(int row, const float* acc) {
+  __device__ void operator()(int t, const float* v) {
+    const int lane = opaque_tid() & 63;
+    if ((lane & 12) != 0) return;   // one lane of each 16-lane row: row lane / 16, batch row lane % 4 (+4)
+    const int row = MT * t + (lane >> 4);
 #pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      float* p = part + (row * SNW + wave) * MB + m;
-      *p = ACC ? *p + acc[m] : acc[m];
+    for (int c = 0; c < (MB > 4 ? 2 : 1); ++c) {
+      const int m = 4 * c + (lane & 3);
+      if (m < MB) {
+        float* p = part + (row * SNW + wave) * MB + m;
+        *p = ACC ? *p + v[c] : v[c];
+      }
     }
   }
 };
@@ -315,22 +394,26 @@ __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, 
   }
 }
 
-// lm_head rows of this wave (whole rows): a running first-index argmax per
-// batch row, kept in lane 63 (where the row sums land), and the optional
-// logits
+// lm_head tiles of this wave (whole tiles): a running first-index argmax per
+// lane over the rows it receives (row 4 t + lane / 16, batch row 4 c + lane
+// % 4, in one lane of each 16-lane row), and the optional logits
 template <int MB>
 struct ArgmaxSink {
-  float bv[MB];
-  int bi[MB];
+  static constexpr int CG = MB > 4 ? 2 : 1;
+  float bv[CG];
+  int bi[CG];
   bf16_t* logits;      // [nrows][vocab] or null
   int vocab, nrows, u0;
-  __device__ void operator()(int row, const float* acc) {
+  __device__ void operator()(int t, const float* v) {
+    const int lane = opaque_tid() & 63;
+    const int idx = u0 + MT * t + (lane >> 4);
+    if ((lane & 12) != 0 || idx >= vocab) return;
 #pragma unroll
-    for (int m = 0; m < MB; ++m) {
-      const float v = rbf(acc[m]);
-      const int idx = u0 + row;
-      if (logits && m < nrows) logits[(int64_t)m * vocab + idx] = (bf16_t)f2bf(v);
-      if (am_better(v, idx, bv[m], bi[m])) { bv[m] = v; bi[m] = idx; }
+    for (int c = 0; c < CG; ++c) {
+      const float lv = rbf(v[c]);
+      const int m = 4 * c + (lane & 3);
+      if (logits && m < nrows) logits[(int64_t)m * vocab + idx] = (bf16_t)f2bf(lv);
+      if (am_better(lv, idx, bv[c], bi[c])) { bv[c] = lv; bi[c] = idx; }
     }
   }
 };
@@ -346,6 +429,13 @@ __host__ __device__ inline int bstep_xcols(int h, int qw, int mb) {
   x = x > bstep_slice(mb) * CH ? x : bstep_slice(mb) * CH;
   return x;
 }
+// their LDS stride (elements): rows EK_BSTEP_XPAD elements past a multiple
+// of 512, so that the 4 batch rows one B-operand read takes at one k fall in
+// different banks
+#ifndef EK_BSTEP_XPAD
+#define EK_BSTEP_XPAD 32
+#endif
+__host__ __device__ inline int bstep_xld(int h, int qw, int mb) { return bstep_xcols(h, qw, mb) + EK_BSTEP_XPAD; }
 // part rows of the largest projection share (lm_head keeps no partials)
 __host__ __device__ inline int bstep_part_rows(int h, int inter, int qkvw, int nwg) {
   int r = 4 * cdiv_i(qkvw / 4, nwg);
@@ -424,13 +514,13 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int64_t lwords = (int64_t)MB * arena_layer_words(h, inter, qkvw, qw);
   constexpr int BSLICE = bstep_slice(MB);
-  const int xcols = bstep_xcols(h, qw, MB);
+  const int xld = bstep_xld(h, qw, MB);
 
   uint32_t* rr = reinterpret_cast<uint32_t*>(smem);
   unsigned char* ph = smem + bstep_rr_bytes(MB, h);
   bf16_t* xs = reinterpret_cast<bf16_t*>(ph);
   uint32_t* xs32 = reinterpret_cast<uint32_t*>(ph);
-  float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)MB * xcols * 2));
+  float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)MB * xld * 2));
   const int part_n = a.part_max * SNW * MB;
   uint32_t* gain_lds = reinterpret_cast<uint32_t*>(reinterpret_cast<unsigned char*>(part) +
                                                    eka::align16((size_t)a.part_max * SNW * MB * 4));   // the norm's gain row
@@ -455,6 +545,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   // the unit's row's exchange words: its slots' units, after the rows before
   llw_t* lx_row = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB + long_words(a.nkv, upre, G, D);
   const int nsl = cdiv_i(inter, BSLICE * CH);   // K slices of the down projection
+  const int lm_units = MT * cdiv_i(a.vocab, MT);   // whole tiles; the rows past vocab re-read its last
 
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
@@ -484,17 +575,17 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         for (int i = tid; i < h / 2; i += SNT) rr[m * (h / 2) + i] = e32[i];
       }
       __syncthreads();
-      add_norm_rows<MB>(rr, nullptr, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
+      add_norm_rows<MB>(rr, nullptr, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
     } else {
       const bool ok = dw_read<MB>(dn_prev, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
       if (!wg_all(ok, s_fail)) return false;
       EK_TS(22);
-      add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
+      add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
       EK_TS(23);
     }
     __syncthreads();
     EK_TS(1);
-    gemv_phase_b<MB>(gq, h, false, ring, xs, xcols, put);
+    gemv_phase_b<MB>(gq, h, false, ring, xs, xld, put);
     __syncthreads();
     EK_TS(2);
     epilogue_ll_b<MB>(gq, part, qkv_ll, qkvw / 4, nrows);
@@ -519,14 +610,14 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     // ---- o projection
     zero_part(part, part_n);
     {
-      // row m's values land xcols apart
+      // row m's values land xld apart
       const bool ok = dw_read<MB>(att_ll, RowsUnits{qw / 4, qw / 8}, nrows * (qw / 8), xs32,
-                                  RowsLds{qw / 8, xcols / 2}, a.err, a.spin);
+                                  RowsLds{qw / 8, xld / 2}, a.err, a.spin);
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(6);
     __syncthreads();
-    gemv_phase_b<MB>(go, qw, false, ring, xs, xcols, put);
+    gemv_phase_b<MB>(go, qw, false, ring, xs, xld, put);
     __syncthreads();
     EK_TS(7);
     epilogue_ll_b<MB>(go, part, o_ll, h / 4, nrows);
@@ -541,13 +632,13 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(16);
-    add_norm_rows<MB>(rr, xs32, gw2, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
+    add_norm_rows<MB>(rr, xs32, gw2, gain_lds, h, nrows, a.eps, xs, xld, s_red);
     EK_TS(17);
     load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm, h, gw1);
     EK_TS(18);
     __syncthreads();
     EK_TS(9);
-    gemv_phase_b<MB>(gg, h, false, ring, xs, xcols, put);
+    gemv_phase_b<MB>(gg, h, false, ring, xs, xld, put);
     __syncthreads();
     EK_TS(10);
     epilogue_swiglu_ll_b<MB>(gg, part, act_ll, inter / 4, nrows);
@@ -571,7 +662,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       if (sl > 0) __syncthreads();   // the previous slice's products have read their LDS rows
       {
         if (sl == 0 || !EARLY) dw_issue<SW>(act_ll + c0 * (CH / 4), src, nrows * su, nx);
-        const bool ok = dw_finish<SW>(act_ll + c0 * (CH / 4), src, nrows * su, nx, xs32, RowsLds{su, xcols / 2},
+        const bool ok = dw_finish<SW>(act_ll + c0 * (CH / 4), src, nrows * su, nx, xs32, RowsLds{su, xld / 2},
                                       a.err, a.spin);
         if (!wg_all(ok, s_fail)) return false;
       }
@@ -582,7 +673,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       if (sl == 0) EK_TS(20);
       else EK_TS(21);
       __syncthreads();
-      gemv_phase_b<MB>(gd, inter, false, ring, xs, xcols, add);
+      gemv_phase_b<MB>(gd, inter, false, ring, xs, xld, add);
       if (sl == 0) EK_TS(12);
       else EK_TS(13);
       // the next slice's first chunks, or the next phase's (every iteration
@@ -594,7 +685,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         prefetch_phase_b<BPF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
                                      0, 4), h, false, ring);
       else
-        prefetch_phase_b<BPF>(make_gp(a.lm_head, h, a.vocab, 0, 1), h, true, ring);
+        prefetch_phase_b<BPF>(make_gp(a.lm_head, h, lm_units, 0, MT), h, true, ring, a.vocab);
     }
     __syncthreads();
     epilogue_ll_b<MB>(down_slice(0), part, dn_ll, h / 4, nrows);
@@ -609,33 +700,43 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     const bool ok = dw_read<MB>(dn_prev, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
     if (!wg_all(ok, s_fail)) return false;
   }
-  add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xcols, s_red);
+  add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
   __syncthreads();
-  const Gp gl = make_gp(a.lm_head, h, a.vocab, 0, 1);
+  const Gp gl = make_gp(a.lm_head, h, lm_units, 0, MT);
   int u0, u1;
   unit_range(gl, u0, u1);
   ArgmaxSink<MB> am;
 #pragma unroll
-  for (int m = 0; m < MB; ++m) { am.bv[m] = -INFINITY; am.bi[m] = 0x7fffffff; }
+  for (int c = 0; c < ArgmaxSink<MB>::CG; ++c) { am.bv[c] = -INFINITY; am.bi[c] = 0x7fffffff; }
   am.logits = a.logits;
   am.vocab = a.vocab;
   am.nrows = nrows;
   am.u0 = u0;
-  gemv_phase_b<MB>(gl, h, true, ring, xs, xcols, am);
-  // the waves' bests (lane 63) -> the workgroup's, per row -> two words per row
-  float* sv = reinterpret_cast<float*>(ph);            // [SNW][MB] (the activation rows are no longer read)
-  int* si = reinterpret_cast<int*>(ph) + SNW * MB;
+  gemv_phase_b<MB>(gl, h, true, ring, xs, xld, am, a.vocab);
+  // the lanes' bests (one lane per 16-lane row and batch row) -> the
+  // workgroup's, per row -> two words per row
+  float* sv = reinterpret_cast<float*>(ph);            // [SNW][4][MB] (the activation rows are no longer read)
+  int* si = reinterpret_cast<int*>(ph) + SNW * 4 * MB;
   __syncthreads();
-  if ((threadIdx.x & 63) == 63) {
+  {
+    const int lane = tid & 63;
+    if ((lane & 12) == 0) {
 #pragma unroll
-    for (int m = 0; m < MB; ++m) { sv[wave_id() * MB + m] = am.bv[m]; si[wave_id() * MB + m] = am.bi[m]; }
+      for (int c = 0; c < ArgmaxSink<MB>::CG; ++c) {
+        const int m = 4 * c + (lane & 3);
+        if (m < MB) {
+          sv[(wave_id() * 4 + (lane >> 4)) * MB + m] = am.bv[c];
+          si[(wave_id() * 4 + (lane >> 4)) * MB + m] = am.bi[c];
+        }
+      }
+    }
   }
   __syncthreads();
   llw_t* am_ll = half + (int64_t)a.nl * lwords;
   if (tid < nrows) {
     float ov = sv[tid];
     int oi = si[tid];
-    for (int w = 1; w < SNW; ++w)
+    for (int w = 1; w < SNW * 4; ++w)
       if (am_better(sv[w * MB + tid], si[w * MB + tid], ov, oi)) { ov = sv[w * MB + tid]; oi = si[w * MB + tid]; }
     ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid), __float_as_uint(ov), AM_TAG);
     ll_put(am_ll + 2 * ((int64_t)blockIdx.x * MB + tid) + 1, (uint32_t)oi, AM_TAG);
@@ -744,7 +845,7 @@ __global__ __launch_bounds__(SNT) void batch_step_kernel(StepArgs a) {
 template <int D, int G, int MB>
 inline size_t bstep_lds_bytes(int h, int qw, int part_rows, int lchunk, int nwg) {
   const size_t rr = bstep_rr_bytes(MB, h);
-  const size_t gemv = eka::align16((size_t)MB * bstep_xcols(h, qw, MB) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4) +
+  const size_t gemv = eka::align16((size_t)MB * bstep_xld(h, qw, MB) * 2) + eka::align16((size_t)part_rows * SNW * MB * 4) +
                       eka::align16((size_t)h / 2 * 4);
   const size_t attn = LongLds<D, G>::bytes(lchunk);
   const size_t fin = (size_t)2 * nwg * MB * 4 + (size_t)MB * 4;

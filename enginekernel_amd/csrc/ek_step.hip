@@ -154,7 +154,7 @@ hipError_t make_batch_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n
   p.lchunk = (int)chunk;
   p.lx = eks::long_words((int)n_kv, (int)(p.nwg / n_kv), g, 128);   // every slot's unit, whatever its row
   const int qw = (int)(n_q * head_dim), qkvw = (int)((n_q + 2 * n_kv) * head_dim);
-  p.kpad_max = eks::bstep_xcols((int)hidden, qw, mb);
+  p.kpad_max = eks::bstep_xld((int)hidden, qw, mb);
   p.part_max = eks::bstep_part_rows((int)hidden, (int)inter, qkvw, p.nwg);
   p.o_rows = 0;
   size_t lds = 0;

@@ -185,6 +185,12 @@ class OracleQwen3:
         """ek_model.py:203 (the torch.matmul branch)."""
         return torch.matmul(x, layer[key].t())
 
+    def _prefill_proj(self, x, layer, key):
+        """ek_model.py:298, :325 and :209 (the prefill's torch.matmul projections). A separate hook
+        from _proj so that a fixture generator can re-run the prefill with
+        another fp32 summation order without changing the decode's."""
+        return torch.matmul(x, layer[key].t())
+
     def prefill(self, input_ids, positions, k_cache, v_cache, attn_bias=None):
         """ek_model.py:280-334, SDPA branch (:315-323). Writes cache slots
         [0, S); returns the final-normed hidden of the last position."""
@@ -201,7 +207,7 @@ class OracleQwen3:
                 x = rms_norm(residual, layer["ln1"], c.rms_eps)
             else:
                 x, residual = add_rms_norm(x, residual, layer["ln1"], c.rms_eps)
-            qkv = torch.matmul(x, layer["qkv"].t())
+            qkv = self._prefill_proj(x, layer, "qkv")
             qk_norm_rope_kv(qkv, layer["qn"], layer["kn"], cos, sin,
                             k_cache[i], v_cache[i], zero_slot,
                             c.num_heads, c.num_kv_heads, c.rms_eps, s)
@@ -212,9 +218,9 @@ class OracleQwen3:
                                                is_causal=attn_bias is None,
                                                scale=self.sm_scale, enable_gqa=True)
             o = o.transpose(1, 2).reshape(b * s, c.q_size)
-            x = torch.matmul(o, layer["o"].t())
+            x = self._prefill_proj(o, layer, "o")
             x, residual = add_rms_norm(x, residual, layer["ln2"], c.rms_eps)
-            x = torch.matmul(silu_mul(torch.matmul(x, layer["gu"].t())), layer["down"].t())
+            x = self._prefill_proj(silu_mul(self._prefill_proj(x, layer, "gu")), layer, "down")
         residual = residual + x
         last = residual.view(b, s, c.hidden_size)[:, -1, :]
         return rms_norm(last, self.final_norm, c.rms_eps)

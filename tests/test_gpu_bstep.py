@@ -4,9 +4,15 @@ kernel, csrc/ek_bstep_impl.h) pinned against the oracle.
 Every Qwen3-4B shape with two layers, the oracle's prefill cache of ragged
 left-padded prompts on both sides, the oracle's tokens fed back (teacher
 forcing): per step and row the step's own logits (its optional [rows, vocab]
-logits output) are within 2e-2 of the oracle's scale, the emitted token is
-the oracle's argmax or within 2 bf16 ulps of its top logit (a near-tie that
-a summation order can flip), and after the steps the prefill slots are
+logits output) are within 2e-2 of the oracle's scale and within 1.5 D + 2
+bf16 ulps of the oracle, where D is the oracle's own summation-order drift
+on the same inputs (the largest |logit difference| against the oracle re-run
+in lockstep with every projection accumulated in another fp32 order: any
+such order is as faithful to the reference as another); the emitted token
+is the oracle's argmax or a token within 2 bf16 ulps of its top logit (a
+near-tie that a summation order can flip; the reference's own exactness
+check, bench/check_exact.py:95-97, counts such differences and fails only
+on a gap above 2 logits), and after the steps the prefill slots are
 untouched, the new cache rows match, and every row's position, the shared
 length and the step counter advanced. Cases: 2, 3, 5 (a row bound of 8 with
 3 rows unused) and 8 rows; config 5 at its stated size (eight prompts of
@@ -15,6 +21,9 @@ needs many keys per split, one with one long row among short ones; and an
 MLP wider than one LDS slice of act rows at every row bound.
 """
 
+import os
+
+import numpy as np
 import pytest
 import torch
 
@@ -26,6 +35,16 @@ from oracle import ek_oracle as O
 pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
 MID_4B = dict(C.QWEN3_4B, num_hidden_layers=2)
+GOLDEN5 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config5_trace.npz")
+
+
+@pytest.fixture(scope="module")
+def full4b(dev):
+    """The 36-layer Qwen3-4B-architecture model of configs 4 and 5."""
+    cfg = dict(C.QWEN3_4B)
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+    model.persistent_rows = 8
+    return cfg, model
 
 
 @pytest.fixture(scope="module")
@@ -40,6 +59,11 @@ def _prompts(lengths, seed):
     return [torch.randint(0, 151936, (n,), generator=g).tolist() for n in lengths]
 
 
+def _reordered(x, layer, key):
+    """A projection summed in another fp32 order: fp32 operands, one fp32 matmul, then bf16."""
+    return torch.matmul(x.float(), layer[key].float().t()).to(BF)
+
+
 def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
     """random_cache: both sides start from the same random cache rows [0, s)
     (rows before a row's first key are padding, masked on both sides) and a
@@ -52,10 +76,12 @@ def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
     total = cap or s + steps + 1
     bucket = bucket or total
     st = O.EagerState(om, b, s, pad, total)
+    sa = O.EagerState(om, b, s, pad, total)    # the reordered oracle's own cache
     om.ensure_rope(total + 1)
+    plain = om._proj
     plan = model.persistent_plan(b, min(total, bucket))
     assert plan is not None and plan[1] >= 1, plan     # the batch kernel: every workgroup attends a split
-    worst, agree = 0.0, 0
+    worst, agree, drift, err_abs, near, flips = 0.0, 0, 0.0, [], 0, []
     with torch.inference_mode():
         if random_cache:
             g = torch.Generator().manual_seed(s)
@@ -64,6 +90,8 @@ def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
             tok = torch.randint(0, cfg["vocab_size"], (b,), generator=g)
         else:
             tok = O.argmax_token(om.prefill(ids, pos, st.k, st.v, bias), om.lm_head)
+        for t, u in zip(st.k + st.v, sa.k + sa.v):
+            u.copy_(t)
         kd = [t.to(dev) for t in st.k]
         vd = [t.to(dev) for t in st.v]
         tokens = tok.to(dev)
@@ -78,23 +106,37 @@ def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
         for i in range(steps):
             l_ref = O.lm_logits(om.decode(tok, st.positions, st.k, st.v, st.slot_t, st.len_t, st.start_t),
                                 om.lm_head).float()
+            try:
+                om._proj = _reordered
+                l_alt = O.lm_logits(om.decode(tok, sa.positions, sa.k, sa.v, sa.slot_t, sa.len_t, sa.start_t),
+                                    om.lm_head).float()
+            finally:
+                om._proj = plain
+            drift = max(drift, (l_alt - l_ref).abs().max().item())
             tokens.copy_(tok)
             model.step(tokens, positions, kd, vd, slot_t, len_t, start_t, ws, out_buf, step_idx, logits=logits)
             lg = logits.float().cpu()
             got = out_buf[i].cpu()
             for r in range(b):
-                rel = (lg[r] - l_ref[r]).abs().max().item() / l_ref[r].abs().max().item()
+                e = (lg[r] - l_ref[r]).abs().max().item()
+                rel = e / l_ref[r].abs().max().item()
                 worst = max(worst, rel)
                 assert rel <= 2e-2, (i, r, rel)
                 t_ref, t_gpu = int(torch.argmax(l_ref[r])), int(got[r])
+                ulp2 = 2 * O.bf16_ulp(float(l_ref[r, t_ref]))
+                err_abs.append((e, ulp2, i, r))
+                top2 = torch.topk(l_ref[r], 2).values
+                near += int(float(top2[0] - top2[1]) <= ulp2)
                 assert t_gpu == int(torch.argmax(lg[r])), (i, r)
                 if t_gpu == t_ref:
                     agree += 1
                 else:
                     gap = float(l_ref[r, t_ref] - l_ref[r, t_gpu])
-                    assert gap <= 2 * O.bf16_ulp(float(l_ref[r, t_ref])), (i, r, t_gpu, t_ref, gap)
+                    assert gap <= ulp2, (i, r, t_gpu, t_ref, gap)
+                    flips.append((i, r, gap))
             tok = torch.argmax(l_ref, -1)
             st.positions = st.positions + 1
+            sa.positions = sa.positions + 1
         K.check_error_word(K.ws_error(ws), "batch steps")
         assert int(step_idx) == steps and int(len_t) == s + steps
         assert torch.equal(positions.cpu(), st.positions)
@@ -108,8 +150,11 @@ def _run(dev, mid, prompts, steps, cap=None, bucket=None, random_cache=False):
                 assert (a - r).abs().max().item() <= 2e-2 * r.abs().max().item()
                 assert not got_c[:, :, n:].cpu().any()
     print(f"batch {b}, contexts {s + 1}..{s + steps}: worst logit error {worst:.4f} of scale, "
-          f"{agree}/{b * steps} tokens equal")
-    assert agree >= b * steps - 2
+          f"max {max(x[0] for x in err_abs):.4f} against the oracle's drift {drift:.4f}; "
+          f"{agree}/{b * steps} tokens equal, flips (step, row, oracle gap) {flips} at {near} near-ties")
+    over = [x for x in err_abs if x[0] > 1.5 * drift + x[1]]
+    assert not over, over[:4]
+    assert len(flips) <= near
     return model
 
 
@@ -143,19 +188,88 @@ def test_batch_step_uneven_rows(dev, mid):
     _run(dev, mid, _prompts((3000, 40, 41, 39), 6), 3, bucket=4096, cap=4096, random_cache=True)
 
 
-def test_batch_rows_as_if_alone_full_depth(dev):
+def test_config5_trace_teacher_forced(dev, full4b):
+    """Config 5 at full depth against the oracle's fixture
+    (tests/golden/config5_trace.npz, written by make_config5_trace.py): the
+    36-layer model, the eight ragged prompts prefilled as one batch on the
+    GPU (cache 8192, the engine's bucket), then 4 steps of the batch kernel
+    fed the oracle's ids. At every step (the prefill's logits, then each
+    step's) and row, the logits at the oracle's top-32 ids are within 1.5 D
+    + 2 bf16 ulps of the oracle's, D the fixture's largest drift (the
+    oracle against itself re-run with every prefill and decode projection
+    summed in another fp32 order); the token is the oracle's, or one whose
+    oracle logit is within D of the oracle's top logit."""
+    from enginekernel_amd.engine import _FastEngine
+    fx = np.load(GOLDEN5)
+    ids, top_ids, top_logits, drift = fx["ids"], fx["top_ids"], fx["top_logits"], fx["drift"]
+    lens, flat = fx["prompt_lens"].tolist(), fx["prompt_ids"].tolist()
+    prompts, o = [], 0
+    for n in lens:
+        prompts.append(flat[o:o + n])
+        o += n
+    cfg, model = full4b
+    eng = _FastEngine(model=model)
+    n, b, V = ids.shape[0], len(prompts), cfg["vocab_size"]
+    floor = float(drift.max())
+    with torch.inference_mode():
+        p_ids, pos, pad, s, bias = eng._pack(prompts)
+        eng._ensure_cache(b, 8192)
+        kb, vb = eng.store.layer_views(0, b)
+        lg = torch.empty(n, b, V, dtype=BF, device=dev)
+        tok = model.argmax_token(model.prefill(p_ids, pos, kb, vb, bias), logits=lg[0])
+        got = [tok.cpu().tolist()]
+        bucket = -(-(s + 256) // 256) * 256
+        ws = K.make_workspace(b, 32, 8, 128, bucket, dev)
+        assert model.persistent_plan(b, bucket)[1] >= 1
+        tokens = torch.zeros(b, dtype=torch.int64, device=dev)
+        positions = torch.as_tensor([s - p for p in pad], dtype=torch.int64, device=dev)
+        slot_t = torch.zeros(b, dtype=torch.int64, device=dev)
+        len_t = torch.full((1,), s, dtype=torch.int64, device=dev)
+        start_t = torch.as_tensor(pad, dtype=torch.int32, device=dev)
+        out_buf = torch.zeros((16, b), dtype=torch.int32, device=dev)
+        step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        forced = torch.as_tensor(ids, dtype=torch.int64, device=dev)
+        for i in range(1, n):
+            tokens.copy_(forced[i - 1])
+            model.step(tokens, positions, kb, vb, slot_t, len_t, start_t, ws, out_buf, step_idx, logits=lg[i])
+            got.append(out_buf[i - 1].cpu().tolist())
+        torch.cuda.synchronize()
+        K.check_error_word(K.ws_error(ws), "config 5 trace")
+        at_top = torch.gather(lg.float().reshape(n * b, V), 1,
+                              torch.as_tensor(top_ids.reshape(n * b, -1), dtype=torch.int64, device=dev))
+        at_top = at_top.cpu().numpy().reshape(n, b, -1)
+    err = np.abs(at_top - top_logits).max(axis=2)
+    ulp2 = np.vectorize(lambda x: 2 * O.bf16_ulp(float(x)))(top_logits[:, :, 0])
+    flips = []
+    for i in range(n):
+        for r in range(b):
+            t_gpu, t_ref = int(got[i][r]), int(ids[i, r])
+            if t_gpu == t_ref:
+                continue
+            hit = np.nonzero(top_ids[i, r] == t_gpu)[0]
+            assert hit.size, (i, r, t_gpu, t_ref)
+            gap = float(top_logits[i, r, 0] - top_logits[i, r, hit[0]])
+            assert gap <= floor, (i, r, t_gpu, t_ref, gap)
+            flips.append((i, r, gap))
+    print(f"config 5 trace (36 layers, 8 rows, {n} steps): max |dlogit| {err.max():.4f} (mean {err.mean():.4f}) "
+          f"against the oracle's drift {floor:.4f} (mean {drift.mean():.4f}); flips (step, row, oracle gap) {flips}; "
+          f"the reordered oracle differs at {int((fx['alt_ids'] != ids).sum())} of {n * b}")
+    assert (err <= 1.5 * floor + ulp2).all(), np.unravel_index(np.argmax(err - 1.5 * floor - ulp2), err.shape)
+
+
+def test_batch_rows_as_if_alone_full_depth(dev, full4b):
     """The 36-layer Qwen3-4B shape, as a property: after one GPU prefill of
     four of config 5's prompts (cache 8192), 3 steps of the batch kernel
     against each row stepped alone by the batch-1 kernel (its own copy of
     its cache row and first key), both fed the batch's tokens. The two
     differ only in fp32 summation order, so their logits agree within the
-    oracle's reorder drift bound at this depth (1.5 x 0.16 + 2 ulps) and a
-    different argmax is a near-tie."""
+    oracle's reorder drift bound at this depth (1.5 D + 2 ulps, D the
+    config-5 fixture's measured drift) and a different argmax is a
+    near-tie."""
     from enginekernel_amd.engine import _FastEngine
     from enginekernel_amd.microbench import batch8_prompts
-    cfg = dict(C.QWEN3_4B)
-    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
-    model.persistent_rows = 8
+    cfg, model = full4b
+    floor = float(np.load(GOLDEN5)["drift"].max())
     eng = _FastEngine(model=model)
     prompts = batch8_prompts(cfg["vocab_size"])[:4]
     b, steps, V = len(prompts), 3, cfg["vocab_size"]
@@ -198,7 +312,7 @@ def test_batch_rows_as_if_alone_full_depth(dev):
                 err = (a - ref).abs().max().item()
                 ulp = O.bf16_ulp(float(ref.abs().max()))
                 worst = max(worst, err)
-                assert err <= 1.5 * 0.16 + 2 * ulp, (i, r, err)
+                assert err <= 1.5 * floor + 2 * ulp, (i, r, err)
                 tb_, t1 = int(outb[i, r]), int(st["out"][i, 0])
                 if tb_ == t1:
                     agree += 1

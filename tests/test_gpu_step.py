@@ -20,6 +20,7 @@ the benchmarked kernel) pinned against the oracle.
 """
 
 import ctypes
+import math
 import os
 
 import numpy as np
@@ -82,9 +83,11 @@ def test_config4_trace_teacher_forced(dev, model4):
     vocabulary): every step within 1.5 D + 2 ulps at the oracle's top-32
     ids, and the mean within 1.5x the mean drift. The argmax equals the
     oracle's, or is a token whose oracle logit is within D of the oracle's
-    top logit (a gap two equally valid summation orders can reverse); such
-    flips may not be more frequent than twice the reordered oracle's own
-    (plus 2)."""
+    top logit (a gap two equally valid summation orders can reverse). Such
+    flips are counted like the reordered oracle's own (the fixture's
+    alt_ids): at most its count A plus 3 sqrt(A), the spread of a Poisson
+    count of mean A (measured: 46 flips, the first at step 24, against A =
+    43)."""
     fx = np.load(GOLDEN)
     ids, top_ids, top_logits = fx["ids"], fx["top_ids"], fx["top_logits"]
     drift = fx["drift"] if "drift" in fx.files else None
@@ -129,7 +132,7 @@ def test_config4_trace_teacher_forced(dev, model4):
     print(f"config 4 trace: {n - len(flips)}/{n} greedy ids equal; flips at steps {flips} (oracle gaps {gaps}); "
           f"the reordered oracle flips at {alt_flips} steps")
     if alt_flips is not None:
-        assert len(flips) <= 2 * alt_flips + 2
+        assert len(flips) <= alt_flips + 3 * math.sqrt(alt_flips)
 
 
 def test_config4_free_running_first_divergence(dev, model4):
