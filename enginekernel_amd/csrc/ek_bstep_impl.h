@@ -20,11 +20,13 @@
 // partials) and the argmax words; workgroup 0 reduces them and advances the
 // step state of every row.
 //
-// Weights are read once per step whatever MB is: each 16-byte weight chunk
-// meets the MB activation chunks (LDS) on the bf16 dot instruction. The
-// residual rows are kept in LDS as bf16 (every add rounds to bf16, so this is
-// exact), one per batch row. Rows past the launch's m (MB is m rounded up to
-// 2, 4 or 8) compute on whatever their LDS rows hold and are never stored.
+// Weights are read once per step whatever MB is: from 4 rows up each 1 KiB
+// weight load (4 rows x 256 B) meets the MB activation rows (LDS) on
+// v_mfma_f32_4x4x4_16b_bf16; at 2 rows each 16-byte weight chunk meets the
+// 2 activation chunks on the bf16 dot instruction. The residual rows are
+// kept in LDS as bf16 (every add rounds to bf16, so this is exact), one per
+// batch row. Rows past the launch's m (MB is m rounded up to 2, 4 or 8)
+// compute on whatever their LDS rows hold and are never stored.
 #pragma once
 
 #include "ek_step_impl.h"
@@ -57,6 +59,134 @@ __host__ __device__ constexpr int bstep_slice(int mb) { return mb <= 4 ? EK_BSTE
 // and one K slice of MB act rows in one round
 template <int MB>
 constexpr int bstep_slice_units() { return (MB * bstep_slice(MB) * CH / 8 + SNT - 1) / SNT; }
+
+// ---------------------------------------------------------------------------
+// projections over 2 activation rows, on the bf16 dot instruction
+// ---------------------------------------------------------------------------
+// (2 rows would fill half of every matrix-core product's columns: the dot
+// instruction does their products in fewer issue slots.) A wave's items of
+// one phase: item i -> (row i / C, chunk i % C) of the workgroup's share,
+// gate rows then up rows for a pair phase; rows are ldw elements apart (ldw
+// > K for a K slice of a wider matrix).
+struct BSpan {
+  const bf16_t* g;    // row u0 of the share
+  const bf16_t* up;   // row up_off + u0 (pair phases)
+  int nu;             // rows of the first half (every row of a plain phase)
+  int C;
+  int64_t ldw;
+  int i0, n;          // this wave's items [i0, i0 + n)
+};
+
+// by_rows: the wave's items are whole rows (rows split evenly over the waves)
+__device__ __forceinline__ BSpan make_bspan(const Gp& P, int64_t ldw, int wave, bool by_rows) {
+  int u0, u1;
+  unit_range(P, u0, u1);
+  const int nu = u1 - u0;
+  BSpan s;
+  s.g = P.w + (int64_t)u0 * ldw;
+  s.up = P.pair ? P.w + (int64_t)(P.up_off + u0) * ldw : s.g;
+  s.nu = P.pair ? nu : 0x7fffffff;
+  s.C = P.C;
+  s.ldw = ldw;
+  if (by_rows) {
+    const int r0 = (int)((uint32_t)nu * (uint32_t)wave / (uint32_t)SNW);
+    const int r1 = (int)((uint32_t)nu * (uint32_t)(wave + 1) / (uint32_t)SNW);
+    s.i0 = r0 * P.C;
+    s.n = (r1 - r0) * P.C;
+  } else {
+    const WaveItems w = wave_items(P, nu, wave);
+    s.i0 = w.i0;
+    s.n = w.n;
+  }
+  return s;
+}
+
+__device__ __forceinline__ const bf16_t* bspan_at(const BSpan& s, int r, int c) {
+  return (r < s.nu ? s.g + (int64_t)r * s.ldw : s.up + (int64_t)(r - s.nu) * s.ldw) + c * CH;
+}
+
+template <int CNT>
+__device__ __forceinline__ void prefetch_rows(const Gp& P, int64_t ldw, bool by_rows, Ring& ring) {
+  const BSpan s = make_bspan(P, ldw, wave_id(), by_rows);
+  const int loff = (opaque_tid() & 63) * 8;
+  int r = s.i0 / s.C, c = s.i0 - (s.i0 / s.C) * s.C;
+#pragma unroll
+  for (int u = 0; u < CNT; ++u) {
+    ring.r[u] = ld16_nt(bspan_at(s, r, c) + loff);
+    if (u + 1 < s.n && ++c == s.C) { c = 0; ++r; }
+  }
+  ring.nready = CNT;
+}
+
+// The wave's row sums over MB activation rows, handed per finished row (or
+// row part, where a wave's items start or end inside a row) to
+// sink.row(row, acc), in lane 63. Each weight chunk meets the MB rows'
+// chunks at the same k, read from LDS one item ahead. The ring works as in
+// gemv_phase.
+template <int MB, typename SINK>
+__device__ __forceinline__ void gemv_rows(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+                                          int xstride, SINK& sink) {
+  const int lane = opaque_tid() & 63, wave = wave_id();
+  const BSpan sp = make_bspan(P, ldw, wave, by_rows);
+  const int n = sp.n, C = sp.C;
+  const int loff = lane * 8;
+  // refill cursor: the item NB places ahead of the one consumed (the last
+  // item again past the end)
+  int rf = sp.i0 / C, cf = sp.i0 - (sp.i0 / C) * C;
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    if (u >= ring.nready) ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
+    if (u + 1 < n && ++cf == C) { cf = 0; ++rf; }
+  }
+  int kf = NB < n ? NB : n - 1;   // item index of the cursor
+  int r = sp.i0 / C, ch = sp.i0 - (sp.i0 / C) * C;
+  uint4 xc[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) xc[m] = *reinterpret_cast<const uint4*>(xs + m * xstride + ch * CH + loff);
+  float acc[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+  auto flush = [&](int row) {
+    wave_sums_dpp_lane63<MB>(acc);
+    if (lane == 63) sink.row(row, acc);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[m] = 0.f;
+  };
+  auto step = [&](const uint4& w) {
+    const int chn = ch + 1 == C ? 0 : ch + 1;
+    uint4 xn[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) xn[m] = *reinterpret_cast<const uint4*>(xs + m * xstride + chn * CH + loff);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[m] = step_dot8(w, xc[m], acc[m]);
+#pragma unroll
+    for (int m = 0; m < MB; ++m) xc[m] = xn[m];
+  };
+  int k0 = 0;
+  for (; k0 + NB <= n; k0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      step(ring.r[u]);
+      ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
+      if (kf + 1 < n) {
+        ++kf;
+        if (++cf == C) { cf = 0; ++rf; }
+      }
+      if (ch == C - 1) flush(r);
+      if (++ch == C) { ch = 0; ++r; }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < NB; ++u) {
+    if (k0 + u < n) {
+      step(ring.r[u]);
+      if (ch == C - 1 || k0 + u == n - 1) flush(r);
+      if (++ch == C) { ch = 0; ++r; }
+    }
+  }
+  if (k0 == n && n > 0 && ch != 0) flush(r);   // the wave's items ended inside a row at a ring edge
+  ring.nready = 0;
+}
 
 // ---------------------------------------------------------------------------
 // projections over MB activation rows, on the matrix cores
@@ -163,8 +293,7 @@ __device__ __forceinline__ const bf16_t* tile_at(const TSpan& s, int t) {
 }
 
 template <int CNT>
-__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring,
-                                                 int rows_end = 0x7fffffff) {
+__device__ __forceinline__ void prefetch_tiles(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, int rows_end) {
   const TSpan s = make_tspan(P, ldw, wave_id(), by_rows, rows_end);
   int t = s.i0 / s.C4, c = s.i0 - (s.i0 / s.C4) * s.C4;
   const bf16_t* tp = tile_at(s, t);
@@ -185,8 +314,8 @@ __device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool 
 // NB places ahead, refilled as soon as its words are moved to the MFMA
 // layout.
 template <int MB, typename SINK>
-__device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
-                                             int xld, SINK& sink, int rows_end = 0x7fffffff) {
+__device__ __forceinline__ void gemv_tiles(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+                                           int xld, SINK& sink, int rows_end) {
   constexpr int CG = MB > 4 ? 2 : 1;   // column groups of 4 batch rows
   const int lane = opaque_tid() & 63;
   const int blk = lane >> 2, j4 = lane & 3;
@@ -217,7 +346,7 @@ __device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_r
       v[c] = tile_sum(acc[c]);
       acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
-    sink(tile, v);
+    sink.tile(tile, v);
   };
   // one item: its weights into the MFMA layout, then the slot's refill,
   // then the products
@@ -267,19 +396,46 @@ __device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_r
   ring.nready = 0;
 }
 
+// the batch's projections: matrix-core tiles from 4 rows up, the dot
+// instruction at 2 rows; rows_end: the matrix's rows, where a tile share
+// may pass them (the lm_head's)
+template <int MB>
+constexpr bool bstep_mfma() { return MB >= 4; }
+
+template <int MB, int CNT>
+__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring,
+                                                 int rows_end = 0x7fffffff) {
+  if constexpr (bstep_mfma<MB>()) prefetch_tiles<CNT>(P, ldw, by_rows, ring, rows_end);
+  else prefetch_rows<CNT>(P, ldw, by_rows, ring);
+}
+
+template <int MB, typename SINK>
+__device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+                                             int xld, SINK& sink, int rows_end = 0x7fffffff) {
+  if constexpr (bstep_mfma<MB>()) gemv_tiles<MB>(P, ldw, by_rows, ring, xs, xld, sink, rows_end);
+  else gemv_rows<MB>(P, ldw, by_rows, ring, xs, xld, sink);
+}
+
 template <int MB, bool ACC>
 struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= the row's sum for batch row m
   float* part;
   int wave;
-  __device__ void operator()(int t, const float* v) {
+  __device__ void row(int r, const float* acc) {   // lane 63: acc[m] of batch row m
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      float* p = part + (r * SNW + wave) * MB + m;
+      *p = ACC ? *p + acc[m] : acc[m];
+    }
+  }
+  __device__ void tile(int t, const float* v) {    // every lane: v[c] of row 4 t + lane / 16, batch row 4 c + lane % 4
     const int lane = opaque_tid() & 63;
-    if ((lane & 12) != 0) return;   // one lane of each 16-lane row: row lane / 16, batch row lane % 4 (+4)
-    const int row = MT * t + (lane >> 4);
+    if ((lane & 12) != 0) return;   // one lane of each 16-lane row
+    const int r = MT * t + (lane >> 4);
 #pragma unroll
     for (int c = 0; c < (MB > 4 ? 2 : 1); ++c) {
       const int m = 4 * c + (lane & 3);
       if (m < MB) {
-        float* p = part + (row * SNW + wave) * MB + m;
+        float* p = part + (r * SNW + wave) * MB + m;
         *p = ACC ? *p + v[c] : v[c];
       }
     }
@@ -394,27 +550,34 @@ __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, 
   }
 }
 
-// lm_head tiles of this wave (whole tiles): a running first-index argmax per
-// lane over the rows it receives (row 4 t + lane / 16, batch row 4 c + lane
-// % 4, in one lane of each 16-lane row), and the optional logits
+// lm_head rows of this wave (whole rows, or whole tiles): a running
+// first-index argmax per batch row over the rows the lane receives (lane 63
+// every row of the wave on the dot path; on the tiles, row 4 t + lane / 16
+// of batch row 4 c + lane % 4 in one lane of each 16-lane row), and the
+// optional logits. A lane's slot k holds batch row k (dot path) or 4 k +
+// lane % 4 (tiles).
 template <int MB>
 struct ArgmaxSink {
-  static constexpr int CG = MB > 4 ? 2 : 1;
-  float bv[CG];
-  int bi[CG];
+  static constexpr int NS = bstep_mfma<MB>() ? (MB > 4 ? 2 : 1) : MB;
+  float bv[NS];
+  int bi[NS];
   bf16_t* logits;      // [nrows][vocab] or null
   int vocab, nrows, u0;
-  __device__ void operator()(int t, const float* v) {
+  __device__ void take(int k, int m, int idx, float v) {
+    const float lv = rbf(v);
+    if (logits && m < nrows) logits[(int64_t)m * vocab + idx] = (bf16_t)f2bf(lv);
+    if (am_better(lv, idx, bv[k], bi[k])) { bv[k] = lv; bi[k] = idx; }
+  }
+  __device__ void row(int r, const float* acc) {
+#pragma unroll
+    for (int m = 0; m < MB; ++m) take(m, m, u0 + r, acc[m]);
+  }
+  __device__ void tile(int t, const float* v) {
     const int lane = opaque_tid() & 63;
     const int idx = u0 + MT * t + (lane >> 4);
     if ((lane & 12) != 0 || idx >= vocab) return;
 #pragma unroll
-    for (int c = 0; c < CG; ++c) {
-      const float lv = rbf(v[c]);
-      const int m = 4 * c + (lane & 3);
-      if (logits && m < nrows) logits[(int64_t)m * vocab + idx] = (bf16_t)f2bf(lv);
-      if (am_better(lv, idx, bv[c], bi[c])) { bv[c] = lv; bi[c] = idx; }
-    }
+    for (int c = 0; c < NS; ++c) take(c, 4 * c + (lane & 3), idx, v[c]);
   }
 };
 
@@ -545,7 +708,9 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   // the unit's row's exchange words: its slots' units, after the rows before
   llw_t* lx_row = half + (int64_t)a.nl * lwords + 2 * (int64_t)gridDim.x * MB + long_words(a.nkv, upre, G, D);
   const int nsl = cdiv_i(inter, BSLICE * CH);   // K slices of the down projection
-  const int lm_units = MT * cdiv_i(a.vocab, MT);   // whole tiles; the rows past vocab re-read its last
+  // the lm_head's share: whole tiles (the rows past vocab re-read its last), or rows
+  const Gp glm = bstep_mfma<MB>() ? make_gp(a.lm_head, h, MT * cdiv_i(a.vocab, MT), 0, MT)
+                                  : make_gp(a.lm_head, h, a.vocab, 0, 1);
 
   const llw_t* dn_prev = nullptr;
   for (int l = 0; l < a.nl; ++l) {
@@ -603,7 +768,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         return false;
     }
     EK_TS(4);
-    prefetch_phase_b<BPF>(go, qw, false, ring);
+    prefetch_phase_b<MB, BPF>(go, qw, false, ring);
     load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
     __syncthreads();
 
@@ -622,7 +787,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     EK_TS(7);
     epilogue_ll_b<MB>(go, part, o_ll, h / 4, nrows);
     EK_TS(8);
-    prefetch_phase_b<BPF>(gg, h, false, ring);
+    prefetch_phase_b<MB, BPF>(gg, h, false, ring);
 
     // ---- r = r + o; norm; gate/up; SwiGLU
     __syncthreads();
@@ -643,7 +808,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     EK_TS(10);
     epilogue_swiglu_ll_b<MB>(gg, part, act_ll, inter / 4, nrows);
     EK_TS(11);
-    prefetch_phase_b<BPF>(down_slice(0), inter, false, ring);
+    prefetch_phase_b<MB, BPF>(down_slice(0), inter, false, ring);
 
     // ---- down projection, one K slice of the act rows at a time (one slice
     //      for a 9728-wide act row up to 4 rows); when their registers fit,
@@ -680,12 +845,12 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       // leaves the ring in the same state, so the products above see a
       // prefetched ring at compile time)
       if (sl + 1 < nsl)
-        prefetch_phase_b<BPF>(down_slice(sl + 1), inter, false, ring);
+        prefetch_phase_b<MB, BPF>(down_slice(sl + 1), inter, false, ring);
       else if (l + 1 < a.nl)
-        prefetch_phase_b<BPF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
+        prefetch_phase_b<MB, BPF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
                                      0, 4), h, false, ring);
       else
-        prefetch_phase_b<BPF>(make_gp(a.lm_head, h, lm_units, 0, MT), h, true, ring, a.vocab);
+        prefetch_phase_b<MB, BPF>(glm, h, true, ring, a.vocab);
     }
     __syncthreads();
     epilogue_ll_b<MB>(down_slice(0), part, dn_ll, h / 4, nrows);
@@ -702,33 +867,40 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   }
   add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
   __syncthreads();
-  const Gp gl = make_gp(a.lm_head, h, lm_units, 0, MT);
   int u0, u1;
-  unit_range(gl, u0, u1);
+  unit_range(glm, u0, u1);
   ArgmaxSink<MB> am;
 #pragma unroll
-  for (int c = 0; c < ArgmaxSink<MB>::CG; ++c) { am.bv[c] = -INFINITY; am.bi[c] = 0x7fffffff; }
+  for (int k = 0; k < ArgmaxSink<MB>::NS; ++k) { am.bv[k] = -INFINITY; am.bi[k] = 0x7fffffff; }
   am.logits = a.logits;
   am.vocab = a.vocab;
   am.nrows = nrows;
   am.u0 = u0;
-  gemv_phase_b<MB>(gl, h, true, ring, xs, xld, am, a.vocab);
-  // the lanes' bests (one lane per 16-lane row and batch row) -> the
-  // workgroup's, per row -> two words per row
-  float* sv = reinterpret_cast<float*>(ph);            // [SNW][4][MB] (the activation rows are no longer read)
+  gemv_phase_b<MB>(glm, h, true, ring, xs, xld, am, a.vocab);
+  // the lanes' bests -> the workgroup's, per row -> two words per row: the
+  // candidates of batch row m in slots [SNW][4][MB] (the activation rows are
+  // no longer read), every slot no lane fills a -inf sentinel
+  float* sv = reinterpret_cast<float*>(ph);
   int* si = reinterpret_cast<int*>(ph) + SNW * 4 * MB;
+  __syncthreads();
+  for (int i = tid; i < SNW * 4 * MB; i += SNT) { sv[i] = -INFINITY; si[i] = 0x7fffffff; }
   __syncthreads();
   {
     const int lane = tid & 63;
-    if ((lane & 12) == 0) {
+    if constexpr (bstep_mfma<MB>()) {
+      if ((lane & 12) == 0) {
 #pragma unroll
-      for (int c = 0; c < ArgmaxSink<MB>::CG; ++c) {
-        const int m = 4 * c + (lane & 3);
-        if (m < MB) {
-          sv[(wave_id() * 4 + (lane >> 4)) * MB + m] = am.bv[c];
-          si[(wave_id() * 4 + (lane >> 4)) * MB + m] = am.bi[c];
+        for (int c = 0; c < ArgmaxSink<MB>::NS; ++c) {
+          const int m = 4 * c + (lane & 3);
+          if (m < MB) {
+            sv[(wave_id() * 4 + (lane >> 4)) * MB + m] = am.bv[c];
+            si[(wave_id() * 4 + (lane >> 4)) * MB + m] = am.bi[c];
+          }
         }
       }
+    } else if (lane == 63) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m) { sv[wave_id() * 4 * MB + m] = am.bv[m]; si[wave_id() * 4 * MB + m] = am.bi[m]; }
     }
   }
   __syncthreads();

@@ -192,6 +192,14 @@ def batch8_bytes(w_bytes: int, kv_row: int, attended: int) -> int:
     return w_bytes + kv_row * attended
 
 
+# HBM bytes per step of the batch kernel at config 5 (batch_step_kernel<128, 4, 8>), from two
+# rocprofv3 PMC runs of `bench.py --config 5 --no-cpu` (FETCH_SIZE 4,561,084 KiB scaled by
+# the 256 MiB device-copy calibration 0.500065, plus WRITE_SIZE 75,088 KiB), measured with the
+# kernel sources of the commit named; re-measure when they change
+BATCH8_TRAFFIC = 9_416_776_470
+BATCH8_TRAFFIC_AT = "32590b2"
+
+
 def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
     """Config 5 on the Qwen3-4B architecture. Returns one record."""
     import torch
@@ -247,7 +255,15 @@ def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
            "bytes_per_step": int(nbytes), "weight_frac": round(w_bytes / step_s / PEAK_HBM, 4),
            "weight_kv_frac": round(nbytes / step_s / PEAK_HBM, 4),
            "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tokens": b * s,
-           "prefill_tokens_per_s": round(b * s / prefill_s, 0)}
+           "prefill_tokens_per_s": round(b * s / prefill_s, 0),
+           # one kernel per replay: its launch time is the replay time
+           "roofline": {"bound": "hbm", "kernel": "eks::batch_step_kernel<128,4,8> (the whole decode step, one launch)",
+                        "achieved": round(nbytes / step_s / 1e9, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                        "frac": round(nbytes / step_s / PEAK_HBM, 4),
+                        "traffic": BATCH8_TRAFFIC if (cap == 8192 and tokens == 256) else None,
+                        "traffic_measured_at": BATCH8_TRAFFIC_AT if (cap == 8192 and tokens == 256) else None,
+                        "bytes_per_launch": int(nbytes), "avg_launch_us": round(step_s * 1e6, 3),
+                        "launches": steps}}
     log(f"config 5: prefill of {b} x {s} (padded) tokens in {prefill_s * 1e3:.2f} ms")
     log(f"config 5: {step_s * 1e3:.4f} ms/step, {rec['tokens_per_s']} tok/s, "
         f"weights {rec['weight_frac']:.1%} / weights+KV {rec['weight_kv_frac']:.1%} of 8 TB/s")
@@ -386,12 +402,14 @@ def run(config: int, log=print) -> dict:
                 "config": {"workload": "config 3: one layer, 32/8 heads, D 128, L swept, splits swept"},
                 "results": attn_sweep(log=log)}
     if config == 5:
-        return {"metric": "batch-8 decode tokens/s and % of HBM roofline (config 5)", "unit": "tokens/s",
-                "higher_is_better": True, "dtype": "bf16",
-                "data": "synthetic (random-init weights seed 0, prompts seed 2)",
+        rec = batch8_decode(log=log)
+        return {"metric": "batch-8 decode tokens/s and % of HBM roofline (config 5)",
+                "value": rec["tokens_per_s"], "unit": "tokens/s", "steps": rec["timed_replays"],
+                "ms_per_step": rec["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "dtype": "bf16", "data": "synthetic (random-init weights seed 0, prompts seed 2)",
                 "config": {"workload": "config 5: Qwen3-4B architecture, batch 8 ragged, the engine's default step "
                                        "(the one-launch batch kernel, eks::batch_step_kernel<128, 4, 8>)"},
-                "results": [batch8_decode(log=log)]}
+                "roofline": rec["roofline"], "results": [rec]}
     if config == 6:
         return {"metric": "batch-1 speculative decode tokens/s vs plain (config 6)", "unit": "tokens/s",
                 "higher_is_better": True, "dtype": "bf16",
