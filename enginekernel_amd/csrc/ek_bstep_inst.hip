@@ -47,10 +47,8 @@ static int occupancy_b(size_t lds) {
 template <>
 hipError_t launch_bstep<EK_BSTEP_MB>(const StepArgs& a, int g, int nwg, hipStream_t st) {
   switch (g) {
-    case 1: return launch_b<1>(a, nwg, st);
     case 2: return launch_b<2>(a, nwg, st);
     case 4: return launch_b<4>(a, nwg, st);
-    case 8: return launch_b<8>(a, nwg, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -58,10 +56,8 @@ hipError_t launch_bstep<EK_BSTEP_MB>(const StepArgs& a, int g, int nwg, hipStrea
 template <>
 int bstep_occupancy<EK_BSTEP_MB>(int g, size_t lds) {
   switch (g) {
-    case 1: return occupancy_b<1>(lds);
     case 2: return occupancy_b<2>(lds);
     case 4: return occupancy_b<4>(lds);
-    case 8: return occupancy_b<8>(lds);
     default: return 0;
   }
 }

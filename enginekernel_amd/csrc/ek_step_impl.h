@@ -383,15 +383,8 @@ __device__ __forceinline__ llw_t* cur_half(const StepArgs& a, uint32_t ep) {
 // The chunk dot product of the projections: on the bf16 dot instruction
 // (the phases after a hand-over are bound by these instructions, not by
 // memory, when their weights are already in registers).
-#ifndef EK_STEP_DOT2
-#define EK_STEP_DOT2 1
-#endif
 __device__ __forceinline__ float step_dot8(const uint4& w, const uint4& x, float acc) {
-#if EK_STEP_DOT2
   return dot8_acc_d2(w, x, acc);
-#else
-  return dot8_acc(w, x, acc);
-#endif
 }
 struct Gp {
   const bf16_t* w;   // [rows, K] row-major

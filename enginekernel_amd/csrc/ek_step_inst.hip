@@ -47,10 +47,8 @@ static int occupancy_one(size_t lds) {
 template <bool LONG>
 static int occupancy_g(int g, size_t lds) {
   switch (g) {
-    case 1: return occupancy_one<EK_STEP_D, 1, LONG>(lds);
     case 2: return occupancy_one<EK_STEP_D, 2, LONG>(lds);
     case 4: return occupancy_one<EK_STEP_D, 4, LONG>(lds);
-    case 8: return occupancy_one<EK_STEP_D, 8, LONG>(lds);
     default: return 0;
   }
 }
@@ -58,10 +56,8 @@ static int occupancy_g(int g, size_t lds) {
 template <bool LONG>
 static hipError_t launch_g(const StepArgs& a, int g, int nwg, hipStream_t st) {
   switch (g) {
-    case 1: return launch_one<EK_STEP_D, 1, LONG>(a, nwg, st);
     case 2: return launch_one<EK_STEP_D, 2, LONG>(a, nwg, st);
     case 4: return launch_one<EK_STEP_D, 4, LONG>(a, nwg, st);
-    case 8: return launch_one<EK_STEP_D, 8, LONG>(a, nwg, st);
     default: return hipErrorInvalidValue;
   }
 }

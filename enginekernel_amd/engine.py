@@ -185,9 +185,42 @@ class _Graph:
 
 
 class _SpecGraph:
-    """engine.py:386-420: one captured draft -> verify -> accept step."""
-    __slots__ = ("graph", "batch", "bucket", "q", "hist", "hist_len", "len_b", "pos_b", "remaining", "start_t",
-                 "out_tok", "out_adv", "step_idx", "tokens")
+    """One captured draft -> verify -> accept step (the loop body the
+    reference captures, engine.py:386-420) and its device state, laid out as
+    _Graph's: the row histories [B, bucket]; ONE int64 block holding, per
+    row, the history length, the keys already cached, the next position and
+    the tokens still owed, then the step counter, seeded by a single
+    host-to-device copy per request; the rows' first keys; the drafted
+    tokens and the per-step outputs."""
+    __slots__ = ("graph", "batch", "bucket", "q", "hist", "state", "hist_len", "len_b", "pos_b", "remaining",
+                 "step_idx", "start_t", "tokens", "out_tok", "out_adv", "_seed64", "_seed32")
+
+    def __init__(self, b: int, bucket: int, q: int, dev) -> None:
+        self.graph = None
+        self.batch, self.bucket, self.q = b, bucket, q
+        self.hist = torch.zeros((b, bucket), dtype=torch.int64, device=dev)
+        self.state = torch.zeros(4 * b + 1, dtype=torch.int64, device=dev)
+        self.hist_len, self.len_b, self.pos_b, self.remaining = (self.state[i * b:(i + 1) * b] for i in range(4))
+        self.step_idx = self.state[4 * b:]
+        self.start_t = torch.zeros(b, dtype=torch.int32, device=dev)
+        self.tokens = torch.zeros((b, q), dtype=torch.int64, device=dev)
+        self.out_tok = torch.zeros((MAX_STEPS, b, q), dtype=torch.int32, device=dev)
+        self.out_adv = torch.zeros((MAX_STEPS, b), dtype=torch.int32, device=dev)
+        self._seed64 = _host_buffer(4 * b + 1, torch.int64)
+        self._seed32 = _host_buffer(b, torch.int32)
+
+    def begin(self, hist_len, cached, positions, owed, start) -> None:
+        """Set the state for a new request from per-row host values: history
+        length, keys already in the cache, next position, tokens still to
+        emit and first real key; the step counter restarts at zero."""
+        b = self.batch
+        seed = self._seed64
+        for i, vals in enumerate((hist_len, cached, positions, owed)):
+            seed[i * b:(i + 1) * b] = torch.as_tensor(vals, dtype=torch.int64)
+        seed[4 * b] = 0
+        self._seed32[:b] = torch.as_tensor(start, dtype=torch.int32)
+        self.state.copy_(seed, non_blocking=True)
+        self.start_t.copy_(self._seed32[:b], non_blocking=True)
 
 
 class _Readback:
@@ -333,7 +366,8 @@ class _FastEngine:
             t.start_t = g.start_t[r0:r1]
             t.len_t, t.step_idx = g.len_t[i:i + 1], g.step_idx[i:i + 1]
             t.out_buf = torch.zeros((MAX_STEPS, r1 - r0), dtype=torch.int32, device=dev)
-            t.ws = self._make_ws(r1 - r0, bucket)[:9] + (g.err,)
+            ws = self._make_ws(r1 - r0, bucket)
+            t.ws = ws[:9] + (g.err, ws[10])   # the graph's shared error word; the splits' exchange words kept
             g.tiles.append(t)
         g.out_buf = g.tiles[0].out_buf if nt == 1 else None
         g.ws = g.tiles[0].ws if nt == 1 else None
@@ -462,38 +496,21 @@ class _FastEngine:
         g.step_idx.add_(1)
 
     def _capture_spec(self, b: int, bucket: int) -> _SpecGraph:
-        """engine.py:386-438: the device state, one eager step from a
-        mid-bucket state, then the capture."""
-        dev = self.device
-        q = _spec_q(b)
-        g = _SpecGraph()
-        g.batch, g.bucket, g.q = b, bucket, q
-        g.hist = torch.zeros((b, bucket), dtype=torch.int64, device=dev)
-        g.hist_len = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.len_b = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.pos_b = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.remaining = torch.zeros(b, dtype=torch.int64, device=dev)
-        g.start_t = torch.zeros(b, dtype=torch.int32, device=dev)
-        g.out_tok = torch.zeros((MAX_STEPS, b, q), dtype=torch.int32, device=dev)
-        g.out_adv = torch.zeros((MAX_STEPS, b), dtype=torch.int32, device=dev)
-        g.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
-        g.tokens = torch.zeros((b, q), dtype=torch.int64, device=dev)
+        """The speculative step's graph: one eager step first (it builds the
+        layer tables and verify buffers that a capture cannot), from the
+        state of a request with one history token and an empty cache (each
+        row then verifies Q new keys at slots 0..Q-1, which a request's
+        prefill and steps overwrite before they are attended), then the
+        capture of the same body; replays read the state begin() sets."""
+        g = _SpecGraph(b, bucket, _spec_q(b), self.device)
         kv = self.store.layer_views(0, b)
-        self.model.buffers(b * q)
-        mid = max(4, bucket // 2)
-        for phase in ("warm", "capture"):
-            g.hist_len.fill_(mid)
-            g.len_b.fill_(mid - 1)
-            g.pos_b.fill_(mid - 1)
-            g.remaining.fill_(1 << 30)
-            g.step_idx.zero_()
-            torch.cuda.synchronize()
-            if phase == "warm":
-                self._spec_body(g, kv)
-                continue
-            g.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g.graph, pool=self.pool):
-                self._spec_body(g, kv)
+        self.model.buffers(b * g.q)
+        g.begin([1] * b, [0] * b, [0] * b, [g.q] * b, [0] * b)
+        self._spec_body(g, kv)
+        torch.cuda.synchronize()
+        g.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g.graph, pool=self.pool):
+            self._spec_body(g, kv)
         torch.cuda.synchronize()
         return g
 
@@ -524,15 +541,9 @@ class _FastEngine:
             yield from self._generate_graph(ids, pos, pad, s, bias, n)
             return
         first = self._first_token(ids, pos, b, s, bias)
-        pad_t = torch.as_tensor(pad, dtype=torch.int64)
         g.hist[:, :s].copy_(ids)
         g.hist[:, s].copy_(first)
-        g.hist_len.fill_(s + 1)
-        g.len_b.fill_(s)
-        g.pos_b.copy_(s - pad_t, non_blocking=True)
-        g.start_t.copy_(pad_t.to(torch.int32), non_blocking=True)
-        g.remaining.fill_(n - 1)
-        g.step_idx.zero_()
+        g.begin([s + 1] * b, [s] * b, [s - p for p in pad], [n - 1] * b, pad)
         yield first.to(torch.int32).cpu().tolist()
 
         if self.spec_rows is None or self.spec_rows[0].shape[1] < b * q + b:

@@ -4,9 +4,14 @@
  * (in elements), scalars by value, and the hipStream_t to launch on (as a
  * void*). It launches asynchronously and returns a hipError_t as int: 0 on
  * success; on a rejected argument, hipErrorInvalidValue (1) and a message
- * readable through ek_last_error(). No entry point allocates, synchronizes
- * or clears the HIP error state, so every one of them may be recorded into
- * a HIP graph. Device scalars that a graph replay must re-read (sequence
+ * readable through ek_last_error(). No entry point allocates or
+ * synchronizes, so every one of them may be recorded into a HIP graph. A
+ * launch's status is read with hipGetLastError() after the launch: that
+ * reports (and consumes) a failed launch, and also an error an earlier HIP
+ * call on the calling thread left pending, which is then returned by this
+ * entry point instead of by the caller's own next check. A failed attribute
+ * or occupancy query inside an entry point is consumed the same way, so
+ * that it is not reported by a later launch. Device scalars that a graph replay must re-read (sequence
  * length, start offsets, tokens, positions, step index) are passed as
  * pointers. bf16 tensors are raw 16-bit patterns; rows handed to 16-byte
  * loads must be 16-byte aligned with lengths that are multiples of 8.
@@ -225,8 +230,9 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
  * beside the projections; otherwise every workgroup attends 1 / split of one
  * kv head's keys), the bytes of the launch-state block and the grid (one workgroup per
  * CU). It handles batch m = 1..8 (2..8 rows: head_dim 128, every workgroup
- * attending a key split of one (row, kv head)), up to 64 layers, head_dim 32/64/128, n_q / n_kv in
- * {1, 2, 4, 8}, hidden (<= 4096), intermediate and n_q * head_dim multiples
+ * attending a key split of one (row, kv head)), up to 64 layers, head_dim 32/64/128, n_q / n_kv of
+ * 2 or 4 (the Qwen3 dense models up to hidden 4096; other groups take the
+ * per-kernel step), hidden (<= 4096), intermediate and n_q * head_dim multiples
  * of 512, and s_cap up to what one split's score rows fit in LDS (about
  * 100 K keys at n_q / n_kv = 4 on 256 CUs), on a device where one workgroup
  * of the kernel fits on every CU at once (its waits need the whole grid
@@ -275,7 +281,8 @@ int ek_decode_step(const int64_t* layer_ptrs, int64_t n_layers, int64_t hidden, 
 
 /* decode_step_noalloc: decode_step without the caller's arena and barrier
  * block -- the launch uses a static per-device array of this library (the
- * 256-byte launch-state block plus a hand-over arena of at most 16 MiB,
+ * launch-state block, about 4.3 KiB -- sizeof(eks::Bar), 4160 bytes, padded
+ * to 256-byte alignment -- plus a hand-over arena of at most 16 MiB,
  * zero at load and held by each device until the process ends), so a call
  * allocates nothing and needs no workspace from the caller. Shapes whose
  * arena (decode_step_plan sizes[0]) exceeds 16 MiB are rejected with

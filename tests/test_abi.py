@@ -65,9 +65,10 @@ def test_decode_step_plan_rejects_unsupported_shapes_without_a_gpu():
     # 4B shape at batch 9: the persistent step takes 1 to 8 rows
     rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 9, 768, 36, sizes)
     assert rc == 1 and b"batch" in lib.ek_last_error()
-    # 32 query heads per kv head: not a supported group
-    rc = lib.ek_decode_step_plan(2560, 9728, 32, 1, 128, 151936, 1, 768, 36, sizes)
-    assert rc == 1 and b"query heads" in lib.ek_last_error()
+    # 32, 8 and 1 query heads per kv head: the persistent step takes groups of 2 and 4
+    for n_q, n_kv in ((32, 1), (64, 8), (8, 8)):
+        rc = lib.ek_decode_step_plan(2560, 9728, n_q, n_kv, 128, 151936, 1, 768, 36, sizes)
+        assert rc == 1 and b"query heads" in lib.ek_last_error(), (n_q, n_kv)
     # 65 layers: the layer table held in LDS has 64 rows
     rc = lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 768, 65, sizes)
     assert rc == 1 and b"64 layers" in lib.ek_last_error()

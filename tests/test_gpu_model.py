@@ -282,6 +282,27 @@ def test_engine_4b_shapes_tokens(dev):
     assert agree >= 14, agree
 
 
+def test_per_kernel_graph_keeps_the_exchange_words(dev):
+    """The per-kernel graph's attention gets the workspace's exchange words
+    (ws[10], G (D + 2) words per split): with a bucket past the fused
+    kernel's, its split rows run the one-launch split form, which writes
+    them. (The reference-style `acc` holds 16 D / 2 words per split, too few
+    at G = 8, or D = 64 with G >= 4, where the attention would drop to the
+    two-launch pair.)"""
+    cfg = dict(MID_4B)
+    model = Qwen3(None, dev, tensors=C.random_weights(cfg, seed=0), config=cfg)
+    model.persistent = False
+    eng = Engine(model=model)
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, 151936, (1200,), generator=g).tolist()
+    assert len(list(eng.generate([prompt], 3))) == 3
+    graphs = [gr for key, gr in eng.graphs.items() if key[0] == 1]
+    assert len(graphs) == 1
+    ws = graphs[0].tiles[0].ws
+    assert len(ws) == 11 and ws[4] > 1, (len(ws), ws[4])
+    assert bool(ws[10].ne(0).any())
+
+
 def test_decode_parity_full_depth_against_the_noise_floor(dev):
     """The full 36-layer Qwen3-4B shape, 12 teacher-forced steps. Through 36
     random-init layers an fp32 summation-order change alone moves the
