@@ -883,21 +883,24 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 //   scores   QK-norm + RoPE of the G query heads (and of the new key, which
 //            stands in for the cache row at the new slot), S^T = K_tile . Q^T
 //            per 16-key tile on the matrix cores, scaled, into an LDS row per
-//            head; the split's max m_s and sum l_s = sum exp(s - m_s) per head
-//   stats    every split's (m_s, l_s) of the head travel as tagged words
-//            (tag: the layer + 1, since every layer of the launch reuses
-//            the region: a layer's words are overwritten only by a workgroup
-//            past that layer's o projection wait, which needs every unit's
-//            combine, hence every read of them, done), so
-//            that every unit forms the same M = max m_s and
-//            L = sum_s l_s exp(m_s - M) (in split order)
-//   PV       p = bf16(exp(s - M) / L), the reference fallback's rounding point
-//            (engine/ek_model.py:475-488), and the split's partial output
-//            sum p v over its keys for all head dims, in fp32
+//            head; the split's max m_s, e = exp(s - m_s) (fp32) in place and
+//            l_s = sum e per head
+//   PV       the split's unnormalised partial output sum e v over its keys,
+//            every head dim, in fp32 -- the reference's split decode kernel
+//            (engine/ek_kernels.py:535-616, the hot path of ek_model.py:401),
+//            whose p stays fp32; only its torch fallback rounds p to bf16
+//            after the global normalisation, which would cost a round of
+//            statistics between the splits before any PV work
+//   publish  (m_s, l_s) per head and the partial output travel as tagged
+//            words (tag: the layer + 1, since every layer of the launch
+//            reuses the region: a layer's words are overwritten only by a
+//            workgroup past that layer's o projection wait, which needs every
+//            unit's combine, hence every read of them, done)
 //   combine  unit s owns head dims [s D/S, (s+1) D/S) of the G query heads
-//            (S <= D / 4: whole dense words): it adds the S splits' partials
-//            of those dims in split order and stores them as the bf16
-//            attention words the o projection awaits.
+//            (S <= D / 4: whole dense words): the log-sum-exp merge of the S
+//            splits (ek_kernels.py:989-1019), M = max m_j, out = sum
+//            exp(m_j - M) o_j / sum exp(m_j - M) l_j in split order, stored
+//            as the bf16 attention words the o projection awaits.
 // The split holding the new slot stores the new key and value rows last.
 // long contexts: 16-key score tiles per wave and value rows per thread in flight
 #ifndef EK_STEP_LUT
@@ -1122,7 +1125,9 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   __syncthreads();
   EK_TS(31);
 
-  // ---- the split's (max, sum of exp) per head: thread -> head tid % G
+  // ---- the split's statistics per head (thread -> head tid % G): its max
+  // m_s, e = exp(s - m_s) in place (fp32, unnormalised) and l_s = sum e;
+  // they travel with the split's partial output, so PV starts at once
   llw_t* st_ll = lx;                                          // [nkv][S][2G]
   llw_t* pt_ll = lx + (int64_t)a.nkv * S * 2 * G;             // [nkv][S][G][D]
   {
@@ -1131,7 +1136,11 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
 #pragma unroll
     for (int w = 1; w < SNW; ++w) ms = fmaxf(ms, stm[w][g]);
     float ls = 0.f;
-    for (int n = tid / G; n < nk32; n += SNT / G) ls += expf(sc[g * cstride + n] - ms);
+    for (int n = tid / G; n < nk32; n += SNT / G) {
+      const float ev = expf(sc[g * cstride + n] - ms);
+      sc[g * cstride + n] = ev;
+      ls += ev;
+    }
 #pragma unroll
     for (int o = G; o < EK_WAVE; o <<= 1) ls += __shfl_xor(ls, o, EK_WAVE);
     if (lane < G) stl[wave][lane] = ls;
@@ -1145,33 +1154,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
       ll_put(my + 2 * tid + 1, __float_as_uint(lt), ltag);
     }
   }
-  // every split's statistics of this head -> M = max m_j and
-  // L = sum l_j exp(m_j - M): wave g for head g, lane j polls split j's two
-  // words itself, then two wave reductions in a fixed order; then
-  // p = bf16(exp(s - M) / L) in place
-  {
-    bool ok = true;
-    if (wave < G) {
-      uint32_t mw = __float_as_uint(-INFINITY), lw32 = 0u;
-      if (lane < S) {
-        const llw_t* w = st_ll + ((int64_t)h * S + lane) * 2 * G + 2 * wave;
-        ok = ll_wait1(w, ltag, mw, a.err, a.spin) && ll_wait1(w + 1, ltag, lw32, a.err, a.spin);
-      }
-      const float mj = __uint_as_float(mw), lj = __uint_as_float(lw32);
-      const float M = wave_max(mj);
-      const float Ls = wave_sum_dpp(mj == -INFINITY ? 0.f : lj * expf(mj - M));
-      if (lane == 0) {
-        stm[0][wave] = M;
-        stl[0][wave] = Ls;
-      }
-    }
-    if (!wg_all(ok, s_fail)) return false;
-    EK_TS(29);
-    const int g = tid % G;
-    const float M = stm[0][g], Ls = stl[0][g];
-    for (int n = tid / G; n < nk32; n += SNT / G) sc[g * cstride + n] = rbf(expf(sc[g * cstride + n] - M) / Ls);
-  }
-  __syncthreads();
+  EK_TS(29);
   EK_TS(32);
 
   // ---- PV: the split's partial output sum p v over its keys, every head dim, fp32
@@ -1237,20 +1220,32 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     ll_put(pt_ll + ((int64_t)h * S + s) * G * D + i, __float_as_uint(t), ltag);
   }
   EK_TS(30);
-  // ---- combine this unit's dims [s dpu, (s+1) dpu) of every query head:
-  // thread t -> output o = t / S (head o / dpu, dim o % dpu), split j = t % S
-  // polls that one word; the S lanes of an output (S <= 64, a power of two,
-  // so they sit in one wave) add theirs by a butterfly, in a fixed order
+  // ---- combine this unit's dims [s dpu, (s+1) dpu) of every query head,
+  // the log-sum-exp merge of the splits (engine/ek_kernels.py:989-1019):
+  // thread t -> output o = t / S (head g = o / dpu, dim o % dpu), split j =
+  // t % S polls that split's partial word and its (m_j, l_j) of head g; the
+  // S lanes of an output (S <= 64, a power of two, so they sit in one wave)
+  // form M = max m_j, then sum exp(m_j - M) o_j and exp(m_j - M) l_j by
+  // butterflies in a fixed order (a split without keys has m_j = -inf)
   {
     bool ok = true;
     for (int t = tid; t < G * D; t += SNT) {   // G * dpu * S = G * D
       const int o = t / S, j = t - o * S;
       const int g = o / dpu, dd = o - g * dpu;
-      uint32_t w = 0u;
-      ok = ok && ll_wait1(pt_ll + (((int64_t)h * S + j) * G + g) * D + s * dpu + dd, ltag, w, a.err, a.spin);
-      float v = __uint_as_float(w);
-      for (int m = 1; m < S; m <<= 1) v += __shfl_xor(v, m, EK_WAVE);
-      if (j == 0) cmb[o] = v;
+      const llw_t* sj = st_ll + ((int64_t)h * S + j) * 2 * G + 2 * g;
+      uint32_t w = 0u, mw = 0u, lw32 = 0u;
+      ok = ok && ll_wait1(sj, ltag, mw, a.err, a.spin) && ll_wait1(sj + 1, ltag, lw32, a.err, a.spin) &&
+           ll_wait1(pt_ll + (((int64_t)h * S + j) * G + g) * D + s * dpu + dd, ltag, w, a.err, a.spin);
+      const float mj = __uint_as_float(mw);
+      float M = mj;
+      for (int m = 1; m < S; m <<= 1) M = fmaxf(M, __shfl_xor(M, m, EK_WAVE));
+      const float sj_w = mj == -INFINITY ? 0.f : expf(mj - M);
+      float num = sj_w * __uint_as_float(w), den = sj_w * __uint_as_float(lw32);
+      for (int m = 1; m < S; m <<= 1) {
+        num += __shfl_xor(num, m, EK_WAVE);
+        den += __shfl_xor(den, m, EK_WAVE);
+      }
+      if (j == 0) cmb[o] = num / den;
     }
     if (!wg_all(ok, s_fail)) return false;
     EK_TS(5);
