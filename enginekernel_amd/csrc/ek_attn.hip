@@ -7,9 +7,13 @@
 //
 // The reference's fallback (engine/ek_model.py:475-488) rounds the softmax
 // probabilities to bf16 before the PV product: p = bf16(exp(s - M) / L) with
-// M, L the max and sum over ALL keys of the row. A one-pass flash-decode
-// cannot round there (it only knows M and L at the end), so the split path
-// takes two launches over the same grid:
+// M, L the max and sum over ALL keys of the row; its GPU kernels (the split
+// decode kernel, engine/ek_kernels.py:535-616, 989-1019) keep p in fp32 and
+// merge the splits by log-sum-exp. The single-launch kernel and the
+// two-launch pair round p where the fallback does; the one-launch split form
+// (below) follows the split decode kernel, which saves the round of split
+// statistics that the fallback's rounding point needs before any PV work.
+// The pair takes two launches over the same grid:
 //
 //   scores   [rope_attn_decode's prologue] QK-norm + RoPE of the G query
 //            heads of this kv head (and, in the split owning the new slot,
@@ -525,11 +529,10 @@ __global__ __launch_bounds__(eka::FNT) void attn_fused_kernel(AttnParams p) {
 // ---------------------------------------------------------------------------
 // When every workgroup of the (split, kv head, row) grid can be resident at
 // once, one launch does it all: unit (b, h, s) is eks::long_attention --
-// scores of its keys on the matrix cores into LDS, its (max, sum) per head
-// as tagged words, every split's words merged into the row's M and L (so p
-// keeps the reference's rounding point), its partial sum p v, and the
-// combine of head dims [s D / S, (s + 1) D / S) from every split's partial
-// words, stored as bf16. Split s takes the keys [lo + s c, lo + (s + 1) c)
+// scores of its keys on the matrix cores into LDS, its max m and e = exp(s -
+// m) (fp32) per head, its unnormalised partial sum e v, both published as
+// tagged words with l = sum e, and the log-sum-exp merge of head dims
+// [s D / S, (s + 1) D / S) from every split's words, stored as bf16. Split s takes the keys [lo + s c, lo + (s + 1) c)
 // of the row's range [lo, len), c = ceil((len - lo) / S). The words go to
 // `part` (per row: n_kv S (2G + G D) of them); their tag is one more than
 // the (row, kv head)'s epoch word in the ticket block, which split 0 moves on
