@@ -417,13 +417,13 @@ __device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_r
 }
 
 template <int MB, bool ACC>
-struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= the row's sum for batch row m
+struct PartWriter {   // part[(row * MB + m) * SNW + wave] (+)= the row's sum for batch row m
   float* part;
   int wave;
   __device__ void row(int r, const float* acc) {   // lane 63: acc[m] of batch row m
 #pragma unroll
     for (int m = 0; m < MB; ++m) {
-      float* p = part + (r * SNW + wave) * MB + m;
+      float* p = part + (r * MB + m) * SNW + wave;
       *p = ACC ? *p + acc[m] : acc[m];
     }
   }
@@ -435,7 +435,7 @@ struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= the row's sum fo
     for (int c = 0; c < (MB > 4 ? 2 : 1); ++c) {
       const int m = 4 * c + (lane & 3);
       if (m < MB) {
-        float* p = part + (r * SNW + wave) * MB + m;
+        float* p = part + (r * MB + m) * SNW + wave;
         *p = ACC ? *p + v[c] : v[c];
       }
     }
@@ -443,11 +443,13 @@ struct PartWriter {   // part[(row * SNW + wave) * MB + m] (+)= the row's sum fo
 };
 
 template <int MB>
+// the waves' partials of one (row, batch row), contiguous: two 16-byte LDS
+// reads, added in wave order
 __device__ __forceinline__ float row_sum_b(const float* part, int r, int m) {
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < SNW; ++w) s += part[(r * SNW + w) * MB + m];
-  return s;
+  static_assert(SNW == 8, "two 16-byte reads per row sum");
+  const float4* p = reinterpret_cast<const float4*>(part + (r * MB + m) * SNW);
+  const float4 a = p[0], b = p[1];
+  return ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;
 }
 
 // row m's dense word (u0 + 4i) / 4 at out + m * rw + u0 / 4 + i, rows m < nrows
@@ -497,9 +499,19 @@ __device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* p
 // order). The gain words come from the registers gw (thread t: words
 // t + j SNT) via the LDS row gl.
 __device__ __forceinline__ uint32_t add2_bf(uint32_t r, uint32_t x) { return pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x)); }
-__device__ __forceinline__ float sq2(uint32_t r, float ss) { return fmaf(hi_bf(r), hi_bf(r), fmaf(lo_bf(r), lo_bf(r), ss)); }
+// ss + the squares of both halves of a word, on the bf16 dot instruction
+// (the bf16 squares are exact in fp32; one instruction instead of two
+// unpacks and two FMAs)
+__device__ __forceinline__ float sq2(uint32_t r, float ss) {
+  const ek_bf16x2 v = __builtin_bit_cast(ek_bf16x2, r);
+  return __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+}
+// bf16(g * bf16(r * rstd)) for both halves of a word: each rounding converts
+// the two values in one instruction (rounding an already rounded value is
+// exact, so the result is that of rounding each value on its own)
 __device__ __forceinline__ uint32_t norm2(uint32_t r, uint32_t g, float rstd) {
-  return pack2(rbf(lo_bf(g) * rbf(lo_bf(r) * rstd)), rbf(hi_bf(g) * rbf(hi_bf(r) * rstd)));
+  const uint32_t t = pack2(lo_bf(r) * rstd, hi_bf(r) * rstd);
+  return pack2(lo_bf(g) * lo_bf(t), hi_bf(g) * hi_bf(t));
 }
 
 template <int MB>

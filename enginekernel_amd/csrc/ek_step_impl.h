@@ -646,10 +646,10 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
 
 // sum of the waves' partials of row_local r, fixed order
 __device__ __forceinline__ float row_sum(const float* part, int r) {
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < SNW; ++w) s += part[r * SNW + w];
-  return s;
+  static_assert(SNW == 8, "two 16-byte reads per row sum");
+  const float4* p = reinterpret_cast<const float4*>(part + r * SNW);
+  const float4 a = p[0], b = p[1];
+  return ((((((a.x + a.y) + a.z) + a.w) + b.x) + b.y) + b.z) + b.w;   // in wave order
 }
 
 // out word (u0 + 4i) / 4 = bf16 rows u0 + 4i .. u0 + 4i + 3 of this
@@ -764,8 +764,9 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
     float r0 = rr[2 * ic], r1 = rr[2 * ic + 1];
     if (xw) {
       const uint32_t x = xw[ic];
-      r0 = rbf(r0 + lo_bf(x));
-      r1 = rbf(r1 + hi_bf(x));
+      const uint32_t t = pack2(r0 + lo_bf(x), r1 + hi_bf(x));   // both bf16 adds' roundings at once
+      r0 = lo_bf(t);
+      r1 = hi_bf(t);
     }
     r0v[j] = r0;
     r1v[j] = r1;
@@ -792,9 +793,10 @@ __device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const ui
 #pragma unroll
   for (int j = 0; j < NGW; ++j) {
     const int i = tid + j * SNT;
-    const float o0 = rbf(lo_bf(gw[j]) * rbf(r0v[j] * rstd));
-    const float o1 = rbf(hi_bf(gw[j]) * rbf(r1v[j] * rstd));
-    if (i < nw) xs32[i] = pack2(o0, o1);
+    // bf16(w * bf16(r * rstd)), two values per rounding (rounding a rounded
+    // value is exact: the same result as one value at a time)
+    const uint32_t t = pack2(r0v[j] * rstd, r1v[j] * rstd);
+    if (i < nw) xs32[i] = pack2(lo_bf(gw[j]) * lo_bf(t), hi_bf(gw[j]) * hi_bf(t));
   }
   zero_pad(xs, k, kpad);
 }
