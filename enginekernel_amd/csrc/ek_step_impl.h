@@ -904,12 +904,16 @@ __device__ __forceinline__ bool attention_phase(const StepArgs& a, const int64_t
 //            exp(m_j - M) o_j / sum exp(m_j - M) l_j in split order, stored
 //            as the bf16 attention words the o projection awaits.
 // The split holding the new slot stores the new key and value rows last.
-// long contexts: 16-key score tiles per wave and value rows per thread in flight
+// long contexts: 16-key score tiles per wave and value rows per thread in
+// flight. Shallow rings: the first tiles load ahead of the heads' wait, whose
+// polls return behind them, and a split of a batch row is often short (1 and
+// 4 measured 3.6 % faster than 2 and 8 on the 8-row batch step, and the same
+// or faster at one row: 4 K / 16 K contexts)
 #ifndef EK_STEP_LUT
-#define EK_STEP_LUT 2
+#define EK_STEP_LUT 1
 #endif
 #ifndef EK_STEP_LVR
-#define EK_STEP_LVR 8
+#define EK_STEP_LVR 4
 #endif
 constexpr int LUT = EK_STEP_LUT;
 constexpr int LVR = EK_STEP_LVR;
