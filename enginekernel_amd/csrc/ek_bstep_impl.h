@@ -34,12 +34,21 @@
 namespace eks {
 
 constexpr int BLLW = 16;      // tagged (argmax) words in flight per thread
-// chunks per wave prefetched ahead of a hand-over wait (config 5, 8 rows:
-// 8 measured 1.7 % faster than 6, 4 or 10-12 no better than 8)
-#ifndef EK_BSTEP_PF
-#define EK_BSTEP_PF 8
+// Weight items in flight per wave (the batch kernel's ring; the batch-1
+// kernel's is NB), and how many of them are prefetched ahead of a hand-over
+// wait. Config 5 (8 rows, the ring / the prefetch): 5 / 5 measured 2.50 ms,
+// 4 / 4 2.51, 6 / 6 2.51, 6 / 4 2.56, 8 / 8 2.54, 8 / 6 2.64; rings of 10 or
+// 12 items, 3.8-4.4 % slower than 8. Fewer bytes in flight per wave leave
+// the hand-over polls, which return behind them, less to wait for.
+#ifndef EK_BSTEP_NB
+#define EK_BSTEP_NB 5
 #endif
+#ifndef EK_BSTEP_PF
+#define EK_BSTEP_PF 5
+#endif
+constexpr int BNB = EK_BSTEP_NB;
 constexpr int BPF = EK_BSTEP_PF;
+using BRing = RingN<BNB>;
 // activation chunks per LDS slice of a row in the down projection: up to 4
 // rows 20 (10240 bf16: a 9728-wide act row in one slice, so the phase has no
 // slice boundary, where the ring drains and the next act words make a round
@@ -108,7 +117,8 @@ __device__ __forceinline__ const bf16_t* bspan_at(const BSpan& s, int r, int c) 
 }
 
 template <int CNT>
-__device__ __forceinline__ void prefetch_rows(const Gp& P, int64_t ldw, bool by_rows, Ring& ring) {
+__device__ __forceinline__ void prefetch_rows(const Gp& P, int64_t ldw, bool by_rows, BRing& ring) {
+  static_assert(CNT <= BNB, "prefetch within the ring");
   const BSpan s = make_bspan(P, ldw, wave_id(), by_rows);
   const int loff = (opaque_tid() & 63) * 8;
   int r = s.i0 / s.C, c = s.i0 - (s.i0 / s.C) * s.C;
@@ -126,21 +136,21 @@ __device__ __forceinline__ void prefetch_rows(const Gp& P, int64_t ldw, bool by_
 // chunks at the same k, read from LDS one item ahead. The ring works as in
 // gemv_phase.
 template <int MB, typename SINK>
-__device__ __forceinline__ void gemv_rows(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+__device__ __forceinline__ void gemv_rows(const Gp& P, int64_t ldw, bool by_rows, BRing& ring, const bf16_t* xs,
                                           int xstride, SINK& sink) {
   const int lane = opaque_tid() & 63, wave = wave_id();
   const BSpan sp = make_bspan(P, ldw, wave, by_rows);
   const int n = sp.n, C = sp.C;
   const int loff = lane * 8;
-  // refill cursor: the item NB places ahead of the one consumed (the last
+  // refill cursor: the item BNB places ahead of the one consumed (the last
   // item again past the end)
   int rf = sp.i0 / C, cf = sp.i0 - (sp.i0 / C) * C;
 #pragma unroll
-  for (int u = 0; u < NB; ++u) {
+  for (int u = 0; u < BNB; ++u) {
     if (u >= ring.nready) ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
     if (u + 1 < n && ++cf == C) { cf = 0; ++rf; }
   }
-  int kf = NB < n ? NB : n - 1;   // item index of the cursor
+  int kf = BNB < n ? BNB : n - 1;   // item index of the cursor
   int r = sp.i0 / C, ch = sp.i0 - (sp.i0 / C) * C;
   uint4 xc[MB];
 #pragma unroll
@@ -165,9 +175,9 @@ __device__ __forceinline__ void gemv_rows(const Gp& P, int64_t ldw, bool by_rows
     for (int m = 0; m < MB; ++m) xc[m] = xn[m];
   };
   int k0 = 0;
-  for (; k0 + NB <= n; k0 += NB) {
+  for (; k0 + BNB <= n; k0 += BNB) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
+    for (int u = 0; u < BNB; ++u) {
       step(ring.r[u]);
       ring.r[u] = ld16_nt(bspan_at(sp, rf, cf) + loff);
       if (kf + 1 < n) {
@@ -179,7 +189,7 @@ __device__ __forceinline__ void gemv_rows(const Gp& P, int64_t ldw, bool by_rows
     }
   }
 #pragma unroll
-  for (int u = 0; u < NB; ++u) {
+  for (int u = 0; u < BNB; ++u) {
     if (k0 + u < n) {
       step(ring.r[u]);
       if (ch == C - 1 || k0 + u == n - 1) flush(r);
@@ -295,7 +305,8 @@ __device__ __forceinline__ const bf16_t* tile_at(const TSpan& s, int t) {
 }
 
 template <int CNT>
-__device__ __forceinline__ void prefetch_tiles(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, int rows_end) {
+__device__ __forceinline__ void prefetch_tiles(const Gp& P, int64_t ldw, bool by_rows, BRing& ring, int rows_end) {
+  static_assert(CNT <= BNB, "prefetch within the ring");
   const TSpan s = make_tspan(P, ldw, wave_id(), by_rows, rows_end);
   int t = s.i0 / s.C4, c = s.i0 - (s.i0 / s.C4) * s.C4;
   const bf16_t* tp = tile_at(s, t);
@@ -313,10 +324,10 @@ __device__ __forceinline__ void prefetch_tiles(const Gp& P, int64_t ldw, bool by
 // l % 4. PartWriter stores (or, for the K slices of one matrix, adds) them
 // as per-wave partials, ArgmaxSink (lm_head, whole tiles per wave) keeps a
 // running argmax. The ring works as in gemv_phase: slot u holds the item
-// NB places ahead, refilled as soon as its words are moved to the MFMA
+// BNB places ahead, refilled as soon as its words are moved to the MFMA
 // layout.
 template <int MB, typename SINK>
-__device__ __forceinline__ void gemv_tiles(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+__device__ __forceinline__ void gemv_tiles(const Gp& P, int64_t ldw, bool by_rows, BRing& ring, const bf16_t* xs,
                                            int xld, SINK& sink, int rows_end) {
   constexpr int CG = MB > 4 ? 2 : 1;   // column groups of 4 batch rows
   const int lane = opaque_tid() & 63;
@@ -324,16 +335,16 @@ __device__ __forceinline__ void gemv_tiles(const Gp& P, int64_t ldw, bool by_row
   const int src = (16 * j4 + blk) * 4;   // ds_bpermute source: row j4's piece blk
   const TSpan sp = make_tspan(P, ldw, wave_id(), by_rows, rows_end);
   const int n = sp.n, C4 = sp.C4;
-  // refill cursor: the item NB places ahead of the one consumed (the last
+  // refill cursor: the item BNB places ahead of the one consumed (the last
   // item again past the end)
   int tf = sp.i0 / C4, cf = sp.i0 - (sp.i0 / C4) * C4;
   const bf16_t* tpf = tile_at(sp, tf);
 #pragma unroll
-  for (int u = 0; u < NB; ++u) {
+  for (int u = 0; u < BNB; ++u) {
     if (u >= ring.nready) ring.r[u] = ld16_nt(tpf + cf * MCH);
     if (u + 1 < n && ++cf == C4) { cf = 0; ++tf; tpf = tile_at(sp, tf); }
   }
-  int kf = NB < n ? NB : n - 1;   // item index of the cursor
+  int kf = BNB < n ? BNB : n - 1;   // item index of the cursor
   int t = sp.i0 / C4, ch = sp.i0 - (sp.i0 / C4) * C4;
   const bf16_t* xr[CG];
 #pragma unroll
@@ -375,9 +386,9 @@ __device__ __forceinline__ void gemv_tiles(const Gp& P, int64_t ldw, bool by_row
     }
   };
   int k0 = 0;
-  for (; k0 + NB <= n; k0 += NB) {
+  for (; k0 + BNB <= n; k0 += BNB) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
+    for (int u = 0; u < BNB; ++u) {
       step(ring.r[u], true);
       if (ch == C4 - 1) flush(t);
       if (++ch == C4) { ch = 0; ++t; }
@@ -387,7 +398,7 @@ __device__ __forceinline__ void gemv_tiles(const Gp& P, int64_t ldw, bool by_row
     }
   }
 #pragma unroll
-  for (int u = 0; u < NB; ++u) {
+  for (int u = 0; u < BNB; ++u) {
     if (k0 + u < n) {
       step(ring.r[u], false);
       if (ch == C4 - 1 || k0 + u == n - 1) flush(t);
@@ -405,14 +416,14 @@ template <int MB>
 constexpr bool bstep_mfma() { return MB >= 4; }
 
 template <int MB, int CNT>
-__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring,
+__device__ __forceinline__ void prefetch_phase_b(const Gp& P, int64_t ldw, bool by_rows, BRing& ring,
                                                  int rows_end = 0x7fffffff) {
   if constexpr (bstep_mfma<MB>()) prefetch_tiles<CNT>(P, ldw, by_rows, ring, rows_end);
   else prefetch_rows<CNT>(P, ldw, by_rows, ring);
 }
 
 template <int MB, typename SINK>
-__device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_rows, Ring& ring, const bf16_t* xs,
+__device__ __forceinline__ void gemv_phase_b(const Gp& P, int64_t ldw, bool by_rows, BRing& ring, const bf16_t* xs,
                                              int xld, SINK& sink, int rows_end = 0x7fffffff) {
   if constexpr (bstep_mfma<MB>()) gemv_tiles<MB>(P, ldw, by_rows, ring, xs, xld, sink, rows_end);
   else gemv_rows<MB>(P, ldw, by_rows, ring, xs, xld, sink);
@@ -711,10 +722,10 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
   const int uS = __builtin_amdgcn_readfirstlane(s_unit[2]), upre = __builtin_amdgcn_readfirstlane(s_unit[3]);
   const bool attends = ub < nrows;
 
-  Ring ring;
+  BRing ring;
   ring.nready = 0;
 #pragma unroll
-  for (int u = 0; u < NB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
+  for (int u = 0; u < BNB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
   uint32_t gw1[NGW], gw2[NGW];
   load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
 

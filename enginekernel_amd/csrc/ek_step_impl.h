@@ -58,7 +58,10 @@ namespace eks {
 
 constexpr int SNT = eka::FNT;          // 512 threads
 constexpr int SNW = SNT / EK_WAVE;     // 8 waves
-constexpr int NB = 8;                  // weight chunks in flight per wave
+#ifndef EK_STEP_NB
+#define EK_STEP_NB 8
+#endif
+constexpr int NB = EK_STEP_NB;          // weight chunks in flight per wave
 #ifndef EK_STEP_PF
 #define EK_STEP_PF 4
 #endif
@@ -456,10 +459,12 @@ __device__ __forceinline__ const bf16_t* span_item(const Span& s, int i) {
 
 // The wave's ring: slots [0, nready) hold items 0 .. nready-1 of the coming
 // phase (loaded ahead by prefetch_phase).
-struct Ring {
-  uint4 r[NB];
+template <int N>
+struct RingN {
+  uint4 r[N];
   int nready;
 };
+using Ring = RingN<NB>;
 
 // The first `cnt` items of phase `pn` into this wave's ring, issued ahead of
 // a wait so that they load while the workgroup waits for its inputs. Loads
@@ -467,6 +472,7 @@ struct Ring {
 // own polls queue behind: ahead of a short hand-over only a few are worth it.
 template <int CNT>
 __device__ __forceinline__ void prefetch_phase(const Gp& pn, Ring& ring) {
+  static_assert(CNT <= NB, "prefetch within the ring");
   const Span sn = make_span(pn, wave_id());
   const int loff = (threadIdx.x & 63) * 8;
 #pragma unroll
