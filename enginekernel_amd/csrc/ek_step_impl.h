@@ -58,21 +58,29 @@ namespace eks {
 
 constexpr int SNT = eka::FNT;          // 512 threads
 constexpr int SNW = SNT / EK_WAVE;     // 8 waves
+// Weight chunks in flight per wave (the ring of a projection phase) and how
+// many of them are prefetched ahead of a hand-over wait, per form of the
+// step: loads return in order, so every chunk in flight when a wait begins is
+// one its polls return behind. Short contexts: a ring of 6 with 3 prefetched
+// measured 0.4 % faster than 8 with 4 (rings of 4, 5 or 7, or 2-4 ahead, no
+// better); before the dense hand-over words 6 ahead had been the best.
+// The split-attention form: 8 with 8 ahead (0.6 % faster than 6 ahead at
+// 4 K and 16 K contexts; a ring of 6 there 0.4 % slower).
 #ifndef EK_STEP_NB
-#define EK_STEP_NB 8
+#define EK_STEP_NB 6
 #endif
-constexpr int NB = EK_STEP_NB;          // weight chunks in flight per wave
 #ifndef EK_STEP_PF
-#define EK_STEP_PF 4
+#define EK_STEP_PF 3
 #endif
-// chunks per wave prefetched ahead of a hand-over wait: 4 (0.6 % faster than
-// 3, 6 or 8 with the dense hand-over words; with {bf16 pair, tag} words, whose
-// polls queued behind twice the loads, 6 was the best)
-constexpr int PF = EK_STEP_PF;
-// the same ahead of the split-attention form's waits
+#ifndef EK_STEP_NB_LONG
+#define EK_STEP_NB_LONG 8
+#endif
 #ifndef EK_STEP_PF_LONG
-#define EK_STEP_PF_LONG 6
+#define EK_STEP_PF_LONG 8
 #endif
+constexpr int NB = EK_STEP_NB;
+constexpr int PF = EK_STEP_PF;
+constexpr int NB_LONG = EK_STEP_NB_LONG;
 constexpr int PF_LONG = EK_STEP_PF_LONG;
 constexpr int OB = 12;                 // o_proj chunks per wave held in registers through attention
 constexpr int CH = 8 * EK_WAVE;        // bf16 elements per chunk (1 KiB)
@@ -464,15 +472,14 @@ struct RingN {
   uint4 r[N];
   int nready;
 };
-using Ring = RingN<NB>;
 
 // The first `cnt` items of phase `pn` into this wave's ring, issued ahead of
 // a wait so that they load while the workgroup waits for its inputs. Loads
 // retire in order, so every item prefetched here is also a load the wait's
 // own polls queue behind: ahead of a short hand-over only a few are worth it.
-template <int CNT>
-__device__ __forceinline__ void prefetch_phase(const Gp& pn, Ring& ring) {
-  static_assert(CNT <= NB, "prefetch within the ring");
+template <int CNT, int R>
+__device__ __forceinline__ void prefetch_phase(const Gp& pn, RingN<R>& ring) {
+  static_assert(CNT <= R, "prefetch within the ring");
   const Span sn = make_span(pn, wave_id());
   const int loff = (threadIdx.x & 63) * 8;
 #pragma unroll
@@ -590,19 +597,20 @@ __device__ __forceinline__ void l2_touch(const Gp& pn, uint32_t& sink) {
 
 // One projection phase: partial dot products of this wave's items into
 // part[row_local * SNW + wave]. The ring is consumed in order and each slot
-// is refilled, right after its chunk is consumed, with the item NB places
-// ahead, so NB chunks stay in flight and a refill never waits for anything
-// but its own slot's previous load. The ring holds items 0 .. NB-1 on entry
+// is refilled, right after its chunk is consumed, with the item R places
+// ahead, so R chunks stay in flight and a refill never waits for anything
+// but its own slot's previous load. The ring holds items 0 .. R-1 on entry
 // when prefetch_phase loaded them. Refills past the wave's last item (every
-// slot is refilled, so that the loads stay countable at compile time and NB
+// slot is refilled, so that the loads stay countable at compile time and R
 // stay in flight) re-read that last item, which the L2 has just fetched.
-__device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t* xs, float* part) {
+template <int R>
+__device__ __forceinline__ void gemv_phase(const Gp& P, RingN<R>& ring, const bf16_t* xs, float* part) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const Span sp = make_span(P, wave);
   const int n = sp.n;
   const int loff = lane * 8;
 #pragma unroll
-  for (int u = 0; u < NB; ++u)
+  for (int u = 0; u < R; ++u)
     if (u >= ring.nready) ring.r[u] = ld16_nt(span_item(sp, sp.i0 + (u < n ? u : 0)) + loff);
   int r = sp.i0 / P.C, ch = sp.i0 - (sp.i0 / P.C) * P.C;   // consume position (row-local, chunk)
   // the activation chunk of the current item; the next item's chunk is read
@@ -611,13 +619,13 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
   uint4 xc = *reinterpret_cast<const uint4*>(xs + ch * CH + loff);
   float acc = 0.f;
   int k0 = 0;
-  for (; k0 + NB <= n; k0 += NB) {
+  for (; k0 + R <= n; k0 += R) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
+    for (int u = 0; u < R; ++u) {
       const int chn = ch + 1 == P.C ? 0 : ch + 1;
       const uint4 xn = *reinterpret_cast<const uint4*>(xs + chn * CH + loff);
       acc = step_dot8(ring.r[u], xc, acc);
-      const int kn = k0 + u + NB;
+      const int kn = k0 + u + R;
       ring.r[u] = ld16_nt(span_item(sp, sp.i0 + (kn < n ? kn : n - 1)) + loff);
       if (ch == P.C - 1) {
         const float sum = wave_sum_dpp(acc);
@@ -629,7 +637,7 @@ __device__ __forceinline__ void gemv_phase(const Gp& P, Ring& ring, const bf16_t
     }
   }
 #pragma unroll
-  for (int u = 0; u < NB; ++u) {
+  for (int u = 0; u < R; ++u) {
     if (k0 + u < n) {
       const int chn = ch + 1 == P.C ? 0 : ch + 1;
       const uint4 xn = *reinterpret_cast<const uint4*>(xs + chn * CH + loff);
@@ -1347,10 +1355,10 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)a.kpad_max * 2));
   const int part_n = a.part_max * SNW;
 
-  Ring ring;
+  RingN<LONG ? NB_LONG : NB> ring;
   ring.nready = 0;
 #pragma unroll
-  for (int u = 0; u < NB; ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
+  for (int u = 0; u < (LONG ? NB_LONG : NB); ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
   // norm gains, loaded a phase ahead of their use: gw1 = input norm of the
   // coming layer (the final norm after the last), gw2 = post-attention norm
   uint32_t gw1[NGW], gw2[NGW];
