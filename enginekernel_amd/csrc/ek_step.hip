@@ -43,13 +43,14 @@ constexpr size_t kLdsLimit = eks::kStepDynLds;        // dynamic LDS per workgro
 // Rows of at most kUnitMaxKeys keys whose scores fit kFusedScoreLds bytes
 // run on the attention units beside the projections; longer ones on the
 // split kernel. At the Qwen3-4B shape the split kernel is the faster one
-// from a 1280-key bucket on (ms per step, split vs units: 1.939 vs 1.971 at
-// a 1280-key bucket, 1.942 vs 2.121 at 1536; 1.941 vs 1.868 at 1024, 1.930 vs
-// 1.673 at 768): the 32 attention units then stream more keys than the
-// projections take to run, while the split kernel's attention is on the
-// critical path of every workgroup (it has a floor of ~1.93 ms).
+// from a 1024-key bucket on (ms per step at contexts ~940, split vs units:
+// 1.824 vs 1.854; at ~640, a 768-key bucket, 1.818 vs 1.702; the split
+// kernel stays at ~1.825 from 1024 to 2048 keys, the units reach 1.953 at
+// 1280 and 2.104 at 1536): the 32 attention units then stream more keys than
+// the projections take to run, while the split kernel's attention is on the
+// critical path of every workgroup.
 #ifndef EK_STEP_UNIT_MAX_KEYS
-#define EK_STEP_UNIT_MAX_KEYS 1024
+#define EK_STEP_UNIT_MAX_KEYS 768
 #endif
 constexpr int64_t kFusedScoreLds = 32 * 1024;
 constexpr int64_t kUnitMaxKeys = EK_STEP_UNIT_MAX_KEYS;

@@ -150,14 +150,14 @@ def test_config4_free_running_first_divergence(dev, model4):
         assert _argmax_ok(got[first_diff], int(ids[first_diff]), top_ids[first_diff], top_logits[first_diff])
 
 
-@pytest.mark.parametrize("prompt_len,steps", [(700, 16), (900, 12), (960, 55)])
+@pytest.mark.parametrize("prompt_len,steps", [(500, 16), (700, 40), (740, 27)])
 def test_persistent_step_long_contexts(dev, prompt_len, steps):
-    """Contexts 701..1023 (the attention units' last bucket is 1024 keys) at
-    every Qwen3-4B shape with two layers: the attention workgroups hold 768
-    keys in registers and stream the rest in tiles. Both sides start from the
-    oracle's prefill cache and are fed the oracle's ids; every step's full
-    logits are within 2e-2 of their scale, the argmax is the oracle's up to
-    a near-tie, and the new cache rows match."""
+    """Contexts 501..767 (the attention units' last bucket is 768 keys, all of
+    which the attention workgroups hold in registers) at every Qwen3-4B shape
+    with two layers. Both sides start from the oracle's prefill cache and are
+    fed the oracle's ids; every step's full logits are within 2e-2 of their
+    scale, the argmax is the oracle's up to a near-tie, and the new cache rows
+    match."""
     cfg = dict(MID_4B)
     tensors = C.random_weights(cfg, seed=0)
     om = O.OracleQwen3(O.OracleConfig(cfg), tensors)
@@ -166,15 +166,15 @@ def test_persistent_step_long_contexts(dev, prompt_len, steps):
     prompt = torch.randint(0, cfg["vocab_size"], (prompt_len,), generator=g).tolist()
     ids, pos, pad, s, bias = O.pack([prompt])
     total = s + steps + 1
-    assert total <= 1024
-    ost = O.EagerState(om, 1, s, pad, 1024)
+    assert total <= 768
+    ost = O.EagerState(om, 1, s, pad, 768)
     with torch.inference_mode():
         tok = O.argmax_token(om.prefill(ids, pos, ost.k, ost.v, bias), om.lm_head)
         kd = [t.to(dev) for t in ost.k]
         vd = [t.to(dev) for t in ost.v]
         st = _state(dev, s)
-        ws = K.make_workspace(1, 32, 8, 128, 1024, dev)
-        plan = model.persistent_plan(1, 1024)
+        ws = K.make_workspace(1, 32, 8, 128, 768, dev)
+        plan = model.persistent_plan(1, 768)
         assert plan is not None and plan[1] == 0
         tokens = tok.to(dev)
         logits = torch.empty(1, cfg["vocab_size"], dtype=BF, device=dev)
@@ -215,7 +215,8 @@ def split_model(dev):
 
 
 @pytest.mark.parametrize("bucket,s,start,steps", [
-    (1280, 1100, 0, 3),       # the first split bucket
+    (1024, 900, 0, 3),        # the first split bucket
+    (1280, 1100, 0, 3),
     (1792, 1700, 0, 3),
     (4096, 4000, 0, 4),       # contexts 4001..4004
     (4096, 2600, 300, 3),     # left padding: keys [300, s) attended
@@ -224,7 +225,7 @@ def split_model(dev):
     (16384, 16380, 0, 3),     # up to the bucket's last slot
 ])
 def test_persistent_step_split_contexts(dev, split_model, bucket, s, start, steps):
-    """Buckets past 1024 keys: the persistent step splits each kv head's keys
+    """Buckets past 768 keys: the persistent step splits each kv head's keys
     over every workgroup (the plan reports the split) and combines the
     splits through the arena, at every Qwen3-4B shape with two layers. Both
     sides start from the same random cache rows [0, s) (rows before `start`
@@ -279,15 +280,15 @@ def test_persistent_step_split_contexts(dev, split_model, bucket, s, start, step
 
 
 def test_persistent_plan_split_bounds(dev):
-    """The split plan at the Qwen3-4B shape: none up to 1024 keys (attention
+    """The split plan at the Qwen3-4B shape: none up to 768 keys (attention
     units beside the projections), 32 splits of a kv head beyond, and a
     clear rejection once one split's score rows exceed the LDS."""
     lib = _hip.load()
     sizes = (ctypes.c_int64 * 4)()
-    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1024, 36, sizes) == 0
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 768, 36, sizes) == 0
     short_arena = sizes[0]
     assert sizes[1] == 0
-    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1025, 36, sizes) == 0
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 769, 36, sizes) == 0
     assert sizes[1] == 32 and sizes[3] == 256
     # the split exchange: (max, sum) per query head and a partial output per
     # split, 8-byte words, in each of the arena's two halves
