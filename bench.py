@@ -50,10 +50,10 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 GATE_UP_TRAFFIC_B1 = 100_153_865
 GATE_UP_TRAFFIC_AT = "1ea3e7e"
 #   the persistent step kernel (step_kernel<128, 4, false>) at batch 1, context 137..146:
-#   3,961,921 KiB / 0.500063 fetched + 4,418 KiB written per launch, 1.0064x its
+#   3,963,795 KiB / 0.500067 fetched + 4,418 KiB written per launch, 1.0069x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_117_509_801
-STEP_TRAFFIC_AT = "d60dc49"
+STEP_TRAFFIC_B1 = 8_121_288_425
+STEP_TRAFFIC_AT = "0fb5a94"
 
 
 def log(msg: str) -> None:
