@@ -344,6 +344,11 @@ __device__ __forceinline__ bool dw_finish(const llw_t* base, SRC src, int n, u32
       return false;
     }
     if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    // the buffer-load builtin reads as ordinary memory: without this
+    // compiler barrier a re-poll may be merged with the earlier load of the
+    // same word (the loop's only other memory operation, the error word's
+    // load, runs once in 64 rounds)
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < W; ++k) {
       const int j = tid + k * SNT;
