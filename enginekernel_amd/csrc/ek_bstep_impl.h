@@ -46,6 +46,10 @@ constexpr int BLLW = 16;      // tagged (argmax) words in flight per thread
 #ifndef EK_BSTEP_PF
 #define EK_BSTEP_PF 5
 #endif
+// units of a projection's share come in pairs of rows: 2560 rows over 256
+// workgroups are then 10 rows each, where 4-row units gave 8 or 12 (the
+// phase ends with the 12-row shares: 0.7-1.1 us later than the 8-row ones)
+constexpr int BGRAN = 2;
 constexpr int BNB = EK_BSTEP_NB;
 constexpr int BPF = EK_BSTEP_PF;
 using BRing = RingN<BNB>;
@@ -272,26 +276,32 @@ __device__ __forceinline__ TSpan make_tspan(const Gp& P, int64_t ldw, int wave, 
   unit_range(P, u0, u1);
   u0 = uni(u0);
   u1 = uni(u1);
-  const int nu = u1 - u0;   // a multiple of MT (the phases' unit granularity)
+  // the share's rows: a multiple of the phase's granularity (2 rows, or MT
+  // for the lm_head); a last tile past them re-reads the share's last row
+  // (an L2 hit) and its sums are dropped
+  const int nu = u1 - u0;
+  const int nt = cdiv_i(nu, MT);   // tiles of a half
   TSpan s;
   const int lpc = opaque_tid() & 15;
   s.g = P.w + (int64_t)u0 * ldw + lpc * 8;
   s.up = P.pair ? P.w + (int64_t)(P.up_off + u0) * ldw + lpc * 8 : s.g;
-  s.tg = uni(P.pair ? nu / MT : 0x7fffffff);
+  s.tg = uni(P.pair ? nt : 0x7fffffff);
   s.C4 = uni(P.K / MCH);
   const int re = (rows_end < u1 ? rows_end : u1) - u0 - 1;
   s.rmax = uni(re > 0 ? re : 0);   // a share without rows re-reads its first row
   s.ldw = ldw;
   if (by_rows) {
-    const int nt = nu / MT;
     const int t0 = (int)((uint32_t)nt * (uint32_t)wave / (uint32_t)SNW);
     const int t1 = (int)((uint32_t)nt * (uint32_t)(wave + 1) / (uint32_t)SNW);
     s.i0 = uni(t0 * s.C4);
     s.n = uni((t1 - t0) * s.C4);
   } else {
-    const WaveItems w = wave_items(P, nu, wave);
-    s.i0 = uni(w.i0);
-    s.n = uni(w.n);
+    // the (tile, chunk) items of both halves, split evenly over the waves
+    const uint32_t ni = (uint32_t)((P.pair ? 2 : 1) * nt * s.C4);
+    const int i0 = (int)(ni * (uint32_t)wave / (uint32_t)SNW);
+    const int i1 = (int)(ni * (uint32_t)(wave + 1) / (uint32_t)SNW);
+    s.i0 = uni(i0);
+    s.n = uni(i1 - i0);
   }
   return s;
 }
@@ -467,14 +477,18 @@ __device__ __forceinline__ float row_sum_b(const float* part, int r, int m) {
 
 // row m's dense word (u0 + 4i) / 4 at out + m * rw + u0 / 4 + i, rows m < nrows
 template <int MB>
+// The share's rows [u0, u1) come in pairs (the phases' granularity is 2
+// rows): pair q of batch row m is the half-word of values u0 + 2 q, +1 of
+// that row's words, stored on its own (a word's other half may be another
+// workgroup's).
 __device__ __forceinline__ void epilogue_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw, int nrows) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nq = (u1 - u0) / 4;
-  for (int i = threadIdx.x; i < nq * nrows; i += SNT) {
-    const int m = i / nq, q = i - m * nq;
-    dw_put(out + m * rw + u0 / 4 + q, pack2(row_sum_b<MB>(part, 4 * q, m), row_sum_b<MB>(part, 4 * q + 1, m)),
-           pack2(row_sum_b<MB>(part, 4 * q + 2, m), row_sum_b<MB>(part, 4 * q + 3, m)));
+  const int np = (u1 - u0) / 2;
+  for (int i = threadIdx.x; i < np * nrows; i += SNT) {
+    const int m = i / np, q = i - m * np;
+    dw_put1(reinterpret_cast<uint32_t*>(out + m * rw) + u0 / 2 + q,
+            pack2(row_sum_b<MB>(part, 2 * q, m), row_sum_b<MB>(part, 2 * q + 1, m)));
   }
 }
 
@@ -486,17 +500,19 @@ __device__ __forceinline__ float swiglu_one_b(const float* part, int nu, int ul,
   return s * up;
 }
 
+// The up rows' partials start at row `nu` of the share on the dot path
+// and at its gate tiles' rows (nu rounded up to MT) on the tiles.
 template <int MB>
 __device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* part, llw_t* out, int64_t rw,
                                                      int nrows) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0, nq = nu / 4;
-  for (int i = threadIdx.x; i < nq * nrows; i += SNT) {
-    const int m = i / nq, q = i - m * nq;
-    dw_put(out + m * rw + u0 / 4 + q,
-           pack2(swiglu_one_b<MB>(part, nu, 4 * q, m), swiglu_one_b<MB>(part, nu, 4 * q + 1, m)),
-           pack2(swiglu_one_b<MB>(part, nu, 4 * q + 2, m), swiglu_one_b<MB>(part, nu, 4 * q + 3, m)));
+  const int nu = u1 - u0, np = nu / 2;
+  const int upo = bstep_mfma<MB>() ? MT * cdiv_i(nu, MT) : nu;
+  for (int i = threadIdx.x; i < np * nrows; i += SNT) {
+    const int m = i / np, q = i - m * np;
+    dw_put1(reinterpret_cast<uint32_t*>(out + m * rw) + u0 / 2 + q,
+            pack2(swiglu_one_b<MB>(part, upo, 2 * q, m), swiglu_one_b<MB>(part, upo, 2 * q + 1, m)));
   }
 }
 
@@ -625,10 +641,15 @@ __host__ __device__ inline int bstep_xcols(int h, int qw, int mb) {
 #endif
 __host__ __device__ inline int bstep_xld(int h, int qw, int mb) { return bstep_xcols(h, qw, mb) + EK_BSTEP_XPAD; }
 // part rows of the largest projection share (lm_head keeps no partials)
+// partial rows of a workgroup: its share of a phase's units (BGRAN rows per
+// unit) rounded up to whole tiles, twice for the gate/up pair
+__host__ __device__ inline int bstep_share_rows(int units, int nwg) {
+  return 4 * cdiv_i(BGRAN * cdiv_i(units / BGRAN, nwg), 4);
+}
 __host__ __device__ inline int bstep_part_rows(int h, int inter, int qkvw, int nwg) {
-  int r = 4 * cdiv_i(qkvw / 4, nwg);
-  r = r > 4 * cdiv_i(h / 4, nwg) ? r : 4 * cdiv_i(h / 4, nwg);
-  r = r > 8 * cdiv_i(inter / 4, nwg) ? r : 8 * cdiv_i(inter / 4, nwg);
+  int r = bstep_share_rows(qkvw, nwg);
+  r = r > bstep_share_rows(h, nwg) ? r : bstep_share_rows(h, nwg);
+  r = r > 2 * bstep_share_rows(inter, nwg) ? r : 2 * bstep_share_rows(inter, nwg);
   return r;
 }
 
@@ -745,13 +766,13 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     llw_t* o_ll = att_ll + (int64_t)MB * qw / 4;
     llw_t* act_ll = o_ll + (int64_t)MB * h / 4;
     llw_t* dn_ll = act_ll + (int64_t)MB * inter / 4;
-    const Gp gq = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, 4);
-    const Gp go = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, 4);
-    const Gp gg = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, 4);
+    const Gp gq = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_QKV]), h, qkvw, 0, BGRAN);
+    const Gp go = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_O]), qw, h, 0, BGRAN);
+    const Gp gg = make_gp(reinterpret_cast<const bf16_t*>(lw[LW_GU]), h, inter, 1, BGRAN);
     const bf16_t* wdown = reinterpret_cast<const bf16_t*>(lw[LW_DOWN]);
     auto down_slice = [&](int sl) {
       const int c0 = sl * BSLICE, c1 = (sl + 1) * BSLICE < inter / CH ? (sl + 1) * BSLICE : inter / CH;
-      return make_gp(wdown + c0 * CH, (c1 - c0) * CH, h, 0, 4);
+      return make_gp(wdown + c0 * CH, (c1 - c0) * CH, h, 0, BGRAN);
     };
 
     // ---- r = (layer 0) embed[token] | r + down(l-1); norm; qkv
@@ -873,7 +894,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
         prefetch_phase_b<MB, BPF>(down_slice(sl + 1), inter, false, ring);
       else if (l + 1 < a.nl)
         prefetch_phase_b<MB, BPF>(make_gp(reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_QKV]), h, qkvw,
-                                     0, 4), h, false, ring);
+                                     0, BGRAN), h, false, ring);
       else
         prefetch_phase_b<MB, BPF>(glm, h, true, ring, a.vocab);
     }

@@ -166,13 +166,22 @@ __device__ __forceinline__ uint32_t ld4(const void* p) { return *(global_u32_t*)
 // Dense hand-over words of the persistent step kernels: word i of a region
 // holds its values 4i .. 4i + 3 (value 4i + j in bits 16j .. 16j + 15, so a
 // region is its bf16 row in memory order), sign bits flipped so that no
-// stored word is zero (zero means "not written yet"), stored with one
-// device-scope store.
+// stored 32-bit half is zero (zero means "not written yet"). A word is one
+// device-scope store, or two: a producer that owns only values 2i, 2i + 1 of
+// a region stores that half alone (dw_put1), so readers check each half.
 constexpr unsigned long long DW_FLIP = 0x8000800080008000ull;
 constexpr uint32_t DW_FLIP32 = 0x80008000u;
 
+// a half of (-0.0, -0.0) would read as unwritten: its first value travels as +0.0
+__device__ __forceinline__ uint32_t dw_half(uint32_t v01) {
+  const uint32_t w = v01 ^ DW_FLIP32;
+  return w ? w : 0x8000u;
+}
 __device__ __forceinline__ void dw_put(unsigned long long* p, uint32_t v01, uint32_t v23) {
-  unsigned long long w = (((unsigned long long)v23 << 32) | v01) ^ DW_FLIP;
-  w = w ? w : 0x8000ull;   // four -0.0 would read as unwritten: the first travels as +0.0
+  const unsigned long long w = ((unsigned long long)dw_half(v23) << 32) | dw_half(v01);
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// values 2i, 2i + 1 of a region, at its 32-bit index i
+__device__ __forceinline__ void dw_put1(uint32_t* p, uint32_t v01) {
+  __hip_atomic_store(p, dw_half(v01), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

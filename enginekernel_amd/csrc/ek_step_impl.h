@@ -284,15 +284,21 @@ __device__ __forceinline__ bool ll_wait1(const llw_t* p, uint32_t tag, uint32_t&
 
 // Two words (16 bytes) at byte offset `off` of a region, loaded with device
 // scope: the cache-policy bits of the agent-scope atomic load (sc1) on a
-// buffer load, since a 16-byte load has no atomic form. Each 8-byte half is
-// what one producer store wrote, and is checked on its own.
+// buffer load, since a 16-byte load has no atomic form. Each 32-bit quarter
+// is checked on its own: a word is one producer store, or two half-word
+// stores from two producers.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dw_rsrc(const llw_t* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<llw_t*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 __device__ __forceinline__ u32x4_t dw_get2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
 }
-__device__ __forceinline__ bool dw_ok2(const u32x4_t& v) { return (v.x | v.y) != 0u && (v.z | v.w) != 0u; }
+// (every quarter nonzero, as one unsigned min and one compare per unit: the
+// same test as four compares, which measured 0.6 % / 1.7 % slower at 1 / 8
+// rows; the min form measured faster than the older per-word test)
+__device__ __forceinline__ bool dw_ok2(const u32x4_t& v) {
+  return __builtin_elementwise_min(__builtin_elementwise_min(v.x, v.y), __builtin_elementwise_min(v.z, v.w)) != 0u;
+}
 
 // Wait until the n units j < n (16 bytes at byte offset src(j) of the region
 // at base, 8 values) are written, and store their values in LDS at
