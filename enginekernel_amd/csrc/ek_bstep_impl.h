@@ -735,6 +735,15 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
                                                    eka::align16((size_t)a.part_max * SNW * MB * 4));   // the norm's gain row
   PartWriter<MB, false> put{part, wave_id()};
   PartWriter<MB, true> add{part, wave_id()};
+  // the residual rows' words into LDS: every 16-byte unit slot of a thread
+  // is loaded (a slot past the last unit re-reads unit 0), so at 8 rows 5
+  // slots per thread, which cover hidden 2560 (2560 units) in one round (8
+  // measured 1 % slower at config 5; 4 rows keep 4: 3 measured slower);
+  // wider rows take more rounds
+  auto read_res = [&](const llw_t* src) -> bool {
+    constexpr int WR = MB == 8 ? 5 : MB;
+    return dw_read<WR>(src, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
+  };
 
   // attention unit of this workgroup (s_unit: row, split, splits, the row's
   // first slot; wave-uniform)
@@ -788,7 +797,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       __syncthreads();
       add_norm_rows<MB>(rr, nullptr, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
     } else {
-      const bool ok = dw_read<MB>(dn_prev, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
+      const bool ok = read_res(dn_prev);
       if (!wg_all(ok, s_fail)) return false;
       EK_TS(22);
       add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
@@ -839,7 +848,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     __syncthreads();
     zero_part(part, part_n);
     {
-      const bool ok = dw_read<MB>(o_ll, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
+      const bool ok = read_res(o_ll);
       if (!wg_all(ok, s_fail)) return false;
     }
     EK_TS(16);
@@ -908,7 +917,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
 
   // ---- final add + norm, lm_head, per-workgroup argmax per row
   {
-    const bool ok = dw_read<MB>(dn_prev, LinUnits{}, nrows * (h / 8), xs32, LinLds{}, a.err, a.spin);
+    const bool ok = read_res(dn_prev);
     if (!wg_all(ok, s_fail)) return false;
   }
   add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
