@@ -64,8 +64,9 @@ constexpr int SNW = SNT / EK_WAVE;     // 8 waves
 // one its polls return behind. Short contexts: a ring of 6 with 3 prefetched
 // measured 0.4 % faster than 8 with 4 (rings of 4, 5 or 7, or 2-4 ahead, no
 // better); before the dense hand-over words 6 ahead had been the best.
-// The split-attention form: 8 with 8 ahead (0.6 % faster than 6 ahead at
-// 4 K and 16 K contexts; a ring of 6 there 0.4 % slower).
+// The split-attention form: 10 with 10 ahead (0.2-0.55 % faster than 8 with
+// 8 from 1.7 K to 32 K contexts; 10 with 8, or 12 with 12, 2 % slower; 8 with
+// 8 had been 0.6 % faster than 8 with 6; a ring of 6 there 0.4 % slower).
 #ifndef EK_STEP_NB
 #define EK_STEP_NB 6
 #endif
@@ -73,10 +74,10 @@ constexpr int SNW = SNT / EK_WAVE;     // 8 waves
 #define EK_STEP_PF 3
 #endif
 #ifndef EK_STEP_NB_LONG
-#define EK_STEP_NB_LONG 8
+#define EK_STEP_NB_LONG 10
 #endif
 #ifndef EK_STEP_PF_LONG
-#define EK_STEP_PF_LONG 8
+#define EK_STEP_PF_LONG 10
 #endif
 constexpr int NB = EK_STEP_NB;
 constexpr int PF = EK_STEP_PF;
