@@ -546,10 +546,16 @@ struct PlainIO {
   bf16_t* out;               // row b's output heads, ldo_h apart
   int64_t ldo_h;
   int nq, nkv;
+  const uint32_t* epoch;     // the (row, kv head)'s epoch word; the words' tag is one more
+  uint32_t* tag_lds;         // where read_heads leaves the tag for the workgroup
+  // (read after read_heads' barrier; thread 0 loaded it behind the first key
+  // tiles, so that its round trip overlaps theirs)
+  __device__ uint32_t tag(uint32_t) const { return *tag_lds; }
   __device__ bool rope() const { return rope_on != 0; }
   __device__ int64_t cs_row(const eks::StepArgs&, int b) const { return positions ? positions[b] : b; }
   template <int D, int G>
   __device__ bool read_heads(const eks::StepArgs&, int h, bf16_t* heads, int*) const {
+    if (threadIdx.x == 0) *tag_lds = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     if (rope_on) {
       for (int i = threadIdx.x; i < (G + 2) * D; i += eks::SNT) {
         const int t = i / D, d = i - t * D;
@@ -577,12 +583,8 @@ __global__ __launch_bounds__(eks::SNT) void attn_onepass_kernel(AttnParams p, in
   __shared__ uint32_t s_tag;
   const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * p.nkv + h;
-  if (threadIdx.x == 0) {
-    s_fail = 0;
-    s_tag = __hip_atomic_load(p.ticket + 2 * bh + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-  }
-  __syncthreads();
-  const uint32_t tag = s_tag;
+  // s_fail is first read after read_heads' barrier, s_tag is written there
+  if (threadIdx.x == 0) s_fail = 0;
   eks::StepArgs a = {};
   a.nq = p.nq; a.nkv = p.nkv; a.eps = p.eps; a.sm_scale = p.sm_scale;
   a.cos = p.cos; a.sin = p.sin; a.ld_cs = p.ld_cs; a.rope_len = p.rope_len;
@@ -595,13 +597,14 @@ __global__ __launch_bounds__(eks::SNT) void attn_onepass_kernel(AttnParams p, in
   lw[eks::LW_VC] = (int64_t)p.vc;
   int64_t hi = *p.seq_len;
   hi = hi < 0 ? 0 : (hi > p.s_cap ? p.s_cap : hi);
-  const PlainIO io{p.q + b * p.ldq_b, p.ldq_h, p.rope, p.positions, p.out + b * p.ldo_b, p.ldo_h, p.nq, p.nkv};
+  const PlainIO io{p.q + b * p.ldq_b, p.ldq_h, p.rope, p.positions, p.out + b * p.ldo_b, p.ldo_h, p.nq, p.nkv,
+                   p.ticket + 2 * bh + 1, &s_tag};
   eks::long_attention<D, G>(a, lw, io, p.part + b * eks::long_words(p.nkv, p.splits, G, D), b, h, s, p.splits, hi,
-                            tag, lds, &s_fail);
+                            0u, lds, &s_fail);
   // also after a wait gave up (the error word is then set): the next launch
   // must not take this launch's words for its own
   if (s == 0 && threadIdx.x == 0)
-    __hip_atomic_store(p.ticket + 2 * bh + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p.ticket + 2 * bh + 1, s_tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The one-launch form's LDS (keys per split at most lchunk), and whether its

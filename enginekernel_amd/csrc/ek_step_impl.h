@@ -985,11 +985,14 @@ struct LongLds {
 // dense attention words. An IO type provides rope() (false: the q heads are
 // already rotated, no new row), cs_row(a, b) (the cos/sin row),
 // read_heads(a, h, heads, s_fail) (the G q heads, then with rope the new key
-// and value, as bf16 rows into LDS; false when a wait gave up) and
-// put4(h, g, d, v) (the combined output of head h G + g, dims d .. d + 3).
+// and value, as bf16 rows into LDS; false when a wait gave up),
+// put4(h, g, d, v) (the combined output of head h G + g, dims d .. d + 3)
+// and tag(t) (the exchange words' tag after read_heads: t, or one the IO
+// read during read_heads).
 struct StepIO {
   const llw_t* qkv;
   llw_t* att;
+  __device__ uint32_t tag(uint32_t t) const { return t; }
   __device__ bool rope() const { return true; }
   __device__ int64_t cs_row(const StepArgs& a, int b) const { return a.positions[b]; }
   template <int D, int G>
@@ -1093,6 +1096,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     }
     if (!io.template read_heads<D, G>(a, h, heads, s_fail)) return false;
   }
+  ltag = io.tag(ltag);
   EK_TS(28);
   if (io.rope()) {
     // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
