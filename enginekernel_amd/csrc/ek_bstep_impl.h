@@ -527,22 +527,6 @@ __device__ __forceinline__ void epilogue_swiglu_ll_b(const Gp& P, const float* p
 // and xw share the LDS), and carries the waves' partial sums (red, fixed
 // order). The gain words come from the registers gw (thread t: words
 // t + j SNT) via the LDS row gl.
-__device__ __forceinline__ uint32_t add2_bf(uint32_t r, uint32_t x) { return pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x)); }
-// ss + the squares of both halves of a word, on the bf16 dot instruction
-// (the bf16 squares are exact in fp32; one instruction instead of two
-// unpacks and two FMAs)
-__device__ __forceinline__ float sq2(uint32_t r, float ss) {
-  const ek_bf16x2 v = __builtin_bit_cast(ek_bf16x2, r);
-  return __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
-}
-// bf16(g * bf16(r * rstd)) for both halves of a word: each rounding converts
-// the two values in one instruction (rounding an already rounded value is
-// exact, so the result is that of rounding each value on its own)
-__device__ __forceinline__ uint32_t norm2(uint32_t r, uint32_t g, float rstd) {
-  const uint32_t t = pack2(lo_bf(r) * rstd, hi_bf(r) * rstd);
-  return pack2(lo_bf(g) * lo_bf(t), hi_bf(g) * hi_bf(t));
-}
-
 template <int MB>
 __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, const uint32_t* gw, uint32_t* gl,
                                               int k, int nrows, float eps, bf16_t* xs, int xstride, float* red) {

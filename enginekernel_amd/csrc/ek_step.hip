@@ -235,10 +235,8 @@ hipError_t make_plan(int64_t hidden, int64_t inter, int64_t n_q, int64_t n_kv, i
   const int n_gemv = p.nwg - n_attn;   // projection workgroups
   p.o_rows = 4 * eks::cdiv_i((int)hidden / 4, n_gemv);
   p.part_max = eks::part_rows_max((int)hidden, (int)inter, qkvw, (int)vocab, n_gemv, p.o_rows);
-  const size_t gemv = eks::step_rr_bytes((int)hidden) + eka::align16((size_t)p.kpad_max * 2) +
-                      eka::align16((size_t)p.part_max * eks::SNW * 4);
-  const size_t attn = lng ? eks::step_rr_bytes((int)hidden) + long_lds((int)head_dim, (int)g, p.lchunk)
-                          : attn_lds((int)head_dim, (int)g, s_cap);
+  const size_t gemv = eka::align16((size_t)p.kpad_max * 2) + eka::align16((size_t)p.part_max * eks::SNW * 4);
+  const size_t attn = lng ? long_lds((int)head_dim, (int)g, p.lchunk) : attn_lds((int)head_dim, (int)g, s_cap);
   p.lds = gemv > attn ? gemv : attn;
   if (p.lds > kLdsLimit)
     return ek_fail(hipErrorInvalidValue, lng ? "decode_step: the context's score rows exceed the LDS of the long-context split"

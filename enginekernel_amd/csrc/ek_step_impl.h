@@ -334,6 +334,40 @@ __device__ __forceinline__ void dw_issue(const llw_t* base, SRC src, int n, u32x
   }
 }
 
+// dw_wait: the wait alone, the words left in v (for a reader that uses them
+// in registers). dw_finish repeats its loop rather than calling it: the
+// batch kernel measured 0.5 % slower with the call.
+template <int W, typename SRC>
+__device__ __forceinline__ bool dw_wait(const llw_t* base, SRC src, int n, u32x4_t* v, int* err, int64_t spin,
+                                        int64_t* rounds = nullptr) {
+  const int tid = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t r = dw_rsrc(base);
+  int64_t it = 0;
+  while (true) {
+    bool done = true;
+#pragma unroll
+    for (int k = 0; k < W; ++k) done = done && (tid + k * SNT >= n || dw_ok2(v[k]));
+    if (done) break;
+    if (rounds) ++*rounds;
+    if (++it > spin) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    if ((it & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    // the buffer-load builtin reads as ordinary memory: without this
+    // compiler barrier a re-poll may be merged with the earlier load of the
+    // same word (the loop's only other memory operation, the error word's
+    // load, runs once in 64 rounds)
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < W; ++k) {
+      const int j = tid + k * SNT;
+      if (j < n && !dw_ok2(v[k])) v[k] = dw_get2(r, src(j));
+    }
+  }
+  return true;
+}
+
 template <int W, typename SRC, typename DST>
 __device__ __forceinline__ bool dw_finish(const llw_t* base, SRC src, int n, u32x4_t* v, uint32_t* dst, DST dix,
                                           int* err, int64_t spin, int64_t* rounds = nullptr) {
@@ -792,59 +826,79 @@ __device__ __forceinline__ void load_gain(const bf16_t* nw, int k, uint32_t* gw)
   }
 }
 
-// rr = bf16(rr + x) over the words this thread owns (x pairs in xw, or no
-// add when xw is null); xs = bf16(w * bf16(rr * rsqrt(mean(rr^2) + eps)))
-// (ek_kernels.py:1025-1059, 1296-1304)
-__device__ __forceinline__ void add_norm(float* rr, const uint32_t* xw, const uint32_t* gw, int k, int kpad,
-                                         float eps, bf16_t* xs, float* red) {
+__device__ __forceinline__ uint32_t add2_bf(uint32_t r, uint32_t x) { return pack2(lo_bf(r) + lo_bf(x), hi_bf(r) + hi_bf(x)); }
+// ss + the squares of both halves of a word, on the bf16 dot instruction
+// (the bf16 squares are exact in fp32; one instruction instead of two
+// unpacks and two FMAs)
+__device__ __forceinline__ float sq2(uint32_t r, float ss) {
+  const ek_bf16x2 v = __builtin_bit_cast(ek_bf16x2, r);
+  return __builtin_amdgcn_fdot2_f32_bf16(v, v, ss, false);
+}
+// bf16(g * bf16(r * rstd)) for both halves of a word: each rounding converts
+// the two values in one instruction (rounding an already rounded value is
+// exact, so the result is that of rounding each value on its own)
+__device__ __forceinline__ uint32_t norm2(uint32_t r, uint32_t g, float rstd) {
+  const uint32_t t = pack2(lo_bf(r) * rstd, hi_bf(r) * rstd);
+  return pack2(lo_bf(g) * lo_bf(t), hi_bf(g) * hi_bf(t));
+}
+
+
+// 16 bytes from global memory (a global, not flat, load)
+typedef const __attribute__((address_space(1))) u32x4_t global_u4_t;
+__device__ __forceinline__ uint4 ld16g(const void* p) {
+  const u32x4_t v = *(global_u4_t*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// the norm gain's unit of this thread (values 8 tid .. +7; loaded at a
+// clamped index, used only by the threads that own a unit)
+__device__ __forceinline__ uint4 load_gain_u(const bf16_t* nw, int k) {
+  const int t = threadIdx.x, nu = k / 8;
+  return ld16g(nw + 8 * (t < nu ? t : 0));
+}
+
+// The residual row held by unit: thread t < k / 8 keeps values 8 t .. +7
+// (bf16 pairs, exact: every add rounds to bf16). rres = bf16(rres + x) when
+// x is given (the hand-over unit this thread waited for, flipped words); the
+// squares' sum of the row (per thread, wave, then the workgroup in wave order
+// through red) and the wait's vote share one barrier; xs's unit t =
+// bf16(g * bf16(r * rsqrt(mean(r^2) + eps))). False when a wait gave up.
+__device__ __forceinline__ bool add_norm_u(uint4& rres, const u32x4_t* x, const uint4& g, int k, int kpad,
+                                           float eps, bf16_t* xs, float* red, bool ok, int* s_fail) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int nw = k / 2;
+  const bool mine = tid < k / 8;
   float ss = 0.f;
-  float r0v[NGW], r1v[NGW];
-  // reads at clamped indices, then masked use (no read under a lane condition)
-#pragma unroll
-  for (int j = 0; j < NGW; ++j) {
-    const int i = tid + j * SNT;
-    const int ic = i < nw ? i : 0;
-    float r0 = rr[2 * ic], r1 = rr[2 * ic + 1];
-    if (xw) {
-      const uint32_t x = xw[ic];
-      const uint32_t t = pack2(r0 + lo_bf(x), r1 + hi_bf(x));   // both bf16 adds' roundings at once
-      r0 = lo_bf(t);
-      r1 = hi_bf(t);
+  if (mine) {
+    if (x) {
+      rres.x = add2_bf(rres.x, x->x ^ DW_FLIP32);
+      rres.y = add2_bf(rres.y, x->y ^ DW_FLIP32);
+      rres.z = add2_bf(rres.z, x->z ^ DW_FLIP32);
+      rres.w = add2_bf(rres.w, x->w ^ DW_FLIP32);
     }
-    r0v[j] = r0;
-    r1v[j] = r1;
-    const float m = i < nw ? 1.f : 0.f;
-    ss = fmaf(r0 * m, r0, ss);
-    ss = fmaf(r1 * m, r1, ss);
-  }
-#pragma unroll
-  for (int j = 0; j < NGW; ++j) {
-    const int i = tid + j * SNT;
-    if (xw && i < nw) {
-      rr[2 * i] = r0v[j];
-      rr[2 * i + 1] = r1v[j];
-    }
+    ss = sq2(rres.w, sq2(rres.z, sq2(rres.y, sq2(rres.x, 0.f))));
   }
   ss = wave_sum_dpp(ss);
   if (lane == 0) red[wave] = ss;
+  if (!ok) *s_fail = 1;
   __syncthreads();
+  if (*s_fail) return false;
   float t = 0.f;
 #pragma unroll
   for (int w = 0; w < SNW; ++w) t += red[w];
   const float rstd = 1.0f / sqrtf(t / (float)k + eps);
-  uint32_t* xs32 = reinterpret_cast<uint32_t*>(xs);
-#pragma unroll
-  for (int j = 0; j < NGW; ++j) {
-    const int i = tid + j * SNT;
-    // bf16(w * bf16(r * rstd)), two values per rounding (rounding a rounded
-    // value is exact: the same result as one value at a time)
-    const uint32_t t = pack2(r0v[j] * rstd, r1v[j] * rstd);
-    if (i < nw) xs32[i] = pack2(lo_bf(gw[j]) * lo_bf(t), hi_bf(gw[j]) * hi_bf(t));
-  }
+  if (mine)
+    reinterpret_cast<uint4*>(xs)[tid] = make_uint4(norm2(rres.x, g.x, rstd), norm2(rres.y, g.y, rstd),
+                                                   norm2(rres.z, g.z, rstd), norm2(rres.w, g.w, rstd));
   zero_pad(xs, k, kpad);
+  return true;
 }
+
+// the residual unit of this thread's hand-over words: waited for into registers
+__device__ __forceinline__ bool wait_res(const llw_t* src, int k, u32x4_t* v, const StepArgs& a) {
+  dw_issue_now<1>(src, LinUnits{}, k / 8, v);
+  return dw_wait<1>(src, LinUnits{}, k / 8, v, a.err, a.spin);
+}
+
 
 // The qkv units (8 values) an attention unit of kv head h reads, in its LDS
 // order: its G query heads, the new key, the new value (byte offsets in the
@@ -1332,8 +1386,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
 // the layer's q/k/v arrive. The other workgroups run every projection and
 // the lm_head. The two roles share no state, so neither's registers are
 // live in the other's code.
-// LDS of a projection workgroup: [residual row, fp32 x h][activation row][wave partials]
-__host__ __device__ inline size_t step_rr_bytes(int h) { return eka::align16((size_t)h * 4); }
+// LDS of a projection workgroup: [activation row][wave partials] (the
+// residual row is held by unit in registers: add_norm_u)
 
 template <int D, int G>
 __device__ __forceinline__ void attention_loop(const StepArgs& a, const int64_t* lwt, uint32_t ep, int64_t hi,
@@ -1383,8 +1437,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   const int n_attn = LONG ? 0 : a.nkv * (D / eka::FDC);
   constexpr int PFM = LONG ? PF_LONG : PF;
 
-  float* rr = reinterpret_cast<float*>(smem);
-  unsigned char* ph = smem + step_rr_bytes(h);
+  unsigned char* ph = smem;
   bf16_t* xs = reinterpret_cast<bf16_t*>(ph);
   uint32_t* xs32 = reinterpret_cast<uint32_t*>(ph);
   float* part = reinterpret_cast<float*>(ph + eka::align16((size_t)a.kpad_max * 2));
@@ -1396,8 +1449,8 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   for (int u = 0; u < (LONG ? NB_LONG : NB); ++u) ring.r[u] = make_uint4(0, 0, 0, 0);
   // norm gains, loaded a phase ahead of their use: gw1 = input norm of the
   // coming layer (the final norm after the last), gw2 = post-attention norm
-  uint32_t gw1[NGW], gw2[NGW];
-  load_gain(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h, gw1);
+  uint4 gw1 = load_gain_u(reinterpret_cast<const bf16_t*>(lwt[LW_LN1]), h), gw2 = gw1;
+  uint4 rres = make_uint4(0u, 0u, 0u, 0u);   // this thread's residual unit (add_norm_u)
 
   llw_t* half = cur_half(a, ep);
   const llw_t* dn_prev = nullptr;
@@ -1419,24 +1472,13 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     if (l == 0) {
       int64_t t = a.tokens[0];
       t = t < 0 ? 0 : (t >= a.vocab ? a.vocab - 1 : t);
-      const uint32_t* e32 = reinterpret_cast<const uint32_t*>(a.embed + t * a.lde);
-      for (int i = tid; i < h / 2; i += SNT) {
-        const uint32_t x = e32[i];
-        rr[2 * i] = lo_bf(x);
-        rr[2 * i + 1] = hi_bf(x);
-      }
-      add_norm(rr, nullptr, gw1, h, kpad_of(h), a.eps, xs, s_red);
+      if (tid < h / 8) rres = ld16g(a.embed + t * a.lde + 8 * tid);
+      add_norm_u(rres, nullptr, gw1, h, kpad_of(h), a.eps, xs, s_red, true, s_fail);
     } else {
       EK_TS(22);
-#ifdef EK_STEP_TRACE
-      int64_t rounds = 0;
-      const bool ok = dw_read<HW, true>(dn_prev, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin, &rounds);
-      if (threadIdx.x == 0) ts_lds[23] = rounds;
-#else
-      const bool ok = dw_read<HW, true>(dn_prev, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin);
-#endif
-      if (!wg_all(ok, s_fail)) return false;
-      add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
+      u32x4_t v[1];
+      const bool ok = wait_res(dn_prev, h, v, a);
+      if (!add_norm_u(rres, v, gw1, h, kpad_of(h), a.eps, xs, s_red, ok, s_fail)) return false;
     }
     EK_TS(26);
     __syncthreads();
@@ -1461,7 +1503,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
         return false;
       EK_TS(4);
       prefetch_phase<PFM>(go, ring);
-      load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
+      gw2 = load_gain_u(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h);
       __syncthreads();
       zero_part(part, part_n);
       {
@@ -1486,7 +1528,7 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       prefetch_phase<PFM>(gg, ring);
       uint32_t sink = 0;
       l2_touch(gg, sink);
-      load_gain(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h, gw2);
+      gw2 = load_gain_u(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h);
       EK_TS(4);
       // ---- o projection
       zero_part(part, part_n);
@@ -1512,22 +1554,15 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
     zero_part(part, part_n);
     {
       EK_TS(15);
-#ifdef EK_STEP_TRACE
-      int64_t rounds = 0;
-      const bool ok = dw_read<HW, true>(o_ll, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin, &rounds);
-      EK_TS(16);
-      if (threadIdx.x == 0) ts_lds[18] = rounds;
-#else
-      const bool ok = dw_read<HW, true>(o_ll, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin);
-#endif
-      if (!wg_all(ok, s_fail)) return false;
+      u32x4_t v[1];
+      const bool ok = wait_res(o_ll, h, v, a);
       EK_TS(17);
+      if (!add_norm_u(rres, v, gw2, h, kpad_of(h), a.eps, xs, s_red, ok, s_fail)) return false;
     }
-    add_norm(rr, xs32, gw2, h, kpad_of(h), a.eps, xs, s_red);
     EK_TS(24);
     // the next input norm's gain loads with the gate/up stream
-    load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm,
-              h, gw1);
+    gw1 = load_gain_u(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm,
+                      h);
     EK_TS(25);
     __syncthreads();
     EK_TS(9);
@@ -1577,10 +1612,10 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
   llw_t* am_ll = half + (int64_t)a.nl * lwords;
   zero_part(part, part_n);
   {
-    const bool ok = dw_read<HW, true>(dn_prev, LinUnits{}, h / 8, xs32, LinLds{}, a.err, a.spin);
-    if (!wg_all(ok, s_fail)) return false;
+    u32x4_t v[1];
+    const bool ok = wait_res(dn_prev, h, v, a);
+    if (!add_norm_u(rres, v, gw1, h, kpad_of(h), a.eps, xs, s_red, ok, s_fail)) return false;
   }
-  add_norm(rr, xs32, gw1, h, kpad_of(h), a.eps, xs, s_red);
   __syncthreads();
   EK_TS(1);
   const Gp gl = on_gemv_wgs(make_gp(a.lm_head, h, a.vocab, 0, 1), n_attn);
@@ -1608,7 +1643,7 @@ __device__ __forceinline__ void finish_step(const StepArgs& a, uint32_t ep, bool
   const int qw = a.nq * D, qkvw = (a.nq + 2 * a.nkv) * D;
   const int n_gemv = (int)gridDim.x - n_attn;
   const llw_t* am_ll = cur_half(a, ep) + (int64_t)a.nl * arena_layer_words(h, a.inter, qkvw, qw);
-  uint32_t* amw = reinterpret_cast<uint32_t*>(smem + step_rr_bytes(h) + eka::align16((size_t)a.kpad_max * 2));
+  uint32_t* amw = reinterpret_cast<uint32_t*>(smem + eka::align16((size_t)a.kpad_max * 2));
   __syncthreads();
   if (ok) ok = wg_all(ll_read(LinSrc{am_ll + 2 * n_attn}, 2 * n_gemv, AM_TAG, amw, a.err, a.spin), s_fail);
   float ov = 0.f;
@@ -1697,13 +1732,14 @@ __global__ __launch_bounds__(SNT) void step_kernel(StepArgs a) {
 }
 
 // LDS bytes of step_kernel<D, G, LONG>: the projection layout, and either
-// an attention unit's (held apart from the residual row only by the
-// attention-only workgroups) or, for long contexts, the split attention's
-// after the residual row (lchunk: keys per split)
+// an attention unit's (the attention-only workgroups') or, for long
+// contexts, the split attention's, which overlays the projection layout
+// (lchunk: keys per split)
 template <int D, int G, bool LONG>
 inline size_t step_lds_bytes(int h, int kpad_max, int part_max, int64_t s_cap, int lchunk) {
-  const size_t gemv = step_rr_bytes(h) + eka::align16((size_t)kpad_max * 2) + eka::align16((size_t)part_max * SNW * 4);
-  const size_t attn = LONG ? step_rr_bytes(h) + LongLds<D, G>::bytes(lchunk)
+  (void)h;
+  const size_t gemv = eka::align16((size_t)kpad_max * 2) + eka::align16((size_t)part_max * SNW * 4);
+  const size_t attn = LONG ? LongLds<D, G>::bytes(lchunk)
                            : eka::align16((size_t)(G + 6) * D * 2) + eka::AttnLds<D, G>::bytes(s_cap);
   return gemv > attn ? gemv : attn;
 }

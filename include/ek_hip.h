@@ -234,7 +234,7 @@ int ek_lm_head_argmax(const void* x, const float* parts, int64_t sk_in, const vo
  * 2 or 4 (the Qwen3 dense models up to hidden 4096; other groups take the
  * per-kernel step), hidden (<= 4096), intermediate and n_q * head_dim multiples
  * of 512, and s_cap up to what one split's score rows fit in LDS (about
- * 100 K keys at n_q / n_kv = 4 on 256 CUs), on a device where one workgroup
+ * 260 K keys at n_q / n_kv = 4 on 256 CUs at one row), on a device where one workgroup
  * of the kernel fits on every CU at once (its waits need the whole grid
  * resident).
  * Plans engine/engine.py:273-282 (_make_ws) for the step below. */

@@ -294,7 +294,10 @@ def test_persistent_plan_split_bounds(dev):
     # split, 8-byte words, in each of the arena's two halves
     assert sizes[0] == short_arena + 2 * 8 * 8 * 32 * (2 * 4 + 4 * 128)
     assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 131072, 36, sizes) == 0
-    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1 << 18, 36, sizes) == 1
+    # 8192 keys per split: 4 score rows of 8193 floats and the unit's 24,320
+    # bytes within the 155,648-byte LDS budget; 16384 keys per split beyond it
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1 << 18, 36, sizes) == 0
+    assert lib.ek_decode_step_plan(2560, 9728, 32, 8, 128, 151936, 1, 1 << 19, 36, sizes) == 1
     assert b"LDS" in lib.ek_last_error()
 
 
