@@ -575,6 +575,78 @@ __device__ __forceinline__ void add_norm_rows(uint32_t* rr, const uint32_t* xw, 
   }
 }
 
+// The residual hand-over and add_norm_rows in one pass over registers: thread
+// t waits for units j = t + q SNT of the words at base (16 bytes, 8 values of
+// row j / (k / 8); every unit once, so nrows * k / 8 <= W * SNT), adds each
+// to its residual piece (rr, the same flat order) and sums the squares of the
+// wave's 64 units of round q. k is a multiple of 512, so those 64 units lie
+// in one row: their sum is chunk c = j / 64 of red, and row m's sum of
+// squares is that of its k / 512 chunks, in order. The barrier of the error
+// vote carries the chunk sums; the waited words never pass through LDS
+// (config 5: 0.7 % faster than staging them for add_norm_rows; 2-6 rows
+// 1.6-1.8 %). False (the error word set) when a wait runs out.
+template <int MB, int W>
+__device__ __forceinline__ bool dw_add_norm(const llw_t* base, uint32_t* rr, const uint32_t* gw, uint32_t* gl, int k,
+                                            int nrows, float eps, bf16_t* xs, int xstride, float* red, int* s_fail,
+                                            int* err, int64_t spin) {
+  const int tid = opaque_tid(), lane = tid & 63;
+  const int u_r = k / 8, n = nrows * u_r;
+#pragma unroll
+  for (int j = 0; j < NGW; ++j) {
+    const int i = tid + j * SNT;
+    if (i < k / 2) gl[i] = gw[j];
+  }
+  u32x4_t v[W];
+  dw_issue<W>(base, LinUnits{}, n, v);
+  const bool ok = dw_wait<W>(base, LinUnits{}, n, v, err, spin);
+  uint4* rr4 = reinterpret_cast<uint4*>(rr);
+  uint4 r[W];
+  float ss[W];
+#pragma unroll
+  for (int q = 0; q < W; ++q) {
+    const int j = tid + q * SNT;
+    ss[q] = 0.f;
+    if (j < n) {
+      const uint4 o = rr4[j];
+      r[q] = make_uint4(add2_bf(o.x, v[q].x ^ DW_FLIP32), add2_bf(o.y, v[q].y ^ DW_FLIP32),
+                        add2_bf(o.z, v[q].z ^ DW_FLIP32), add2_bf(o.w, v[q].w ^ DW_FLIP32));
+      rr4[j] = r[q];
+      ss[q] = sq2(r[q].w, sq2(r[q].z, sq2(r[q].y, sq2(r[q].x, 0.f))));
+    }
+  }
+  wave_sums_dpp_lane63<W>(ss);
+  if (lane == 63) {
+#pragma unroll
+    for (int q = 0; q < W; ++q)
+      if (tid + q * SNT < n) red[(tid + q * SNT) >> 6] = ss[q];
+  }
+  if (!wg_all(ok, s_fail)) return false;
+  const int cpr = u_r >> 6;
+  float rs = 0.f;
+  if (lane < nrows) {
+    float t = 0.f;
+    for (int c = 0; c < cpr; ++c) t += red[lane * cpr + c];
+    rs = 1.0f / sqrtf(t / (float)k + eps);
+  }
+  const uint4* g4 = reinterpret_cast<const uint4*>(gl);
+  const int xs4 = xstride / 8;
+  const uint32_t inv = (65536u + (uint32_t)cpr - 1u) / (uint32_t)cpr;
+#pragma unroll
+  for (int q = 0; q < W; ++q) {
+    const int j = __builtin_amdgcn_readfirstlane(tid - lane + q * SNT);
+    if (j < n) {
+      const int m = (int)(((uint32_t)j >> 6) * inv >> 16);
+      const float rstd = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rs), m));
+      const int c = j - m * u_r + lane;
+      const uint4 g = g4[c];
+      reinterpret_cast<uint4*>(xs)[m * xs4 + c] =
+          make_uint4(norm2(r[q].x, g.x, rstd), norm2(r[q].y, g.y, rstd), norm2(r[q].z, g.z, rstd),
+                     norm2(r[q].w, g.w, rstd));
+    }
+  }
+  return true;
+}
+
 // lm_head rows of this wave (whole rows, or whole tiles): a running
 // first-index argmax per batch row over the rows the lane receives (lane 63
 // every row of the wave on the dot path; on the tiles, row 4 t + lane / 16
@@ -781,10 +853,15 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
       __syncthreads();
       add_norm_rows<MB>(rr, nullptr, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
     } else {
-      const bool ok = read_res(dn_prev);
-      if (!wg_all(ok, s_fail)) return false;
-      EK_TS(22);
-      add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
+      constexpr int WR = MB == 8 ? 5 : MB;
+      if (nrows * (h / 8) <= WR * SNT) {
+        if (!dw_add_norm<MB, WR>(dn_prev, rr, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red, s_fail, a.err, a.spin))
+          return false;
+      } else {
+        const bool ok = read_res(dn_prev);
+        if (!wg_all(ok, s_fail)) return false;
+        add_norm_rows<MB>(rr, xs32, gw1, gain_lds, h, nrows, a.eps, xs, xld, s_red);
+      }
       EK_TS(23);
     }
     __syncthreads();
@@ -832,11 +909,16 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
     __syncthreads();
     zero_part(part, part_n);
     {
-      const bool ok = read_res(o_ll);
-      if (!wg_all(ok, s_fail)) return false;
+      constexpr int WR = MB == 8 ? 5 : MB;
+      if (nrows * (h / 8) <= WR * SNT) {
+        if (!dw_add_norm<MB, WR>(o_ll, rr, gw2, gain_lds, h, nrows, a.eps, xs, xld, s_red, s_fail, a.err, a.spin))
+          return false;
+      } else {
+        const bool ok = read_res(o_ll);
+        if (!wg_all(ok, s_fail)) return false;
+        add_norm_rows<MB>(rr, xs32, gw2, gain_lds, h, nrows, a.eps, xs, xld, s_red);
+      }
     }
-    EK_TS(16);
-    add_norm_rows<MB>(rr, xs32, gw2, gain_lds, h, nrows, a.eps, xs, xld, s_red);
     EK_TS(17);
     load_gain(l + 1 < a.nl ? reinterpret_cast<const bf16_t*>(lwt[(l + 1) * LW_FIELDS + LW_LN1]) : a.fnorm, h, gw1);
     EK_TS(18);
