@@ -81,6 +81,7 @@ struct AttnParams {
   uint32_t* ticket;           // [B * nkv][2]: arrivals of this launch, epoch
   int* err;                   // set to 1 when the combine's wait for a split gives up (may be null)
   int64_t spin;               // polls of that wait before it gives up
+  int qvec;                   // q rows and heads 16-byte aligned (the one-launch form loads them whole)
 };
 
 struct Range { int64_t lo, hi, len; };
@@ -546,17 +547,24 @@ struct PlainIO {
   bf16_t* out;               // row b's output heads, ldo_h apart
   int64_t ldo_h;
   int nq, nkv;
-  const uint32_t* epoch;     // the (row, kv head)'s epoch word; the words' tag is one more
+  // loaded at the kernel's entry, ahead of everything that depends on the
+  // row's length (no wait until the length's, which returns behind them):
+  uint32_t ep;               // the (row, kv head)'s epoch word; the words' tag is one more
   uint32_t* tag_lds;         // where read_heads leaves the tag for the workgroup
-  // (read after read_heads' barrier; thread 0 loaded it behind the first key
-  // tiles, so that its round trip overlaps theirs)
+  int hvec;                  // the heads as 16-byte pieces, hv (aligned rows)
+  uint4 hv;                  // (thread i: elements 8 i .. 8 i + 7 of the heads' LDS rows)
+  int64_t st;                // the row's first key
+  static constexpr bool kTrim = true;
   __device__ uint32_t tag(uint32_t) const { return *tag_lds; }
+  __device__ int64_t start(const eks::StepArgs&, int) const { return st; }
   __device__ bool rope() const { return rope_on != 0; }
   __device__ int64_t cs_row(const eks::StepArgs&, int b) const { return positions ? positions[b] : b; }
   template <int D, int G>
   __device__ bool read_heads(const eks::StepArgs&, int h, bf16_t* heads, int*) const {
-    if (threadIdx.x == 0) *tag_lds = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    if (rope_on) {
+    if (threadIdx.x == 0) *tag_lds = ep + 1u;
+    if (hvec) {
+      if ((int)threadIdx.x < (rope_on ? G + 2 : G) * D / 8) *reinterpret_cast<uint4*>(heads + 8 * threadIdx.x) = hv;
+    } else if (rope_on) {
       for (int i = threadIdx.x; i < (G + 2) * D; i += eks::SNT) {
         const int t = i / D, d = i - t * D;
         const int head = t < G ? h * G + t : (t == G ? nq + h : nq + nkv + h);
@@ -597,8 +605,17 @@ __global__ __launch_bounds__(eks::SNT) void attn_onepass_kernel(AttnParams p, in
   lw[eks::LW_VC] = (int64_t)p.vc;
   int64_t hi = *p.seq_len;
   hi = hi < 0 ? 0 : (hi > p.s_cap ? p.s_cap : hi);
-  const PlainIO io{p.q + b * p.ldq_b, p.ldq_h, p.rope, p.positions, p.out + b * p.ldo_b, p.ldo_h, p.nq, p.nkv,
-                   p.ticket + 2 * bh + 1, &s_tag};
+  PlainIO io{p.q + b * p.ldq_b, p.ldq_h, p.rope, p.positions, p.out + b * p.ldo_b, p.ldo_h, p.nq, p.nkv,
+             0u, &s_tag, p.qvec, make_uint4(0u, 0u, 0u, 0u), (int64_t)p.start[b]};
+  io.ep = __hip_atomic_load(p.ticket + 2 * bh + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (p.qvec && (int)threadIdx.x < (((p.rope ? G + 2 : G) * D / 8 + 63) & ~63)) {   // whole waves
+    // piece i: the q heads (rope: then the new key and value heads) in order
+    const int n16 = (p.rope ? G + 2 : G) * D / 8;
+    const int e = 8 * ((int)threadIdx.x < n16 ? (int)threadIdx.x : 0), t = e / D, d = e - t * D;
+    const bf16_t* src = p.rope ? io.q + (int64_t)(t < G ? h * G + t : (t == G ? p.nq + h : p.nq + p.nkv + h)) * D + d
+                               : io.q + (int64_t)(h * G + t) * p.ldq_h + d;
+    io.hv = *reinterpret_cast<const uint4*>(src);
+  }
   eks::long_attention<D, G>(a, lw, io, p.part + b * eks::long_words(p.nkv, p.splits, G, D), b, h, s, p.splits, hi,
                             0u, lds, &s_fail);
   // also after a wait gave up (the error word is then set): the next launch
@@ -729,6 +746,7 @@ int ek_attn_decode(const void* q, int64_t ldq_b, int64_t ldq_h, int rope, const 
   p.sm_scale = sm_scale; p.eps = eps;
   p.part = (unsigned long long*)part; p.ticket = ticket;
   p.err = err; p.spin = ek_wait_limit(int64_t(1) << 22);
+  p.qvec = (reinterpret_cast<uintptr_t>(q) & 15) == 0 && ldq_b % 8 == 0 && (rope || ldq_h % 8 == 0);
   hipStream_t st = (hipStream_t)stream;
   switch (head_dim) {
     case 32: return launch_attn_g<32>(p, (int)g, (int)b, part_words, st);

@@ -1040,13 +1040,22 @@ struct LongLds {
 // already rotated, no new row), cs_row(a, b) (the cos/sin row),
 // read_heads(a, h, heads, s_fail) (the G q heads, then with rope the new key
 // and value, as bf16 rows into LDS; false when a wait gave up),
-// put4(h, g, d, v) (the combined output of head h G + g, dims d .. d + 3)
-// and tag(t) (the exchange words' tag after read_heads: t, or one the IO
-// read during read_heads).
+// put4(h, g, d, v) (the combined output of head h G + g, dims d .. d + 3),
+// tag(t) (the exchange words' tag after read_heads: t, or one the IO read
+// before), start(a, b) (row b's first key) and kTrim: whether the key and
+// value rings stop refilling at the wave's last rows. A refill past them
+// loads row `last`, a load that the code after the ring, which takes its
+// registers, then waits for (a memory round trip); skipping them costs the
+// rings' last rounds a condition. The one-launch attention kernel gains
+// (config 3 at 4 K keys: 12.2 -> 10.7 us with the entry loads), the step
+// kernels lose (8 rows at config 5: 2 % slower).
+
 struct StepIO {
   const llw_t* qkv;
   llw_t* att;
+  static constexpr bool kTrim = false;
   __device__ uint32_t tag(uint32_t t) const { return t; }
+  __device__ int64_t start(const StepArgs& a, int b) const { return a.start_t[b]; }
   __device__ bool rope() const { return true; }
   __device__ int64_t cs_row(const StepArgs& a, int b) const { return a.positions[b]; }
   template <int D, int G>
@@ -1096,7 +1105,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   float* sc = reinterpret_cast<float*>(p0 + 2 * L::ST + L::RED + L::CMB);   // [G][stride]
   const int64_t cstride = L::stride(a.lchunk);
 
-  int64_t lo = a.start_t[b];
+  int64_t lo = io.start(a, b);
   lo = lo < 0 ? 0 : lo;
   const int64_t nrel = hi > lo ? hi - lo : 0;
   const int64_t chunk = (nrel + S - 1) / S;   // <= a.lchunk (the caller's split count ensures it)
@@ -1186,26 +1195,60 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   float mrun = -INFINITY;
   const int ntw = wave < ntile ? (int)((ntile - 1 - wave) / SNW) + 1 : 0;   // this wave's tiles
   const int srel = own ? (int)(slot - k0) : -1;                              // the new slot's key
-  for (int k = 0; k < ntw; k += UT) {
+  auto score_tile = [&](int u, int k, bool refill) {
+    const int t = wave + (k + u) * SNW;
+    const int tb = t << 4;
+    if (tb + r16 == srel) {   // the new key, from LDS
 #pragma unroll
-    for (int u = 0; u < UT; ++u) {
-      const int t = wave + (k + u) * SNW;
-      const int tb = t << 4;
-      if (tb + r16 == srel) {   // the new key, from LDS
+      for (int i = 0; i < KS; ++i) kt[u][i] = *reinterpret_cast<const uint4*>(&knew_bf[32 * i + 8 * q4]);
+    }
+    eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < KS; ++i) kt[u][i] = *reinterpret_cast<const uint4*>(&knew_bf[32 * i + 8 * q4]);
-      }
-      eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < KS; ++i) c = eka::mfma16x16x32(kt[u][i], qb[i], c);
+    if (refill) load_tile(u, t + SNW * UT);   // refill the slot
 #pragma unroll
-      for (int i = 0; i < KS; ++i) c = eka::mfma16x16x32(kt[u][i], qb[i], c);
-      load_tile(u, t + SNW * UT);   // refill the slot
+    for (int e = 0; e < 4; ++e) {
+      const int rel = tb + 4 * q4 + e;
+      const float sv = c[e] * a.sm_scale;
+      const bool ok = r16 < G && rel < nk32;
+      if (ok) sc[r16 * cstride + rel] = sv;
+      mrun = ok ? fmaxf(mrun, sv) : mrun;
+    }
+  };
+  if constexpr (IO::kTrim) {
+    // rounds whose refills all lie within the wave's tiles, then the last
+    // one or two, which refill only tiles the wave has
+    int k = 0;
+    for (; k + 2 * UT <= ntw; k += UT) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int rel = tb + 4 * q4 + e;
-        const float sv = c[e] * a.sm_scale;
-        const bool ok = r16 < G && rel < nk32;
-        if (ok) sc[r16 * cstride + rel] = sv;
-        mrun = ok ? fmaxf(mrun, sv) : mrun;
+      for (int u = 0; u < UT; ++u) score_tile(u, k, true);
+    }
+    for (; k < ntw; k += UT) {
+#pragma unroll
+      for (int u = 0; u < UT; ++u) score_tile(u, k, k + u + UT < ntw);
+    }
+  } else {
+    for (int k = 0; k < ntw; k += UT) {
+#pragma unroll
+      for (int u = 0; u < UT; ++u) {
+        const int t = wave + (k + u) * SNW;
+        const int tb = t << 4;
+        if (tb + r16 == srel) {   // the new key, from LDS
+#pragma unroll
+          for (int i = 0; i < KS; ++i) kt[u][i] = *reinterpret_cast<const uint4*>(&knew_bf[32 * i + 8 * q4]);
+        }
+        eka::f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < KS; ++i) c = eka::mfma16x16x32(kt[u][i], qb[i], c);
+        load_tile(u, t + SNW * UT);   // refill the slot
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int rel = tb + 4 * q4 + e;
+          const float sv = c[e] * a.sm_scale;
+          const bool ok = r16 < G && rel < nk32;
+          if (ok) sc[r16 * cstride + rel] = sv;
+          mrun = ok ? fmaxf(mrun, sv) : mrun;
+        }
       }
     }
   }
@@ -1214,6 +1257,10 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   // lane-contiguous across a key row), a ring of VR rows per thread
   const int dc = tid % DCH, kg = tid / DCH;
   const int nper = nk32 > kg ? (nk32 - kg + NKG - 1) / NKG : 0;
+  // the wave's most and fewest rows (its first and last lanes' key groups)
+  const int kgf = (tid & ~(EK_WAVE - 1)) / DCH, kgl = (tid | (EK_WAVE - 1)) / DCH;
+  const int nperw = nk32 > kgf ? (nk32 - kgf + NKG - 1) / NKG : 0;
+  const int npermin = nk32 > kgl ? (nk32 - kgl + NKG - 1) / NKG : 0;
   const bf16_t* vbase = vc + (k0 + kg) * a.css + 8 * dc;
   const bf16_t* vlast = vc + last * a.css + 8 * dc;
   const int vstep = NKG * (int)a.css;
@@ -1291,18 +1338,42 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     // scheduling barrier keeps each refill where it stands (the scheduler
     // otherwise sinks all of them to the loop's end, and every round then
     // waits for the whole ring)
-    int j0 = 0;
-    for (; j0 + VR <= nper; j0 += VR) {
+    if constexpr (IO::kTrim) {
+      // rounds whose rows and refills exist for every lane run unconditioned;
+      // the last one or two use each lane's own rows and refill only rows
+      // the wave has
+      int j0 = 0;
+      for (; j0 + 2 * VR <= npermin; j0 += VR) {
 #pragma unroll
-      for (int u = 0; u < VR; ++u) {
-        use(vr[u], j0 + u);
-        vr[u] = ld16_nt(vaddr(j0 + u + VR));
-        __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < VR; ++u) {
+          use(vr[u], j0 + u);
+          vr[u] = ld16_nt(vaddr(j0 + u + VR));
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
-    }
+      for (; j0 < nperw; j0 += VR) {
+        const bool whole = j0 + VR <= npermin;
 #pragma unroll
-    for (int u = 0; u < VR; ++u)
-      if (j0 + u < nper) use(vr[u], j0 + u);
+        for (int u = 0; u < VR; ++u) {
+          if (whole || j0 + u < nper) use(vr[u], j0 + u);
+          if (j0 + u + VR < nperw) vr[u] = ld16_nt(vaddr(j0 + u + VR));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+      int j0 = 0;
+      for (; j0 + VR <= nper; j0 += VR) {
+#pragma unroll
+        for (int u = 0; u < VR; ++u) {
+          use(vr[u], j0 + u);
+          vr[u] = ld16_nt(vaddr(j0 + u + VR));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < VR; ++u)
+        if (j0 + u < nper) use(vr[u], j0 + u);
+    }
     EK_TS(33);
     // key groups with the same dims: lanes dc, dc + DCH, ... of the wave, then the waves
 #pragma unroll
