@@ -1375,18 +1375,34 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
         if (j0 + u < nper) use(vr[u], j0 + u);
     }
     EK_TS(33);
-    // key groups with the same dims: lanes dc, dc + DCH, ... of the wave, then the waves
+    // key groups with the same dims: lanes dc, dc + DCH, ... of the wave, then
+    // the waves. Lanes under 16 apart add by shuffles, 16 and 32 apart by row
+    // swaps (v_permlane16_swap, v_permlane32_swap), which also transpose: the
+    // N = 8 G sums end in N / 4 registers, row r of register i holding sum
+    // i + (r & 1) N / 2 + (r >> 1) N / 4 (the same additions in the same
+    // order as a butterfly over 16 then 32 lanes)
+    constexpr int N = 8 * G;
+    float* av = &acc[0][0];
 #pragma unroll
-    for (int o = DCH; o < EK_WAVE; o <<= 1)
+    for (int o = DCH; o < 16; o <<= 1)
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+      for (int i = 0; i < N; ++i) av[i] += __shfl_xor(av[i], o, EK_WAVE);
+    float t16[N / 2], t32[N / 4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] += __shfl_xor(acc[g][e], o, EK_WAVE);
-    if (lane < DCH) {
+    for (int i = 0; i < N / 2; ++i) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(av[i]), __float_as_uint(av[i + N / 2]), false, false);
+      t16[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+    for (int i = 0; i < N / 4; ++i) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(t16[i]), __float_as_uint(t16[i + N / 4]), false, false);
+      t32[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if ((lane & 15) < DCH) {
+      const int r = lane >> 4;
+      const int off = (r & 1) * (N / 2) + (r >> 1) * (N / 4);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) red[(wave * G + g) * D + 8 * dc + e] = acc[g][e];
+      for (int i = 0; i < N / 4; ++i) red[(wave * G + (i + off) / 8) * D + 8 * dc + ((i + off) & 7)] = t32[i];
     }
   }
   EK_TS(34);
