@@ -50,10 +50,10 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 GATE_UP_TRAFFIC_B1 = 100_153_865
 GATE_UP_TRAFFIC_AT = "1ea3e7e"
 #   the persistent step kernel (step_kernel<128, 4, false>) at batch 1, context 137..146:
-#   3,963,795 KiB / 0.500067 fetched + 4,418 KiB written per launch, 1.0069x its
+#   3,965,313 KiB / 0.500066 fetched + 4,418 KiB written per launch, 1.0072x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_121_288_425
-STEP_TRAFFIC_AT = "0fb5a94"
+STEP_TRAFFIC_B1 = 8_124_409_651
+STEP_TRAFFIC_AT = "ed8b905"
 
 
 def log(msg: str) -> None:
