@@ -555,6 +555,7 @@ struct PlainIO {
   uint4 hv;                  // (thread i: elements 8 i .. 8 i + 7 of the heads' LDS rows)
   int64_t st;                // the row's first key
   static constexpr bool kTrim = true;
+  static constexpr int kLateTiles = 0;
   __device__ uint32_t tag(uint32_t) const { return *tag_lds; }
   __device__ int64_t start(const eks::StepArgs&, int) const { return st; }
   __device__ bool rope() const { return rope_on != 0; }

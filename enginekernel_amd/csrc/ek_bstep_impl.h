@@ -875,7 +875,7 @@ __device__ __forceinline__ bool batch_pass(const StepArgs& a, const int64_t* lwt
 
     // ---- split attention (its LDS overlays the activation rows and partials)
     if (attends) {
-      if (!long_attention<D, G>(a, lw, StepIO{qkv_ll + (int64_t)ub * (qkvw / 4), att_ll + (int64_t)ub * (qw / 4)},
+      if (!long_attention<D, G>(a, lw, BStepIO<MB>{StepIO{qkv_ll + (int64_t)ub * (qkvw / 4), att_ll + (int64_t)ub * (qw / 4)}},
                                 lx_row, ub, uh, us, uS, hi, (uint32_t)l + 1u, ph, s_fail
 #ifdef EK_STEP_TRACE
                                 , ts_lds

@@ -1042,18 +1042,20 @@ struct LongLds {
 // and value, as bf16 rows into LDS; false when a wait gave up),
 // put4(h, g, d, v) (the combined output of head h G + g, dims d .. d + 3),
 // tag(t) (the exchange words' tag after read_heads: t, or one the IO read
-// before), start(a, b) (row b's first key) and kTrim: whether the key and
-// value rings stop refilling at the wave's last rows. A refill past them
-// loads row `last`, a load that the code after the ring, which takes its
-// registers, then waits for (a memory round trip); skipping them costs the
-// rings' last rounds a condition. The one-launch attention kernel gains
-// (config 3 at 4 K keys: 12.2 -> 10.7 us with the entry loads), the step
-// kernels lose (8 rows at config 5: 2 % slower).
+// before), start(a, b) (row b's first key), kLateTiles (key tiles per wave
+// that load once the heads are in, beyond the LUT loaded before them) and
+// kTrim: whether the key and value rings stop refilling at the wave's last
+// rows. A refill past them loads row `last`, a load that the code after the
+// ring, which takes its registers, then waits for (a memory round trip);
+// skipping them costs the rings' last rounds a condition. The one-launch
+// attention kernel gains (config 3 at 4 K keys: 12.2 -> 10.7 us with the
+// entry loads), the step kernels lose (8 rows at config 5: 2 % slower).
 
 struct StepIO {
   const llw_t* qkv;
   llw_t* att;
   static constexpr bool kTrim = false;
+  static constexpr int kLateTiles = 0;
   __device__ uint32_t tag(uint32_t t) const { return t; }
   __device__ int64_t start(const StepArgs& a, int b) const { return a.start_t[b]; }
   __device__ bool rope() const { return true; }
@@ -1070,6 +1072,16 @@ struct StepIO {
   }
 };
 
+// The batch kernel's: at 8 rows a second key tile per wave, loaded once the
+// heads are in, so that its round trip overlaps QK-norm/RoPE and the first
+// tile's products (config 5: 2.388 -> 2.361 ms per step, 6 rows 2.349 ->
+// 2.313). Where splits hold about one tile per wave it costs: 2 and 4 rows
+// ran 1.1 % slower with it, the batch-1 split step at 4 K keys 2.5 %.
+template <int MB>
+struct BStepIO : StepIO {
+  static constexpr int kLateTiles = MB == 8 ? 1 : 0;
+};
+
 template <int D, int G, typename IO>
 // Unit (kv head h, split s of S) of batch row b; io holds row b's inputs and
 // output, lx its nkv S units' exchange words; ltag tags these words. The
@@ -1083,7 +1095,10 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
                                                ) {
   using L = LongLds<D, G>;
   constexpr int KS = D / 32;       // 32-dim k-steps of a score tile
-  constexpr int UT = LUT;          // 16-key score tiles per wave in flight
+  // 16-key score tiles per wave in flight: LUT from the start, IO::kLateTiles
+  // more once the heads are in (loads issued ahead of a hand-over's polls
+  // delay them)
+  constexpr int UT = LUT + IO::kLateTiles;
   constexpr int DCH = D / 8;       // 16-byte chunks per key row
   constexpr int NKG = SNT / DCH;   // key groups of the PV product
   constexpr int VR = LVR;          // value rows per thread in flight
@@ -1141,7 +1156,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   };
   // the first tiles load before the heads are awaited (they do not depend on them)
 #pragma unroll
-  for (int u = 0; u < UT; ++u) load_tile(u, wave + u * SNW);
+  for (int u = 0; u < LUT; ++u) load_tile(u, wave + u * SNW);
 
   // the unit's q heads, new key and new value, and the gains / cos / sin rows
   {
@@ -1160,6 +1175,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     if (!io.template read_heads<D, G>(a, h, heads, s_fail)) return false;
   }
   ltag = io.tag(ltag);
+#pragma unroll
+  for (int u = LUT; u < UT; ++u) load_tile(u, wave + u * SNW);
   EK_TS(28);
   if (io.rope()) {
     // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
