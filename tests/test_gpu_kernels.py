@@ -549,6 +549,48 @@ def test_attn_one_launch_and_pair(dev, rope, b, d, nq, nkv, slen, pads, cap, spl
     assert ws[8].cpu()[..., 1].eq(2).all() and ws[8].cpu()[..., 0].eq(0).all()
 
 
+@pytest.mark.parametrize("rope", [0, 1])
+def test_attn_one_launch_unaligned_heads(dev, rope):
+    """The one-launch kernel loads the heads as 16-byte pieces at entry when
+    the q rows and heads are 16-byte aligned, else element by element. The
+    same heads one element into a wider buffer (rows 2 bytes off 16, and an
+    odd row stride) take the element path: the output (and with rope the new
+    K/V row) must be bit-identical to the aligned call's, on two launches in
+    a row (the second at a shorter length)."""
+    b, d, nq, nkv, cap, splits = 2, 128, 32, 8, 4096, 16
+    g = _gen(4242 + rope)
+    start = torch.tensor([0, 33], dtype=torch.int32)
+    kc = torch.randn(b, nkv, cap, d, generator=g).to(BF)
+    vc = torch.randn(b, nkv, cap, d, generator=g).to(BF)
+    width = (nq + 2 * nkv) * d if rope else nq * d
+    x = torch.randn(b, width, generator=g).to(BF)
+    wide = torch.zeros(b, width + 3, dtype=BF)
+    wide[:, 1:width + 1] = x
+    xa, xu = x.to(dev), wide.to(dev)[:, 1:width + 1]
+    assert xu.data_ptr() % 16 and xu.stride(0) % 8
+    qn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF).to(dev)
+    kn = (1 + 0.1 * torch.randn(d, generator=g)).to(BF).to(dev)
+    cos_t, sin_t = (t.to(dev) for t in O.build_rope(d, 1e6, 4096))
+    pos = torch.tensor([3000, 2999], device=dev)
+    for slen in (3001, 1500):
+        outs = []
+        for src in (xa, xu):
+            ws = K.make_workspace(b, nq, nkv, d, cap, dev, splits=splits, chunk=cap // splits)
+            kcd, vcd = kc.to(dev), vc.to(dev)
+            if rope:
+                run = lambda: K.rope_attn_decode(src, qn, kn, cos_t, sin_t, kcd, vcd, torch.tensor([slen], device=dev),
+                                                 start.to(dev), ws, d ** -0.5, nq, 1e-6, positions=pos).clone()
+            else:
+                run = lambda: K.flash_decode(src.view(b, nq, d), kcd, vcd, torch.tensor([slen], device=dev),
+                                             start.to(dev), ws, d ** -0.5).clone()
+            got, ran = _attn_form(ws, nq // nkv, cap, run)
+            assert ran == "one launch", ran
+            K.check_error_word(K.ws_error(ws), "unaligned heads")
+            outs.append((got.cpu(), kcd[:, :, slen - 1].cpu(), vcd[:, :, slen - 1].cpu()))
+        for a_, u_ in zip(*outs):
+            assert torch.equal(a_, u_), (rope, slen)
+
+
 # ----------------------------------------------------------------------------
 # prefill attention (ek_model.py:315-323, SDPA with the _pack mask)
 # ----------------------------------------------------------------------------
