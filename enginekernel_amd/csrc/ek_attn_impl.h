@@ -36,7 +36,7 @@ namespace eka {
 
 // QK-norm + rotate-half RoPE of one head (one wave); writes the bf16-valued
 // result as fp32 to `dst` (LDS) and, if `gdst`, as bf16 to global memory.
-template <int D>
+template <int D, bool F32 = true>
 __device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w, const bf16_t* cr,
                                                const bf16_t* sr, float eps, float* dst, bf16_t* gdst) {
   constexpr int PER = D > 64 ? D / 64 : 1;
@@ -64,7 +64,7 @@ __device__ __forceinline__ void head_norm_rope(const bf16_t* x, const bf16_t* w,
     const float tp = rbf(bf2f(w[pd]) * rbf(xp[i] * rstd));
     const float rot = d < HALF ? -tp : tp;
     const float o = rbf(rbf(tn * bf2f(cr[d])) + rbf(rot * bf2f(sr[d])));
-    dst[d] = o;
+    if constexpr (F32) dst[d] = o;
     if (gdst) gdst[d] = (bf16_t)f2bf(o);
   }
 }
@@ -150,7 +150,7 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
   using L = AttnLds<D, G>;
   float* sc_lds = reinterpret_cast<float*>(lds);                       // [G][cap] by key - lo
   unsigned char* fx = lds + L::scores(a.cap);
-  float (*qs)[D] = reinterpret_cast<float (*)[D]>(fx);
+  bf16_t (*qs)[D] = reinterpret_cast<bf16_t (*)[D]>(fx);   // the q heads, normed and rotated (bf16)
   float* knew = reinterpret_cast<float*>(fx + L::QS);
   uint16_t* vnew = reinterpret_cast<uint16_t*>(fx + L::QS + L::KNEW);
   float (*stm)[8] = reinterpret_cast<float (*)[8]>(fx + L::QS + L::KNEW + L::VNEW);
@@ -222,14 +222,14 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
     const int units = G + ((fresh || writer) ? 1 : 0);
     for (int u = wave; u < units; u += FNW) {
       if (u < G) {
-        head_norm_rope<D>(a.qh + u * a.q_stride, a.qn, a.cr, a.sr, a.eps, qs[u], nullptr);
+        head_norm_rope<D, false>(a.qh + u * a.q_stride, a.qn, a.cr, a.sr, a.eps, nullptr, qs[u]);
       } else {
         head_norm_rope<D>(a.kh, a.kn, a.cr, a.sr, a.eps, knew, knew_bf);
       }
     }
     if (fresh && tid < FDC) vnew[tid] = a.vh[d0 + tid];
   } else {
-    for (int i = tid; i < G * D; i += FNT) qs[i / D][i % D] = bf2f(a.qh[(i / D) * a.q_stride + i % D]);
+    for (int i = tid; i < G * D; i += FNT) qs[i / D][i % D] = a.qh[(i / D) * a.q_stride + i % D];
   }
 
   __syncthreads();
@@ -243,14 +243,8 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
 #pragma unroll
   for (int i = 0; i < KS; ++i) {
     const int g = r16 < G ? r16 : 0;
-    uint32_t w[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int dd = 32 * i + 8 * q4 + 2 * e;
-      const float2 v = *reinterpret_cast<const float2*>(&qs[g][dd]);
-      w[e] = (f2bf(v.x) | (f2bf(v.y) << 16)) & qmask;
-    }
-    qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    const uint4 v = *reinterpret_cast<const uint4*>(&qs[g][32 * i + 8 * q4]);
+    qb[i] = make_uint4(v.x & qmask, v.y & qmask, v.z & qmask, v.w & qmask);
   }
   EK_ATTN_MARK(20);
   // pass 1: scores into the LDS rows and each lane's running max (no

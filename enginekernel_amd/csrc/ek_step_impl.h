@@ -1109,7 +1109,7 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
 
   bf16_t* heads = reinterpret_cast<bf16_t*>(lds);
   bf16_t* rope = reinterpret_cast<bf16_t*>(lds + L::HEADS);
-  float (*qs)[D] = reinterpret_cast<float (*)[D]>(lds + L::HEADS + L::ROPE);
+  bf16_t (*qs)[D] = reinterpret_cast<bf16_t (*)[D]>(lds + L::HEADS + L::ROPE);   // normed, rotated q (bf16)
   float* knf = reinterpret_cast<float*>(lds + L::HEADS + L::ROPE + L::QS);
   bf16_t* knew_bf = reinterpret_cast<bf16_t*>(lds + L::HEADS + L::ROPE + L::QS + L::KNF);
   unsigned char* p0 = lds + L::HEADS + L::ROPE + L::QS + L::KNF + L::KNB;
@@ -1181,11 +1181,11 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
   if (io.rope()) {
     // QK-norm + RoPE: head u < G the query heads, u = G the new key (wave u % 8)
     for (int u = wave; u <= G; u += SNW) {
-      if (u < G) eka::head_norm_rope<D>(heads + u * D, rope, rope + 2 * D, rope + 3 * D, a.eps, qs[u], nullptr);
+      if (u < G) eka::head_norm_rope<D, false>(heads + u * D, rope, rope + 2 * D, rope + 3 * D, a.eps, nullptr, qs[u]);
       else eka::head_norm_rope<D>(heads + G * D, rope + D, rope + 2 * D, rope + 3 * D, a.eps, knf, knew_bf);
     }
   } else {
-    for (int i = tid; i < G * D; i += SNT) qs[i / D][i % D] = bf2f(heads[i]);
+    for (int i = tid; i < G * D; i += SNT) qs[i / D][i % D] = heads[i];
   }
   __syncthreads();
 
@@ -1196,13 +1196,8 @@ __device__ __forceinline__ bool long_attention(const StepArgs& a, const int64_t*
     const int g = r16 < G ? r16 : 0;
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int dd = 32 * i + 8 * q4 + 2 * e;
-        w[e] = (f2bf(qs[g][dd]) | (f2bf(qs[g][dd + 1]) << 16)) & qmask;
-      }
-      qb[i] = make_uint4(w[0], w[1], w[2], w[3]);
+      const uint4 v = *reinterpret_cast<const uint4*>(&qs[g][32 * i + 8 * q4]);
+      qb[i] = make_uint4(v.x & qmask, v.y & qmask, v.z & qmask, v.w & qmask);
     }
   }
   // The wave's tiles run in rounds of UT with no early exit (an exit inside
