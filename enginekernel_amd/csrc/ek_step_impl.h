@@ -736,10 +736,11 @@ __device__ __forceinline__ float row_sum(const float* part, int r) {
 __device__ __forceinline__ void epilogue_ll(const Gp& P, const float* part, llw_t* out) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nq = (u1 - u0) / 4;
-  for (int i = threadIdx.x; i < nq; i += SNT)
-    dw_put(out + u0 / 4 + i, pack2(row_sum(part, 4 * i), row_sum(part, 4 * i + 1)),
-           pack2(row_sum(part, 4 * i + 2), row_sum(part, 4 * i + 3)));
+  // a thread per row pair (32-bit halves of the words): twice the threads of
+  // a thread per word, each with half the row sums on its path
+  const int np = (u1 - u0) / 2;
+  for (int i = threadIdx.x; i < np; i += SNT)
+    dw_put1(reinterpret_cast<uint32_t*>(out) + u0 / 2 + i, pack2(row_sum(part, 2 * i), row_sum(part, 2 * i + 1)));
 }
 
 // act = bf16(bf16(silu(bf16 g)) * bf16 u)   (ek_kernels.py:1247-1261, :1062-1076)
@@ -753,10 +754,10 @@ __device__ __forceinline__ float swiglu_one(const float* part, int nu, int ul) {
 __device__ __forceinline__ void epilogue_swiglu_ll(const Gp& P, const float* part, llw_t* out) {
   int u0, u1;
   unit_range(P, u0, u1);
-  const int nu = u1 - u0, nq = nu / 4;
-  for (int i = threadIdx.x; i < nq; i += SNT)
-    dw_put(out + u0 / 4 + i, pack2(swiglu_one(part, nu, 4 * i), swiglu_one(part, nu, 4 * i + 1)),
-           pack2(swiglu_one(part, nu, 4 * i + 2), swiglu_one(part, nu, 4 * i + 3)));
+  const int nu = u1 - u0, np = nu / 2;
+  for (int i = threadIdx.x; i < np; i += SNT)
+    dw_put1(reinterpret_cast<uint32_t*>(out) + u0 / 2 + i,
+            pack2(swiglu_one(part, nu, 2 * i), swiglu_one(part, nu, 2 * i + 1)));
 }
 
 // (a better, b) under "larger value, then lower index"; index 0x7fffffff = none
