@@ -383,14 +383,18 @@ __device__ __forceinline__ bool attn_unit(const AttnUnit& a, unsigned char* lds,
   __syncthreads();
   EK_ATTN_MARK(19);
   if (a.ll_out) {
-    for (int i = tid; i < G * FDC / 4; i += FNT) {
-      const int g = i / (FDC / 4), d = 4 * (i % (FDC / 4));
-      float t[4] = {0.f, 0.f, 0.f, 0.f};
+    // a thread per pair of dims (32-bit halves of the words): half the sums
+    // on each thread's path
+    for (int i = tid; i < G * FDC / 2; i += FNT) {
+      const int g = i / (FDC / 2), d = 2 * (i % (FDC / 2));
+      float t0 = 0.f, t1 = 0.f;
 #pragma unroll
-      for (int w = 0; w < FNW; ++w)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) t[e] += outp[w][g][d + e];
-      dw_put(a.ll_out + (g * a.out_stride + d0 + d) / 4, pack2(t[0], t[1]), pack2(t[2], t[3]));
+      for (int w = 0; w < FNW; ++w) {
+        const float2 v = *reinterpret_cast<const float2*>(&outp[w][g][d]);
+        t0 += v.x;
+        t1 += v.y;
+      }
+      dw_put1(reinterpret_cast<uint32_t*>(a.ll_out) + (g * a.out_stride + d0 + d) / 2, pack2(t0, t1));
     }
     store_new_row();
     return true;
