@@ -581,22 +581,27 @@ __device__ __forceinline__ void hold_phase(const Gp& P, uint4* ob) {
   for (int u = 0; u < OB; ++u) ob[u] = ld16_nt(span_item(sn, sn.i0 + (u < sn.n ? u : 0)) + loff);
 }
 
+// The held-by-column products: row u's partial over chunk `wave` (this
+// lane's 8 values of it in xw) -> part[u * SNW + wave]
+__device__ __forceinline__ void held_col_products(const uint4* ob, const uint4& xw, float* part, int nr) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  float acc[OB];
+#pragma unroll
+  for (int u = 0; u < OB; ++u) acc[u] = step_dot8(ob[u], xw, 0.f);
+  wave_sums_dpp_lane63<OB>(acc);
+  if (lane == 63) {
+#pragma unroll
+    for (int u = 0; u < OB; ++u)
+      if (u < nr) part[u * SNW + wave] = acc[u];
+  }
+}
+
 __device__ __forceinline__ void gemv_held_phase(const Gp& P, const uint4* ob, const bf16_t* xs, float* part) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   {
     int u0, nr;
     if (held_by_column(P, u0, nr)) {
-      // row u's partial over chunk `wave` -> part[u * SNW + wave]
-      const uint4 xw = *reinterpret_cast<const uint4*>(xs + wave * CH + lane * 8);
-      float acc[OB];
-#pragma unroll
-      for (int u = 0; u < OB; ++u) acc[u] = step_dot8(ob[u], xw, 0.f);
-      wave_sums_dpp_lane63<OB>(acc);
-      if (lane == 63) {
-#pragma unroll
-        for (int u = 0; u < OB; ++u)
-          if (u < nr) part[u * SNW + wave] = acc[u];
-      }
+      held_col_products(ob, *reinterpret_cast<const uint4*>(xs + wave * CH + lane * 8), part, nr);
       return;
     }
   }
@@ -1631,19 +1636,36 @@ __device__ __forceinline__ bool projection_pass(const StepArgs& a, const int64_t
       gw2 = load_gain_u(reinterpret_cast<const bf16_t*>(lw[LW_LN2]), h);
       EK_TS(4);
       // ---- o projection
-      zero_part(part, part_n);
-      {
-        const bool ok = dw_read<HW, true>(att_ll, LinUnits{}, qw / 8, xs32, LinLds{}, a.err, a.spin);
+      int hu0, hnr;
+      if (held_by_column(go, hu0, hnr) && qw == SNT * 8) {
+        // held by column, wave w's chunk of the attention row is its lanes'
+        // 16-byte units (thread t: unit t), the output of kv head w's
+        // attention units: each wave waits for its own chunk into registers
+        // and runs its products at once; the workgroup meets (and votes)
+        // only before the epilogue
+        u32x4_t v[1];
+        const bool ok = wait_res(att_ll, qw, v, a);
         if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
+        EK_TS(6);
+        held_col_products(ob, make_uint4(v[0].x ^ DW_FLIP32, v[0].y ^ DW_FLIP32, v[0].z ^ DW_FLIP32,
+                                          v[0].w ^ DW_FLIP32), part, hnr);
+        EK_TS(30);
         if (!wg_all(ok, s_fail)) return false;
+      } else {
+        zero_part(part, part_n);
+        {
+          const bool ok = dw_read<HW, true>(att_ll, LinUnits{}, qw / 8, xs32, LinLds{}, a.err, a.spin);
+          if (sink == 0x9e3779b9u) s_redi[0] = 0;   // keeps the L2 loads; their data is not used
+          if (!wg_all(ok, s_fail)) return false;
+        }
+        zero_pad(xs, qw, kpad_of(qw));
+        EK_TS(6);
+        __syncthreads();
+        EK_TS(29);
+        gemv_held_phase(go, ob, xs, part);
+        EK_TS(30);
+        __syncthreads();
       }
-      zero_pad(xs, qw, kpad_of(qw));
-      EK_TS(6);
-      __syncthreads();
-      EK_TS(29);
-      gemv_held_phase(go, ob, xs, part);
-      EK_TS(30);
-      __syncthreads();
       EK_TS(7);
       epilogue_ll(go, part, o_ll);
       EK_TS(8);
