@@ -50,10 +50,10 @@ PEAK_HBM = 8.0e12   # MI355X HBM3E, bytes/s (spec sheet)
 GATE_UP_TRAFFIC_B1 = 100_153_865
 GATE_UP_TRAFFIC_AT = "1ea3e7e"
 #   the persistent step kernel (step_kernel<128, 4, false>) at batch 1, context 137..146:
-#   3,966,027 KiB / 0.500065 fetched + 4,418 KiB written per launch, 1.0074x its
+#   3,966,165 KiB / 0.500066 fetched + 4,418 KiB written per launch, 1.0075x its
 #   8,065,954,304 algorithmic bytes (the rest is hand-over polling)
-STEP_TRAFFIC_B1 = 8_125_890_846
-STEP_TRAFFIC_AT = "c7d3c89"
+STEP_TRAFFIC_B1 = 8_126_157_727
+STEP_TRAFFIC_AT = "081d385"
 
 
 def log(msg: str) -> None:

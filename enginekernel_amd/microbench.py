@@ -193,11 +193,11 @@ def batch8_bytes(w_bytes: int, kv_row: int, attended: int) -> int:
 
 
 # HBM bytes per step of the batch kernel at config 5 (batch_step_kernel<128, 4, 8>), from two
-# rocprofv3 PMC runs of `bench.py --config 5 --no-cpu` (FETCH_SIZE 4,529,567 KiB scaled by
-# the 256 MiB device-copy calibration 0.500065, plus WRITE_SIZE 76,384 KiB), measured with the
+# rocprofv3 PMC runs of `bench.py --config 5 --no-cpu` (FETCH_SIZE 4,529,238 KiB scaled by
+# the 256 MiB device-copy calibration 0.500066, plus WRITE_SIZE 76,384 KiB), measured with the
 # kernel sources of the commit named; re-measure when they change
-BATCH8_TRAFFIC = 9_353_564_210
-BATCH8_TRAFFIC_AT = "c7d3c89"
+BATCH8_TRAFFIC = 9_352_871_508
+BATCH8_TRAFFIC_AT = "081d385"
 
 
 def batch8_decode(tokens: int = 256, cap: int = 8192, log=print):
