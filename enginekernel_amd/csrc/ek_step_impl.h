@@ -37,11 +37,12 @@
 // L2 to the lines l2_touch places there.
 //
 // Projections: a phase's output rows (gate/up row pairs for SwiGLU) are split
-// evenly over the workgroups in pairs (so that every output word is produced
-// by one workgroup); a workgroup's (row, 1 KiB chunk) items are split evenly
-// over its 8 waves. Lanes stream 16 B of a chunk (a wave reads 1 KiB per load
-// instruction); fp32 FMA accumulation (bf16 products are exact), a butterfly
-// per row segment, and a fixed-order sum of the waves' partials in LDS.
+// evenly over the workgroups in units of four rows (so that every output word
+// is produced by one workgroup, its two 32-bit halves by two threads); a
+// workgroup's (row, 1 KiB chunk) items are split evenly over its 8 waves.
+// Lanes stream 16 B of a chunk (a wave reads 1 KiB per load instruction); fp32
+// accumulation of exact bf16 products, a butterfly per row segment, and a
+// fixed-order sum of the waves' partials in LDS.
 //
 // Rounding points are the reference fallback's (engine/ek_model.py:360-416,
 // 475-493): bf16 residual adds, fp32 norm statistics rounded to bf16 before
